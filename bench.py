@@ -1,0 +1,216 @@
+"""Benchmark: W4A8 decode GEMV (K=2048, N=8192, one token) on one MI355X.
+
+A step is one GEMV launch (the decode combine over one CQ-W4 matrix).  The
+timed region replays a HIP graph that sweeps `--copies` distinct weight
+copies (>= 64 => > 512 MiB, so bytes come from HBM, not the 256 MiB
+Infinity Cache), bracketed by torch.cuda.synchronize() and timed with HIP
+events on the stream the kernels run on.  Algorithmic bytes per launch =
+codes N*K/2 + norms N*(K/128)*2 + int8 activations K + scales (K/128)*4 +
+f32 output N*4 = 8,685,632 B.
+
+The CPU baseline leg times the oracle (the reference's portable x86-64
+decode path restated in C, OpenMP row split as the reference's team splits
+it) on the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "needle-rs_amd"))
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+K, N, GROUP = 2048, 8192, 128
+
+
+def algorithmic_bytes(M: int, K: int, N: int) -> int:
+    G = K // GROUP
+    return N * K // 2 + N * G * 2 + M * K + M * G * 4 + M * N * 4
+
+
+def read_traffic(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (profiles/*.md)."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    return float(m.group(1)) if m else None
+
+
+def time_graph(fn_sweep, reps: int, warmup: int, torch):
+    """Capture fn_sweep (a list of launches) in a graph; return ms per replay."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fn_sweep()  # eager warm-up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn_sweep()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            g.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def gpu_gemv(args, nh, torch):
+    G = K // GROUP
+    w, x = nh.seeded_normals([N * K, K], 0)
+    w *= 0.02
+    q0 = nh.QMat.from_f32(w, N, K)
+    packed, norms = q0.download()
+    mats = [q0] + [nh.QMat.from_cq(packed, norms, N, K) for _ in range(args.copies - 1)]
+    xd = torch.from_numpy(x).cuda()
+    a = nh.QAct.new(xd, 1, K)
+    y = torch.empty(N, dtype=torch.float32, device="cuda")
+
+    def sweep():
+        for m in mats:
+            m.matmul_into(a, y, N, 0)
+
+    reps = max(1, args.steps // args.copies)
+    warm = max(1, args.warmup // args.copies)
+    ms_sweep = time_graph(sweep, reps, warm, torch)
+    ms_launch = ms_sweep / len(mats)
+    # sanity: the graph's result equals an eager launch (no oracle here)
+    ref = mats[-1].matmul(a)[0]
+    torch.cuda.synchronize()
+    if not torch.equal(ref, y):
+        raise SystemExit("graph replay and eager GEMV disagree")
+    if not torch.isfinite(y).all():
+        raise SystemExit("non-finite GEMV output")
+    nbytes = algorithmic_bytes(1, K, N)
+    gbs = nbytes / (ms_launch * 1e-3) / 1e9
+    return {"ms_launch": ms_launch, "gbs": gbs, "bytes": nbytes, "launches": reps * len(mats), "x": x,
+            "packed": packed, "norms": norms, "G": G}
+
+
+def gpu_sweeps(nh, torch):
+    """Secondary lines: the prefill GEMM sweep and the LM-head shapes."""
+    out = []
+    shapes = [(M, k, n) for M in (64, 256, 1024) for (k, n) in ((768, 2304), (768, 3072), (3072, 768))]
+    shapes += [(M, 768, 32768) for M in (1, 8, 64)]
+    for M, k, n in shapes:
+        w, x = nh.seeded_normals([n * k, M * k], 0)
+        w *= 0.02
+        copies = 8 if n * k < 8 * 2 ** 20 else 4
+        mats = [nh.QMat.from_f32(w, n, k)]
+        p, nr = mats[0].download()
+        mats += [nh.QMat.from_cq(p, nr, n, k) for _ in range(copies - 1)]
+        a = nh.QAct.new(torch.from_numpy(x).cuda(), M, k)
+        y = torch.empty((M, n), dtype=torch.float32, device="cuda")
+
+        def sweep():
+            for m in mats:
+                m.matmul_into(a, y, n, 0)
+
+        ms = time_graph(sweep, 20, 3, torch) / len(mats)
+        ops = 2.0 * M * n * k
+        nbytes = algorithmic_bytes(M, k, n)
+        tops = ops / (ms * 1e-3) / 1e12
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        ai = ops / nbytes
+        roof = min(INT8_PEAK_TOPS, ai * HBM_PEAK_GBS / 1e3)
+        out.append({"M": M, "K": k, "N": n, "us": round(ms * 1e3, 3), "TOPS": round(tops, 2),
+                    "GBs": round(gbs, 1), "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                    "frac_min_roofline": round(tops / roof, 4)})
+    return out
+
+
+def cpu_baseline(gpu, seconds: float):
+    """The oracle's decode GEMV (reference x86-64 portable path) on the host."""
+    import numpy as np
+
+    import oracle as o
+
+    threads = o.default_threads()
+    q = o.OQMat.from_cq(gpu["packed"], gpu["norms"], N, K)
+    a = o.OQAct.new(gpu["x"], 1, K)
+    y = np.zeros((1, N), dtype=np.float32)
+    q.matmul_into(a, y, N, 0, threads)  # warm-up
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        q.matmul_into(a, y, N, 0, threads)
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or calls >= 2000:
+            break
+    per = el / calls
+    return {"value": round(gpu["bytes"] / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{calls} full K=2048 N=8192 decode GEMVs over {el:.1f} s (one weight copy, host-resident)",
+            "ms_per_call": round(per * 1e3, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=12800)
+    ap.add_argument("--warmup", type=int, default=640)
+    ap.add_argument("--copies", type=int, default=64)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
+                                   "(the W4A8 path shards by output rows, see DESIGN.md)"}))
+        sys.exit(2)
+    if args.copies < 1:
+        raise SystemExit("--copies must be >= 1")
+
+    import torch
+
+    import needle_hip as nh
+
+    nh.init(0)
+    torch.cuda.synchronize()
+    gpu = gpu_gemv(args, nh, torch)
+    steps = gpu["launches"]
+    line = {
+        "metric": "W4A8 GEMV HBM GB/s (K=2048, N=8192, decode combine)",
+        "value": round(gpu["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(gpu["ms_launch"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w4(cq codebook)/a8 int8, i32 accumulate, f32 combine",
+        "data": "synthetic seeded: W=0.02*N(0,1) (threefry, seed 0) through CQ-W4 group 128; x=N(0,1)",
+        "config": {"workload": "single W4A8 decode GEMV, K=2048 N=8192 M=1, rotating "
+                               f"{args.copies} HBM-resident weight copies", "K": K, "N": N, "M": 1,
+                   "copies": args.copies, "bytes_per_launch": gpu["bytes"]},
+        "roofline": {"bound": "hbm", "achieved": round(gpu["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gpu["gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic("gemv_decode_k2048_n8192_pmc.md")},
+    }
+    if not args.no_sweep:
+        line["secondary"] = gpu_sweeps(nh, torch)
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(gpu, args.cpu_seconds)
+        line["cpu_baseline"]["gpu_over_cpu"] = round(gpu["gbs"] / line["cpu_baseline"]["value"], 1)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

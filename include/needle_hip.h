@@ -1,0 +1,127 @@
+/*
+ * needle_hip.h -- C ABI of the MI355X (gfx950) packed CQ-W4 x A8 runtime.
+ *
+ * Drop-in for the operator level of needle-rs's packed CQ runtime
+ * (crates/needle-engine/src/qlinear.rs): a Rust `needle-hip` crate binds
+ * these with `extern "C"` declarations and the
+ * QMat/QAct/QLinear methods forward to them.  Conventions follow the
+ * reference's C API (crates/needle-ffi/src/lib.rs:30-33,180-183): every
+ * entry point returns an int, 0 (or a count) on success and a negative
+ * NH_E* code on failure, with the reason in nh_last_error().  Nothing
+ * aborts across the ABI; the reference's assert!/panic sites
+ * (qlinear.rs:221,469) become NH_EINVAL.
+ *
+ * Memory: matrices and activations are opaque handles that own device
+ * memory (HBM).  Activation inputs, outputs and id lists are DEVICE
+ * pointers; archive bytes (nh_qmat_from_cq) and f32 weights
+ * (nh_qmat_from_f32) are HOST pointers borrowed for the call only, like
+ * needle_load (lib.rs:57-77).  `stream` is a hipStream_t (NULL: the null
+ * stream).  Calls on one handle are serialized by the caller, as the
+ * reference's engine mutex does (lib.rs:18-28).
+ */
+#ifndef NEEDLE_HIP_H
+#define NEEDLE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NH_OK 0
+#define NH_EINVAL (-1)   /* bad argument or shape (the reference asserts) */
+#define NH_ESMALL (-2)   /* caller buffer too small (needle_complete's -2) */
+#define NH_EDEVICE (-3)  /* HIP runtime error / no gfx950 device */
+#define NH_ENOMEM (-4)   /* device allocation failed */
+#define NH_ESTATE (-5)   /* nh_init not called */
+
+typedef struct nh_qmat nh_qmat; /* a CQ matrix resident in HBM (QMat / fused QLinear) */
+typedef struct nh_qact nh_qact; /* rotated int8 activations resident in HBM (QAct) */
+
+/* ---- runtime ----------------------------------------------------------- */
+/* Select the device and prepare the code tables.  No reference counterpart
+ * (the CPU engine needs no device); idempotent per device. */
+int nh_init(int device);
+/* Text of the last failure on this thread (needle_last_error, lib.rs:180-183). */
+const char* nh_last_error(void);
+/* Library ABI version (major*100 + minor). */
+int nh_version(void);
+
+/* ---- matrices (QMat, qlinear.rs:43-61) --------------------------------- */
+/* QMat::from_cq (qlinear.rs:220-236) over a .cact CQ blob as CqView holds
+ * it (crates/needle-core/src/cact.rs:497-525): `packed` is out x row_bytes
+ * (row_bytes = in_pad * bits / 8), `norms` is out x groups f16 bit
+ * patterns.  group must be 128 (the reference asserts); bits must be 4.
+ * The blob is re-laid out into the tiled HBM layout during the call. */
+int nh_qmat_from_cq(const uint8_t* packed, uint64_t packed_bytes, const uint16_t* norms, uint64_t norms_count,
+                    int out, int in_dim, int bits, int group, nh_qmat** h);
+/* QMat::from_f32 (qlinear.rs:239-242): cq_pack (crates/needle-core/src/quant.rs:233-256)
+ * of host f32 w[out][in_dim] run on the GPU, then uploaded as from_cq. */
+int nh_qmat_from_f32(const float* w, int out, int in_dim, nh_qmat** h);
+/* QLinear::new (qlinear.rs:501-519): parts fused by row concatenation
+ * (q|k|v|gate, crates/needle-engine/src/weights.rs:484-490).  The parts
+ * stay valid and owned by the caller. */
+int nh_qlinear_new(nh_qmat* const* parts, int n, nh_qmat** h);
+int nh_qmat_free(nh_qmat* h);
+/* out, in_dim, bits of a matrix. */
+int nh_qmat_shape(const nh_qmat* h, int* out, int* in_dim, int* bits);
+/* QMat::bytes (qlinear.rs:287-289): packed codes + f16 norms. */
+int64_t nh_qmat_bytes(const nh_qmat* h);
+/* The archive-layout codes and norms back on the host (for .cact export and
+ * checks): out x in_pad*bits/8 bytes and out x groups f16. */
+int nh_qmat_download(const nh_qmat* h, uint8_t* packed, uint64_t packed_bytes, uint16_t* norms, uint64_t norms_count);
+/* QMat::row (qlinear.rs:309-323) for each id: out[i][in_dim] = dequantized
+ * row ids[i] (embedding / engram lookups). */
+int nh_qmat_rows(const nh_qmat* h, const uint32_t* ids, int n, float* out, void* stream);
+
+/* ---- activations (QAct, qlinear.rs:63-72) ------------------------------ */
+/* QAct::empty_rows (qlinear.rs:175-178): room for up to `rows` token rows. */
+int nh_qact_new(int rows, int in_dim, int bits, nh_qact** a);
+int nh_qact_free(nh_qact* a);
+/* QAct::new (qlinear.rs:191-207): x[rows][in_dim] f32 -> per (row, 128-group)
+ * FWHT, int8 (amax * K127, round half away), scale.  With a non-NULL f16
+ * `norm_scale[in_dim]` the zero-centred RMSNorm is fused in front:
+ * zcn16 / norm_apply16 (crates/needle-engine/src/infer.rs:455-473,614-635)
+ * as the decode and prefill drivers apply it
+ * (crates/needle-engine/src/infer/step.rs:470-479, infer/chunk.rs:187-193). */
+int nh_act_prep(nh_qact* a, const float* x, int rows, int in_dim, const uint16_t* norm_scale, void* stream);
+/* Current token count of an activation. */
+int nh_qact_rows(const nh_qact* a);
+/* The int8 codes in the reference's act_pos layout (qlinear.rs:145-147)
+ * and the scales, on the host: xq[rows][groups][128], sx[rows][groups]. */
+int nh_qact_download(const nh_qact* a, int8_t* xq, uint64_t xq_bytes, float* sx, uint64_t sx_count);
+
+/* ---- products ---------------------------------------------------------- */
+/* QMat::matmul_into (qlinear.rs:468-487): y[t*ldy + col0 + r] for every
+ * token t and row r.  One token: the decode combine (qlinear.rs:340-350),
+ * else the prefill combine (qlinear.rs:353-363) with block = t < rows/4*4
+ * (qlinear.rs:397). */
+int nh_matmul(const nh_qmat* w, const nh_qact* a, float* y, int ldy, int col0, void* stream);
+/* The prefill combine with one block flag per token (1: (norm*cbs)*sx,
+ * 0: norm*(cbs*sx)): a batched feed of several <=32-token chunks gives
+ * each token its in-chunk flag (crates/needle-engine/src/infer.rs:1105-1132). */
+int nh_matmul_flags(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
+                    void* stream);
+/* QMat::single_row (qlinear.rs:454-456) for each id: out[i] = row ids[i]
+ * against token 0 with the block combine. */
+int nh_single_rows(const nh_qmat* w, const nh_qact* a, const uint32_t* ids, int n, float* out, void* stream);
+/* Model::head_logits_sparse (crates/needle-engine/src/infer.rs:1145-1166):
+ * logits[out_rows] = NEG except the ids, scored with single_row. */
+int nh_head_logits_sparse(const nh_qmat* w, const nh_qact* a, const uint32_t* ids, int n, int out_rows,
+                          float* logits, void* stream);
+/* The exact integer partial sums (qlinear.rs:325-337,356), for the
+ * bit-exact check: one token -> int32 lanes[out][groups][4]; more ->
+ * int32 totals[rows][out][groups]. */
+int nh_debug_partials(const nh_qmat* w, const nh_qact* a, int32_t* out, void* stream);
+
+/* ---- seeded inputs (host) ---------------------------------------------- */
+/* jax.random.normal for float32 from a threefry key, as
+ * crates/needle-train/src/rand.rs:205-217 computes it, into host memory. */
+int nh_normal(uint32_t key0, uint32_t key1, uint64_t n, float* out);
+/* jax.random.split (rand.rs:161-163): out = {key0, key1, sub0, sub1}. */
+int nh_split(uint32_t key0, uint32_t key1, uint32_t* out4);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,97 @@
+// Device helpers shared by the gfx950 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nh {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// A streamed 16-byte load (read once, non-temporal hint).
+__device__ __forceinline__ uint4 load_stream(const uint4* p) {
+    u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// The v_perm code tables, passed by value (scalar registers).
+struct Lut {
+    uint32_t a_hi, a_lo, b_hi, b_lo;
+};
+
+// Four selector bytes (each 0..15) -> four int8 codebook values:
+// perm(A, s) ^ perm(B, s ^ 8).  v_perm_b32 returns table bytes for
+// selector values 0..7 and 0x00 / 0xFF constants for 8..15; the tables are
+// solved on the host so the XOR of the two lookups is the codebook byte.
+__device__ __forceinline__ uint32_t expand4(uint32_t s, const Lut& t) {
+    return __builtin_amdgcn_perm(t.a_hi, t.a_lo, s) ^ __builtin_amdgcn_perm(t.b_hi, t.b_lo, s ^ 0x08080808u);
+}
+
+// One packed code dword (8 codes, LSB-first nibbles) -> int8 weights of its
+// even positions (lo) and odd positions (hi).
+__device__ __forceinline__ void expand8(uint32_t w, const Lut& t, uint32_t& lo, uint32_t& hi) {
+    lo = expand4(w & 0x0F0F0F0Fu, t);
+    hi = expand4((w >> 4) & 0x0F0F0F0Fu, t);
+}
+
+// Exact integer sum of one 16-byte code chunk (32 weights: dwords k = 0..3
+// of one decode lane) against its 32 activation bytes (x0 = k 0,1; x1 = k
+// 2,3, each dword pair [even positions, odd positions]).
+__device__ __forceinline__ int dot_chunk(uint4 c, uint4 x0, uint4 x1, const Lut& t) {
+    uint32_t lo, hi;
+    int acc = 0;
+    expand8(c.x, t, lo, hi);
+    acc = __builtin_amdgcn_sdot4((int)lo, (int)x0.x, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)hi, (int)x0.y, acc, false);
+    expand8(c.y, t, lo, hi);
+    acc = __builtin_amdgcn_sdot4((int)lo, (int)x0.z, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)hi, (int)x0.w, acc, false);
+    expand8(c.z, t, lo, hi);
+    acc = __builtin_amdgcn_sdot4((int)lo, (int)x1.x, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)hi, (int)x1.y, acc, false);
+    expand8(c.w, t, lo, hi);
+    acc = __builtin_amdgcn_sdot4((int)lo, (int)x1.z, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)hi, (int)x1.w, acc, false);
+    return acc;
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// The 128-point unnormalised Sylvester FWHT of a group held two elements
+// per lane (position p = lane in v0, p = lane + 64 in v1), stages
+// h = 1, 2, ..., 64 as crates/needle-core/src/quant.rs:91-105 orders them:
+// x[j] = a + b, x[j + h] = a - b.  Each output is one add of the same two
+// operands as on the CPU, so the result is bit-identical.
+__device__ __forceinline__ void fwht128(float& v0, float& v1, int lane) {
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1) {
+        float p0 = __shfl_xor(v0, h, 64);
+        float p1 = __shfl_xor(v1, h, 64);
+        bool upper = (lane & h) != 0;
+        v0 = upper ? (p0 - v0) : (v0 + p0);
+        v1 = upper ? (p1 - v1) : (v1 + p1);
+    }
+    float a = v0, b = v1;
+    v0 = a + b;
+    v1 = a - b;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// `(v * inv).round().clamp(-128, 127) as i8` (crates/needle-engine/src/qlinear.rs:137-139).
+__device__ __forceinline__ int8_t quant_one(float v, float inv) {
+    float r = roundf(v * inv);
+    r = fminf(fmaxf(r, -128.0f), 127.0f);
+    return (int8_t)(int)r;
+}
+
+__device__ __forceinline__ float bits_f32(uint32_t b) { return __builtin_bit_cast(float, b); }
+
+}  // namespace nh

@@ -1,0 +1,93 @@
+// Internal declarations shared by the runtime (nh_api.hip) and the kernel
+// translation units.  gfx950 only.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+namespace nh {
+
+constexpr int GROUP = 128;
+// Rows per tile of the HBM code layout: one tile-group block is 16 rows x
+// 4 lanes x 16 bytes = 1 KiB, read by one wavefront load.
+constexpr int TILE_ROWS = 16;
+// Token rows an activation buffer is padded to (the GEMM reads whole
+// 64-token tiles; padding rows hold zeros and are never stored).
+constexpr int ACT_PAD = 64;
+
+// The int8 codebook as v_perm tables: value(s) = perm(A, s) ^ perm(B, s ^ 8)
+// for the 4-bit selector s a code is stored as.
+struct LutTables {
+    uint32_t a_hi, a_lo, b_hi, b_lo;
+    uint8_t sel_of_code[16];   // code -> stored selector nibble
+    uint8_t code_of_sel[16];   // inverse
+};
+
+struct QMatMeta {
+    int out;       // logical rows
+    int out_pad;   // rows padded to TILE_ROWS
+    int in_dim;
+    int groups;
+    int bits;
+    float cbs;               // int8 codebook scale
+    int8_t vals[16];         // code -> int8 codebook value
+    float fvals[16];         // code -> f32 codebook value
+    LutTables lut;
+};
+
+}  // namespace nh
+
+struct nh_qmat {
+    nh::QMatMeta m;
+    // HBM: codes in the tiled layout (see nh_api.hip), norms [out_pad][groups]
+    // f16 bits, and the per-selector f32 codebook for row dequantization.
+    uint4* d_codes = nullptr;
+    uint16_t* d_norms = nullptr;
+    float* d_fsel = nullptr;
+    // Host copy of the archive-layout codes and norms (fusion, download).
+    std::vector<uint8_t> h_packed;   // out x groups*64
+    std::vector<uint16_t> h_norms;   // out x groups
+};
+
+struct nh_qact {
+    int cap_rows;   // allocated rows (multiple of ACT_PAD)
+    int rows;       // rows of the last prep
+    int in_dim;
+    int groups;
+    int bits;
+    int8_t* d_xq = nullptr;   // [cap_rows][groups][128], tiled act order
+    float* d_sx = nullptr;    // [cap_rows][groups]
+};
+
+namespace nh {
+
+// Error plumbing: kernels' host launchers return hipError_t.
+void set_error(const std::string& msg);
+
+// Byte offset (0..127) inside a group's activation block of natural
+// position p: dword d = p / 8 of the packed codes belongs to decode lane
+// l = d % 4 (qlinear.rs:333) and is the k = d / 4 -th dword of that lane's
+// chunk; its even positions meet bytes 0..3, its odd ones bytes 4..7.
+__host__ __device__ inline int act_offset(int p) {
+    int d = p >> 3, j = p & 7;
+    int l = d & 3, k = d >> 2;
+    return ((l * 4 + k) << 3) + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
+}
+
+// Launchers (one per kernel translation unit).
+hipError_t launch_act_prep(const float* x, int rows, int in_dim, int groups, const uint16_t* norm_scale,
+                           int8_t* xq, float* sx, hipStream_t s);
+hipError_t launch_gemv(const nh_qmat* w, const nh_qact* a, float* y, int col0, int32_t* dbg_lanes, hipStream_t s);
+hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
+                       int32_t* dbg_totals, hipStream_t s);
+hipError_t launch_single_rows(const nh_qmat* w, const nh_qact* a, const uint32_t* ids, int n, float* out,
+                              float* scatter_logits, int scatter_n, hipStream_t s);
+hipError_t launch_fill(float* p, float v, int n, hipStream_t s);
+hipError_t launch_rows(const nh_qmat* w, const uint32_t* ids, int n, float* out, hipStream_t s);
+hipError_t launch_cq_pack(const float* w, int rows, int d, int groups, const float* cb, uint8_t* packed,
+                          uint16_t* norms, hipStream_t s);
+
+}  // namespace nh

@@ -1,0 +1,324 @@
+"""Host-side mirror of needle-rs's packed CQ runtime over the MI355X C ABI.
+
+The classes follow crates/needle-engine/src/qlinear.rs (QMat, QAct,
+QLinear) method by method; every call goes through
+``libneedle_hip.so`` (include/needle_hip.h), whose gfx950 kernels do the
+work.  Device buffers are torch tensors on ``cuda:0`` (plumbing only).
+There is no CPU fallback: without a built library or a gfx950 device every
+entry point raises ``NeedleHipError``.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+import torch  # loaded first so the library binds to torch's HIP runtime
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libneedle_hip.so")
+GROUP = 128
+NEG = np.frombuffer(np.uint32(0xF149F2CA).tobytes(), dtype=np.float32)[0]
+
+# Every exported symbol of include/needle_hip.h, with (restype, argtypes).
+P = C.c_void_p
+I = C.c_int
+SIGNATURES = {
+    "nh_init": (I, [I]),
+    "nh_last_error": (C.c_char_p, []),
+    "nh_version": (I, []),
+    "nh_qmat_from_cq": (I, [P, C.c_uint64, P, C.c_uint64, I, I, I, I, P]),
+    "nh_qmat_from_f32": (I, [P, I, I, P]),
+    "nh_qlinear_new": (I, [P, I, P]),
+    "nh_qmat_free": (I, [P]),
+    "nh_qmat_shape": (I, [P, P, P, P]),
+    "nh_qmat_bytes": (C.c_int64, [P]),
+    "nh_qmat_download": (I, [P, P, C.c_uint64, P, C.c_uint64]),
+    "nh_qmat_rows": (I, [P, P, I, P, P]),
+    "nh_qact_new": (I, [I, I, I, P]),
+    "nh_qact_free": (I, [P]),
+    "nh_act_prep": (I, [P, P, I, I, P, P]),
+    "nh_qact_rows": (I, [P]),
+    "nh_qact_download": (I, [P, P, C.c_uint64, P, C.c_uint64]),
+    "nh_matmul": (I, [P, P, P, I, I, P]),
+    "nh_matmul_flags": (I, [P, P, P, P, I, I, P]),
+    "nh_single_rows": (I, [P, P, P, I, P, P]),
+    "nh_head_logits_sparse": (I, [P, P, P, I, I, P, P]),
+    "nh_debug_partials": (I, [P, P, P, P]),
+    "nh_normal": (I, [C.c_uint32, C.c_uint32, C.c_uint64, P]),
+    "nh_split": (I, [C.c_uint32, C.c_uint32, P]),
+}
+
+
+class NeedleHipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"needle_hip error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+_ready = False
+
+
+def load_library():
+    """dlopen libneedle_hip.so (no device work)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise NeedleHipError(-3, f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        lib = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+    return _lib
+
+
+def _check(rc: int) -> int:
+    if rc < 0:
+        raise NeedleHipError(rc, _lib.nh_last_error().decode(errors="replace"))
+    return rc
+
+
+def init(device: int = 0):
+    """Select the gfx950 device (nh_init)."""
+    global _ready
+    lib = load_library()
+    if not _ready:
+        if not torch.cuda.is_available():
+            raise NeedleHipError(-3, "no HIP device visible")
+        torch.cuda.set_device(device)
+        _check(lib.nh_init(device))
+        _ready = True
+    return lib
+
+
+def _stream(stream=None):
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return C.c_void_p(s.cuda_stream)
+
+
+def _dptr(t: torch.Tensor):
+    assert t.is_cuda and t.is_contiguous()
+    return C.c_void_p(t.data_ptr())
+
+
+def _hptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.c_void_p)
+
+
+class QAct:
+    """Rotated int8 activations in HBM (qlinear.rs:63-72, 166-208)."""
+
+    def __init__(self, rows: int, in_dim: int, bits: int = 4):
+        lib = init()
+        h = C.c_void_p()
+        _check(lib.nh_qact_new(rows, in_dim, bits, C.byref(h)))
+        self.h = h
+        self.cap = rows
+        self.in_dim = in_dim
+        self.bits = bits
+        self.groups = (in_dim + GROUP - 1) // GROUP
+
+    @classmethod
+    def empty_rows(cls, rows: int, in_dim: int, bits: int = 4) -> "QAct":
+        return cls(rows, in_dim, bits)
+
+    @classmethod
+    def new(cls, x: torch.Tensor, rows: int, in_dim: int, bits: int = 4, norm_scale: torch.Tensor | None = None,
+            stream=None) -> "QAct":
+        """QAct::new(x, rows, in_dim, bits); with ``norm_scale`` (f16 [in_dim])
+        the zero-centred RMSNorm is fused in front (zcn16)."""
+        a = cls(rows, in_dim, bits)
+        a.prep(x, rows, norm_scale, stream)
+        return a
+
+    def prep(self, x: torch.Tensor, rows: int | None = None, norm_scale: torch.Tensor | None = None, stream=None):
+        rows = rows if rows is not None else x.numel() // self.in_dim
+        assert x.dtype == torch.float32 and x.numel() >= rows * self.in_dim
+        ns = None
+        if norm_scale is not None:
+            assert norm_scale.dtype in (torch.float16, torch.int16, torch.uint16) and norm_scale.numel() == self.in_dim
+            ns = _dptr(norm_scale)
+        _check(_lib.nh_act_prep(self.h, _dptr(x), rows, self.in_dim, ns, _stream(stream)))
+        return self
+
+    @property
+    def rows(self) -> int:
+        return _check(_lib.nh_qact_rows(self.h))
+
+    def download(self):
+        """(xq int8 [rows, groups, 128] in act_pos order, sx f32 [rows, groups])."""
+        rows = self.rows
+        xq = np.zeros((rows, self.groups, GROUP), dtype=np.int8)
+        sx = np.zeros((rows, self.groups), dtype=np.float32)
+        _check(_lib.nh_qact_download(self.h, _hptr(xq), xq.nbytes, _hptr(sx), sx.size))
+        return xq, sx
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.nh_qact_free(self.h)
+            self.h = None
+
+
+class QMat:
+    """A CQ-W4 matrix resident in HBM (qlinear.rs:43-61, 218-488)."""
+
+    def __init__(self, h):
+        self.h = h
+        out, ind, bits = C.c_int(), C.c_int(), C.c_int()
+        _check(_lib.nh_qmat_shape(h, C.byref(out), C.byref(ind), C.byref(bits)))
+        self.out, self.in_dim, self.bits = out.value, ind.value, bits.value
+        self.groups = (self.in_dim + GROUP - 1) // GROUP
+
+    @classmethod
+    def from_cq(cls, packed: np.ndarray, norms: np.ndarray, out: int, in_dim: int, bits: int = 4,
+                group: int = GROUP) -> "QMat":
+        """QMat::from_cq over a CqView blob: packed u8 [out, row_bytes], norms f16 bits."""
+        lib = init()
+        packed = np.ascontiguousarray(packed, dtype=np.uint8)
+        norms = np.ascontiguousarray(norms, dtype=np.uint16)
+        h = C.c_void_p()
+        _check(lib.nh_qmat_from_cq(_hptr(packed), packed.nbytes, _hptr(norms), norms.size, out, in_dim, bits, group,
+                                   C.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def from_f32(cls, w: np.ndarray, out: int, in_dim: int) -> "QMat":
+        """QMat::from_f32: cq_pack on the GPU, then upload."""
+        lib = init()
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        assert w.size == out * in_dim
+        h = C.c_void_p()
+        _check(lib.nh_qmat_from_f32(_hptr(w), out, in_dim, C.byref(h)))
+        return cls(h)
+
+    def bytes(self) -> int:
+        return _check(_lib.nh_qmat_bytes(self.h))
+
+    def act_bits(self) -> int:
+        return self.bits
+
+    def download(self):
+        """(packed u8 [out, groups*64], norms u16 [out, groups]) in archive layout."""
+        packed = np.zeros((self.out, self.groups * GROUP * self.bits // 8), dtype=np.uint8)
+        norms = np.zeros((self.out, self.groups), dtype=np.uint16)
+        _check(_lib.nh_qmat_download(self.h, _hptr(packed), packed.nbytes, _hptr(norms), norms.size))
+        return packed, norms
+
+    def matmul_into(self, a: QAct, y: torch.Tensor, ldy: int, col0: int, stream=None):
+        _check(_lib.nh_matmul(self.h, a.h, _dptr(y), ldy, col0, _stream(stream)))
+
+    def matmul(self, a: QAct, stream=None) -> torch.Tensor:
+        y = torch.empty((a.rows, self.out), dtype=torch.float32, device="cuda")
+        self.matmul_into(a, y, self.out, 0, stream)
+        return y
+
+    def matmul_flags(self, a: QAct, block: torch.Tensor, stream=None) -> torch.Tensor:
+        """The prefill combine with an explicit block flag per token."""
+        y = torch.empty((a.rows, self.out), dtype=torch.float32, device="cuda")
+        assert block.dtype == torch.uint8 and block.numel() >= a.rows
+        _check(_lib.nh_matmul_flags(self.h, a.h, _dptr(block), _dptr(y), self.out, 0, _stream(stream)))
+        return y
+
+    def single_rows(self, ids: torch.Tensor, a: QAct, stream=None) -> torch.Tensor:
+        assert ids.dtype == torch.int32 or ids.dtype == torch.uint32
+        out = torch.empty(ids.numel(), dtype=torch.float32, device="cuda")
+        _check(_lib.nh_single_rows(self.h, a.h, _dptr(ids), ids.numel(), _dptr(out), _stream(stream)))
+        return out
+
+    def single_row(self, r: int, a: QAct) -> float:
+        ids = torch.tensor([r], dtype=torch.int32, device="cuda")
+        return float(self.single_rows(ids, a).cpu()[0])
+
+    def rows(self, ids: torch.Tensor, stream=None) -> torch.Tensor:
+        out = torch.empty((ids.numel(), self.in_dim), dtype=torch.float32, device="cuda")
+        _check(_lib.nh_qmat_rows(self.h, _dptr(ids), ids.numel(), _dptr(out), _stream(stream)))
+        return out
+
+    def row(self, r: int) -> torch.Tensor:
+        return self.rows(torch.tensor([r], dtype=torch.int32, device="cuda"))[0]
+
+    def partials(self, a: QAct, stream=None) -> torch.Tensor:
+        """int32 lanes [out, groups, 4] (one token) or totals [rows, out, groups]."""
+        shape = (self.out, self.groups, 4) if a.rows == 1 else (a.rows, self.out, self.groups)
+        out = torch.empty(shape, dtype=torch.int32, device="cuda")
+        _check(_lib.nh_debug_partials(self.h, a.h, _dptr(out), _stream(stream)))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.nh_qmat_free(self.h)
+            self.h = None
+
+
+class QLinear:
+    """Fused projections (qlinear.rs:493-574): parts concatenated by rows."""
+
+    def __init__(self, parts):
+        lib = init()
+        arr = (C.c_void_p * len(parts))(*[p.h.value for p in parts])
+        h = C.c_void_p()
+        _check(lib.nh_qlinear_new(C.cast(arr, C.c_void_p), len(parts), C.byref(h)))
+        self.fused = QMat(h)
+        self.out = self.fused.out
+        self.in_dim = self.fused.in_dim
+        self.part_rows = [p.out for p in parts]
+
+    def act_bits(self) -> int:
+        return self.fused.bits
+
+    def matmul(self, a: QAct, stream=None) -> torch.Tensor:
+        return self.fused.matmul(a, stream)
+
+    def rows_into(self, a: QAct, y: torch.Tensor, ldy: int, stream=None):
+        self.fused.matmul_into(a, y, ldy, 0, stream)
+
+    def apply(self, x: torch.Tensor, rows: int) -> torch.Tensor:
+        return self.matmul(QAct.new(x, rows, self.in_dim, self.act_bits()))
+
+    def bytes(self) -> int:
+        return self.fused.bytes()
+
+
+def head_logits_sparse(embedding: QMat, a: QAct, ids: torch.Tensor, out_rows: int, stream=None) -> torch.Tensor:
+    """Model::head_logits_sparse (crates/needle-engine/src/infer.rs:1145-1166)."""
+    logits = torch.empty(out_rows, dtype=torch.float32, device="cuda")
+    _check(_lib.nh_head_logits_sparse(embedding.h, a.h, _dptr(ids), ids.numel(), out_rows, _dptr(logits),
+                                      _stream(stream)))
+    return logits
+
+
+def head_logits(embedding: QMat, h: torch.Tensor, out_rows: int) -> torch.Tensor:
+    """Model::head_logits (crates/needle-engine/src/infer.rs:1135-1141)."""
+    a = QAct.new(h, 1, h.numel(), embedding.act_bits())
+    return embedding.matmul(a)[0, :out_rows]
+
+
+# ------------------------------------------------------------- seeded inputs
+def split(key):
+    """jax.random.split (crates/needle-train/src/rand.rs:161-163)."""
+    lib = load_library()
+    out = np.zeros(4, dtype=np.uint32)
+    _check(lib.nh_split(int(key[0]), int(key[1]), _hptr(out)))
+    return [int(out[0]), int(out[1])], [int(out[2]), int(out[3])]
+
+
+def normal(key, n: int) -> np.ndarray:
+    """jax.random.normal float32 (crates/needle-train/src/rand.rs:205-217)."""
+    lib = load_library()
+    out = np.zeros(n, dtype=np.float32)
+    _check(lib.nh_normal(int(key[0]), int(key[1]), n, _hptr(out)))
+    return out
+
+
+def seeded_normals(sizes, seed: int = 0):
+    """key = prng_key(seed); per tensor: (key, sub) = split(key); normal(sub, n)."""
+    key = [(seed >> 32) & 0xFFFFFFFF, seed & 0xFFFFFFFF]
+    outs = []
+    for n in sizes:
+        key, sub = split(key)
+        outs.append(normal(sub, n))
+    return outs
