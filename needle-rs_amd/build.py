@@ -31,6 +31,8 @@ FLAGS = [
     "-ffp-contract=off",
     "-fno-fast-math",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA results in ordinary VGPRs: the epilogue reads every one of them.
+    "-mllvm", "--amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-result",
 ]

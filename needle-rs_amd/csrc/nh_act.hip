@@ -16,6 +16,7 @@
 namespace nh {
 
 constexpr int ACT_THREADS = 256;
+constexpr int ACT_MAX_DIM = 32 * GROUP;  // 4096 inputs (16 KiB of LDS)
 
 __global__ __launch_bounds__(ACT_THREADS) void k_act_prep(const float* __restrict__ x, int in_dim, int groups,
                                                           const uint16_t* __restrict__ norm_scale,
@@ -23,8 +24,12 @@ __global__ __launch_bounds__(ACT_THREADS) void k_act_prep(const float* __restric
     const int row = blockIdx.x;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
-    const float* xr = x + (size_t)row * in_dim;
+    __shared__ float xr[ACT_MAX_DIM];
     __shared__ float s_r;
+    // The row once from HBM, coalesced; every later read is LDS.
+    const float* xg = x + (size_t)row * in_dim;
+    for (int i = threadIdx.x; i < in_dim; i += ACT_THREADS) xr[i] = xg[i];
+    __syncthreads();
 
     float r = 1.0f;
     if (norm_scale) {

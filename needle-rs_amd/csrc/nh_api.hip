@@ -212,8 +212,12 @@ static int upload(std::vector<uint8_t>&& packed, std::vector<uint16_t>&& norms, 
     float fsel[16];
     for (int s = 0; s < 16; ++s) fsel[s] = m.fvals[m.lut.code_of_sel[s]];
     hipError_t e;
-    if ((e = hipMalloc(&q->d_codes, tiled.size() * 4)) != hipSuccess ||
-        (e = hipMalloc(&q->d_norms, np.size() * 2)) != hipSuccess || (e = hipMalloc(&q->d_fsel, 64)) != hipSuccess) {
+    // Tail padding: the GEMM stages whole 8-group chunks, so its reads run up
+    // to 7 groups past a row's last group (codes: 7 tile-group blocks of
+    // 1 KiB; norms: 7 entries).  The padding is read, never used.
+    if ((e = hipMalloc(&q->d_codes, tiled.size() * 4 + CODE_TAIL_PAD)) != hipSuccess ||
+        (e = hipMalloc(&q->d_norms, np.size() * 2 + NORM_TAIL_PAD)) != hipSuccess ||
+        (e = hipMalloc(&q->d_fsel, 64)) != hipSuccess) {
         nh_qmat_free(q);
         return fail(NH_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
     }
@@ -422,10 +426,12 @@ int nh_qact_new(int rows, int in_dim, int bits, nh_qact** a) {
     q->groups = groups;
     q->bits = bits;
     const size_t nx = (size_t)q->cap_rows * groups * GROUP, ns = (size_t)q->cap_rows * groups;
-    hipError_t e = hipMalloc(&q->d_xq, nx);
-    if (e == hipSuccess) e = hipMalloc(&q->d_sx, ns * 4);
-    if (e == hipSuccess) e = hipMemset(q->d_xq, 0, nx);
-    if (e == hipSuccess) e = hipMemset(q->d_sx, 0, ns * 4);
+    // Tail padding for the GEMM's whole-chunk staging (up to 7 groups past
+    // the last row's end), zeroed with the rest.
+    hipError_t e = hipMalloc(&q->d_xq, nx + ACT_TAIL_PAD);
+    if (e == hipSuccess) e = hipMalloc(&q->d_sx, ns * 4 + SX_TAIL_PAD);
+    if (e == hipSuccess) e = hipMemset(q->d_xq, 0, nx + ACT_TAIL_PAD);
+    if (e == hipSuccess) e = hipMemset(q->d_sx, 0, ns * 4 + SX_TAIL_PAD);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         nh_qact_free(q);

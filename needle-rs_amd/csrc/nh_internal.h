@@ -17,6 +17,13 @@ constexpr int TILE_ROWS = 16;
 // Token rows an activation buffer is padded to (the GEMM reads whole
 // 64-token tiles; padding rows hold zeros and are never stored).
 constexpr int ACT_PAD = 64;
+// Bytes past the end of each device buffer that the GEMM's whole-chunk
+// (8-group) staging may read: 8 groups of codes per 16-row tile (1 KiB
+// each), norms, int8 activations (128 B per group) and scales.
+constexpr size_t CODE_TAIL_PAD = 8 * 1024;
+constexpr size_t NORM_TAIL_PAD = 8 * 2 * 4;
+constexpr size_t ACT_TAIL_PAD = 8 * 128;
+constexpr size_t SX_TAIL_PAD = 8 * 4 * 4;
 
 // The int8 codebook as v_perm tables: value(s) = perm(A, s) ^ perm(B, s ^ 8)
 // for the 4-bit selector s a code is stored as.
