@@ -27,28 +27,31 @@
 
 namespace nh {
 
-constexpr int GEMM_ROWS = 64;  // weight rows per workgroup (4 wavefronts x 16)
-constexpr int GC = 8;          // groups per LDS chunk
-
 __device__ __forceinline__ int swz(int tok, int b) { return b ^ (tok & 7); }
 
-template <int BM>
-__host__ __device__ constexpr size_t gemm_lds_bytes(int nbuf) {
-    return (size_t)nbuf * ((size_t)BM * GC * 128 + (size_t)BM * GC * 8 + (size_t)GEMM_ROWS * GC * 8);
+// LDS bytes of one chunk buffer: activations [tok][gi][blk] (128 B per
+// token-group), scales [gi][tok] float2, norms [gi][row] float2.
+template <int BM, int NW, int GC>
+__host__ __device__ constexpr int gemm_buf_bytes() {
+    return BM * GC * 128 + BM * GC * 8 + 16 * NW * GC * 8;
 }
 
-template <int BM, bool GENERAL, bool DBG>
-__global__ __launch_bounds__(256) void k_gemm(const uint2* __restrict__ codes, const uint16_t* __restrict__ norms,
-                                              const uint4* __restrict__ xq, const float* __restrict__ sx,
-                                              const uint8_t* __restrict__ block, int blocked, float* __restrict__ y,
-                                              int ldy, int col0, int32_t* __restrict__ dbg, int out, int out_pad,
-                                              int M, int G, float cbs, Lut lut) {
+// NW wavefronts, each owning 16 weight rows (one MFMA row tile) against all
+// BM tokens of the workgroup; K walked in chunks of GC groups.
+template <int BM, int NW, int GC, bool GENERAL, bool DBG>
+__global__ __launch_bounds__(64 * NW, 2) void k_gemm(
+    const uint2* __restrict__ codes, const uint16_t* __restrict__ norms, const uint4* __restrict__ xq,
+    const float* __restrict__ sx, const uint8_t* __restrict__ block, int blocked, float* __restrict__ y, int ldy,
+    int col0, int32_t* __restrict__ dbg, int out, int out_pad, int M, int G, float cbs, Lut lut) {
+    constexpr int T = 64 * NW;
+    constexpr int ROWS = 16 * NW;
     constexpr int TT = BM / 16;  // token tiles per wavefront
-    // LDS chunk buffer: activations [tok][gi][blk] (128 B per token-group),
-    // scales [gi][tok] float2, norms [gi][row] float2.
     constexpr int XB = BM * GC * 128;
     constexpr int SB = BM * GC * 8;
-    constexpr int BUF_BYTES = XB + SB + GEMM_ROWS * GC * 8;
+    constexpr int BUF_BYTES = gemm_buf_bytes<BM, NW, GC>();
+    constexpr int XINST = BM * GC * 8 / 64;  // 1 KiB global->LDS instructions per chunk
+    static_assert(XINST % NW == 0, "activation staging splits evenly over wavefronts");
+    static_assert((ROWS * GC) % T == 0 && (BM * GC) <= 2 * T, "table staging fits the thread count");
     extern __shared__ uint4 lds[];
     char* const lbase = reinterpret_cast<char*>(lds);
     const int nchunks = (G + GC - 1) / GC;
@@ -56,70 +59,76 @@ __global__ __launch_bounds__(256) void k_gemm(const uint2* __restrict__ codes, c
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
     const int r = lane & 15, q = lane >> 4;
-    const int row0 = blockIdx.x * GEMM_ROWS;
+    const int row0 = blockIdx.x * ROWS;
     const int m0 = blockIdx.y * BM;
     const int tile = (row0 >> 4) + wave;  // this wavefront's 16-row code tile
     const bool tile_ok = tile * 16 < out_pad;
     const int ctile = tile_ok ? tile : 0;  // clamped: loads stay in bounds
 
-    // Per-lane LDS byte offsets inside a chunk buffer; everything that
-    // varies with the tile t, the group gi or the row v is a compile-time
-    // constant folded into the ds_read offset field.
-    const uint32_t xo0 = (uint32_t)(r * GC * 128 + swz(r, q) * 16);      // B fragment, k-half 0
-    const uint32_t xo1 = (uint32_t)(r * GC * 128 + swz(r, 4 + q) * 16);  // k-half 1
-    const uint32_t so = XB + r * 8;                                       // + gi * BM * 8 + t * 128
-    const uint32_t no = XB + SB + (wave * 16 + 4 * q) * 8;                // + gi * 512 + v * 8
+    // Per-lane LDS byte offsets inside a chunk buffer; tile, group and row
+    // terms are compile-time constants folded into the ds_read offsets.
+    const uint32_t xo0 = (uint32_t)(r * GC * 128 + swz(r, q) * 16);
+    const uint32_t xo1 = (uint32_t)(r * GC * 128 + swz(r, 4 + q) * 16);
+    const uint32_t so = XB + r * 8;                         // + gi * BM * 8 + t * 128
+    const uint32_t no = XB + SB + (wave * 16 + 4 * q) * 8;  // + gi * ROWS * 8 + v * 8
 
-    // Global sources.  Codes: the two 8-byte pieces per group of this lane's
-    // A fragments (chunks l = q/2 and 2 + q/2, dword pair q & 1).
+    // Codes: the two 8-byte pieces per group of this lane's A fragments
+    // (chunks l = q/2 and 2 + q/2, dword pair q & 1).
     const uint2* cb0 = codes + (((size_t)ctile * G * 64 + r * 4 + (q >> 1)) * 2 + (q & 1));
-    const uint2* cb1 = cb0 + 4;  // chunk l + 2
-    // Activations: lane j fills slot j of a token's 1 KiB row: group j / 8,
-    // physical block j % 8 = logical block ^ (tok & 7).
-    const int xg = lane >> 3, xpb = lane & 7;
-    // Scales / norms staged through registers: thread tid covers entries
-    // tid and tid + 256 of the [gi][tok] / [gi][row] tables.
-    float s_reg[2], n_reg[2];
+    const uint2* cb1 = cb0 + 4;
+    constexpr int SPT = (BM * GC + T - 1) / T;  // scale entries per thread
+    constexpr int NPT = ROWS * GC / T;         // norm entries per thread
+    float s_reg[SPT], n_reg[NPT];
     uint2 cwa[GC][2], cwb[GC][2];
 
     // Reads past the last group of a row land in the next row or in the
-    // allocation's tail padding (one chunk's worth, see nh_api.hip); those
+    // allocation's tail padding (8 groups' worth, see nh_internal.h); those
     // slots are staged but never used.
     const size_t xrow = (size_t)G * 8;  // uint4 per token row
     auto stage_load = [&](int c, int b, uint2 (&cdst)[GC][2]) __attribute__((always_inline)) {
         const int gb = c * GC;
         char* xdst = lbase + b * BUF_BYTES;
-        const uint4* xs = xq + (size_t)(m0 + wave) * xrow + (gb + xg) * 8 + (xpb ^ wave);
 #pragma unroll
-        for (int i = 0; i < BM / 4; ++i) {
-            const int tok = i * 4 + wave;
-            // physical block xpb holds logical block xpb ^ (tok & 7); tok & 7
-            // alternates between wave and wave + 4 with i.
-            const uint4* src = xs + (size_t)i * 4 * xrow + ((i & 1) ? ((xpb ^ wave ^ 4) - (xpb ^ wave)) : 0);
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(xdst + tok * (GC * 128)), 16,
-                                             0, 0);
+        for (int i = 0; i < XINST / NW; ++i) {
+            const int k = i * NW + wave;  // this instruction's 1 KiB of the chunk buffer
+            const int u = k * 64 + lane;  // uint4 slot
+            const int tok = u / (GC * 8), rem = u % (GC * 8);
+            const int gi = rem >> 3, blk = (rem & 7) ^ (tok & 7);
+            const uint4* src = xq + (size_t)(m0 + tok) * xrow + (gb + gi) * 8 + blk;
+            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(xdst + k * 1024), 16, 0, 0);
         }
-        s_reg[0] = sx[(size_t)(m0 + (tid % BM)) * G + gb + tid / BM];
-        if constexpr (BM * GC > 256) s_reg[1] = sx[(size_t)(m0 + (tid % BM)) * G + gb + (256 + tid) / BM];
-        const int nrow = row0 + (tid & 63) < out_pad ? row0 + (tid & 63) : 0;
-        n_reg[0] = f16_bits_to_f32(norms[(size_t)nrow * G + gb + (tid >> 6)]);
-        n_reg[1] = f16_bits_to_f32(norms[(size_t)nrow * G + gb + 4 + (tid >> 6)]);
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const int L = i * T + tid;  // [gi][tok]
+            const int Lc = L < BM * GC ? L : 0;
+            s_reg[i] = sx[(size_t)(m0 + Lc % BM) * G + gb + Lc / BM];
+        }
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) {
+            const int L = i * T + tid;  // [gi][row]
+            const int row = L % ROWS;
+            const int nrow = row0 + row < out_pad ? row0 + row : 0;
+            n_reg[i] = f16_bits_to_f32(norms[(size_t)nrow * G + gb + L / ROWS]);
+        }
         const uint2* c0 = cb0 + (size_t)gb * 128;
         const uint2* c1 = cb1 + (size_t)gb * 128;
 #pragma unroll
-        for (int k = 0; k < GC; ++k) {
-            cdst[k][0] = c0[k * 128];
-            cdst[k][1] = c1[k * 128];
+        for (int kk = 0; kk < GC; ++kk) {
+            cdst[kk][0] = c0[kk * 128];
+            cdst[kk][1] = c1[kk * 128];
         }
     };
     // After the staged loads landed: the register-staged tables.
     auto stage_store = [&](int b) __attribute__((always_inline)) {
         float2* sdst = reinterpret_cast<float2*>(lbase + b * BUF_BYTES + XB);
         float2* ndst = reinterpret_cast<float2*>(lbase + b * BUF_BYTES + XB + SB);
-        sdst[tid] = make_float2(s_reg[0], cbs * s_reg[0]);
-        if constexpr (BM * GC > 256) sdst[256 + tid] = make_float2(s_reg[1], cbs * s_reg[1]);
-        ndst[tid] = make_float2(n_reg[0], n_reg[0] * cbs);
-        ndst[256 + tid] = make_float2(n_reg[1], n_reg[1] * cbs);
+#pragma unroll
+        for (int i = 0; i < SPT; ++i) {
+            const int L = i * T + tid;
+            if (L < BM * GC) sdst[L] = make_float2(s_reg[i], cbs * s_reg[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) ndst[i * T + tid] = make_float2(n_reg[i], n_reg[i] * cbs);
     };
 
     // ---- per-lane output bookkeeping: token column r of each tile
@@ -153,7 +162,7 @@ __global__ __launch_bounds__(256) void k_gemm(const uint2* __restrict__ codes, c
         }
         float2 nr[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) nr[v] = *reinterpret_cast<const float2*>(bb + no + gi * GEMM_ROWS * 8 + v * 8);
+        for (int v = 0; v < 4; ++v) nr[v] = *reinterpret_cast<const float2*>(bb + no + gi * ROWS * 8 + v * 8);
         float2 sc[TT];
 #pragma unroll
         for (int t = 0; t < TT; ++t) sc[t] = *reinterpret_cast<const float2*>(bb + so + gi * BM * 8 + t * 128);
@@ -230,54 +239,50 @@ __global__ __launch_bounds__(256) void k_gemm(const uint2* __restrict__ codes, c
     }
 }
 
-template <int BM, bool GENERAL>
+template <int BM, int NW, int GC, bool GENERAL>
 static hipError_t run(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
                       int32_t* dbg, hipStream_t s) {
     const QMatMeta& m = w->m;
     const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
     const int M = a->rows;
     const int nchunks = (m.groups + GC - 1) / GC;
-    const size_t lds = gemm_lds_bytes<BM>(nchunks > 1 ? 2 : 1);
-    dim3 grid((m.out_pad + GEMM_ROWS - 1) / GEMM_ROWS, (M + BM - 1) / BM), blockdim(256);
+    const size_t lds = (size_t)(nchunks > 1 ? 2 : 1) * gemm_buf_bytes<BM, NW, GC>();
+    dim3 grid((m.out_pad + 16 * NW - 1) / (16 * NW), (M + BM - 1) / BM), blockdim(64 * NW);
     const int blocked = M / 4 * 4;
-    if (dbg)
-        hipLaunchKernelGGL((k_gemm<BM, GENERAL, true>), grid, blockdim, lds, s, (const uint2*)w->d_codes, w->d_norms,
-                           (const uint4*)a->d_xq, a->d_sx, block, blocked, y, ldy, col0, dbg, m.out, m.out_pad, M,
-                           m.groups, m.cbs, lut);
-    else
-        hipLaunchKernelGGL((k_gemm<BM, GENERAL, false>), grid, blockdim, lds, s, (const uint2*)w->d_codes,
-                           w->d_norms, (const uint4*)a->d_xq, a->d_sx, block, blocked, y, ldy, col0, dbg, m.out,
-                           m.out_pad, M, m.groups, m.cbs, lut);
+    auto kern = dbg ? k_gemm<BM, NW, GC, GENERAL, true> : k_gemm<BM, NW, GC, GENERAL, false>;
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm<BM, NW, GC, GENERAL, true>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 2 * gemm_buf_bytes<BM, NW, GC>());
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)k_gemm<BM, NW, GC, GENERAL, false>,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 2 * gemm_buf_bytes<BM, NW, GC>());
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    hipLaunchKernelGGL(kern, grid, blockdim, lds, s, (const uint2*)w->d_codes, w->d_norms, (const uint4*)a->d_xq,
+                       a->d_sx, block, blocked, y, ldy, col0, dbg, m.out, m.out_pad, M, m.groups, m.cbs, lut);
     return hipGetLastError();
 }
 
-template <int BM>
-static void set_lds_limits() {
-    hipFuncSetAttribute((const void*)k_gemm<BM, false, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)gemm_lds_bytes<BM>(2));
-    hipFuncSetAttribute((const void*)k_gemm<BM, true, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)gemm_lds_bytes<BM>(2));
-    hipFuncSetAttribute((const void*)k_gemm<BM, false, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)gemm_lds_bytes<BM>(2));
-    hipFuncSetAttribute((const void*)k_gemm<BM, true, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                        (int)gemm_lds_bytes<BM>(2));
+template <int BM, int NW, int GC>
+static hipError_t pick(bool general, const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy,
+                       int col0, int32_t* dbg, hipStream_t s) {
+    return general ? run<BM, NW, GC, true>(w, a, block, y, ldy, col0, dbg, s)
+                   : run<BM, NW, GC, false>(w, a, block, y, ldy, col0, dbg, s);
 }
 
 hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
                        int32_t* dbg, hipStream_t s) {
-    static bool limits = false;
-    if (!limits) {
-        set_lds_limits<32>();
-        set_lds_limits<64>();
-        limits = true;
-    }
     // Tokens past rows / 4 * 4 (or flagged) take the remainder combine.
     const bool general = block != nullptr || a->rows % 4 != 0;
-    // Activation buffers hold whole multiples of 64 token rows, so both tile
-    // heights read inside the allocation.
-    if (a->rows <= 32)
-        return general ? run<32, true>(w, a, block, y, ldy, col0, dbg, s) : run<32, false>(w, a, block, y, ldy, col0, dbg, s);
-    return general ? run<64, true>(w, a, block, y, ldy, col0, dbg, s) : run<64, false>(w, a, block, y, ldy, col0, dbg, s);
+    // Four wavefronts (64 rows) per workgroup and 8-group chunks measured
+    // fastest on the prefill shapes (eight wavefronts sharing one staging
+    // were slower at M = 64 and no faster at M = 1024).  Activation buffers
+    // hold whole multiples of 64 token rows, so both tile heights read
+    // inside them.
+    if (a->rows <= 32) return pick<32, 4, 8>(general, w, a, block, y, ldy, col0, dbg, s);
+    return pick<64, 4, 8>(general, w, a, block, y, ldy, col0, dbg, s);
 }
 
 }  // namespace nh
