@@ -3,7 +3,7 @@
  *
  * Drop-in for the operator level of needle-rs's packed CQ runtime
  * (crates/needle-engine/src/qlinear.rs): a Rust `needle-hip` crate binds
- * these with `extern "C"` declarations (see INTEGRATION.md) and the
+ * these with `extern "C"` declarations and the
  * QMat/QAct/QLinear methods forward to them.  Conventions follow the
  * reference's C API (crates/needle-ffi/src/lib.rs:30-33,180-183): every
  * entry point returns an int, 0 (or a count) on success and a negative
