@@ -24,6 +24,7 @@ namespace nh {
 
 static thread_local std::string g_err;
 static int g_device = -1;
+static int g_cus = 0;
 static bool g_lut_ok = false;
 static LutTables g_lut4;
 static int8_t g_cb8[16];
@@ -32,6 +33,8 @@ static float g_cbs4;
 static std::mutex g_init_mu;
 
 void set_error(const std::string& msg) { g_err = msg; }
+
+int device_cus() { return g_cus > 0 ? g_cus : 1; }
 
 static int fail(int code, const std::string& msg) {
     set_error(msg);
@@ -212,18 +215,16 @@ static int upload(std::vector<uint8_t>&& packed, std::vector<uint16_t>&& norms, 
     float fsel[16];
     for (int s = 0; s < 16; ++s) fsel[s] = m.fvals[m.lut.code_of_sel[s]];
     hipError_t e;
-    // Tail padding: the GEMM stages whole 8-group chunks, so its reads run up
-    // to 7 groups past a row's last group (codes: 7 tile-group blocks of
-    // 1 KiB; norms: 7 entries).  The padding is read, never used.
-    if ((e = hipMalloc(&q->d_codes, tiled.size() * 4 + CODE_TAIL_PAD)) != hipSuccess ||
-        (e = hipMalloc(&q->d_norms, np.size() * 2 + NORM_TAIL_PAD)) != hipSuccess ||
-        (e = hipMalloc(&q->d_fsel, 64)) != hipSuccess) {
+    if ((e = hipMalloc(&q->d_codes, tiled.size() * 4)) != hipSuccess ||
+        (e = hipMalloc(&q->d_w8, tiled.size() * 8)) != hipSuccess ||
+        (e = hipMalloc(&q->d_norms, np.size() * 2)) != hipSuccess || (e = hipMalloc(&q->d_fsel, 64)) != hipSuccess) {
         nh_qmat_free(q);
         return fail(NH_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
     }
     if ((e = hipMemcpy(q->d_codes, tiled.data(), tiled.size() * 4, hipMemcpyHostToDevice)) != hipSuccess ||
         (e = hipMemcpy(q->d_norms, np.data(), np.size() * 2, hipMemcpyHostToDevice)) != hipSuccess ||
-        (e = hipMemcpy(q->d_fsel, fsel, 64, hipMemcpyHostToDevice)) != hipSuccess) {
+        (e = hipMemcpy(q->d_fsel, fsel, 64, hipMemcpyHostToDevice)) != hipSuccess ||
+        (e = launch_expand_w8(q, nullptr)) != hipSuccess || (e = hipDeviceSynchronize()) != hipSuccess) {
         nh_qmat_free(q);
         return hip_fail(e, "upload");
     }
@@ -298,6 +299,7 @@ int nh_init(int device) {
     if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
         return fail(NH_EDEVICE, std::string("device is ") + prop.gcnArchName + ", this library is built for gfx950");
     NH_HIP(hipSetDevice(device), "hipSetDevice");
+    NH_HIP(hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, device), "hipDeviceGetAttribute");
     if (!ensure_tables()) return fail(NH_EDEVICE, "no v_perm table pair reproduces the int8 codebook");
     g_device = device;
     return NH_OK;
@@ -353,6 +355,8 @@ int nh_qmat_from_f32(const float* w, int out, int in_dim, nh_qmat** h) {
 int nh_qlinear_new(nh_qmat* const* parts, int n, nh_qmat** h) {
     if (int rc = check_ready()) return rc;
     if (!parts || n <= 0 || !h) return fail(NH_EINVAL, "no parts");
+    for (int i = 0; i < n; ++i)
+        if (!parts[i]) return fail(NH_EINVAL, "null part");
     const QMatMeta& m0 = parts[0]->m;
     int out = 0;
     for (int i = 0; i < n; ++i) {
@@ -374,6 +378,7 @@ int nh_qlinear_new(nh_qmat* const* parts, int n, nh_qmat** h) {
 int nh_qmat_free(nh_qmat* h) {
     if (!h) return NH_OK;
     if (h->d_codes) hipFree(h->d_codes);
+    if (h->d_w8) hipFree(h->d_w8);
     if (h->d_norms) hipFree(h->d_norms);
     if (h->d_fsel) hipFree(h->d_fsel);
     delete h;
@@ -426,12 +431,10 @@ int nh_qact_new(int rows, int in_dim, int bits, nh_qact** a) {
     q->groups = groups;
     q->bits = bits;
     const size_t nx = (size_t)q->cap_rows * groups * GROUP, ns = (size_t)q->cap_rows * groups;
-    // Tail padding for the GEMM's whole-chunk staging (up to 7 groups past
-    // the last row's end), zeroed with the rest.
-    hipError_t e = hipMalloc(&q->d_xq, nx + ACT_TAIL_PAD);
-    if (e == hipSuccess) e = hipMalloc(&q->d_sx, ns * 4 + SX_TAIL_PAD);
-    if (e == hipSuccess) e = hipMemset(q->d_xq, 0, nx + ACT_TAIL_PAD);
-    if (e == hipSuccess) e = hipMemset(q->d_sx, 0, ns * 4 + SX_TAIL_PAD);
+    hipError_t e = hipMalloc(&q->d_xq, nx);
+    if (e == hipSuccess) e = hipMalloc(&q->d_sx, ns * 4);
+    if (e == hipSuccess) e = hipMemset(q->d_xq, 0, nx);
+    if (e == hipSuccess) e = hipMemset(q->d_sx, 0, ns * 4);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         nh_qact_free(q);

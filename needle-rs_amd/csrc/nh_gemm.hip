@@ -5,16 +5,23 @@
 // groups in order.  Block tokens are t < rows / 4 * 4 (qlinear.rs:397) or
 // an explicit per-token flag.
 //
-// Workgroup tile: 64 weight rows x BM tokens; wavefront w owns rows
-// 16w..16w+15 (one MFMA row tile) against all BM tokens.  The K dimension
-// is walked in chunks of up to GC groups: a chunk's activations (int8),
-// scales and norms are staged in LDS by the whole workgroup (double
-// buffered, the next chunk's global loads in flight during this chunk's
-// math), and each wavefront keeps its own rows' 4-bit codes for the chunk
-// in registers, expanding them to int8 (two v_perm lookups per four codes)
-// right before use.  Inside a chunk the groups run back to back with no
-// barrier: per group two v_mfma_i32_16x16x64_i8 per token tile into a fresh
-// int32 accumulator, then the float epilogue.
+// Weights: the GEMM reads the matrix's int8 copy (made once at upload by
+// k_expand_w8 from the 4-bit codes), stored as the MFMA A fragments
+// themselves: per 16-row tile and group, [half h][lane][16 bytes], 2 KiB.
+// Keeping the int4 -> int8 expansion out of the product removes half of
+// its vector-ALU work; the copy costs in_dim bytes per row of HBM.
+//
+// Work item: a panel of ROWS = 16 * NW weight rows x BM tokens; wavefront
+// w owns the 16-row MFMA tile w of the panel against all BM tokens.  The
+// grid is persistent: each workgroup walks its items (blockIdx.x,
+// + gridDim.x, ...) and every item's K dimension in chunks of GC groups (GC
+// divides G), as one flat sequence of steps.  A step's activations (int8),
+// scales and norms are staged in LDS by the whole workgroup, double
+// buffered; each wavefront's A fragments go straight to registers.  The
+// next step's global loads (possibly the next item's first chunk) are in
+// flight while this step computes; the activations are then written to the
+// other LDS buffer.  Per group: two v_mfma_i32_16x16x64_i8 per token tile
+// into a fresh int32 accumulator, then the float epilogue.
 //
 // MFMA operand note: lane L supplies A and B bytes of the same k-slice
 // (L / 16), both cut from the same 16-byte block of the group's activation
@@ -29,131 +36,194 @@ namespace nh {
 
 __device__ __forceinline__ int swz(int tok, int b) { return b ^ (tok & 7); }
 
-// LDS bytes of one chunk buffer: activations [tok][gi][blk] (128 B per
-// token-group), scales [gi][tok] float2, norms [gi][row] float2.
-template <int BM, int NW, int GC>
-__host__ __device__ constexpr int gemm_buf_bytes() {
-    return BM * GC * 128 + BM * GC * 8 + 16 * NW * GC * 8;
+// The int8 A-fragment copy of a tiled code matrix: one wavefront per
+// (16-row tile, group).  Lane L = 16 q + r holds row r's k-block q of each
+// 64-wide half: the 8-byte code pieces of chunks l = q / 2 (half 0) and
+// 2 + q / 2 (half 1), dword pair q & 1, expanded to int8.
+__global__ __launch_bounds__(64) void k_expand_w8(const uint2* __restrict__ codes, uint4* __restrict__ w8, Lut lut) {
+    const int tg = blockIdx.x;  // tile * G + g
+    const int lane = threadIdx.x;
+    const int r = lane & 15, q = lane >> 4;
+    const uint2* c = codes + (((size_t)tg * 64 + r * 4 + (q >> 1)) * 2 + (q & 1));
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint2 cw = c[h * 4];
+        uint32_t e0, e1, e2, e3;
+        expand8(cw.x, lut, e0, e1);
+        expand8(cw.y, lut, e2, e3);
+        w8[((size_t)tg * 2 + h) * 64 + lane] = make_uint4(e0, e1, e2, e3);
+    }
 }
 
-// NW wavefronts, each owning 16 weight rows (one MFMA row tile) against all
-// BM tokens of the workgroup; K walked in chunks of GC groups.
+hipError_t launch_expand_w8(const nh_qmat* w, hipStream_t s) {
+    const QMatMeta& m = w->m;
+    const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
+    const int blocks = m.out_pad / 16 * m.groups;
+    hipLaunchKernelGGL(k_expand_w8, dim3(blocks), dim3(64), 0, s, (const uint2*)w->d_codes, w->d_w8, lut);
+    return hipGetLastError();
+}
+
+// Dynamic LDS bytes of one step buffer: activations [tok][gi][blk] (128 B
+// per token-group, 16-byte blocks swizzled by token).  The scale
+// ([gi][tok]) and norm ([gi][row]) float2 tables are a static LDS array.
+template <int BM, int GC>
+__host__ __device__ constexpr int gemm_act_bytes() {
+    return BM * GC * 128;
+}
+
 template <int BM, int NW, int GC, bool GENERAL, bool DBG>
-__global__ __launch_bounds__(64 * NW, 2) void k_gemm(
-    const uint2* __restrict__ codes, const uint16_t* __restrict__ norms, const uint4* __restrict__ xq,
+__global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
+    const uint4* __restrict__ w8, const uint16_t* __restrict__ norms, const uint4* __restrict__ xq,
     const float* __restrict__ sx, const uint8_t* __restrict__ block, int blocked, float* __restrict__ y, int ldy,
-    int col0, int32_t* __restrict__ dbg, int out, int out_pad, int M, int G, float cbs, Lut lut) {
+    int col0, int vec_store, int32_t* __restrict__ dbg, int out, int out_pad, int M, int G, float cbs, int panels,
+    int items) {
     constexpr int T = 64 * NW;
     constexpr int ROWS = 16 * NW;
     constexpr int TT = BM / 16;  // token tiles per wavefront
     constexpr int XB = BM * GC * 128;
     constexpr int SB = BM * GC * 8;
-    constexpr int BUF_BYTES = gemm_buf_bytes<BM, NW, GC>();
-    constexpr int XINST = BM * GC * 8 / 64;  // 1 KiB global->LDS instructions per chunk
-    static_assert(XINST % NW == 0, "activation staging splits evenly over wavefronts");
-    static_assert((ROWS * GC) % T == 0 && (BM * GC) <= 2 * T, "table staging fits the thread count");
+    constexpr int TAB = BM * GC + ROWS * GC;  // float2 entries per table buffer
+    static_assert(XB % (1024 * NW) == 0, "activation staging splits evenly over wavefronts");
+    constexpr int XPT = XB / 1024 / NW;           // 16-byte activation loads per thread per step
+    constexpr int SPT = (BM * GC + T - 1) / T;    // scale entries per thread
+    constexpr int NPT = (ROWS * GC + T - 1) / T;  // norm entries per thread
     extern __shared__ uint4 lds[];
+    __shared__ float2 tabs[2][TAB];
     char* const lbase = reinterpret_cast<char*>(lds);
-    const int nchunks = (G + GC - 1) / GC;
+    const int nchunks = G / GC;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, in an SGPR
     const int r = lane & 15, q = lane >> 4;
-    const int row0 = blockIdx.x * ROWS;
-    const int m0 = blockIdx.y * BM;
-    const int tile = (row0 >> 4) + wave;  // this wavefront's 16-row code tile
-    const bool tile_ok = tile * 16 < out_pad;
-    const int ctile = tile_ok ? tile : 0;  // clamped: loads stay in bounds
+    const int my_items = (items - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int nsteps = my_items * nchunks;
+    if (nsteps <= 0) return;
 
-    // Per-lane LDS byte offsets inside a chunk buffer; tile, group and row
-    // terms are compile-time constants folded into the ds_read offsets.
+    // Per-lane constants.  Activation slot u = (i * NW + wave) * 64 + lane
+    // of a step buffer holds token u / (8 GC), group (u / 8) % GC and
+    // 16-byte block (u % 8) ^ (token & 7) of that token's group.
+    uint32_t xoff[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+        const int u = (i * NW + wave) * 64 + lane;
+        const int tok = u / (GC * 8), rem = u % (GC * 8);
+        xoff[i] = (uint32_t)(tok * G * 128 + (rem >> 3) * 128 + ((rem & 7) ^ (tok & 7)) * 16);
+    }
     const uint32_t xo0 = (uint32_t)(r * GC * 128 + swz(r, q) * 16);
     const uint32_t xo1 = (uint32_t)(r * GC * 128 + swz(r, 4 + q) * 16);
-    const uint32_t so = XB + r * 8;                         // + gi * BM * 8 + t * 128
-    const uint32_t no = XB + SB + (wave * 16 + 4 * q) * 8;  // + gi * ROWS * 8 + v * 8
+    const uint32_t so = r * 8;                          // + gi * BM * 8 + t * 128
+    const uint32_t no = SB + (wave * 16 + 4 * q) * 8;  // + gi * ROWS * 8 + v * 8
 
-    // Codes: the two 8-byte pieces per group of this lane's A fragments
-    // (chunks l = q/2 and 2 + q/2, dword pair q & 1).
-    const uint2* cb0 = codes + (((size_t)ctile * G * 64 + r * 4 + (q >> 1)) * 2 + (q & 1));
-    const uint2* cb1 = cb0 + 4;
-    constexpr int SPT = (BM * GC + T - 1) / T;  // scale entries per thread
-    constexpr int NPT = ROWS * GC / T;         // norm entries per thread
-    float s_reg[SPT], n_reg[NPT];
-    uint2 cwa[GC][2], cwb[GC][2];
-
-    // Reads past the last group of a row land in the next row or in the
-    // allocation's tail padding (8 groups' worth, see nh_internal.h); those
-    // slots are staged but never used.
-    const size_t xrow = (size_t)G * 8;  // uint4 per token row
-    auto stage_load = [&](int c, int b, uint2 (&cdst)[GC][2]) __attribute__((always_inline)) {
-        const int gb = c * GC;
-        char* xdst = lbase + b * BUF_BYTES;
-#pragma unroll
-        for (int i = 0; i < XINST / NW; ++i) {
-            const int k = i * NW + wave;  // this instruction's 1 KiB of the chunk buffer
-            const int u = k * 64 + lane;  // uint4 slot
-            const int tok = u / (GC * 8), rem = u % (GC * 8);
-            const int gi = rem >> 3, blk = (rem & 7) ^ (tok & 7);
-            const uint4* src = xq + (size_t)(m0 + tok) * xrow + (gb + gi) * 8 + blk;
-            __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(xdst + k * 1024), 16, 0, 0);
+    // Step bookkeeping: item k of this workgroup, chunk c.  The division
+    // runs once per item.
+    struct Pos {
+        int k, c, row0, m0;
+    };
+    auto set_item = [&](Pos& p) __attribute__((always_inline)) {
+        const int item = (int)blockIdx.x + p.k * (int)gridDim.x;
+        const int tt = item / panels;
+        p.row0 = (item - tt * panels) * ROWS;
+        p.m0 = tt * BM;
+    };
+    auto advance = [&](Pos& p) __attribute__((always_inline)) {
+        if (++p.c == nchunks) {
+            p.c = 0;
+            if (p.k + 1 < my_items) {
+                ++p.k;
+                set_item(p);
+            } else {
+                p.c = nchunks - 1;  // past the last step: reload the last step
+            }
         }
+    };
+
+    u32x4 xr[XPT];
+    float s_reg[SPT];
+    uint16_t n_reg[NPT];
+    v4i aa[GC][2], ab[GC][2];
+
+    // The global loads of step p: activations, tables and this wavefront's
+    // A fragments into registers.  Tables stay raw until stage_store (a
+    // conversion here would wait on every load in flight).
+    auto stage_load = [&](const Pos& p, v4i (&adst)[GC][2]) __attribute__((always_inline)) {
+        const int gb = p.c * GC;
+        const char* xbase = reinterpret_cast<const char*>(xq) + ((size_t)p.m0 * G + gb) * 128;
+#pragma unroll
+        for (int i = 0; i < XPT; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xbase + xoff[i]);
 #pragma unroll
         for (int i = 0; i < SPT; ++i) {
             const int L = i * T + tid;  // [gi][tok]
             const int Lc = L < BM * GC ? L : 0;
-            s_reg[i] = sx[(size_t)(m0 + Lc % BM) * G + gb + Lc / BM];
+            s_reg[i] = sx[(size_t)(p.m0 + Lc % BM) * G + gb + Lc / BM];
         }
 #pragma unroll
         for (int i = 0; i < NPT; ++i) {
             const int L = i * T + tid;  // [gi][row]
-            const int row = L % ROWS;
-            const int nrow = row0 + row < out_pad ? row0 + row : 0;
-            n_reg[i] = f16_bits_to_f32(norms[(size_t)nrow * G + gb + L / ROWS]);
+            const int Lc = L < ROWS * GC ? L : 0;
+            const int row = p.row0 + Lc % ROWS;
+            n_reg[i] = norms[(size_t)(row < out_pad ? row : 0) * G + gb + Lc / ROWS];
         }
-        const uint2* c0 = cb0 + (size_t)gb * 128;
-        const uint2* c1 = cb1 + (size_t)gb * 128;
+        const int tile = (p.row0 >> 4) + wave;
+        const int ctile = tile * 16 < out_pad ? tile : 0;  // clamped: loads stay in bounds
+        const v4i* a = reinterpret_cast<const v4i*>(w8) + ((size_t)ctile * G + gb) * 128 + lane;
 #pragma unroll
-        for (int kk = 0; kk < GC; ++kk) {
-            cdst[kk][0] = c0[kk * 128];
-            cdst[kk][1] = c1[kk * 128];
+        for (int gi = 0; gi < GC; ++gi) {
+            adst[gi][0] = a[gi * 128];
+            adst[gi][1] = a[gi * 128 + 64];
         }
     };
-    // After the staged loads landed: the register-staged tables.
+    // After the loads landed: activations and tables into LDS buffer b.
     auto stage_store = [&](int b) __attribute__((always_inline)) {
-        float2* sdst = reinterpret_cast<float2*>(lbase + b * BUF_BYTES + XB);
-        float2* ndst = reinterpret_cast<float2*>(lbase + b * BUF_BYTES + XB + SB);
+        char* xdst = lbase + b * XB;
+#pragma unroll
+        for (int i = 0; i < XPT; ++i) *reinterpret_cast<u32x4*>(xdst + (i * NW + wave) * 1024 + lane * 16) = xr[i];
 #pragma unroll
         for (int i = 0; i < SPT; ++i) {
             const int L = i * T + tid;
-            if (L < BM * GC) sdst[L] = make_float2(s_reg[i], cbs * s_reg[i]);
+            if ((BM * GC) % T == 0 || L < BM * GC) tabs[b][L] = make_float2(s_reg[i], cbs * s_reg[i]);
         }
 #pragma unroll
-        for (int i = 0; i < NPT; ++i) ndst[i * T + tid] = make_float2(n_reg[i], n_reg[i] * cbs);
+        for (int i = 0; i < NPT; ++i) {
+            const int L = i * T + tid;
+            const float nv = f16_bits_to_f32(n_reg[i]);
+            if ((ROWS * GC) % T == 0 || L < ROWS * GC) tabs[b][BM * GC + L] = make_float2(nv, nv * cbs);
+        }
     };
 
-    // ---- per-lane output bookkeeping: token column r of each tile
-    bool blk[TT];
-#pragma unroll
-    for (int t = 0; t < TT; ++t) {
-        const int m = m0 + t * 16 + r;
-        blk[t] = !GENERAL || (m < M ? (block ? block[m] != 0 : m < blocked) : true);
-    }
     float acc[TT][4];
+    bool blk[TT];
+    Pos cur{0, 0, 0, 0}, nxt, done{0, 0, 0, 0};
+    set_item(cur);
+    auto begin_item = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < TT; ++t)
+        for (int t = 0; t < TT; ++t) {
+            const int m = cur.m0 + t * 16 + r;
+            blk[t] = !GENERAL || (m < M ? (block ? block[m] != 0 : m < blocked) : true);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[t][v] = 0.0f;
+            for (int v = 0; v < 4; ++v) acc[t][v] = 0.0f;
+        }
+    };
+    auto end_item = [&](const Pos& p) __attribute__((always_inline)) {
+        if (!y) return;
+        const int n0 = p.row0 + wave * 16 + 4 * q;
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const int m = p.m0 + t * 16 + r;
+            if (m >= M) continue;
+            float* dst = y + (size_t)m * ldy + col0 + n0;
+            if (vec_store && n0 + 3 < out) {
+                *reinterpret_cast<float4*>(dst) = make_float4(acc[t][0], acc[t][1], acc[t][2], acc[t][3]);
+            } else {
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (n0 + v < out) dst[v] = acc[t][v];
+            }
+        }
+    };
 
-    // One group: all B fragments, every tile's two MFMAs into its own
-    // accumulator (independent, so they pipeline), then the epilogues.
-    auto do_group = [&](const uint2 (&cg)[2], const char* bb, int gi, int g) __attribute__((always_inline)) {
-        uint32_t e0, e1, e2, e3, f0, f1, f2, f3;
-        expand8(cg[0].x, lut, e0, e1);
-        expand8(cg[0].y, lut, e2, e3);
-        expand8(cg[1].x, lut, f0, f1);
-        expand8(cg[1].y, lut, f2, f3);
-        const v4i a0 = {(int)e0, (int)e1, (int)e2, (int)e3};
-        const v4i a1 = {(int)f0, (int)f1, (int)f2, (int)f3};
+    // One group: B fragments from LDS, every token tile's two MFMAs into its
+    // own accumulator (independent, so they pipeline), then the epilogues.
+    auto do_group = [&](const v4i (&ag)[GC][2], const char* bb, const char* tb, int gi) __attribute__((always_inline)) {
         v4i b0[TT], b1[TT];
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
@@ -162,23 +232,23 @@ __global__ __launch_bounds__(64 * NW, 2) void k_gemm(
         }
         float2 nr[4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) nr[v] = *reinterpret_cast<const float2*>(bb + no + gi * ROWS * 8 + v * 8);
+        for (int v = 0; v < 4; ++v) nr[v] = *reinterpret_cast<const float2*>(tb + no + gi * ROWS * 8 + v * 8);
         float2 sc[TT];
 #pragma unroll
-        for (int t = 0; t < TT; ++t) sc[t] = *reinterpret_cast<const float2*>(bb + so + gi * BM * 8 + t * 128);
+        for (int t = 0; t < TT; ++t) sc[t] = *reinterpret_cast<const float2*>(tb + so + gi * BM * 8 + t * 128);
         v4i d[TT];
 #pragma unroll
-        for (int t = 0; t < TT; ++t) d[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[t], v4i{0, 0, 0, 0}, 0, 0, 0);
+        for (int t = 0; t < TT; ++t) d[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ag[gi][0], b0[t], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-        for (int t = 0; t < TT; ++t) d[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[t], d[t], 0, 0, 0);
+        for (int t = 0; t < TT; ++t) d[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ag[gi][1], b1[t], d[t], 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
             if (DBG) {
-                const int m = m0 + t * 16 + r;
+                const int m = cur.m0 + t * 16 + r;
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    const int n = row0 + wave * 16 + 4 * q + v;
-                    if (m < M && n < out) dbg[((size_t)m * out + n) * G + g] = d[t][v];
+                    const int n = cur.row0 + wave * 16 + 4 * q + v;
+                    if (m < M && n < out) dbg[((size_t)m * out + n) * G + cur.c * GC + gi] = d[t][v];
                 }
             }
             if (!GENERAL) {
@@ -194,95 +264,128 @@ __global__ __launch_bounds__(64 * NW, 2) void k_gemm(
             }
         }
     };
-    // One chunk from LDS buffer B with codes cg, prefetching chunk c + 1
-    // (into the other buffer and code registers cn) first.
-    auto do_chunk = [&](auto Bc, int c, const uint2 (&cg)[GC][2], uint2 (&cn)[GC][2]) __attribute__((always_inline)) {
+    // Step `cur` from LDS buffer B with A fragments ag, prefetching step
+    // `nxt` (into the other buffer and fragment registers an) first.
+    //
+    // The prefetch, its LDS stores and the barrier run on every step (the
+    // last step reloads its own, cached, data): with no path that skips
+    // them, the compiler's wait before this step's first use of its A
+    // registers counts the prefetch loads as issued after them and does not
+    // wait for the prefetch.
+    auto do_step = [&](auto Bc, const v4i (&ag)[GC][2], v4i (&an)[GC][2]) __attribute__((always_inline)) {
         constexpr int B = decltype(Bc)::value;
-        const bool more = c + 1 < nchunks;
-        if (more) stage_load(c + 1, B ^ 1, cn);
-        const int gb = c * GC;
-        const int gcc = min(GC, G - gb);
-        const char* bb = lbase + B * BUF_BYTES;
+        nxt = cur;
+        advance(nxt);
+        stage_load(nxt, an);
+        if (cur.c == 0) {
+            // The previous item's outputs are stored here, behind this
+            // step's prefetch: the wait at the start of the next step's
+            // prefetch (for registers it reuses) then finds them long done.
+            if (cur.k > 0) end_item(done);
+            begin_item();
+        }
+        const char* bb = lbase + B * XB;
+        const char* tb = reinterpret_cast<const char*>(&tabs[B][0]);
+        // Scheduling fences keep the prefetch loads ahead of the compute and
+        // its LDS stores behind it (hoisted stores would wait for the
+        // prefetch in the middle of the compute).
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int gi = 0; gi < GC; ++gi) {
-            if (gi >= gcc) break;
-            do_group(cg[gi], bb, gi, gb + gi);
-        }
-        if (more) {
-            // Buffer B ^ 1 was last read in the previous chunk, which every
-            // wavefront left through the barrier below.
-            __builtin_amdgcn_s_waitcnt(0);
-            stage_store(B ^ 1);
-            __syncthreads();
-        }
+        for (int gi = 0; gi < GC; ++gi) do_group(ag, bb, tb, gi);
+        __builtin_amdgcn_sched_barrier(0);
+        // Buffer B ^ 1 was last read in the previous step, which every
+        // wavefront left through the barrier below.
+        stage_store(B ^ 1);
+        __syncthreads();
+        if (cur.c == nchunks - 1) done = cur;
+        cur = nxt;
     };
 
-    stage_load(0, 0, cwa);
-    __builtin_amdgcn_s_waitcnt(0);
+    stage_load(cur, aa);
     stage_store(0);
     __syncthreads();
-    // Chunks in pairs so buffers and code registers alternate statically.
-    for (int c = 0; c < nchunks; c += 2) {
-        do_chunk(std::integral_constant<int, 0>{}, c, cwa, cwb);
-        if (c + 1 < nchunks) do_chunk(std::integral_constant<int, 1>{}, c + 1, cwb, cwa);
+    // Steps in pairs so buffers and fragment registers alternate statically.
+    for (int s = 0; s < nsteps; s += 2) {
+        do_step(std::integral_constant<int, 0>{}, aa, ab);
+        if (s + 1 < nsteps) do_step(std::integral_constant<int, 1>{}, ab, aa);
     }
-    if (!y || !tile_ok) return;
-#pragma unroll
-    for (int t = 0; t < TT; ++t) {
-        const int m = m0 + t * 16 + r;
-        if (m >= M) continue;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int n = row0 + wave * 16 + 4 * q + v;
-            if (n < out) y[(size_t)m * ldy + col0 + n] = acc[t][v];
-        }
-    }
+    end_item(done);
+}
+
+// Workgroups of one kernel that fit on a CU at once.
+template <typename K>
+static int occupancy(K kern, int threads, size_t lds) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, lds) != hipSuccess || n < 1) n = 1;
+    return n;
 }
 
 template <int BM, int NW, int GC, bool GENERAL>
 static hipError_t run(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
                       int32_t* dbg, hipStream_t s) {
+    constexpr int ROWS = 16 * NW;
     const QMatMeta& m = w->m;
-    const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
     const int M = a->rows;
-    const int nchunks = (m.groups + GC - 1) / GC;
-    const size_t lds = (size_t)(nchunks > 1 ? 2 : 1) * gemm_buf_bytes<BM, NW, GC>();
-    dim3 grid((m.out_pad + 16 * NW - 1) / (16 * NW), (M + BM - 1) / BM), blockdim(64 * NW);
-    const int blocked = M / 4 * 4;
+    const int panels = (m.out_pad + ROWS - 1) / ROWS;
+    const int ttiles = (M + BM - 1) / BM;
+    const int items = panels * ttiles;
+    const size_t lds = 2 * (size_t)gemm_act_bytes<BM, GC>();
     auto kern = dbg ? k_gemm<BM, NW, GC, GENERAL, true> : k_gemm<BM, NW, GC, GENERAL, false>;
-    static bool attr = false;
-    if (!attr) {
+    static int per_cu = 0;
+    if (!per_cu) {
         hipError_t e = hipFuncSetAttribute((const void*)k_gemm<BM, NW, GC, GENERAL, true>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 2 * gemm_buf_bytes<BM, NW, GC>());
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)k_gemm<BM, NW, GC, GENERAL, false>,
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, 2 * gemm_buf_bytes<BM, NW, GC>());
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        attr = true;
+        per_cu = occupancy(k_gemm<BM, NW, GC, GENERAL, false>, 64 * NW, lds);
     }
-    hipLaunchKernelGGL(kern, grid, blockdim, lds, s, (const uint2*)w->d_codes, w->d_norms, (const uint4*)a->d_xq,
-                       a->d_sx, block, blocked, y, ldy, col0, dbg, m.out, m.out_pad, M, m.groups, m.cbs, lut);
+    // Persistent grid: at most one resident wave of workgroups, each taking
+    // the same number of items.
+    const int slots = device_cus() * per_cu;
+    const int rounds = (items + slots - 1) / slots;
+    const int grid = (items + rounds - 1) / rounds;
+    const int vec = ((uintptr_t)y % 16 == 0 && ldy % 4 == 0 && col0 % 4 == 0) ? 1 : 0;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NW), lds, s, w->d_w8, w->d_norms, (const uint4*)a->d_xq, a->d_sx,
+                       block, M / 4 * 4, y, ldy, col0, vec, dbg, m.out, m.out_pad, M, m.groups, m.cbs, panels, items);
     return hipGetLastError();
 }
 
-template <int BM, int NW, int GC>
-static hipError_t pick(bool general, const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy,
-                       int col0, int32_t* dbg, hipStream_t s) {
-    return general ? run<BM, NW, GC, true>(w, a, block, y, ldy, col0, dbg, s)
-                   : run<BM, NW, GC, false>(w, a, block, y, ldy, col0, dbg, s);
+// 32-token tiles with the largest chunk (3, 4, 2 or 1 groups) that divides G.
+static hipError_t run32(bool general, const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy,
+                        int col0, int32_t* dbg, hipStream_t s) {
+    const int G = w->m.groups;
+#define NH_GEMM_GC(GCV)                                                              \
+    if (G % GCV == 0)                                                                \
+        return general ? run<32, 4, GCV, true>(w, a, block, y, ldy, col0, dbg, s) \
+                       : run<32, 4, GCV, false>(w, a, block, y, ldy, col0, dbg, s);
+    NH_GEMM_GC(3)
+    NH_GEMM_GC(4)
+    NH_GEMM_GC(2)
+#undef NH_GEMM_GC
+    return general ? run<32, 4, 1, true>(w, a, block, y, ldy, col0, dbg, s)
+                   : run<32, 4, 1, false>(w, a, block, y, ldy, col0, dbg, s);
 }
 
 hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
                        int32_t* dbg, hipStream_t s) {
     // Tokens past rows / 4 * 4 (or flagged) take the remainder combine.
     const bool general = block != nullptr || a->rows % 4 != 0;
-    // Four wavefronts (64 rows) per workgroup and 8-group chunks measured
-    // fastest on the prefill shapes (eight wavefronts sharing one staging
-    // were slower at M = 64 and no faster at M = 1024).  Activation buffers
-    // hold whole multiples of 64 token rows, so both tile heights read
-    // inside them.
-    if (a->rows <= 32) return pick<32, 4, 8>(general, w, a, block, y, ldy, col0, dbg, s);
-    return pick<64, 4, 8>(general, w, a, block, y, ldy, col0, dbg, s);
+    // Activation buffers hold whole multiples of ACT_PAD token rows, so
+    // every token tile reads inside them.
+    static_assert(ACT_PAD % 64 == 0, "token tiles stay inside the activation buffer");
+    // The steps wait on load latency more than on arithmetic, so what pays
+    // is workgroups per CU.  With enough 64 x 64 items for two rounds of the
+    // whole chip, one-group steps (small registers and LDS: four workgroups
+    // per CU) on 64-token tiles measured fastest; below that, 32-token tiles
+    // (twice the items) with 3- or 4-group steps.
+    const int M = a->rows;
+    const long items64 = (long)((w->m.out_pad + 63) / 64) * ((M + 63) / 64);
+    if (M > 32 && items64 >= 2L * device_cus())
+        return general ? run<64, 4, 1, true>(w, a, block, y, ldy, col0, dbg, s)
+                       : run<64, 4, 1, false>(w, a, block, y, ldy, col0, dbg, s);
+    return run32(general, w, a, block, y, ldy, col0, dbg, s);
 }
 
 }  // namespace nh

@@ -17,13 +17,6 @@ constexpr int TILE_ROWS = 16;
 // Token rows an activation buffer is padded to (the GEMM reads whole
 // 64-token tiles; padding rows hold zeros and are never stored).
 constexpr int ACT_PAD = 64;
-// Bytes past the end of each device buffer that the GEMM's whole-chunk
-// (8-group) staging may read: 8 groups of codes per 16-row tile (1 KiB
-// each), norms, int8 activations (128 B per group) and scales.
-constexpr size_t CODE_TAIL_PAD = 8 * 1024;
-constexpr size_t NORM_TAIL_PAD = 8 * 2 * 4;
-constexpr size_t ACT_TAIL_PAD = 8 * 128;
-constexpr size_t SX_TAIL_PAD = 8 * 4 * 4;
 
 // The int8 codebook as v_perm tables: value(s) = perm(A, s) ^ perm(B, s ^ 8)
 // for the 4-bit selector s a code is stored as.
@@ -53,6 +46,9 @@ struct nh_qmat {
     // f16 bits, and the per-selector f32 codebook for row dequantization.
     uint4* d_codes = nullptr;
     uint16_t* d_norms = nullptr;
+    // The same codes as int8 MFMA A fragments for the GEMM: per 16-row tile
+    // and group, [half][lane][16 bytes] (k_expand_w8).
+    uint4* d_w8 = nullptr;
     float* d_fsel = nullptr;
     // Host copy of the archive-layout codes and norms (fusion, download).
     std::vector<uint8_t> h_packed;   // out x groups*64
@@ -73,6 +69,8 @@ namespace nh {
 
 // Error plumbing: kernels' host launchers return hipError_t.
 void set_error(const std::string& msg);
+// Compute units of the device selected by nh_init.
+int device_cus();
 
 // Byte offset (0..127) inside a group's activation block of natural
 // position p: dword d = p / 8 of the packed codes belongs to decode lane
@@ -88,6 +86,7 @@ __host__ __device__ inline int act_offset(int p) {
 hipError_t launch_act_prep(const float* x, int rows, int in_dim, int groups, const uint16_t* norm_scale,
                            int8_t* xq, float* sx, hipStream_t s);
 hipError_t launch_gemv(const nh_qmat* w, const nh_qact* a, float* y, int col0, int32_t* dbg_lanes, hipStream_t s);
+hipError_t launch_expand_w8(const nh_qmat* w, hipStream_t s);
 hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
                        int32_t* dbg_totals, hipStream_t s);
 hipError_t launch_single_rows(const nh_qmat* w, const nh_qact* a, const uint32_t* ids, int n, float* out,
