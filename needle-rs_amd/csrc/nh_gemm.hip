@@ -352,20 +352,22 @@ static hipError_t run(const nh_qmat* w, const nh_qact* a, const uint8_t* block, 
     return hipGetLastError();
 }
 
-// 32-token tiles with the largest chunk (3, 4, 2 or 1 groups) that divides G.
-static hipError_t run32(bool general, const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy,
-                        int col0, int32_t* dbg, hipStream_t s) {
+// BM-token tiles on NW wavefronts with the largest chunk (3, 4, 2 or 1
+// groups) that divides G.
+template <int BM, int NW>
+static hipError_t run_gc(bool general, const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy,
+                         int col0, int32_t* dbg, hipStream_t s) {
     const int G = w->m.groups;
-#define NH_GEMM_GC(GCV)                                                              \
-    if (G % GCV == 0)                                                                \
-        return general ? run<32, 4, GCV, true>(w, a, block, y, ldy, col0, dbg, s) \
-                       : run<32, 4, GCV, false>(w, a, block, y, ldy, col0, dbg, s);
+#define NH_GEMM_GC(GCV)                                                               \
+    if (G % GCV == 0)                                                                 \
+        return general ? run<BM, NW, GCV, true>(w, a, block, y, ldy, col0, dbg, s) \
+                       : run<BM, NW, GCV, false>(w, a, block, y, ldy, col0, dbg, s);
     NH_GEMM_GC(3)
     NH_GEMM_GC(4)
     NH_GEMM_GC(2)
 #undef NH_GEMM_GC
-    return general ? run<32, 4, 1, true>(w, a, block, y, ldy, col0, dbg, s)
-                   : run<32, 4, 1, false>(w, a, block, y, ldy, col0, dbg, s);
+    return general ? run<BM, NW, 1, true>(w, a, block, y, ldy, col0, dbg, s)
+                   : run<BM, NW, 1, false>(w, a, block, y, ldy, col0, dbg, s);
 }
 
 hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
@@ -376,16 +378,19 @@ hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block,
     // every token tile reads inside them.
     static_assert(ACT_PAD % 64 == 0, "token tiles stay inside the activation buffer");
     // The steps wait on load latency more than on arithmetic, so what pays
-    // is workgroups per CU.  With enough 64 x 64 items for two rounds of the
-    // whole chip, one-group steps (small registers and LDS: four workgroups
-    // per CU) on 64-token tiles measured fastest; below that, 32-token tiles
-    // (twice the items) with 3- or 4-group steps.
-    const int M = a->rows;
-    const long items64 = (long)((w->m.out_pad + 63) / 64) * ((M + 63) / 64);
-    if (M > 32 && items64 >= 2L * device_cus())
+    // is parallel work: take the largest tile that still gives every CU an
+    // item (and is no taller than the tokens), else the smallest.  Measured
+    // on the prefill and LM-head shapes: 64 x 64 tiles with one-group steps
+    // (four workgroups per CU) for the largest products, 64-row x 32-token
+    // tiles with 3-group steps in the middle, 32-row x 16-token tiles for
+    // prompt chunks and small batches.
+    const int M = a->rows, cus = device_cus(), out_pad = w->m.out_pad;
+    auto items = [&](int rows, int bm) { return (long)((out_pad + rows - 1) / rows) * ((M + bm - 1) / bm); };
+    if (M > 48 && items(64, 64) >= cus)
         return general ? run<64, 4, 1, true>(w, a, block, y, ldy, col0, dbg, s)
                        : run<64, 4, 1, false>(w, a, block, y, ldy, col0, dbg, s);
-    return run32(general, w, a, block, y, ldy, col0, dbg, s);
+    if (M > 16 && items(64, 32) >= cus) return run_gc<32, 4>(general, w, a, block, y, ldy, col0, dbg, s);
+    return run_gc<16, 2>(general, w, a, block, y, ldy, col0, dbg, s);
 }
 
 }  // namespace nh
