@@ -71,12 +71,24 @@ __host__ __device__ constexpr int gemm_act_bytes() {
     return BM * GC * 128;
 }
 
-template <int BM, int NW, int GC, bool GENERAL, bool DBG>
+// One group's A fragments as held in registers: the int8 fragments
+// themselves (halves 0 and 1), or (W4) the 4-bit code pieces they expand
+// from, expanded right before use.
+template <bool W4>
+struct AFrag {
+    v4i h[2];
+};
+template <>
+struct AFrag<true> {
+    uint32_t c[4];
+};
+
+template <int BM, int NW, int GC, bool GENERAL, bool DBG, bool W4>
 __global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
-    const uint4* __restrict__ w8, const uint16_t* __restrict__ norms, const uint4* __restrict__ xq,
-    const float* __restrict__ sx, const uint8_t* __restrict__ block, int blocked, float* __restrict__ y, int ldy,
-    int col0, int vec_store, int32_t* __restrict__ dbg, int out, int out_pad, int M, int G, float cbs, int panels,
-    int items) {
+    const uint4* __restrict__ w8, const uint2* __restrict__ codes, Lut lut, const uint16_t* __restrict__ norms,
+    const uint4* __restrict__ xq, const float* __restrict__ sx, const uint8_t* __restrict__ block, int blocked,
+    float* __restrict__ y, int ldy, int col0, int vec_store, int32_t* __restrict__ dbg, int out, int out_pad, int M,
+    int G, float cbs, int panels, int items) {
     constexpr int T = 64 * NW;
     constexpr int ROWS = 16 * NW;
     constexpr int TT = BM / 16;  // token tiles per wavefront
@@ -140,12 +152,12 @@ __global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
     u32x4 xr[XPT];
     float s_reg[SPT];
     uint16_t n_reg[NPT];
-    v4i aa[GC][2], ab[GC][2];
+    AFrag<W4> aa[GC], ab[GC];
 
     // The global loads of step p: activations, tables and this wavefront's
     // A fragments into registers.  Tables stay raw until stage_store (a
     // conversion here would wait on every load in flight).
-    auto stage_load = [&](const Pos& p, v4i (&adst)[GC][2]) __attribute__((always_inline)) {
+    auto stage_load = [&](const Pos& p, AFrag<W4> (&adst)[GC]) __attribute__((always_inline)) {
         const int gb = p.c * GC;
         const char* xbase = reinterpret_cast<const char*>(xq) + ((size_t)p.m0 * G + gb) * 128;
 #pragma unroll
@@ -165,11 +177,24 @@ __global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
         }
         const int tile = (p.row0 >> 4) + wave;
         const int ctile = tile * 16 < out_pad ? tile : 0;  // clamped: loads stay in bounds
-        const v4i* a = reinterpret_cast<const v4i*>(w8) + ((size_t)ctile * G + gb) * 128 + lane;
+        if constexpr (W4) {
+            // Chunks l = q / 2 and 2 + q / 2 of row r, dword pair q & 1.
+            const uint2* c = codes + ((((size_t)ctile * G + gb) * 64 + r * 4 + (q >> 1)) * 2 + (q & 1));
 #pragma unroll
-        for (int gi = 0; gi < GC; ++gi) {
-            adst[gi][0] = a[gi * 128];
-            adst[gi][1] = a[gi * 128 + 64];
+            for (int gi = 0; gi < GC; ++gi) {
+                const uint2 c0 = c[gi * 128], c1 = c[gi * 128 + 4];
+                adst[gi].c[0] = c0.x;
+                adst[gi].c[1] = c0.y;
+                adst[gi].c[2] = c1.x;
+                adst[gi].c[3] = c1.y;
+            }
+        } else {
+            const v4i* a = reinterpret_cast<const v4i*>(w8) + ((size_t)ctile * G + gb) * 128 + lane;
+#pragma unroll
+            for (int gi = 0; gi < GC; ++gi) {
+                adst[gi].h[0] = a[gi * 128];
+                adst[gi].h[1] = a[gi * 128 + 64];
+            }
         }
     };
     // After the loads landed: activations and tables into LDS buffer b.
@@ -223,7 +248,20 @@ __global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
 
     // One group: B fragments from LDS, every token tile's two MFMAs into its
     // own accumulator (independent, so they pipeline), then the epilogues.
-    auto do_group = [&](const v4i (&ag)[GC][2], const char* bb, const char* tb, int gi) __attribute__((always_inline)) {
+    auto do_group = [&](const AFrag<W4> (&ag)[GC], const char* bb, const char* tb, int gi) __attribute__((always_inline)) {
+        v4i a0, a1;
+        if constexpr (W4) {
+            uint32_t e0, e1, e2, e3, f0, f1, f2, f3;
+            expand8(ag[gi].c[0], lut, e0, e1);
+            expand8(ag[gi].c[1], lut, e2, e3);
+            expand8(ag[gi].c[2], lut, f0, f1);
+            expand8(ag[gi].c[3], lut, f2, f3);
+            a0 = v4i{(int)e0, (int)e1, (int)e2, (int)e3};
+            a1 = v4i{(int)f0, (int)f1, (int)f2, (int)f3};
+        } else {
+            a0 = ag[gi].h[0];
+            a1 = ag[gi].h[1];
+        }
         v4i b0[TT], b1[TT];
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
@@ -238,9 +276,9 @@ __global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
         for (int t = 0; t < TT; ++t) sc[t] = *reinterpret_cast<const float2*>(tb + so + gi * BM * 8 + t * 128);
         v4i d[TT];
 #pragma unroll
-        for (int t = 0; t < TT; ++t) d[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ag[gi][0], b0[t], v4i{0, 0, 0, 0}, 0, 0, 0);
+        for (int t = 0; t < TT; ++t) d[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0[t], v4i{0, 0, 0, 0}, 0, 0, 0);
 #pragma unroll
-        for (int t = 0; t < TT; ++t) d[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ag[gi][1], b1[t], d[t], 0, 0, 0);
+        for (int t = 0; t < TT; ++t) d[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1[t], d[t], 0, 0, 0);
 #pragma unroll
         for (int t = 0; t < TT; ++t) {
             if (DBG) {
@@ -272,7 +310,7 @@ __global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
     // them, the compiler's wait before this step's first use of its A
     // registers counts the prefetch loads as issued after them and does not
     // wait for the prefetch.
-    auto do_step = [&](auto Bc, const v4i (&ag)[GC][2], v4i (&an)[GC][2]) __attribute__((always_inline)) {
+    auto do_step = [&](auto Bc, const AFrag<W4> (&ag)[GC], AFrag<W4> (&an)[GC]) __attribute__((always_inline)) {
         constexpr int B = decltype(Bc)::value;
         nxt = cur;
         advance(nxt);
@@ -320,26 +358,27 @@ static int occupancy(K kern, int threads, size_t lds) {
     return n;
 }
 
-template <int BM, int NW, int GC, bool GENERAL>
+template <int BM, int NW, int GC, bool GENERAL, bool W4>
 static hipError_t run(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
                       int32_t* dbg, hipStream_t s) {
     constexpr int ROWS = 16 * NW;
     const QMatMeta& m = w->m;
+    const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
     const int M = a->rows;
     const int panels = (m.out_pad + ROWS - 1) / ROWS;
     const int ttiles = (M + BM - 1) / BM;
     const int items = panels * ttiles;
     const size_t lds = 2 * (size_t)gemm_act_bytes<BM, GC>();
-    auto kern = dbg ? k_gemm<BM, NW, GC, GENERAL, true> : k_gemm<BM, NW, GC, GENERAL, false>;
+    auto kern = dbg ? k_gemm<BM, NW, GC, GENERAL, true, W4> : k_gemm<BM, NW, GC, GENERAL, false, W4>;
     static int per_cu = 0;
     if (!per_cu) {
-        hipError_t e = hipFuncSetAttribute((const void*)k_gemm<BM, NW, GC, GENERAL, true>,
+        hipError_t e = hipFuncSetAttribute((const void*)k_gemm<BM, NW, GC, GENERAL, true, W4>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)k_gemm<BM, NW, GC, GENERAL, false>,
+            e = hipFuncSetAttribute((const void*)k_gemm<BM, NW, GC, GENERAL, false, W4>,
                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
-        per_cu = occupancy(k_gemm<BM, NW, GC, GENERAL, false>, 64 * NW, lds);
+        per_cu = occupancy(k_gemm<BM, NW, GC, GENERAL, false, W4>, 64 * NW, lds);
     }
     // Persistent grid: at most one resident wave of workgroups, each taking
     // the same number of items.
@@ -347,27 +386,28 @@ static hipError_t run(const nh_qmat* w, const nh_qact* a, const uint8_t* block, 
     const int rounds = (items + slots - 1) / slots;
     const int grid = (items + rounds - 1) / rounds;
     const int vec = ((uintptr_t)y % 16 == 0 && ldy % 4 == 0 && col0 % 4 == 0) ? 1 : 0;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NW), lds, s, w->d_w8, w->d_norms, (const uint4*)a->d_xq, a->d_sx,
-                       block, M / 4 * 4, y, ldy, col0, vec, dbg, m.out, m.out_pad, M, m.groups, m.cbs, panels, items);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NW), lds, s, w->d_w8, (const uint2*)w->d_codes, lut, w->d_norms,
+                       (const uint4*)a->d_xq, a->d_sx, block, M / 4 * 4, y, ldy, col0, vec, dbg, m.out, m.out_pad, M,
+                       m.groups, m.cbs, panels, items);
     return hipGetLastError();
 }
 
 // BM-token tiles on NW wavefronts with the largest chunk (3, 4, 2 or 1
 // groups) that divides G.
-template <int BM, int NW>
+template <int BM, int NW, bool W4>
 static hipError_t run_gc(bool general, const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy,
                          int col0, int32_t* dbg, hipStream_t s) {
     const int G = w->m.groups;
-#define NH_GEMM_GC(GCV)                                                               \
-    if (G % GCV == 0)                                                                 \
-        return general ? run<BM, NW, GCV, true>(w, a, block, y, ldy, col0, dbg, s) \
-                       : run<BM, NW, GCV, false>(w, a, block, y, ldy, col0, dbg, s);
+#define NH_GEMM_GC(GCV)                                                                   \
+    if (G % GCV == 0)                                                                     \
+        return general ? run<BM, NW, GCV, true, W4>(w, a, block, y, ldy, col0, dbg, s) \
+                       : run<BM, NW, GCV, false, W4>(w, a, block, y, ldy, col0, dbg, s);
     NH_GEMM_GC(3)
     NH_GEMM_GC(4)
     NH_GEMM_GC(2)
 #undef NH_GEMM_GC
-    return general ? run<BM, NW, 1, true>(w, a, block, y, ldy, col0, dbg, s)
-                   : run<BM, NW, 1, false>(w, a, block, y, ldy, col0, dbg, s);
+    return general ? run<BM, NW, 1, true, W4>(w, a, block, y, ldy, col0, dbg, s)
+                   : run<BM, NW, 1, false, W4>(w, a, block, y, ldy, col0, dbg, s);
 }
 
 hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
@@ -383,14 +423,17 @@ hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block,
     // on the prefill and LM-head shapes: 64 x 64 tiles with one-group steps
     // (four workgroups per CU) for the largest products, 64-row x 32-token
     // tiles with 3-group steps in the middle, 32-row x 16-token tiles for
-    // prompt chunks and small batches.
+    // prompt chunks and small batches.  Up to 16 tokens the product is
+    // bound by the weight stream, so it reads the 4-bit codes (half the
+    // bytes of the int8 copy) and expands them in the kernel.
     const int M = a->rows, cus = device_cus(), out_pad = w->m.out_pad;
     auto items = [&](int rows, int bm) { return (long)((out_pad + rows - 1) / rows) * ((M + bm - 1) / bm); };
     if (M > 48 && items(64, 64) >= cus)
-        return general ? run<64, 4, 1, true>(w, a, block, y, ldy, col0, dbg, s)
-                       : run<64, 4, 1, false>(w, a, block, y, ldy, col0, dbg, s);
-    if (M > 16 && items(64, 32) >= cus) return run_gc<32, 4>(general, w, a, block, y, ldy, col0, dbg, s);
-    return run_gc<16, 2>(general, w, a, block, y, ldy, col0, dbg, s);
+        return general ? run<64, 4, 1, true, false>(w, a, block, y, ldy, col0, dbg, s)
+                       : run<64, 4, 1, false, false>(w, a, block, y, ldy, col0, dbg, s);
+    if (M > 16 && items(64, 32) >= cus) return run_gc<32, 4, false>(general, w, a, block, y, ldy, col0, dbg, s);
+    if (M <= 16) return run_gc<16, 2, true>(general, w, a, block, y, ldy, col0, dbg, s);
+    return run_gc<16, 2, false>(general, w, a, block, y, ldy, col0, dbg, s);
 }
 
 }  // namespace nh
