@@ -209,8 +209,9 @@ static int upload(std::vector<uint8_t>&& packed, std::vector<uint16_t>&& norms, 
     memcpy(m.fvals, g_cb4, sizeof g_cb4);
     m.lut = g_lut4;
     std::vector<uint32_t> tiled;
-    relayout(packed.data(), out, out_pad, groups, m.lut, tiled);
-    std::vector<uint16_t> np((size_t)out_pad * groups, 0);
+    const int out_alloc = (out + PANEL_ROWS - 1) / PANEL_ROWS * PANEL_ROWS;
+    relayout(packed.data(), out, out_alloc, groups, m.lut, tiled);
+    std::vector<uint16_t> np((size_t)out_alloc * groups, 0);
     memcpy(np.data(), norms.data(), (size_t)out * groups * 2);
     float fsel[16];
     for (int s = 0; s < 16; ++s) fsel[s] = m.fvals[m.lut.code_of_sel[s]];

@@ -58,7 +58,7 @@ __global__ __launch_bounds__(64) void k_expand_w8(const uint2* __restrict__ code
 hipError_t launch_expand_w8(const nh_qmat* w, hipStream_t s) {
     const QMatMeta& m = w->m;
     const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
-    const int blocks = m.out_pad / 16 * m.groups;
+    const int blocks = (m.out + PANEL_ROWS - 1) / PANEL_ROWS * (PANEL_ROWS / 16) * m.groups;
     hipLaunchKernelGGL(k_expand_w8, dim3(blocks), dim3(64), 0, s, (const uint2*)w->d_codes, w->d_w8, lut);
     return hipGetLastError();
 }
@@ -69,6 +69,12 @@ hipError_t launch_expand_w8(const nh_qmat* w, hipStream_t s) {
 template <int BM, int GC>
 __host__ __device__ constexpr int gemm_act_bytes() {
     return BM * GC * 128;
+}
+
+// A raw buffer resource over `bytes` bytes at p (gfx9 descriptor word 3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)(bytes < 0xffffffffu ? bytes : 0xffffffffu),
+                                             0x00020000);
 }
 
 // One group's A fragments as held in registers: the int8 fragments
@@ -87,8 +93,8 @@ template <int BM, int NW, int GC, bool GENERAL, bool DBG, bool W4>
 __global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
     const uint4* __restrict__ w8, const uint2* __restrict__ codes, Lut lut, const uint16_t* __restrict__ norms,
     const uint4* __restrict__ xq, const float* __restrict__ sx, const uint8_t* __restrict__ block, int blocked,
-    float* __restrict__ y, int ldy, int col0, int vec_store, int32_t* __restrict__ dbg, int out, int out_pad, int M,
-    int G, float cbs, int panels, int items) {
+    float* __restrict__ y, int ldy, int col0, int vec_store, int32_t* __restrict__ dbg, int out, int out_alloc,
+    int cap_rows, int M, int G, float cbs, int panels, int items) {
     constexpr int T = 64 * NW;
     constexpr int ROWS = 16 * NW;
     constexpr int TT = BM / 16;  // token tiles per wavefront
@@ -126,6 +132,23 @@ __global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
     const uint32_t so = r * 8;                          // + gi * BM * 8 + t * 128
     const uint32_t no = SB + (wave * 16 + 4 * q) * 8;  // + gi * ROWS * 8 + v * 8
 
+    // Table entries this thread stages: scales [gi][tok], norms [gi][row]
+    // (threads past a table's end reload entry 0, never stored).
+    uint32_t soff[SPT], noff[NPT];
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+        const int L = i * T + tid < BM * GC ? i * T + tid : 0;
+        soff[i] = (uint32_t)((L % BM) * G + L / BM);
+    }
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int L = i * T + tid < ROWS * GC ? i * T + tid : 0;
+        noff[i] = (uint32_t)((L % ROWS) * G + L / ROWS);
+    }
+    // 4-bit A pieces: chunks l = q / 2 and 2 + q / 2 of row r, dword pair
+    // q & 1 (uint2 units within a tile-group block).
+    const uint32_t coff = (uint32_t)((r * 4 + (q >> 1)) * 2 + (q & 1));
+
     // Step bookkeeping: item k of this workgroup, chunk c.  The division
     // runs once per item.
     struct Pos {
@@ -157,43 +180,45 @@ __global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
     // The global loads of step p: activations, tables and this wavefront's
     // A fragments into registers.  Tables stay raw until stage_store (a
     // conversion here would wait on every load in flight).
+    // Buffer resources over the inputs: every staging load is a buffer load
+    // with a loop-invariant per-lane offset and the step's uniform offset in
+    // a scalar register, so a step computes no vector addresses (and no
+    // address temporary reuses a register a load is still filling).  Device
+    // matrix copies hold whole 64-row panels: no row clamps.
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(xq, (size_t)cap_rows * G * 128);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(sx, (size_t)cap_rows * G * 4);
+    const __amdgpu_buffer_rsrc_t rn = make_rsrc(norms, (size_t)out_alloc * G * 2);
+    const __amdgpu_buffer_rsrc_t ra =
+        W4 ? make_rsrc(codes, (size_t)out_alloc * G * 64) : make_rsrc(w8, (size_t)out_alloc * G * 128);
     auto stage_load = [&](const Pos& p, AFrag<W4> (&adst)[GC]) __attribute__((always_inline)) {
         const int gb = p.c * GC;
-        const char* xbase = reinterpret_cast<const char*>(xq) + ((size_t)p.m0 * G + gb) * 128;
+        const int xs = (p.m0 * G + gb) * 128;
 #pragma unroll
-        for (int i = 0; i < XPT; ++i) xr[i] = *reinterpret_cast<const u32x4*>(xbase + xoff[i]);
+        for (int i = 0; i < XPT; ++i)
+            xr[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, (int)xoff[i], xs, 0));
 #pragma unroll
-        for (int i = 0; i < SPT; ++i) {
-            const int L = i * T + tid;  // [gi][tok]
-            const int Lc = L < BM * GC ? L : 0;
-            s_reg[i] = sx[(size_t)(p.m0 + Lc % BM) * G + gb + Lc / BM];
-        }
+        for (int i = 0; i < SPT; ++i)
+            s_reg[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, (int)soff[i] * 4,
+                                                                                     (p.m0 * G + gb) * 4, 0));
 #pragma unroll
-        for (int i = 0; i < NPT; ++i) {
-            const int L = i * T + tid;  // [gi][row]
-            const int Lc = L < ROWS * GC ? L : 0;
-            const int row = p.row0 + Lc % ROWS;
-            n_reg[i] = norms[(size_t)(row < out_pad ? row : 0) * G + gb + Lc / ROWS];
-        }
-        const int tile = (p.row0 >> 4) + wave;
-        const int ctile = tile * 16 < out_pad ? tile : 0;  // clamped: loads stay in bounds
+        for (int i = 0; i < NPT; ++i)
+            n_reg[i] = __builtin_amdgcn_raw_buffer_load_b16(rn, (int)noff[i] * 2, (p.row0 * G + gb) * 2, 0);
+        const int tg = ((p.row0 >> 4) + wave) * G + gb;  // this wavefront's tile, first group
         if constexpr (W4) {
-            // Chunks l = q / 2 and 2 + q / 2 of row r, dword pair q & 1.
-            const uint2* c = codes + ((((size_t)ctile * G + gb) * 64 + r * 4 + (q >> 1)) * 2 + (q & 1));
 #pragma unroll
             for (int gi = 0; gi < GC; ++gi) {
-                const uint2 c0 = c[gi * 128], c1 = c[gi * 128 + 4];
-                adst[gi].c[0] = c0.x;
-                adst[gi].c[1] = c0.y;
-                adst[gi].c[2] = c1.x;
-                adst[gi].c[3] = c1.y;
+                const auto c0 = __builtin_amdgcn_raw_buffer_load_b64(ra, (int)coff * 8 + gi * 1024, tg * 1024, 0);
+                const auto c1 = __builtin_amdgcn_raw_buffer_load_b64(ra, (int)coff * 8 + gi * 1024 + 32, tg * 1024, 0);
+                adst[gi].c[0] = (uint32_t)c0[0];
+                adst[gi].c[1] = (uint32_t)c0[1];
+                adst[gi].c[2] = (uint32_t)c1[0];
+                adst[gi].c[3] = (uint32_t)c1[1];
             }
         } else {
-            const v4i* a = reinterpret_cast<const v4i*>(w8) + ((size_t)ctile * G + gb) * 128 + lane;
 #pragma unroll
             for (int gi = 0; gi < GC; ++gi) {
-                adst[gi].h[0] = a[gi * 128];
-                adst[gi].h[1] = a[gi * 128 + 64];
+                adst[gi].h[0] = __builtin_amdgcn_raw_buffer_load_b128(ra, lane * 16 + gi * 2048, tg * 2048, 0);
+                adst[gi].h[1] = __builtin_amdgcn_raw_buffer_load_b128(ra, lane * 16 + gi * 2048 + 1024, tg * 2048, 0);
             }
         }
     };
@@ -387,8 +412,9 @@ static hipError_t run(const nh_qmat* w, const nh_qact* a, const uint8_t* block, 
     const int grid = (items + rounds - 1) / rounds;
     const int vec = ((uintptr_t)y % 16 == 0 && ldy % 4 == 0 && col0 % 4 == 0) ? 1 : 0;
     hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NW), lds, s, w->d_w8, (const uint2*)w->d_codes, lut, w->d_norms,
-                       (const uint4*)a->d_xq, a->d_sx, block, M / 4 * 4, y, ldy, col0, vec, dbg, m.out, m.out_pad, M,
-                       m.groups, m.cbs, panels, items);
+                       (const uint4*)a->d_xq, a->d_sx, block, M / 4 * 4, y, ldy, col0, vec, dbg, m.out,
+                       (m.out + PANEL_ROWS - 1) / PANEL_ROWS * PANEL_ROWS, a->cap_rows, M, m.groups, m.cbs, panels,
+                       items);
     return hipGetLastError();
 }
 

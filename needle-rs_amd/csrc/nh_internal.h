@@ -14,6 +14,10 @@ constexpr int GROUP = 128;
 // Rows per tile of the HBM code layout: one tile-group block is 16 rows x
 // 4 lanes x 16 bytes = 1 KiB, read by one wavefront load.
 constexpr int TILE_ROWS = 16;
+// Rows the device copies of a matrix (codes, int8 fragments, norms) are
+// padded to: the GEMM reads whole panels of up to 64 rows without clamping
+// row indices; padding rows hold zeros and are never stored.
+constexpr int PANEL_ROWS = 64;
 // Token rows an activation buffer is padded to (the GEMM reads whole
 // 64-token tiles; padding rows hold zeros and are never stored).
 constexpr int ACT_PAD = 64;
