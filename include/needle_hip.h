@@ -50,9 +50,12 @@ int nh_version(void);
 /* ---- matrices (QMat, qlinear.rs:43-61) --------------------------------- */
 /* QMat::from_cq (qlinear.rs:220-236) over a .cact CQ blob as CqView holds
  * it (crates/needle-core/src/cact.rs:497-525): `packed` is out x row_bytes
- * (row_bytes = in_pad * bits / 8), `norms` is out x groups f16 bit
- * patterns.  group must be 128 (the reference asserts); bits must be 4.
- * The blob is re-laid out into the tiled HBM layout during the call. */
+ * (row_bytes = in_pad * bits / 8; ternary records pack at 2 bits),
+ * `norms` is out x groups f16 bit patterns.  group must be 128 (the
+ * reference asserts); bits is 2, 4 or 5 (ternary, quant.rs:12, with the
+ * code remap of qlinear.rs:226-227).  The blob is re-laid out into the
+ * tiled HBM layout (plus an int8 copy for the batched products) during
+ * the call. */
 int nh_qmat_from_cq(const uint8_t* packed, uint64_t packed_bytes, const uint16_t* norms, uint64_t norms_count,
                     int out, int in_dim, int bits, int group, nh_qmat** h);
 /* QMat::from_f32 (qlinear.rs:239-242): cq_pack (crates/needle-core/src/quant.rs:233-256)
@@ -75,7 +78,9 @@ int nh_qmat_download(const nh_qmat* h, uint8_t* packed, uint64_t packed_bytes, u
 int nh_qmat_rows(const nh_qmat* h, const uint32_t* ids, int n, float* out, void* stream);
 
 /* ---- activations (QAct, qlinear.rs:63-72) ------------------------------ */
-/* QAct::empty_rows (qlinear.rs:175-178): room for up to `rows` token rows. */
+/* QAct::empty_rows (qlinear.rs:175-178): room for up to `rows` token rows,
+ * in the layout of `bits`-bit matrices (2 or 4; a ternary matrix reads
+ * the 2-bit layout, nh_qmat_shape reports its bits as 2). */
 int nh_qact_new(int rows, int in_dim, int bits, nh_qact** a);
 int nh_qact_free(nh_qact* a);
 /* QAct::new (qlinear.rs:191-207): x[rows][in_dim] f32 -> per (row, 128-group)

@@ -19,7 +19,7 @@ constexpr int ACT_THREADS = 256;
 constexpr int ACT_MAX_DIM = 32 * GROUP;  // 4096 inputs (16 KiB of LDS)
 
 __global__ __launch_bounds__(ACT_THREADS) void k_act_prep(const float* __restrict__ x, int in_dim, int groups,
-                                                          const uint16_t* __restrict__ norm_scale,
+                                                          int bits, const uint16_t* __restrict__ norm_scale,
                                                           int8_t* __restrict__ xq, float* __restrict__ sx) {
     const int row = blockIdx.x;
     const int wave = threadIdx.x >> 6;
@@ -83,16 +83,16 @@ __global__ __launch_bounds__(ACT_THREADS) void k_act_prep(const float* __restric
         float s = m > 0.0f ? m * k127 : 1.0f;
         float inv = 1.0f / s;
         int8_t* q = xq + ((size_t)row * groups + g) * GROUP;
-        q[act_offset(lane)] = quant_one(v0, inv);
-        q[act_offset(lane + 64)] = quant_one(v1, inv);
+        q[act_offset(lane, bits)] = quant_one(v0, inv);
+        q[act_offset(lane + 64, bits)] = quant_one(v1, inv);
         if (lane == 0) sx[(size_t)row * groups + g] = s;
     }
 }
 
-hipError_t launch_act_prep(const float* x, int rows, int in_dim, int groups, const uint16_t* norm_scale, int8_t* xq,
-                           float* sx, hipStream_t s) {
+hipError_t launch_act_prep(const float* x, int rows, int in_dim, int groups, int bits, const uint16_t* norm_scale,
+                           int8_t* xq, float* sx, hipStream_t s) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(k_act_prep, dim3(rows), dim3(ACT_THREADS), 0, s, x, in_dim, groups, norm_scale, xq, sx);
+    hipLaunchKernelGGL(k_act_prep, dim3(rows), dim3(ACT_THREADS), 0, s, x, in_dim, groups, bits, norm_scale, xq, sx);
     return hipGetLastError();
 }
 

@@ -76,6 +76,27 @@ static void codebook4(float* cb) {
     }
 }
 
+// quant.rs:19 (LM2), 15 (TERNARY_C), 55-68: the 2-bit centroids and the
+// ternary record's three levels over sqrt(128).  Returns the count.
+static const uint64_t LM2_BITS[4] = {0xbff81b52e4028034ull, 0xbfdce467275b97c2ull, 0x3fdcfd177c54d348ull,
+                                     0x3ff828af1c856640ull};
+static int codebook2(bool ternary, float* cb) {
+    const double s = std::sqrt(128.0);
+    if (ternary) {
+        const double t = 1.2240064;
+        cb[0] = (float)(-t / s);
+        cb[1] = (float)(0.0 / s);
+        cb[2] = (float)(t / s);
+        return 3;
+    }
+    for (int i = 0; i < 4; ++i) {
+        double c;
+        memcpy(&c, &LM2_BITS[i], 8);
+        cb[i] = (float)(c / s);
+    }
+    return 4;
+}
+
 // int8_codebook (qlinear.rs:211-216): scale = amax * K127, values
 // round-half-away(v * (1 / scale)) saturated.
 static void int8_codebook(const float* cb, int n, int8_t* cb8, float* scale) {
@@ -194,7 +215,29 @@ static void relayout(const uint8_t* packed, int out, int out_pad, int groups, co
     for (auto& t : th) t.join();
 }
 
-static int upload(std::vector<uint8_t>&& packed, std::vector<uint16_t>&& norms, int out, int in_dim, nh_qmat** h) {
+// 2-bit archive codes (rows x groups*32, four codes per byte, LSB first) ->
+// tiled: decode lane l = (p % 64) / 16 owns packed dwords l and 4 + l of a
+// group, stored as the pair at uint2 index
+// ((n / 16 * groups + g) * 16 + n % 16) * 4 + l.
+static void relayout2(const uint8_t* packed, int out, int out_pad, int groups, std::vector<uint32_t>& tiled) {
+    tiled.assign((size_t)out_pad * groups * 8, 0u);
+    for (int n = 0; n < out; ++n)
+        for (int g = 0; g < groups; ++g) {
+            const uint8_t* src = packed + ((size_t)n * groups + g) * 32;
+            for (int l = 0; l < 4; ++l)
+                for (int h = 0; h < 2; ++h) {
+                    uint32_t v;
+                    memcpy(&v, src + 4 * (4 * h + l), 4);
+                    tiled[(((size_t)(n / TILE_ROWS) * groups + g) * TILE_ROWS + n % TILE_ROWS) * 8 + l * 2 + h] = v;
+                }
+        }
+}
+
+// QMat::build (qlinear.rs:244-265) for the code width `bits` (2 or 4), with
+// from_cq's ternary remap (qlinear.rs:222-227): code 3 is the first level,
+// codes 0..2 the rest; codes without a level are 0.
+static int upload(std::vector<uint8_t>&& packed, std::vector<uint16_t>&& norms, int out, int in_dim, int bits,
+                  bool ternary, nh_qmat** h) {
     const int groups = (in_dim + GROUP - 1) / GROUP;
     const int out_pad = (out + TILE_ROWS - 1) / TILE_ROWS * TILE_ROWS;
     nh_qmat* q = new nh_qmat();
@@ -203,21 +246,41 @@ static int upload(std::vector<uint8_t>&& packed, std::vector<uint16_t>&& norms, 
     m.out_pad = out_pad;
     m.in_dim = in_dim;
     m.groups = groups;
-    m.bits = 4;
-    m.cbs = g_cbs4;
-    memcpy(m.vals, g_cb8, 16);
-    memcpy(m.fvals, g_cb4, sizeof g_cb4);
-    m.lut = g_lut4;
+    m.bits = bits;
+    m.ternary = ternary;
     std::vector<uint32_t> tiled;
     const int out_alloc = (out + PANEL_ROWS - 1) / PANEL_ROWS * PANEL_ROWS;
-    relayout(packed.data(), out, out_alloc, groups, m.lut, tiled);
+    float fsel[16] = {0};
+    if (bits == 4) {
+        m.cbs = g_cbs4;
+        memcpy(m.vals, g_cb8, 16);
+        memcpy(m.fvals, g_cb4, sizeof g_cb4);
+        m.lut = g_lut4;
+        relayout(packed.data(), out, out_alloc, groups, m.lut, tiled);
+        for (int s = 0; s < 16; ++s) fsel[s] = m.fvals[m.lut.code_of_sel[s]];
+    } else {
+        float cb[4];
+        int8_t cb8[4];
+        const int ncb = codebook2(ternary, cb);
+        int8_codebook(cb, ncb, cb8, &m.cbs);
+        memset(m.vals, 0, sizeof m.vals);
+        memset(m.fvals, 0, sizeof m.fvals);
+        memset(&m.lut, 0, sizeof m.lut);
+        for (int c = 0; c < 4; ++c) {
+            const int k = ternary ? (c == 3 ? 0 : c + 1) : c;
+            m.vals[c] = k < ncb ? cb8[k] : 0;
+            m.fvals[c] = k < ncb ? cb[k] : 0.0f;
+            m.lut.a_lo |= (uint32_t)(uint8_t)m.vals[c] << (8 * c);
+            m.lut.sel_of_code[c] = m.lut.code_of_sel[c] = (uint8_t)c;
+            fsel[c] = m.fvals[c];
+        }
+        relayout2(packed.data(), out, out_alloc, groups, tiled);
+    }
     std::vector<uint16_t> np((size_t)out_alloc * groups, 0);
     memcpy(np.data(), norms.data(), (size_t)out * groups * 2);
-    float fsel[16];
-    for (int s = 0; s < 16; ++s) fsel[s] = m.fvals[m.lut.code_of_sel[s]];
     hipError_t e;
     if ((e = hipMalloc(&q->d_codes, tiled.size() * 4)) != hipSuccess ||
-        (e = hipMalloc(&q->d_w8, tiled.size() * 8)) != hipSuccess ||
+        (e = hipMalloc(&q->d_w8, (size_t)out_alloc * groups * 128)) != hipSuccess ||
         (e = hipMalloc(&q->d_norms, np.size() * 2)) != hipSuccess || (e = hipMalloc(&q->d_fsel, 64)) != hipSuccess) {
         nh_qmat_free(q);
         return fail(NH_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
@@ -311,16 +374,21 @@ int nh_qmat_from_cq(const uint8_t* packed, uint64_t packed_bytes, const uint16_t
     if (int rc = check_ready()) return rc;
     if (!h || !packed || !norms) return fail(NH_EINVAL, "null argument");
     if (group != GROUP) return fail(NH_EINVAL, "CQ group size " + std::to_string(group) + " is not supported");
-    if (bits != 4) return fail(NH_EINVAL, "only 4-bit CQ records are supported");
+    // Widths of quant.rs:12,51-60: 2 and 4 bits, and ternary records (5),
+    // which pack at 2 bits (quant.rs:286).
+    if (bits != 2 && bits != 4 && bits != 5)
+        return fail(NH_EINVAL, "CQ records of " + std::to_string(bits) + " bits are not supported");
+    const bool ternary = bits == 5;
+    const int cbits = ternary ? 2 : bits;
     if (out <= 0 || in_dim <= 0) return fail(NH_EINVAL, "empty matrix");
     const int groups = (in_dim + GROUP - 1) / GROUP;
     if (groups > 32) return fail(NH_EINVAL, "in_dim above 4096 is not supported");
-    const uint64_t row_bytes = (uint64_t)groups * GROUP * bits / 8;
+    const uint64_t row_bytes = (uint64_t)groups * GROUP * cbits / 8;
     if (packed_bytes < row_bytes * (uint64_t)out) return fail(NH_ESMALL, "packed blob shorter than out x row_bytes");
     if (norms_count < (uint64_t)groups * out) return fail(NH_ESMALL, "norms shorter than out x groups");
     std::vector<uint8_t> p(packed, packed + row_bytes * out);
     std::vector<uint16_t> nn(norms, norms + (size_t)groups * out);
-    return upload(std::move(p), std::move(nn), out, in_dim, h);
+    return upload(std::move(p), std::move(nn), out, in_dim, cbits, ternary, h);
 }
 
 int nh_qmat_from_f32(const float* w, int out, int in_dim, nh_qmat** h) {
@@ -350,7 +418,7 @@ int nh_qmat_from_f32(const float* w, int out, int in_dim, nh_qmat** h) {
     hipFree(dp);
     hipFree(dn);
     if (e != hipSuccess) return hip_fail(e, "cq_pack");
-    return upload(std::move(packed), std::move(norms), out, in_dim, h);
+    return upload(std::move(packed), std::move(norms), out, in_dim, 4, false, h);
 }
 
 int nh_qlinear_new(nh_qmat* const* parts, int n, nh_qmat** h) {
@@ -373,7 +441,7 @@ int nh_qlinear_new(nh_qmat* const* parts, int n, nh_qmat** h) {
         packed.insert(packed.end(), parts[i]->h_packed.begin(), parts[i]->h_packed.end());
         norms.insert(norms.end(), parts[i]->h_norms.begin(), parts[i]->h_norms.end());
     }
-    return upload(std::move(packed), std::move(norms), out, m0.in_dim, h);
+    return upload(std::move(packed), std::move(norms), out, m0.in_dim, m0.bits, m0.ternary, h);
 }
 
 int nh_qmat_free(nh_qmat* h) {
@@ -422,7 +490,7 @@ int nh_qmat_rows(const nh_qmat* h, const uint32_t* ids, int n, float* out, void*
 int nh_qact_new(int rows, int in_dim, int bits, nh_qact** a) {
     if (int rc = check_ready()) return rc;
     if (!a || rows <= 0 || in_dim <= 0) return fail(NH_EINVAL, "bad activation shape");
-    if (bits != 4) return fail(NH_EINVAL, "only the 4-bit activation layout is supported");
+    if (bits != 2 && bits != 4) return fail(NH_EINVAL, "activation layouts exist for 2- and 4-bit codes");
     const int groups = (in_dim + GROUP - 1) / GROUP;
     if (groups > 32) return fail(NH_EINVAL, "in_dim above 4096 is not supported");
     nh_qact* q = new nh_qact();
@@ -464,7 +532,7 @@ int nh_act_prep(nh_qact* a, const float* x, int rows, int in_dim, const uint16_t
     if (rows <= 0 || rows > a->cap_rows) return fail(NH_EINVAL, "rows outside the activation's capacity");
     if (in_dim != a->in_dim) return fail(NH_EINVAL, "in_dim does not match the activation");
     if (norm_scale && in_dim % 16 != 0) return fail(NH_EINVAL, "the fused norm needs in_dim a multiple of 16");
-    NH_HIP(launch_act_prep(x, rows, in_dim, a->groups, norm_scale, a->d_xq, a->d_sx, (hipStream_t)stream),
+    NH_HIP(launch_act_prep(x, rows, in_dim, a->groups, a->bits, norm_scale, a->d_xq, a->d_sx, (hipStream_t)stream),
            "act_prep");
     a->rows = rows;
     return NH_OK;
@@ -478,9 +546,13 @@ int nh_qact_download(const nh_qact* a, int8_t* xq, uint64_t xq_bytes, float* sx,
     if (xq) {
         std::vector<int8_t> t(nx);
         NH_HIP(hipMemcpy(t.data(), a->d_xq, nx, hipMemcpyDeviceToHost), "download xq");
-        // act_pos (qlinear.rs:145-147), 4-bit: (p % 2) * 64 + p / 2.
+        // act_pos (qlinear.rs:145-147): 2-bit (p % 4) * 32 + p / 4, 4-bit
+        // (p % 2) * 64 + p / 2.
         for (size_t u = 0; u < (size_t)a->rows * a->groups; ++u)
-            for (int p = 0; p < GROUP; ++p) xq[u * GROUP + (p % 2) * 64 + p / 2] = t[u * GROUP + act_offset(p)];
+            for (int p = 0; p < GROUP; ++p) {
+                const int ap = a->bits == 2 ? (p % 4) * 32 + p / 4 : (p % 2) * 64 + p / 2;
+                xq[u * GROUP + ap] = t[u * GROUP + act_offset(p, a->bits)];
+            }
     }
     if (sx) NH_HIP(hipMemcpy(sx, a->d_sx, ns * 4, hipMemcpyDeviceToHost), "download sx");
     return NH_OK;

@@ -56,6 +56,29 @@ __device__ __forceinline__ int dot_chunk(uint4 c, uint4 x0, uint4 x1, const Lut&
     return acc;
 }
 
+// Four 2-bit code fields k of a packed dword (one per byte) -> four int8
+// codebook values: one v_perm lookup in the 4-byte table t (byte c = value
+// of code c; selector bytes 0..3 pick bytes of the second operand).
+__device__ __forceinline__ uint32_t expand2(uint32_t w, int k, uint32_t t) {
+    return __builtin_amdgcn_perm(0u, t, (w >> (2 * k)) & 0x03030303u);
+}
+
+// Exact integer sum of one 2-bit chunk (packed dwords l and 4 + l of a
+// group: 32 codes of decode lane l) against its 32 activation bytes: x0
+// holds dword l's fields k = 0..3 as four 4-byte blocks, x1 dword 4 + l's.
+__device__ __forceinline__ int dot_chunk2(uint2 c, uint4 x0, uint4 x1, uint32_t t) {
+    int acc = 0;
+    acc = __builtin_amdgcn_sdot4((int)expand2(c.x, 0, t), (int)x0.x, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)expand2(c.x, 1, t), (int)x0.y, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)expand2(c.x, 2, t), (int)x0.z, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)expand2(c.x, 3, t), (int)x0.w, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)expand2(c.y, 0, t), (int)x1.x, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)expand2(c.y, 1, t), (int)x1.y, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)expand2(c.y, 2, t), (int)x1.z, acc, false);
+    acc = __builtin_amdgcn_sdot4((int)expand2(c.y, 3, t), (int)x1.w, acc, false);
+    return acc;
+}
+
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }

@@ -40,17 +40,31 @@ __device__ __forceinline__ int swz(int tok, int b) { return b ^ (tok & 7); }
 // (16-row tile, group).  Lane L = 16 q + r holds row r's k-block q of each
 // 64-wide half: the 8-byte code pieces of chunks l = q / 2 (half 0) and
 // 2 + q / 2 (half 1), dword pair q & 1, expanded to int8.
-__global__ __launch_bounds__(64) void k_expand_w8(const uint2* __restrict__ codes, uint4* __restrict__ w8, Lut lut) {
+//
+// 2-bit: the B operand's k-block q of half h is activation bytes
+// h * 64 + q * 16 .. + 16, i.e. decode lane l = 2 h + q / 2's chunk, dword
+// d' = q % 2 of it (packed dword 4 d' + l), fields k = 0..3 as 4-byte
+// blocks; the A fragment expands the same packed dword field by field.
+template <int BITS>
+__global__ __launch_bounds__(64) void k_expand_w8(const void* __restrict__ codes, uint4* __restrict__ w8, Lut lut) {
     const int tg = blockIdx.x;  // tile * G + g
     const int lane = threadIdx.x;
     const int r = lane & 15, q = lane >> 4;
-    const uint2* c = codes + (((size_t)tg * 64 + r * 4 + (q >> 1)) * 2 + (q & 1));
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const uint2 cw = c[h * 4];
         uint32_t e0, e1, e2, e3;
-        expand8(cw.x, lut, e0, e1);
-        expand8(cw.y, lut, e2, e3);
+        if constexpr (BITS == 4) {
+            const uint2 cw = reinterpret_cast<const uint2*>(codes)[((size_t)tg * 64 + r * 4 + (q >> 1)) * 2 + (q & 1) + h * 4];
+            expand8(cw.x, lut, e0, e1);
+            expand8(cw.y, lut, e2, e3);
+        } else {
+            const uint2 cw = reinterpret_cast<const uint2*>(codes)[(size_t)tg * 64 + r * 4 + 2 * h + (q >> 1)];
+            const uint32_t w = (q & 1) ? cw.y : cw.x;
+            e0 = expand2(w, 0, lut.a_lo);
+            e1 = expand2(w, 1, lut.a_lo);
+            e2 = expand2(w, 2, lut.a_lo);
+            e3 = expand2(w, 3, lut.a_lo);
+        }
         w8[((size_t)tg * 2 + h) * 64 + lane] = make_uint4(e0, e1, e2, e3);
     }
 }
@@ -59,7 +73,8 @@ hipError_t launch_expand_w8(const nh_qmat* w, hipStream_t s) {
     const QMatMeta& m = w->m;
     const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
     const int blocks = (m.out + PANEL_ROWS - 1) / PANEL_ROWS * (PANEL_ROWS / 16) * m.groups;
-    hipLaunchKernelGGL(k_expand_w8, dim3(blocks), dim3(64), 0, s, (const uint2*)w->d_codes, w->d_w8, lut);
+    auto kern = m.bits == 2 ? k_expand_w8<2> : k_expand_w8<4>;
+    hipLaunchKernelGGL(kern, dim3(blocks), dim3(64), 0, s, (const void*)w->d_codes, w->d_w8, lut);
     return hipGetLastError();
 }
 
@@ -458,7 +473,7 @@ hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block,
         return general ? run<64, 4, 1, true, false>(w, a, block, y, ldy, col0, dbg, s)
                        : run<64, 4, 1, false, false>(w, a, block, y, ldy, col0, dbg, s);
     if (M > 16 && items(64, 32) >= cus) return run_gc<32, 4, false>(general, w, a, block, y, ldy, col0, dbg, s);
-    if (M <= 16) return run_gc<16, 2, true>(general, w, a, block, y, ldy, col0, dbg, s);
+    if (M <= 16 && w->m.bits == 4) return run_gc<16, 2, true>(general, w, a, block, y, ldy, col0, dbg, s);
     return run_gc<16, 2, false>(general, w, a, block, y, ldy, col0, dbg, s);
 }
 

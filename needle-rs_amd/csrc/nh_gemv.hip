@@ -1,31 +1,33 @@
-// Decode GEMV: one token against a CQ-W4 matrix with the reference's decode
+// Decode GEMV: one token against a CQ matrix with the reference's decode
 // combine (crates/needle-engine/src/qlinear.rs:340-350): four float lanes
-// per row, lane l fed by positions p with (p % 32) / 8 == l, scale
+// per row, lane l fed by positions p with (p % 32) / 8 == l (4-bit) or
+// (p % 64) / 16 == l (2-bit, qlinear.rs:333), scale
 // (sx * cbs) * norm, lane_l = fma(sum_l, scale, lane_l) over groups in
 // order, y = (l0 + l1) + (l2 + l3).
 //
 // HBM-bound.  A workgroup owns one 16-row tile.  Its S wavefronts split the
 // tile's groups (GPS each); in a wavefront, lane = 4 * row + l, so each
 // load instruction reads the tile-group block (16 rows x 4 lanes x 16 B)
-// as 1 KiB of contiguous HBM.  A lane's 16 bytes are exactly its decode
-// lane's 32 codes of the group, so its integer sum is the reference's
+// as 1 KiB (4-bit; 512 B for 2-bit) of contiguous HBM.  A lane's 16 (8)
+// bytes are exactly its decode lane's 32 codes of the group, so its integer sum is the reference's
 // lane sum L[n][g][l] (qlinear.rs:327-337) with no cross-lane reduction.
 // Every load (codes, activations, norms, scales) is issued before any
 // arithmetic, so a launch costs one memory round trip; each wavefront
 // turns its groups into (float(L), scale) pairs and wave 0 runs the
 // group-ordered fma chain from LDS.
+#include <type_traits>
+
 #include "nh_device.h"
 #include "nh_internal.h"
 
 namespace nh {
 
-template <int GPS, int S, bool DBG>
-__global__ __launch_bounds__(S * 64) void k_gemv(const uint4* __restrict__ codes, const uint16_t* __restrict__ norms,
+template <int GPS, int S, int BITS, bool DBG>
+__global__ __launch_bounds__(S * 64) void k_gemv(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
                                                  const uint4* __restrict__ xq, const float* __restrict__ sx,
-                                                 float* __restrict__ y, int32_t* __restrict__ dbg, int out,
+                                                 float* __restrict__ y, int32_t* __restrict__ dbg, int out, int G,
                                                  float cbs, Lut lut) {
-    constexpr int G = GPS * S;
-    static_assert(S * 64 >= G * 8, "one thread per activation uint4");
+    static_assert(S * 64 >= GPS * S * 8, "one thread per activation uint4");
     const int tile = blockIdx.x;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -36,27 +38,38 @@ __global__ __launch_bounds__(S * 64) void k_gemv(const uint4* __restrict__ codes
     // The token's activations (G * 128 bytes) go to LDS once per workgroup;
     // their load is issued first so waiting for it does not wait for the
     // code stream behind it.
-    __shared__ uint4 xs[G * 8];
+    __shared__ uint4 xs[GPS * S * 8];
     uint4 xv = make_uint4(0, 0, 0, 0);
     if (threadIdx.x < G * 8) xv = xq[threadIdx.x];
-    uint4 c[GPS];
+    // A lane's chunk: 16 bytes (4-bit: 32 codes) or 8 (2-bit: 32 codes).
+    using Chunk = typename std::conditional<BITS == 4, uint4, uint2>::type;
+    Chunk c[GPS];
     uint16_t nb[GPS];
     float sxv[GPS];
 #pragma unroll
-    for (int j = 0; j < GPS; ++j) c[j] = load_stream(codes + ((size_t)(tile * G + g0 + j) * 64 + lane));
-#pragma unroll
     for (int j = 0; j < GPS; ++j) {
-        nb[j] = norms[(size_t)n * G + g0 + j];
-        sxv[j] = sx[g0 + j];
+        // Groups past G (when S * GPS > G) reload group 0; never used.
+        const int g = g0 + j < G ? g0 + j : 0;
+        if constexpr (BITS == 4)
+            c[j] = load_stream(reinterpret_cast<const uint4*>(codes) + ((size_t)(tile * G + g) * 64 + lane));
+        else
+            c[j] = reinterpret_cast<const uint2*>(codes)[(size_t)(tile * G + g) * 64 + lane];
+        nb[j] = norms[(size_t)n * G + g];
+        sxv[j] = sx[g];
     }
     if (threadIdx.x < G * 8) xs[threadIdx.x] = xv;
     __syncthreads();
     float lf[GPS], sc[GPS];
 #pragma unroll
     for (int j = 0; j < GPS; ++j) {
-        const uint4* xp = xs + ((g0 + j) * 4 + l) * 2;
-        const int isum = dot_chunk(c[j], xp[0], xp[1], lut);
-        if (DBG && n < out) dbg[((size_t)n * G + g0 + j) * 4 + l] = isum;
+        const int g = g0 + j < G ? g0 + j : 0;
+        const uint4* xp = xs + (g * 4 + l) * 2;
+        int isum;
+        if constexpr (BITS == 4)
+            isum = dot_chunk(c[j], xp[0], xp[1], lut);
+        else
+            isum = dot_chunk2(c[j], xp[0], xp[1], lut.a_lo);
+        if (DBG && n < out && g0 + j < G) dbg[((size_t)n * G + g0 + j) * 4 + l] = isum;
         lf[j] = (float)isum;
         sc[j] = (sxv[j] * cbs) * f16_bits_to_f32(nb[j]);
     }
@@ -64,14 +77,14 @@ __global__ __launch_bounds__(S * 64) void k_gemv(const uint4* __restrict__ codes
     float acc = 0.0f;
     if constexpr (S == 1) {
 #pragma unroll
-        for (int g = 0; g < G; ++g) acc = __builtin_fmaf(lf[g], sc[g], acc);
+        for (int j = 0; j < GPS; ++j)
+            if (j < G) acc = __builtin_fmaf(lf[j], sc[j], acc);
     } else {
-        __shared__ float2 part[G][64];
+        __shared__ float2 part[GPS * S][64];
 #pragma unroll
         for (int j = 0; j < GPS; ++j) part[g0 + j][lane] = make_float2(lf[j], sc[j]);
         __syncthreads();
         if (wave != 0) return;
-#pragma unroll
         for (int g = 0; g < G; ++g) {
             const float2 p = part[g][lane];
             acc = __builtin_fmaf(p.x, p.y, acc);
@@ -83,39 +96,44 @@ __global__ __launch_bounds__(S * 64) void k_gemv(const uint4* __restrict__ codes
     if (y && l == 0 && n < out) y[n] = u;
 }
 
-template <int GPS, int S>
+template <int GPS, int S, int BITS>
 static hipError_t run(const nh_qmat* w, const nh_qact* a, float* y, int32_t* dbg, hipStream_t s) {
     const QMatMeta& m = w->m;
     const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
     dim3 grid(m.out_pad / TILE_ROWS), block(S * 64);
     if (dbg)
-        hipLaunchKernelGGL((k_gemv<GPS, S, true>), grid, block, 0, s, w->d_codes, w->d_norms,
-                           (const uint4*)a->d_xq, a->d_sx, y, dbg, m.out, m.cbs, lut);
+        hipLaunchKernelGGL((k_gemv<GPS, S, BITS, true>), grid, block, 0, s, w->d_codes, w->d_norms,
+                           (const uint4*)a->d_xq, a->d_sx, y, dbg, m.out, m.groups, m.cbs, lut);
     else
-        hipLaunchKernelGGL((k_gemv<GPS, S, false>), grid, block, 0, s, w->d_codes, w->d_norms,
-                           (const uint4*)a->d_xq, a->d_sx, y, dbg, m.out, m.cbs, lut);
+        hipLaunchKernelGGL((k_gemv<GPS, S, BITS, false>), grid, block, 0, s, w->d_codes, w->d_norms,
+                           (const uint4*)a->d_xq, a->d_sx, y, dbg, m.out, m.groups, m.cbs, lut);
     return hipGetLastError();
 }
 
-// Groups per wavefront and wavefronts per tile for each supported group
-// count: two to four groups per lane keeps 2-4 KiB of loads in flight per
-// wavefront while giving the big shapes several wavefronts per CU.
+// Groups per wavefront (GPS) and wavefronts per tile (S) by group count:
+// two to four groups per lane keeps 2-4 KiB of loads in flight per
+// wavefront while giving the big shapes several wavefronts per CU.  Any G
+// up to 32 maps to the smallest listed G' >= G (wavefronts skip the
+// groups past G).
+template <int BITS>
+static hipError_t dispatch(const nh_qmat* w, const nh_qact* a, float* y, int32_t* dbg, hipStream_t s) {
+    const int G = w->m.groups;
+    if (G <= 1) return run<1, 1, BITS>(w, a, y, dbg, s);
+    if (G <= 2) return run<2, 1, BITS>(w, a, y, dbg, s);
+    if (G <= 3) return run<3, 1, BITS>(w, a, y, dbg, s);
+    if (G <= 4) return run<2, 2, BITS>(w, a, y, dbg, s);
+    if (G <= 6) return run<3, 2, BITS>(w, a, y, dbg, s);
+    if (G <= 8) return run<2, 4, BITS>(w, a, y, dbg, s);
+    if (G <= 12) return run<3, 4, BITS>(w, a, y, dbg, s);
+    if (G <= 16) return run<4, 4, BITS>(w, a, y, dbg, s);
+    if (G <= 24) return run<4, 6, BITS>(w, a, y, dbg, s);
+    if (G <= 32) return run<4, 8, BITS>(w, a, y, dbg, s);
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemv(const nh_qmat* w, const nh_qact* a, float* y, int col0, int32_t* dbg, hipStream_t s) {
     float* yc = y ? y + col0 : nullptr;
-    switch (w->m.groups) {
-    case 1: return run<1, 1>(w, a, yc, dbg, s);
-    case 2: return run<2, 1>(w, a, yc, dbg, s);
-    case 3: return run<3, 1>(w, a, yc, dbg, s);
-    case 4: return run<2, 2>(w, a, yc, dbg, s);
-    case 5: return run<5, 1>(w, a, yc, dbg, s);
-    case 6: return run<3, 2>(w, a, yc, dbg, s);
-    case 8: return run<2, 4>(w, a, yc, dbg, s);
-    case 12: return run<3, 4>(w, a, yc, dbg, s);
-    case 16: return run<4, 4>(w, a, yc, dbg, s);
-    case 24: return run<4, 6>(w, a, yc, dbg, s);
-    case 32: return run<4, 8>(w, a, yc, dbg, s);
-    default: return hipErrorInvalidValue;
-    }
+    return w->m.bits == 2 ? dispatch<2>(w, a, yc, dbg, s) : dispatch<4>(w, a, yc, dbg, s);
 }
 
 }  // namespace nh

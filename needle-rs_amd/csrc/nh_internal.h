@@ -35,10 +35,14 @@ struct QMatMeta {
     int out_pad;   // rows padded to TILE_ROWS
     int in_dim;
     int groups;
-    int bits;
+    int bits;                // 2 or 4 bits per code
+    bool ternary;            // a ternary record (2-bit codes, remapped)
     float cbs;               // int8 codebook scale
     int8_t vals[16];         // code -> int8 codebook value
     float fvals[16];         // code -> f32 codebook value
+    // 4-bit: the v_perm table pair and selector map.  2-bit: codes are
+    // stored as they are and lut.a_lo holds vals[0..3] as bytes (one v_perm
+    // lookup with the 2-bit code as selector).
     LutTables lut;
 };
 
@@ -77,17 +81,26 @@ void set_error(const std::string& msg);
 int device_cus();
 
 // Byte offset (0..127) inside a group's activation block of natural
-// position p: dword d = p / 8 of the packed codes belongs to decode lane
-// l = d % 4 (qlinear.rs:333) and is the k = d / 4 -th dword of that lane's
-// chunk; its even positions meet bytes 0..3, its odd ones bytes 4..7.
-__host__ __device__ inline int act_offset(int p) {
-    int d = p >> 3, j = p & 7;
-    int l = d & 3, k = d >> 2;
+// position p, for the code width `bits` of the matrices it feeds.  Each
+// decode lane l (qlinear.rs:333) owns 32 contiguous bytes at l * 32.
+//  4-bit: dword d = p / 8 of the packed codes belongs to lane l = d % 4 and
+//    is the k = d / 4 -th dword of its chunk; its even positions meet bytes
+//    0..3 of an 8-byte block, its odd ones bytes 4..7.
+//  2-bit: dword d = p / 16 belongs to lane l = d % 4 (positions with
+//    (p % 64) / 16 == l) as its d / 4 -th dword; the 2-bit field k = p % 4
+//    of its byte b = (p / 4) % 4 meets byte b of 4-byte block k.
+__host__ __device__ inline int act_offset(int p, int bits) {
+    if (bits == 2) {
+        const int d = p >> 4, l = d & 3;
+        return l * 32 + ((d >> 2) * 4 + (p & 3)) * 4 + ((p >> 2) & 3);
+    }
+    const int d = p >> 3, j = p & 7;
+    const int l = d & 3, k = d >> 2;
     return ((l * 4 + k) << 3) + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
 }
 
 // Launchers (one per kernel translation unit).
-hipError_t launch_act_prep(const float* x, int rows, int in_dim, int groups, const uint16_t* norm_scale,
+hipError_t launch_act_prep(const float* x, int rows, int in_dim, int groups, int bits, const uint16_t* norm_scale,
                            int8_t* xq, float* sx, hipStream_t s);
 hipError_t launch_gemv(const nh_qmat* w, const nh_qact* a, float* y, int col0, int32_t* dbg_lanes, hipStream_t s);
 hipError_t launch_expand_w8(const nh_qmat* w, hipStream_t s);

@@ -14,7 +14,8 @@ namespace nh {
 constexpr int SR_WAVES = 4;
 constexpr int SR_MAX_GROUPS = 32;
 
-__global__ __launch_bounds__(SR_WAVES * 64) void k_single_rows(const uint4* __restrict__ codes,
+template <int BITS>
+__global__ __launch_bounds__(SR_WAVES * 64) void k_single_rows(const void* __restrict__ codes,
                                                                const uint16_t* __restrict__ norms,
                                                                const uint4* __restrict__ xq,
                                                                const float* __restrict__ sx,
@@ -35,9 +36,12 @@ __global__ __launch_bounds__(SR_WAVES * 64) void k_single_rows(const uint4* __re
         const int g = gs + 16 * j;
         int s = 0;
         if (g < G) {
-            const uint4 c = codes[((size_t)tile * G + g) * 64 + rt * 4 + l];
+            const size_t ci = ((size_t)tile * G + g) * 64 + rt * 4 + l;
             const uint4* xp = xq + (g * 4 + l) * 2;
-            s = dot_chunk(c, xp[0], xp[1], lut);
+            if constexpr (BITS == 4)
+                s = dot_chunk(reinterpret_cast<const uint4*>(codes)[ci], xp[0], xp[1], lut);
+            else
+                s = dot_chunk2(reinterpret_cast<const uint2*>(codes)[ci], xp[0], xp[1], lut.a_lo);
         }
         s += __shfl_xor(s, 1, 64);
         s += __shfl_xor(s, 2, 64);
@@ -62,8 +66,9 @@ hipError_t launch_single_rows(const nh_qmat* w, const nh_qact* a, const uint32_t
     if (n <= 0) return hipSuccess;
     if (w->m.groups > SR_MAX_GROUPS) return hipErrorInvalidValue;
     const Lut lut{w->m.lut.a_hi, w->m.lut.a_lo, w->m.lut.b_hi, w->m.lut.b_lo};
-    hipLaunchKernelGGL(k_single_rows, dim3((n + SR_WAVES - 1) / SR_WAVES), dim3(SR_WAVES * 64), 0, s, w->d_codes,
-                       w->d_norms, (const uint4*)a->d_xq, a->d_sx, ids, n, w->m.out, w->m.groups, w->m.cbs, lut, out,
+    auto kern = w->m.bits == 2 ? k_single_rows<2> : k_single_rows<4>;
+    hipLaunchKernelGGL(kern, dim3((n + SR_WAVES - 1) / SR_WAVES), dim3(SR_WAVES * 64), 0, s, w->d_codes, w->d_norms,
+                       (const uint4*)a->d_xq, a->d_sx, ids, n, w->m.out, w->m.groups, w->m.cbs, lut, out,
                        scatter_logits, scatter_n);
     return hipGetLastError();
 }
@@ -83,14 +88,25 @@ hipError_t launch_fill(float* p, float v, int n, hipStream_t s) {
 // QMat::row (crates/needle-engine/src/qlinear.rs:309-323): per group
 // cb[code] * norm, then the normalised rotation.  One wavefront per
 // (id, group), two positions per lane.
-__device__ __forceinline__ uint32_t code_sel_at(const uint4* codes, int tile, int G, int g, int rt, int p) {
-    const int d = p >> 3, j = p & 7;
-    const int l = d & 3, k = d >> 2;
-    const uint32_t* chunk = (const uint32_t*)(codes + ((size_t)tile * G + g) * 64 + rt * 4 + l);
-    return (chunk[k] >> (4 * j)) & 15u;
+// The stored selector of natural position p: 4-bit dword d = p / 8 is
+// dword d / 4 of lane d % 4's 16-byte chunk; 2-bit dword d = p / 16 is
+// dword d / 4 of lane d % 4's 8-byte chunk, field p % 4 of byte (p / 4) % 4.
+template <int BITS>
+__device__ __forceinline__ uint32_t code_sel_at(const void* codes, int tile, int G, int g, int rt, int p) {
+    const size_t ci = ((size_t)tile * G + g) * 64 + rt * 4;
+    if constexpr (BITS == 4) {
+        const int d = p >> 3;
+        const uint32_t* chunk = (const uint32_t*)(reinterpret_cast<const uint4*>(codes) + ci + (d & 3));
+        return (chunk[d >> 2] >> (4 * (p & 7))) & 15u;
+    } else {
+        const int d = p >> 4;
+        const uint32_t* chunk = (const uint32_t*)(reinterpret_cast<const uint2*>(codes) + ci + (d & 3));
+        return (chunk[d >> 2] >> (8 * ((p >> 2) & 3) + 2 * (p & 3))) & 3u;
+    }
 }
 
-__global__ __launch_bounds__(256) void k_rows(const uint4* __restrict__ codes, const uint16_t* __restrict__ norms,
+template <int BITS>
+__global__ __launch_bounds__(256) void k_rows(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
                                               const float* __restrict__ fsel, const uint32_t* __restrict__ ids,
                                               int n, int out, int G, int in_dim, float* __restrict__ dst) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -102,8 +118,8 @@ __global__ __launch_bounds__(256) void k_rows(const uint4* __restrict__ codes, c
     const uint32_t rr = ok ? row : 0u;
     const int tile = rr / TILE_ROWS, rt = rr % TILE_ROWS;
     const float norm = f16_bits_to_f32(norms[(size_t)rr * G + g]);
-    float v0 = fsel[code_sel_at(codes, tile, G, g, rt, lane)] * norm;
-    float v1 = fsel[code_sel_at(codes, tile, G, g, rt, lane + 64)] * norm;
+    float v0 = fsel[code_sel_at<BITS>(codes, tile, G, g, rt, lane)] * norm;
+    float v1 = fsel[code_sel_at<BITS>(codes, tile, G, g, rt, lane + 64)] * norm;
     fwht128(v0, v1, lane);
     const float hs = bits_f32(0x3db504f3u);
     v0 *= hs;
@@ -118,7 +134,8 @@ __global__ __launch_bounds__(256) void k_rows(const uint4* __restrict__ codes, c
 hipError_t launch_rows(const nh_qmat* w, const uint32_t* ids, int n, float* out, hipStream_t s) {
     if (n <= 0) return hipSuccess;
     const int units = n * w->m.groups;
-    hipLaunchKernelGGL(k_rows, dim3((units + 3) / 4), dim3(256), 0, s, w->d_codes, w->d_norms, w->d_fsel, ids, n,
+    auto kern = w->m.bits == 2 ? k_rows<2> : k_rows<4>;
+    hipLaunchKernelGGL(kern, dim3((units + 3) / 4), dim3(256), 0, s, w->d_codes, w->d_norms, w->d_fsel, ids, n,
                        w->m.out, w->m.groups, w->m.in_dim, out);
     return hipGetLastError();
 }

@@ -164,7 +164,8 @@ class QAct:
 
 
 class QMat:
-    """A CQ-W4 matrix resident in HBM (qlinear.rs:43-61, 218-488)."""
+    """A CQ matrix (2- or 4-bit codes, or a ternary record) resident in HBM
+    (qlinear.rs:43-61, 218-488)."""
 
     def __init__(self, h):
         self.h = h
@@ -176,7 +177,8 @@ class QMat:
     @classmethod
     def from_cq(cls, packed: np.ndarray, norms: np.ndarray, out: int, in_dim: int, bits: int = 4,
                 group: int = GROUP) -> "QMat":
-        """QMat::from_cq over a CqView blob: packed u8 [out, row_bytes], norms f16 bits."""
+        """QMat::from_cq over a CqView blob: packed u8 [out, row_bytes], norms f16 bits;
+        bits 2, 4 or 5 (ternary)."""
         lib = init()
         packed = np.ascontiguousarray(packed, dtype=np.uint8)
         norms = np.ascontiguousarray(norms, dtype=np.uint16)
@@ -202,7 +204,7 @@ class QMat:
         return self.bits
 
     def download(self):
-        """(packed u8 [out, groups*64], norms u16 [out, groups]) in archive layout."""
+        """(packed u8 [out, groups*128*bits/8], norms u16 [out, groups]) in archive layout."""
         packed = np.zeros((self.out, self.groups * GROUP * self.bits // 8), dtype=np.uint8)
         norms = np.zeros((self.out, self.groups), dtype=np.uint16)
         _check(_lib.nh_qmat_download(self.h, _hptr(packed), packed.nbytes, _hptr(norms), norms.size))
