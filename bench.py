@@ -118,7 +118,7 @@ def gpu_gemv_steady(gpu, copies, nh, torch):
         for _ in range(8):
             big.matmul_into(a, y, nbig, 0)
 
-    ms = time_graph(sweep, 5, 1, torch) / 8
+    ms = time_graph(sweep, 20, 2, torch) / 8
     nbytes = algorithmic_bytes(1, K, nbig)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"workload": f"one launch of the same decode GEMV over N={nbig} rows (the {copies} copies fused by row), "
@@ -161,6 +161,32 @@ def gpu_sweeps(nh, torch):
     return out
 
 
+def gemm_shape(spec: str, launches: int, nh, torch):
+    """One prefill product M x K x N (seeded as the sweep), `launches` eager
+    launches timed with HIP events on the launch stream: the command the
+    GEMM profiles are taken from."""
+    M, k, n = (int(v) for v in spec.split(","))
+    w, x = nh.seeded_normals([n * k, M * k], 0)
+    w *= 0.02
+    q = nh.QMat.from_f32(w, n, k)
+    a = nh.QAct.new(torch.from_numpy(x).cuda(), M, k)
+    y = torch.empty((M, n), dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        q.matmul_into(a, y, n, 0)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(launches):
+        q.matmul_into(a, y, n, 0)
+    end.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / launches
+    ops = 2.0 * M * n * k
+    return {"gemm": {"M": M, "K": k, "N": n}, "launches": launches, "us_per_launch": round(us, 3),
+            "TOPS": round(ops / (us * 1e-6) / 1e12, 2), "frac_int8_peak": round(ops / (us * 1e-6) / 1e12 / INT8_PEAK_TOPS, 4)}
+
+
 def cpu_baseline(gpu, seconds: float):
     """The oracle's decode GEMV (reference x86-64 portable path) on the host."""
     import numpy as np
@@ -196,6 +222,9 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device-to-device copy of BYTES (scales rocprofv3 byte counters)")
+    ap.add_argument("--gemm-shape", default="", metavar="M,K,N",
+                    help="only run one prefill product shape, eagerly (for GEMM profiles)")
+    ap.add_argument("--launches", type=int, default=200, help="launches for --gemm-shape")
     args = ap.parse_args()
     if args.copy_calibration:
         import torch
@@ -220,6 +249,9 @@ def main():
 
     nh.init(0)
     torch.cuda.synchronize()
+    if args.gemm_shape:
+        print(json.dumps(gemm_shape(args.gemm_shape, args.launches, nh, torch)))
+        return
     gpu = gpu_gemv(args, nh, torch)
     steps = gpu["launches"]
     line = {

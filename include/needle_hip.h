@@ -65,6 +65,9 @@ int nh_qmat_from_f32(const float* w, int out, int in_dim, nh_qmat** h);
  * (q|k|v|gate, crates/needle-engine/src/weights.rs:484-490).  The parts
  * stay valid and owned by the caller. */
 int nh_qlinear_new(nh_qmat* const* parts, int n, nh_qmat** h);
+/* QMat::slice_rows (qlinear.rs:268-276): rows r0..r1 of h as their own
+ * matrix (per-layer slices of stacked records, weights.rs:383-388). */
+int nh_qmat_slice_rows(const nh_qmat* h, int r0, int r1, nh_qmat** out);
 int nh_qmat_free(nh_qmat* h);
 /* out, in_dim, bits of a matrix. */
 int nh_qmat_shape(const nh_qmat* h, int* out, int* in_dim, int* bits);

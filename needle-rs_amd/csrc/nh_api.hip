@@ -444,6 +444,16 @@ int nh_qlinear_new(nh_qmat* const* parts, int n, nh_qmat** h) {
     return upload(std::move(packed), std::move(norms), out, m0.in_dim, m0.bits, m0.ternary, h);
 }
 
+int nh_qmat_slice_rows(const nh_qmat* h, int r0, int r1, nh_qmat** out) {
+    if (int rc = check_ready()) return rc;
+    if (!h || !out) return fail(NH_EINVAL, "null argument");
+    if (r0 < 0 || r1 <= r0 || r1 > h->m.out) return fail(NH_EINVAL, "row range outside the matrix");
+    const size_t rb = h->h_packed.size() / h->m.out, G = h->m.groups;
+    std::vector<uint8_t> packed(h->h_packed.begin() + r0 * rb, h->h_packed.begin() + r1 * rb);
+    std::vector<uint16_t> norms(h->h_norms.begin() + r0 * G, h->h_norms.begin() + r1 * G);
+    return upload(std::move(packed), std::move(norms), r1 - r0, h->m.in_dim, h->m.bits, h->m.ternary, out);
+}
+
 int nh_qmat_free(nh_qmat* h) {
     if (!h) return NH_OK;
     if (h->d_codes) hipFree(h->d_codes);

@@ -30,6 +30,7 @@ SIGNATURES = {
     "nh_qmat_from_cq": (I, [P, C.c_uint64, P, C.c_uint64, I, I, I, I, P]),
     "nh_qmat_from_f32": (I, [P, I, I, P]),
     "nh_qlinear_new": (I, [P, I, P]),
+    "nh_qmat_slice_rows": (I, [P, I, I, P]),
     "nh_qmat_free": (I, [P]),
     "nh_qmat_shape": (I, [P, P, P, P]),
     "nh_qmat_bytes": (C.c_int64, [P]),
@@ -199,6 +200,12 @@ class QMat:
 
     def bytes(self) -> int:
         return _check(_lib.nh_qmat_bytes(self.h))
+
+    def slice_rows(self, r0: int, r1: int) -> "QMat":
+        """QMat::slice_rows: rows r0..r1 as their own matrix."""
+        h = C.c_void_p()
+        _check(_lib.nh_qmat_slice_rows(self.h, r0, r1, C.byref(h)))
+        return QMat(h)
 
     def act_bits(self) -> int:
         return self.bits

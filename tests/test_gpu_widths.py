@@ -166,3 +166,23 @@ def test_width_mismatch_and_fusion(nh):
     p, n = q2.download()
     assert np.array_equal(p, packed2) and np.array_equal(n, norms2)
     assert q2.bytes() == 40 * 2 * 32 + 40 * 2 * 2
+
+
+@pytest.mark.parametrize("bits", [2, 4])
+def test_slice_rows(nh, bits):
+    # QMat::slice_rows (qlinear.rs:268-276) as weights.rs:383-388 uses it.
+    say(f"slice_rows bits={bits}")
+    out, K = 96, 384
+    packed, norms = random_record(out, K, bits, seed=90)
+    q = nh.QMat.from_cq(packed, norms, out, K, bits)
+    s = q.slice_rows(24, 72)
+    assert (s.out, s.in_dim, s.bits) == (48, K, bits)
+    p, n = s.download()
+    assert np.array_equal(p, packed[24:72]) and np.array_equal(n, norms[24:72])
+    x = o.seeded_normals([3 * K], 91)[0]
+    a = nh.QAct.new(dev(x), 3, K, bits)
+    y = s.matmul(a).cpu().numpy()
+    want = o.OQMat.from_cq(packed[24:72], norms[24:72], 48, K, bits).matmul(o.OQAct.new(x, 3, K, bits))
+    assert bits_equal(y, want)
+    with pytest.raises(nh.NeedleHipError):
+        q.slice_rows(50, 40)
