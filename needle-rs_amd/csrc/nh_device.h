@@ -9,6 +9,15 @@ namespace nh {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
+// The value of lane (lane ^ 1) / (lane ^ 2) within each group of four
+// lanes, by DPP quad permutes (no LDS round trip, unlike a shuffle).
+__device__ __forceinline__ float quad_xor1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_xor2(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+
 // A streamed 16-byte load (read once, non-temporal hint).
 __device__ __forceinline__ uint4 load_stream(const uint4* p) {
     u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));

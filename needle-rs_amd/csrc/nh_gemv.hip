@@ -91,8 +91,8 @@ __global__ __launch_bounds__(S * 64) void k_gemv(const void* __restrict__ codes,
         }
     }
     // (l0 + l1) + (l2 + l3) across the row's four lanes.
-    float t = acc + __shfl_xor(acc, 1, 64);
-    float u = t + __shfl_xor(t, 2, 64);
+    const float t = acc + quad_xor1(acc);
+    const float u = t + quad_xor2(t);
     if (y && l == 0 && n < out) y[n] = u;
 }
 
