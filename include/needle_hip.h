@@ -37,6 +37,7 @@ extern "C" {
 
 typedef struct nh_qmat nh_qmat; /* a CQ matrix resident in HBM (QMat / fused QLinear) */
 typedef struct nh_qact nh_qact; /* rotated int8 activations resident in HBM (QAct) */
+typedef struct nh_weights nh_weights; /* every matmul weight of a .cact archive in HBM (QWeights) */
 
 /* ---- runtime ----------------------------------------------------------- */
 /* Select the device and prepare the code tables.  No reference counterpart
@@ -121,6 +122,38 @@ int nh_head_logits_sparse(const nh_qmat* w, const nh_qact* a, const uint32_t* id
  * bit-exact check: one token -> int32 lanes[out][groups][4]; more ->
  * int32 totals[rows][out][groups]. */
 int nh_debug_partials(const nh_qmat* w, const nh_qact* a, int32_t* out, void* stream);
+
+/* ---- archives (QWeights, crates/needle-engine/src/weights.rs:136-148) --- */
+/* Weights::from_archive_mode with fast = true (weights.rs:314-467) over the
+ * bytes of a .cact archive (Archive::from_raw, crates/needle-core/src/cact.rs:577-583),
+ * borrowed for the call only as needle_load borrows them
+ * (crates/needle-ffi/src/lib.rs:57-77).  The header, codebook and directory
+ * are parsed with the reference's checks (cact.rs:120-131,213-230,593-614),
+ * the canonical record order is walked and checked (weights.rs:318-464),
+ * and only then is anything uploaded, so a malformed archive returns
+ * NH_EINVAL (with the reference's message) even without nh_init.  CQ records
+ * upload as nh_qmat_from_cq, f16/f32 matmul records as nh_qmat_from_f32
+ * (Cursor::big, weights.rs:113-128).  The matrices are fused as QWeights
+ * holds them: q|k|v|gate and out per layer, the mHC pre|post|res rows of
+ * each layer, engram key|value per site; engram tables and the embedding
+ * stay whole. */
+int nh_weights_load(const uint8_t* bytes, uint64_t n, nh_weights** w);
+int nh_weights_free(nh_weights* w);
+/* The 49 header words in archive order (cact.rs:80-118); copies up to n of
+ * them and returns 49. */
+int nh_weights_header(const nh_weights* w, uint32_t* words, int n);
+#define NH_W_EMBEDDING 0    /* QWeights::embedding (index 0) */
+#define NH_W_QKVG 1         /* QWeights::qkvg[layer] */
+#define NH_W_OUT 2          /* QWeights::out[layer] */
+#define NH_W_PHI 3          /* QWeights::phi[layer] */
+#define NH_W_ENGRAM_TABLE 4 /* QWeights::engram_tables[site] */
+#define NH_W_ENGRAM_KV 5    /* QWeights::engram_kv[site] */
+/* Number of matrices of a kind. */
+int nh_weights_count(const nh_weights* w, int kind);
+/* A matrix of a kind, owned by w (valid until nh_weights_free). */
+int nh_weights_get(const nh_weights* w, int kind, int index, const nh_qmat** m);
+/* QWeights::bytes (weights.rs:151-155): packed codes + f16 norms of every matrix. */
+int64_t nh_weights_bytes(const nh_weights* w);
 
 /* ---- seeded inputs (host) ---------------------------------------------- */
 /* jax.random.normal for float32 from a threefry key, as

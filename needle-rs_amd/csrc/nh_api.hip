@@ -36,6 +36,8 @@ void set_error(const std::string& msg) { g_err = msg; }
 
 int device_cus() { return g_cus > 0 ? g_cus : 1; }
 
+bool ready() { return g_device >= 0 && g_lut_ok; }
+
 static int fail(int code, const std::string& msg) {
     set_error(msg);
     return code;

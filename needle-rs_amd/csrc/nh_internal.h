@@ -79,6 +79,8 @@ namespace nh {
 void set_error(const std::string& msg);
 // Compute units of the device selected by nh_init.
 int device_cus();
+// nh_init has selected a device and built the code tables.
+bool ready();
 
 // Byte offset (0..127) inside a group's activation block of natural
 // position p, for the code width `bits` of the matrices it feeds.  Each

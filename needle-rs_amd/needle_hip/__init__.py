@@ -46,6 +46,12 @@ SIGNATURES = {
     "nh_single_rows": (I, [P, P, P, I, P, P]),
     "nh_head_logits_sparse": (I, [P, P, P, I, I, P, P]),
     "nh_debug_partials": (I, [P, P, P, P]),
+    "nh_weights_load": (I, [P, C.c_uint64, P]),
+    "nh_weights_free": (I, [P]),
+    "nh_weights_header": (I, [P, P, I]),
+    "nh_weights_count": (I, [P, I]),
+    "nh_weights_get": (I, [P, I, I, P]),
+    "nh_weights_bytes": (C.c_int64, [P]),
     "nh_normal": (I, [C.c_uint32, C.c_uint32, C.c_uint64, P]),
     "nh_split": (I, [C.c_uint32, C.c_uint32, P]),
 }
@@ -168,8 +174,11 @@ class QMat:
     """A CQ matrix (2- or 4-bit codes, or a ternary record) resident in HBM
     (qlinear.rs:43-61, 218-488)."""
 
-    def __init__(self, h):
+    def __init__(self, h, owner=None):
+        # A matrix owned by another handle (QWeights) keeps that handle
+        # alive and is not freed here.
         self.h = h
+        self._owner = owner
         out, ind, bits = C.c_int(), C.c_int(), C.c_int()
         _check(_lib.nh_qmat_shape(h, C.byref(out), C.byref(ind), C.byref(bits)))
         self.out, self.in_dim, self.bits = out.value, ind.value, bits.value
@@ -258,9 +267,9 @@ class QMat:
         return out
 
     def __del__(self):
-        if getattr(self, "h", None) and _lib is not None:
+        if getattr(self, "h", None) and _lib is not None and getattr(self, "_owner", None) is None:
             _lib.nh_qmat_free(self.h)
-            self.h = None
+        self.h = None
 
 
 class QLinear:
@@ -290,6 +299,71 @@ class QLinear:
 
     def bytes(self) -> int:
         return self.fused.bytes()
+
+
+# Header words of a .cact archive (crates/needle-core/src/cact.rs:80-118).
+HEADER_WORDS = ("tag", "num_tensors", "codebook_len", "kv_window", "kv_bits", "vocab", "out_vocab", "d_model",
+                "num_heads", "num_kv_heads", "num_layers", "qk_head_dim", "v_head_dim", "max_seq_len", "hada_n",
+                "mhc_lanes", "sliding_window", "global_mask_lo", "global_mask_hi", "qkv_conv_taps", "engram_slots",
+                "engram_sub_dim", "num_engram_tables", "engram_conv_taps", "engram_conv_dilation",
+                "engram_seed_heads", "num_engram_orders")
+W_EMBEDDING, W_QKVG, W_OUT, W_PHI, W_ENGRAM_TABLE, W_ENGRAM_KV = range(6)
+
+
+class QWeights:
+    """QWeights (crates/needle-engine/src/weights.rs:136-148): every matmul
+    weight of a .cact archive, packed in HBM, as
+    Weights::from_archive_mode(fast = true) reads them (weights.rs:314-467).
+    embedding; qkvg / out per layer (q|k|v|gate fused); phi per layer (mHC
+    pre|post|res rows fused); engram_tables and engram_kv (key|value fused)
+    per site."""
+
+    def __init__(self, h):
+        self.h = h
+        words = (C.c_uint32 * 49)()
+        _check(_lib.nh_weights_header(h, C.cast(words, C.c_void_p), 49))
+        self.header_words = list(words)
+        self.header = dict(zip(HEADER_WORDS, self.header_words))
+        self.header["rope_theta"] = float(np.frombuffer(np.uint32(words[48]).tobytes(), dtype=np.float32)[0])
+
+        def kind(k):
+            n = _lib.nh_weights_count(h, k)
+            _check(n)
+            out = []
+            for i in range(n):
+                m = C.c_void_p()
+                _check(_lib.nh_weights_get(h, k, i, C.byref(m)))
+                out.append(QMat(m, owner=self))
+            return out
+
+        self.embedding = kind(W_EMBEDDING)[0]
+        self.qkvg = kind(W_QKVG)
+        self.out = kind(W_OUT)
+        self.phi = kind(W_PHI)
+        self.engram_tables = kind(W_ENGRAM_TABLE)
+        self.engram_kv = kind(W_ENGRAM_KV)
+
+    @classmethod
+    def from_archive(cls, data) -> "QWeights":
+        """Read the archive bytes (bytes or a u8 array); they are borrowed for
+        the call only."""
+        lib = init()
+        buf = np.frombuffer(data, dtype=np.uint8) if isinstance(data, (bytes, bytearray)) else \
+            np.ascontiguousarray(data, dtype=np.uint8)
+        h = C.c_void_p()
+        _check(lib.nh_weights_load(_hptr(buf), buf.nbytes, C.byref(h)))
+        return cls(h)
+
+    def bytes(self) -> int:
+        """QWeights::bytes (weights.rs:151-155)."""
+        n = _lib.nh_weights_bytes(self.h)
+        _check(int(n) if n < 0 else 0)
+        return int(n)
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.nh_weights_free(self.h)
+        self.h = None
 
 
 def head_logits_sparse(embedding: QMat, a: QAct, ids: torch.Tensor, out_rows: int, stream=None) -> torch.Tensor:
