@@ -30,6 +30,11 @@ INT8_PEAK_TOPS = 5000.0
 K, N, GROUP = 2048, 8192, 128
 
 
+def progress(msg: str):
+    """A progress line on stderr (stdout carries only the JSON line)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def algorithmic_bytes(M: int, K: int, N: int) -> int:
     G = K // GROUP
     return N * K // 2 + N * G * 2 + M * K + M * G * 4 + M * N * 4
@@ -161,6 +166,84 @@ def gpu_sweeps(nh, torch):
     return out
 
 
+def needle3_products(nh, torch):
+    """Secondary line: the CQ-W4 x A8 products of the Needle-3 forward at its
+    default geometry (crates/needle-core/src/config.rs:61-100: d 768, 20
+    layers, vocab 16384, q|k|v|gate 576+96+128+768, 5 engram sites), with
+    random-init weights 0.02*N(0,1) packed to CQ-W4 and fused as QWeights
+    holds them (crates/needle-engine/src/weights.rs:480-495).
+
+    Products only: attention, mHC, the engram conv and the MLP are not on
+    this path, so these times are the products' share of a step, not the
+    model's tokens/s.  Decode, per token (infer/step.rs:364,481,575,727):
+    engram key|value at each site, q|k|v|gate (RMSNorm fused into its A8
+    prep) and out per layer, the tied head over the whole embedding; every
+    product behind its A8 prep.  Prefill, per 512-token sequence
+    (infer/chunk.rs:197,274,350): the same products per 32-token chunk, the
+    head once."""
+    import numpy as np
+
+    d, layers, vocab, sites, chunk, seq = 768, 20, 16384, 5, 32, 512
+    parts = (576, 96, 128, 768)
+    seed = [1000]
+
+    def mat(n, k):
+        seed[0] += 1
+        (w,) = nh.seeded_normals([n * k], seed[0])
+        w *= 0.02
+        return nh.QMat.from_f32(w, n, k)
+
+    head = mat(vocab, d)
+    qkvg = [nh.QLinear([mat(n, d) for n in parts]) for _ in range(layers)]
+    outp = [mat(d, parts[3]) for _ in range(layers)]
+    ekv = [nh.QLinear([mat(d, d), mat(d, d)]) for _ in range(sites)]
+    xs = nh.seeded_normals([chunk * d], 77)[0]
+    x = torch.from_numpy(xs).cuda()
+    ns = torch.from_numpy(np.float16(1.0 + 0.1 * xs[:d]).view(np.uint16).astype(np.int16)).cuda()
+    nq = sum(parts)
+
+    def products(rows, a, ys):
+        for e in ekv:
+            a.prep(x, rows)
+            e.rows_into(a, ys["e"], 2 * d)
+        for lq, lo in zip(qkvg, outp):
+            a.prep(x, rows, ns)
+            lq.rows_into(a, ys["q"], nq)
+            a.prep(x, rows)
+            lo.matmul_into(a, ys["o"], d, 0)
+
+    def buffers(rows):
+        return {"e": torch.empty((rows, 2 * d), device="cuda"), "q": torch.empty((rows, nq), device="cuda"),
+                "o": torch.empty((rows, d), device="cuda"), "h": torch.empty(vocab, device="cuda")}
+
+    a1, y1 = nh.QAct(1, d), buffers(1)
+
+    def token():
+        products(1, a1, y1)
+        a1.prep(x, 1, ns)
+        head.matmul_into(a1, y1["h"], vocab, 0)
+
+    ac, yc = nh.QAct(chunk, d), buffers(chunk)
+
+    def sequence():
+        for _ in range(seq // chunk):
+            products(chunk, ac, yc)
+        a1.prep(x, 1, ns)
+        head.matmul_into(a1, y1["h"], vocab, 0)
+
+    dec_ms = time_graph(token, 50, 3, torch)
+    pre_ms = time_graph(sequence, 10, 2, torch)
+    launches = 2 * (sites + 2 * layers + 1)
+    return {"workload": "Needle-3 CQ-W4 x A8 products only (random-init weights; attention, mHC, engram conv and "
+                        "MLP not included): decode per token, prefill per 512-token sequence in 32-token chunks",
+            "products_only": True, "launches_per_token": launches,
+            "decode_us_per_token": round(dec_ms * 1e3, 2),
+            "decode_products_tok_s": round(1e3 / dec_ms, 1),
+            "decode_us_per_launch": round(dec_ms * 1e3 / launches, 3),
+            "prefill_us_per_seq512": round(pre_ms * 1e3, 1),
+            "prefill_products_tok_s": round(seq * 1e3 / pre_ms, 1)}
+
+
 def gemm_shape(spec: str, launches: int, nh, torch):
     """One prefill product M x K x N (seeded as the sweep), `launches` eager
     launches timed with HIP events on the launch stream: the command the
@@ -253,6 +336,7 @@ def main():
         print(json.dumps(gemm_shape(args.gemm_shape, args.launches, nh, torch)))
         return
     gpu = gpu_gemv(args, nh, torch)
+    progress(f"decode GEMV: {gpu['ms_launch'] * 1e3:.3f} us per launch")
     steps = gpu["launches"]
     line = {
         "metric": "W4A8 GEMV HBM GB/s (K=2048, N=8192, decode combine)",
@@ -276,7 +360,11 @@ def main():
     }
     if not args.no_sweep:
         line["steady_state"] = gpu_gemv_steady(gpu, args.copies, nh, torch)
+        progress("steady state done")
         line["secondary"] = gpu_sweeps(nh, torch)
+        progress("GEMM sweep done")
+        line["needle3_products"] = needle3_products(nh, torch)
+        progress("Needle-3 products done")
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(gpu, args.cpu_seconds)
         line["cpu_baseline"]["gpu_over_cpu"] = round(gpu["gbs"] / line["cpu_baseline"]["value"], 1)
