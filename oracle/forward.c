@@ -1,0 +1,761 @@
+/* The Needle-3 decode step on the CPU, restated from the reference's
+ * native engine (crates/needle-engine/src/infer/step.rs:171-760 and the
+ * helpers of crates/needle-engine/src/infer.rs), x86-64 portable branches,
+ * in the same float-operation order (fmaf where Rust has mul_add).
+ *
+ * TEST INFRASTRUCTURE: the parity checker (and CPU baseline) for a GPU
+ * forward; nothing in the product links it.
+ *
+ * Scope: Model::step_native for one token with attend = None (no attention
+ * span: every position keeps its own KV slot, slot_of(p) = p), Outputs =
+ * logits, no cells, no rollback.  The libm functions the reference takes
+ * from the Rust `libm` crate (expf, exp, powf, sincosf) are glibc's here:
+ * equal to them except for rare last-ulp differences, so results that
+ * pass through them are parity unpinned at that boundary.
+ */
+#define _GNU_SOURCE /* sincosf */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "cq_oracle.h"
+#include "forward.h"
+
+/* ------------------------------------------------------------- constants */
+/* infer.rs:30-38 */
+static float bits_f(uint32_t b) {
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+#define INV_SQRT_QK bits_f(0x3e13cd3au)
+#define Q21 bits_f(0x49fffff8u)
+#define C21 bits_f(0x35000004u)
+#define NATIVE_TEAM 4
+/* crates/needle-core/src/config.rs:10-13 */
+#define ENGRAM_CONV_TAPS 4
+#define ENGRAM_SEED 0x9E3779B9u
+#define ENGRAM_PRIME 0x01000193u
+#define HADA_COND_RANK 8
+#define NB 32
+#define HN (NB * NB)
+
+/* ---------------------------------------------------------------- helpers */
+
+/* nexp (infer.rs:353-367). */
+float nf_nexp(float x) {
+    x = fminf(fmaxf(x, bits_f(0xc2b0c0a5u)), bits_f(0x42b0c0a5u));
+    const float k = rintf(x * bits_f(0x3fb8aa3bu));
+    float r = fmaf(k, bits_f(0xbf318000u), x);
+    r = fmaf(k, bits_f(0x395e8083u), r);
+    float p = fmaf(bits_f(0x39506967u), r, bits_f(0x3ab743ceu));
+    p = fmaf(r, p, bits_f(0x3c088908u));
+    p = fmaf(r, p, bits_f(0x3d2aa9c1u));
+    p = fmaf(r, p, bits_f(0x3e2aaaaau));
+    p = fmaf(r, p, 0.5f);
+    const float y = fmaf(r * r, p, r);
+    const uint32_t sb = (uint32_t)((int32_t)k << 23) + 0x3f800000u;
+    const float s = bits_f(sb);
+    return fmaf(s, y, s);
+}
+
+/* zcn (infer.rs:426-444) with an f32 scale. */
+static void zcn(const float* x, const float* s, size_t n, float* out) {
+    const float r = cq_rinv(cq_dot16(x, x, n), n);
+    for (size_t i = 0; i < n; ++i) {
+        const float t = x[i] * r;
+        out[i] = fmaf(t, s[i], t);
+    }
+}
+
+/* zcn16_inplace (infer.rs:475-494). */
+static void zcn16_inplace(float* x, const uint16_t* s, size_t n) {
+    const float r = cq_rinv(cq_dot16(x, x, n), n);
+    for (size_t i = 0; i < n; ++i) {
+        const float t = x[i] * r;
+        x[i] = fmaf(t, cq_f16_to_f32(s[i]), t);
+    }
+}
+
+/* rope_rotate (infer.rs:637-665). */
+void nf_rope_rotate(float* x, size_t n, const float* cs, const float* sn) {
+    const size_t half = n / 2;
+    for (size_t f = 0; f < half; ++f) {
+        const float a = x[f], b = x[f + half];
+        x[f] = fmaf(-sn[f], b, cs[f] * a);
+        x[f + half] = fmaf(sn[f], a, cs[f] * b);
+    }
+}
+
+/* idot (infer.rs:769-775). */
+static int32_t idot(const int8_t* a, const int8_t* b, size_t n) {
+    int32_t s = 0;
+    for (size_t i = 0; i < n; ++i) s += (int32_t)a[i] * (int32_t)b[i];
+    return s;
+}
+
+/* cond_weights (infer.rs:1640-1656), portable branch. */
+void nf_cond_weights(const float* h2, size_t d, const uint16_t* cond_v, float out[8]) {
+    float acc[4][8];
+    memset(acc, 0, sizeof acc);
+    for (size_t j = 0; j < d; ++j) {
+        float* a = acc[j % 4];
+        for (int k = 0; k < 8; ++k) a[k] = fmaf(h2[j], cq_f16_to_f32(cond_v[j * 8 + k]), a[k]);
+    }
+    float lg[8], e[8], m = -INFINITY;
+    for (int k = 0; k < 8; ++k) {
+        lg[k] = ((acc[2][k] + acc[3][k]) + acc[1][k]) + acc[0][k];
+        m = fmaxf(m, lg[k]);
+    }
+    for (int k = 0; k < 8; ++k) e[k] = expf(lg[k] - m);
+    const float sum = e[7] + ((e[6] + (e[5] + e[4])) + ((e[3] + e[2]) + (e[1] + e[0])));
+    const float inv = 1.0f / sum;
+    for (int k = 0; k < 8; ++k) out[k] = e[k] * inv;
+}
+
+/* mix8 (infer.rs:2343-2380), portable branch, all 16 tiles or the first
+ * `tiles`: out[r][c] = sum_j ct[j][r] * rows[j][c] (fma chain from j = 0);
+ * transposed, out[c][r].  ct / rows are f16 (`h` set) or f32. */
+static inline float at(const void* p, int half, size_t i) {
+    return half ? cq_f16_to_f32(((const uint16_t*)p)[i]) : ((const float*)p)[i];
+}
+
+void nf_mix8(int transpose, const void* ct, int ct_half, const void* rows, int rows_half, float* out, int tiles) {
+    for (int t = 0; t < tiles; ++t) {
+        const int r0 = (t / 4) * 8, c0 = (t % 4) * 8;
+        for (int r = r0; r < r0 + 8; ++r) {
+            float o[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int j = 0; j < NB; ++j) {
+                const float c = at(ct, ct_half, (size_t)j * NB + r);
+                for (int k = 0; k < 8; ++k) o[k] = fmaf(c, at(rows, rows_half, (size_t)j * NB + c0 + k), o[k]);
+            }
+            for (int k = 0; k < 8; ++k) {
+                const int cc = c0 + k;
+                out[transpose ? cc * NB + r : r * NB + cc] = o[k];
+            }
+        }
+    }
+}
+
+/* sinkhorn64 (infer.rs:2501-2528). */
+void nf_sinkhorn64(const float z[16], float out[16]) {
+    double e[16];
+    for (int r = 0; r < 4; ++r) {
+        const double m = (double)fmaxf(fmaxf(z[r * 4], z[r * 4 + 1]), fmaxf(z[r * 4 + 2], z[r * 4 + 3]));
+        for (int c = 0; c < 4; ++c) e[r * 4 + c] = exp((double)z[r * 4 + c] - m);
+    }
+    for (int it = 0; it < 20; ++it) {
+        for (int r = 0; r < 4; ++r) {
+            const double inv = 1.0 / ((e[r * 4] + e[r * 4 + 1]) + (e[r * 4 + 2] + e[r * 4 + 3]));
+            for (int c = 0; c < 4; ++c) e[r * 4 + c] *= inv;
+        }
+        for (int c = 0; c < 4; ++c) {
+            const double inv = 1.0 / ((e[c] + e[4 + c]) + (e[8 + c] + e[12 + c]));
+            for (int r = 0; r < 4; ++r) e[r * 4 + c] *= inv;
+        }
+    }
+    for (int i = 0; i < 16; ++i) out[i] = (float)e[i];
+}
+
+/* chunk_exp (infer.rs:2222-2279), x86-64 branch: numerators in place and
+ * their sum in the engine's order. */
+float nf_chunk_exp(float* s, size_t l, float m) {
+    size_t i = 0;
+    float a[4] = {0, 0, 0, 0}, b[4] = {0, 0, 0, 0};
+    while (i + 8 <= l) {
+        for (int k = 0; k < 4; ++k) {
+            const float e = nf_nexp(s[i + k] - m);
+            s[i + k] = e;
+            a[k] += e;
+        }
+        for (int k = 0; k < 4; ++k) {
+            const float e = nf_nexp(s[i + 4 + k] - m);
+            s[i + 4 + k] = e;
+            b[k] += e;
+        }
+        i += 8;
+    }
+    while (i + 4 <= l) {
+        for (int k = 0; k < 4; ++k) {
+            const float e = nf_nexp(s[i + k] - m);
+            s[i + k] = e;
+            a[k] += e;
+        }
+        i += 4;
+    }
+    float t[4];
+    for (int k = 0; k < 4; ++k) t[k] = a[k] + b[k];
+    float sum = (t[0] + t[1]) + (t[2] + t[3]);
+    if (l - i >= 2) {
+        const float e0 = expf(s[i] - m), e1 = expf(s[i + 1] - m);
+        s[i] = e0;
+        s[i + 1] = e1;
+        sum = (e0 + sum) + e1;
+        i += 2;
+    }
+    if (l - i == 1) {
+        const float e = expf(s[i] - m);
+        s[i] = e;
+        sum += e;
+    }
+    return sum;
+}
+
+/* digits21 (infer.rs:2171-2220), portable branch: round half away. */
+void nf_digits21(const float* w, size_t n, float qw, int8_t* hi, int8_t* mid, int8_t* lo) {
+    for (size_t i = 0; i < n; ++i) {
+        const int32_t wq = (int32_t)roundf(w[i] * qw);
+        hi[i] = (int8_t)(wq >> 14);
+        mid[i] = (int8_t)((wq >> 7) & 127);
+        lo[i] = (int8_t)(wq & 127);
+    }
+}
+
+/* key_chunks (infer.rs:2093-2101): (count, size). */
+void nf_key_chunks(size_t n, size_t nkv, size_t* count, size_t* size) {
+    size_t k = 2 * NATIVE_TEAM / nkv;
+    if (k < 1) k = 1;
+    size_t c = (n + 255) / 256;
+    if (k * 64 <= n && c < k) c = k;
+    if (c < 1) c = 1;
+    const size_t chunk = ((n + c - 1) / c + 15) / 16 * 16;
+    *size = chunk;
+    *count = chunk ? (n + chunk - 1) / chunk : 0;
+}
+
+/* ------------------------------------------------------------------ model */
+
+struct nf_layer16 {
+    uint16_t *kron[6], *cond_v, *cond_u, *d1, *d2, *b2, *d3, *d4, *norm_in, *post_norm, *pre_hada, *q_taps, *k_taps,
+        *v_taps, *q_norm, *k_norm;
+    float a_pre, a_post, a_res, attn_gate, b_pre[4], b_post[4], b_res[16];
+    int8_t* phi_q;  /* Phi8 (infer.rs:850-867): ncols x nc */
+    float* phi_s;
+};
+
+struct nf_model {
+    nf_config c;
+    struct nf_layer16* L;
+    const cq_qmat* embedding;
+    const cq_qlinear** qkvg;
+    const cq_qlinear** out;
+    const cq_qmat** etables;
+    const cq_qlinear** ekv;
+    float** etaps;       /* per site [4][d] */
+    float* final_norm;   /* [d] */
+    int32_t *perm1, *perm2;
+    float *freq, *sd, *cd;  /* RoPE tables (Tables::new, infer.rs:935-947) */
+    int site_of_layer[64];
+};
+
+struct nf_session {
+    size_t cap;     /* positions */
+    size_t len;     /* tokens fed */
+    uint32_t* tokens;
+    /* per layer: k8 [pos][nkv][qk], ks [pos][nkv], v8t [nkv][vd][cap], vs [pos][nkv], hist (last taps-1 rows) */
+    int8_t** k8;
+    float** ks;
+    int8_t** v8t;
+    float** vs;
+    float** hist;    /* [taps - 1][width], newest last */
+    size_t hrows;
+    /* engram value history per site: [pos][d] int8 + [pos][d/32] */
+    int8_t** ev8;
+    float** evs;
+    /* RoPE state of the newest position */
+    int rope_ok;
+    size_t rope_pos;
+    float *rope_c, *rope_s;
+    float* xs;       /* the residual lanes [n][d] */
+};
+
+static uint16_t* dup16(const uint16_t* p, size_t n) {
+    uint16_t* q = (uint16_t*)malloc(n * 2);
+    memcpy(q, p, n * 2);
+    return q;
+}
+
+nf_model* nf_model_new(const nf_config* c) {
+    nf_model* m = (nf_model*)calloc(1, sizeof *m);
+    m->c = *c;
+    m->L = (struct nf_layer16*)calloc((size_t)c->layers, sizeof *m->L);
+    m->qkvg = (const cq_qlinear**)calloc((size_t)c->layers, sizeof(void*));
+    m->out = (const cq_qlinear**)calloc((size_t)c->layers, sizeof(void*));
+    m->etables = (const cq_qmat**)calloc((size_t)c->sites + 1, sizeof(void*));
+    m->ekv = (const cq_qlinear**)calloc((size_t)c->sites + 1, sizeof(void*));
+    m->etaps = (float**)calloc((size_t)c->sites + 1, sizeof(float*));
+    for (int l = 0; l < 64; ++l) m->site_of_layer[l] = -1;
+    for (int s = 0; s < c->sites; ++s) m->site_of_layer[c->site_layers[s]] = s;
+    /* Tables::new: freq = powf(theta, i * (-2 / qk)), then sincosf. */
+    const int half = c->qk / 2;
+    m->freq = (float*)malloc(sizeof(float) * half);
+    m->sd = (float*)malloc(sizeof(float) * half);
+    m->cd = (float*)malloc(sizeof(float) * half);
+    const float coef = -2.0f / (float)c->qk;
+    for (int i = 0; i < half; ++i) {
+        m->freq[i] = powf(c->rope_theta, (float)i * coef);
+        sincosf(m->freq[i], &m->sd[i], &m->cd[i]);
+    }
+    return m;
+}
+
+void nf_model_free(nf_model* m) {
+    if (!m) return;
+    for (int l = 0; l < m->c.layers; ++l) {
+        struct nf_layer16* L = &m->L[l];
+        for (int k = 0; k < 6; ++k) free(L->kron[k]);
+        free(L->cond_v), free(L->cond_u), free(L->d1), free(L->d2), free(L->b2), free(L->d3), free(L->d4);
+        free(L->norm_in), free(L->post_norm), free(L->pre_hada), free(L->q_taps), free(L->k_taps), free(L->v_taps);
+        free(L->q_norm), free(L->k_norm), free(L->phi_q), free(L->phi_s);
+    }
+    for (int s = 0; s < m->c.sites; ++s) free(m->etaps[s]);
+    free(m->L), free(m->qkvg), free(m->out), free(m->etables), free(m->ekv), free(m->etaps);
+    free(m->final_norm), free(m->perm1), free(m->perm2), free(m->freq), free(m->sd), free(m->cd);
+    free(m);
+}
+
+void nf_set_layer_f16(nf_model* m, int l, int which, const uint16_t* v, size_t n) {
+    struct nf_layer16* L = &m->L[l];
+    uint16_t** slot = NULL;
+    switch (which) {
+        case NF_KRON0: case NF_KRON1: case NF_KRON2: case NF_KRON3: case NF_KRON4: case NF_KRON5:
+            slot = &L->kron[which - NF_KRON0]; break;
+        case NF_COND_V: slot = &L->cond_v; break;
+        case NF_COND_U: slot = &L->cond_u; break;
+        case NF_D1: slot = &L->d1; break;
+        case NF_D2: slot = &L->d2; break;
+        case NF_B2: slot = &L->b2; break;
+        case NF_D3: slot = &L->d3; break;
+        case NF_D4: slot = &L->d4; break;
+        case NF_NORM_IN: slot = &L->norm_in; break;
+        case NF_POST_NORM: slot = &L->post_norm; break;
+        case NF_PRE_HADA: slot = &L->pre_hada; break;
+        case NF_Q_TAPS: slot = &L->q_taps; break;
+        case NF_K_TAPS: slot = &L->k_taps; break;
+        case NF_V_TAPS: slot = &L->v_taps; break;
+        case NF_Q_NORM: slot = &L->q_norm; break;
+        case NF_K_NORM: slot = &L->k_norm; break;
+        default: return;
+    }
+    free(*slot);
+    *slot = dup16(v, n);
+}
+
+void nf_set_layer_scalars(nf_model* m, int l, float a_pre, float a_post, float a_res, float attn_gate,
+                          const float* b_pre, const float* b_post, const float* b_res) {
+    struct nf_layer16* L = &m->L[l];
+    L->a_pre = a_pre, L->a_post = a_post, L->a_res = a_res, L->attn_gate = attn_gate;
+    memcpy(L->b_pre, b_pre, 4 * sizeof(float));
+    memcpy(L->b_post, b_post, 4 * sizeof(float));
+    memcpy(L->b_res, b_res, 16 * sizeof(float));
+}
+
+/* Phi8::new over the dequantized fused pre|post|res rows of a layer. */
+void nf_set_phi(nf_model* m, int l, const float* w, size_t rows, size_t width) {
+    struct nf_layer16* L = &m->L[l];
+    free(L->phi_q), free(L->phi_s);
+    L->phi_q = (int8_t*)malloc(rows * width);
+    L->phi_s = (float*)malloc(rows * sizeof(float));
+    for (size_t r = 0; r < rows; ++r) L->phi_s[r] = cq_quant_i8(w + r * width, width, L->phi_q + r * width);
+}
+
+void nf_set_matrices(nf_model* m, const cq_qmat* embedding, const cq_qlinear* const* qkvg, const cq_qlinear* const* out,
+                     const cq_qmat* const* etables, const cq_qlinear* const* ekv) {
+    m->embedding = embedding;
+    for (int l = 0; l < m->c.layers; ++l) m->qkvg[l] = qkvg[l], m->out[l] = out[l];
+    for (int s = 0; s < m->c.sites; ++s) m->etables[s] = etables[s], m->ekv[s] = ekv[s];
+}
+
+void nf_set_engram_taps(nf_model* m, int site, const float* taps, size_t n) {
+    free(m->etaps[site]);
+    m->etaps[site] = (float*)malloc(n * sizeof(float));
+    memcpy(m->etaps[site], taps, n * sizeof(float));
+}
+
+void nf_set_globals(nf_model* m, const float* final_norm, const int32_t* perm1, const int32_t* perm2) {
+    const int d = m->c.d;
+    free(m->final_norm), free(m->perm1), free(m->perm2);
+    m->final_norm = (float*)malloc(d * sizeof(float));
+    memcpy(m->final_norm, final_norm, d * sizeof(float));
+    m->perm1 = (int32_t*)malloc(HN * sizeof(int32_t));
+    m->perm2 = (int32_t*)malloc(HN * sizeof(int32_t));
+    memcpy(m->perm1, perm1, HN * sizeof(int32_t));
+    memcpy(m->perm2, perm2, HN * sizeof(int32_t));
+}
+
+/* ---------------------------------------------------------------- session */
+
+static int width_of(const nf_config* c) { return (c->nh + c->nkv) * c->qk + c->nkv * c->vd; }
+
+nf_session* nf_session_new(const nf_model* m, size_t cap) {
+    const nf_config* c = &m->c;
+    nf_session* s = (nf_session*)calloc(1, sizeof *s);
+    s->cap = cap;
+    s->tokens = (uint32_t*)calloc(cap, sizeof(uint32_t));
+    s->k8 = (int8_t**)calloc((size_t)c->layers, sizeof(void*));
+    s->ks = (float**)calloc((size_t)c->layers, sizeof(void*));
+    s->v8t = (int8_t**)calloc((size_t)c->layers, sizeof(void*));
+    s->vs = (float**)calloc((size_t)c->layers, sizeof(void*));
+    s->hist = (float**)calloc((size_t)c->layers, sizeof(void*));
+    const int W = width_of(c), keep = c->taps > 1 ? c->taps - 1 : 1;
+    for (int l = 0; l < c->layers; ++l) {
+        s->k8[l] = (int8_t*)calloc(cap * c->nkv * c->qk, 1);
+        s->ks[l] = (float*)calloc(cap * c->nkv, sizeof(float));
+        s->v8t[l] = (int8_t*)calloc((size_t)c->nkv * c->vd * cap, 1);
+        s->vs[l] = (float*)calloc(cap * c->nkv, sizeof(float));
+        s->hist[l] = (float*)calloc((size_t)keep * W, sizeof(float));
+    }
+    s->ev8 = (int8_t**)calloc((size_t)c->sites + 1, sizeof(void*));
+    s->evs = (float**)calloc((size_t)c->sites + 1, sizeof(void*));
+    for (int e = 0; e < c->sites; ++e) {
+        s->ev8[e] = (int8_t*)calloc(cap * c->d, 1);
+        s->evs[e] = (float*)calloc(cap * (c->d / 32), sizeof(float));
+    }
+    s->rope_c = (float*)calloc((size_t)c->qk / 2, sizeof(float));
+    s->rope_s = (float*)calloc((size_t)c->qk / 2, sizeof(float));
+    s->xs = (float*)calloc((size_t)c->lanes * c->d, sizeof(float));
+    return s;
+}
+
+void nf_session_free(const nf_model* m, nf_session* s) {
+    if (!s) return;
+    for (int l = 0; l < m->c.layers; ++l) free(s->k8[l]), free(s->ks[l]), free(s->v8t[l]), free(s->vs[l]), free(s->hist[l]);
+    for (int e = 0; e < m->c.sites; ++e) free(s->ev8[e]), free(s->evs[e]);
+    free(s->k8), free(s->ks), free(s->v8t), free(s->vs), free(s->hist), free(s->ev8), free(s->evs);
+    free(s->tokens), free(s->rope_c), free(s->rope_s), free(s->xs);
+    free(s);
+}
+
+size_t nf_session_len(const nf_session* s) { return s->len; }
+
+/* attend_head_ref (infer.rs:1871-2007) with attend = None, nested = false:
+ * keys are positions lo..pos (inclusive), slot = position. */
+static void attend_head(const nf_model* m, const nf_session* s, int l, const float* qh, int kvh, size_t lo, size_t pos,
+                        float* out) {
+    const nf_config* c = &m->c;
+    const size_t qk = c->qk, vd = c->vd, nkv = c->nkv, cap = s->cap;
+    int8_t q8[64];
+    const float qs = cq_quant_i8(qh, qk, q8) * INV_SQRT_QK;
+    const size_t n = pos + 1 - lo;
+    size_t count, chunk;
+    nf_key_chunks(n, nkv, &count, &chunk);
+    float* sc = (float*)malloc(chunk * sizeof(float));
+    float* scale = (float*)malloc(chunk * sizeof(float));
+    int32_t* dots = (int32_t*)malloc(chunk * sizeof(int32_t));
+    int8_t* dig = (int8_t*)malloc(3 * chunk);
+    float pm[8], psum[8], po[8][64];
+    int np = 0;
+    for (size_t c0 = 0; c0 < n; c0 += chunk) {
+        const size_t len = chunk < n - c0 ? chunk : n - c0;
+        const size_t blocked = len / 4 * 4;
+        const size_t slot0 = lo + c0;
+        for (size_t i = 0; i < len; ++i)
+            dots[i] = idot(q8, s->k8[l] + ((slot0 + i) * nkv + kvh) * qk, qk);
+        for (size_t i = 0; i < len; ++i) scale[i] = s->ks[l][(slot0 + i) * nkv + kvh];
+        for (size_t i = 0; i < blocked; ++i) sc[i] = (scale[i] * (float)dots[i]) * qs;
+        for (size_t i = blocked; i < len; ++i) sc[i] = (scale[i] * qs) * (float)dots[i];
+        float mx = -INFINITY;
+        for (size_t i = 0; i < len; ++i) mx = fmaxf(mx, sc[i]);
+        const float sum = nf_chunk_exp(sc, len, mx);
+        for (size_t i = 0; i < len; ++i) scale[i] = s->vs[l][(slot0 + i) * nkv + kvh];
+        float wmax = 0.0f;
+        for (size_t i = 0; i < len; ++i) {
+            sc[i] *= scale[i];
+            wmax = fmaxf(wmax, sc[i]);
+        }
+        const float qw = Q21 / wmax;
+        int8_t *hi = dig, *mid = dig + chunk, *lo8 = dig + 2 * chunk;
+        nf_digits21(sc, len, qw, hi, mid, lo8);
+        const float cw = wmax * C21;
+        /* one run of consecutive slots: slot0 .. slot0 + len */
+        for (size_t dm = 0; dm < vd; ++dm) {
+            const int8_t* row = s->v8t[l] + ((size_t)kvh * vd + dm) * cap + slot0;
+            const int32_t a = idot(hi, row, len), b = idot(mid, row, len), cc = idot(lo8, row, len);
+            po[np][dm] = fmaf(16384.0f, (float)a, fmaf(128.0f, (float)b, (float)cc)) * cw;
+        }
+        pm[np] = mx;
+        psum[np] = sum;
+        ++np;
+    }
+    if (np == 1) {
+        const float inv = 1.0f / psum[0];
+        for (size_t i = 0; i < vd; ++i) out[i] = po[0][i] * inv;
+    } else {
+        float big = -1e30f;
+        for (int p = 0; p < np; ++p) big = fmaxf(big, pm[p]);
+        float acc[64] = {0}, total = 0.0f;
+        for (int p = 0; p < np; ++p) {
+            const float w = expf(pm[p] - big);
+            for (size_t i = 0; i < vd; ++i) acc[i] = fmaf(po[p][i], w, acc[i]);
+            total = fmaf(w, psum[p], total);
+        }
+        const float inv = 1.0f / total;
+        for (size_t i = 0; i < vd; ++i) out[i] = acc[i] * inv;
+    }
+    free(sc), free(scale), free(dots), free(dig);
+}
+
+/* Model::step_native (step.rs:171-760) for one token; logits [out_rows]. */
+int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int nthreads) {
+    const nf_config* c = &m->c;
+    const int n = c->lanes, d = c->d, nc = n * d, L = c->layers;
+    const int qk = c->qk, vd = c->vd, nh = c->nh, nkv = c->nkv;
+    const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd, W = qd + kd + vdim, taps = c->taps;
+    const int half = qk / 2, group = nh / nkv, sites = c->sites;
+    const size_t p0 = s->len;
+    if (p0 >= s->cap || n != 4 || qk > 64 || vd > 64 || c->norders * c->eheads > 16 || L > 64) return -1;
+    s->tokens[p0] = tok;
+    s->len = p0 + 1;
+
+    /* embedding row * sqrt(d) into every lane (step.rs:228-235) */
+    float* xs = s->xs;
+    float* row = (float*)malloc(sizeof(float) * d);
+    cq_qmat_row(m->embedding, tok, row);
+    const float scale = sqrtf((float)d);
+    for (int lane = 0; lane < n; ++lane)
+        for (int i = 0; i < d; ++i) xs[lane * d + i] = row[i] * scale;
+
+    /* engram rows and their key|value products, value history and conv
+     * (step.rs:245-269, 346-391) */
+    const int norders = c->norders, eheads = c->eheads, ntab = norders * eheads, sub = c->engram_sub;
+    float* ekv = (float*)calloc((size_t)sites * 2 * d + 1, sizeof(float));
+    float* evals = (float*)calloc((size_t)sites * d + 1, sizeof(float));
+    if (sites > 0) {
+        long erow[16];
+        const int stride = c->seed_heads > 0 ? c->seed_heads : eheads;
+        for (int oi = 0; oi < norders; ++oi)
+            for (int h = 0; h < eheads; ++h) {
+                const int order = c->orders[oi], tbl = oi * eheads + h;
+                erow[tbl] = -1;
+                if (p0 + 1 < (size_t)order) continue;
+                uint32_t acc = ENGRAM_SEED * (uint32_t)(oi * stride + h + 1);
+                for (int j = 0; j < order; ++j) {
+                    const uint32_t t = p0 >= (size_t)j ? s->tokens[p0 - j] : 0;
+                    acc = (acc ^ t) * ENGRAM_PRIME;
+                }
+                acc ^= acc >> 15;
+                erow[tbl] = (long)tbl * c->engram_slots + (long)(acc % (uint32_t)c->engram_slots);
+            }
+        float* er = (float*)malloc(sizeof(float) * d);
+        float* trow = (float*)malloc(sizeof(float) * sub);
+        for (int e = 0; e < sites; ++e) {
+            memset(er, 0, sizeof(float) * d);
+            for (int tbl = 0; tbl < ntab; ++tbl)
+                if (erow[tbl] >= 0) {
+                    cq_qmat_row(m->etables[e], (size_t)erow[tbl], trow);
+                    memcpy(er + tbl * sub, trow, sizeof(float) * sub);
+                }
+            cq_qact* a = cq_qact_new(er, 1, d, m->ekv[e]->parts[0]->bits, 1);
+            cq_qlinear_matmul(m->ekv[e], a, ekv + (size_t)e * 2 * d, 1);
+            cq_qact_free(a);
+            /* int8 value history, groups of 32 */
+            for (int g = 0; g < d / 32; ++g)
+                s->evs[e][p0 * (d / 32) + g] =
+                    cq_quant_i8(ekv + (size_t)e * 2 * d + d + g * 32, 32, s->ev8[e] + p0 * d + g * 32);
+        }
+        free(er), free(trow);
+        const int dil = c->dilation;
+        for (int e = 0; e < sites; ++e) {
+            float* dst = evals + (size_t)e * d;
+            for (int j = 0; j < ENGRAM_CONV_TAPS; ++j) {
+                if (p0 < (size_t)(j * dil)) break;
+                const size_t pj = p0 - (size_t)j * dil;
+                const int8_t* q8 = s->ev8[e] + pj * d;
+                const float* qs = s->evs[e] + pj * (d / 32);
+                const float* tw = m->etaps[e] + (size_t)j * d;
+                for (int k = 0; k < d; ++k) dst[k] = fmaf(tw[k], qs[k / 32] * (float)q8[k], dst[k]);
+            }
+        }
+    }
+
+    /* RoPE rows for this position (rope_rows, infer.rs:1716-1747) */
+    float cs[32], sn[32];
+    if (s->rope_ok && s->rope_pos + 1 == p0) {
+        for (int f = 0; f < half; ++f) {
+            cs[f] = fmaf(-m->sd[f], s->rope_s[f], m->cd[f] * s->rope_c[f]);
+            sn[f] = fmaf(m->sd[f], s->rope_c[f], m->cd[f] * s->rope_s[f]);
+        }
+    } else {
+        for (int f = 0; f < half; ++f) sincosf(m->freq[f] * (float)p0, &sn[f], &cs[f]);
+    }
+    memcpy(s->rope_c, cs, sizeof(float) * half);
+    memcpy(s->rope_s, sn, sizeof(float) * half);
+    s->rope_ok = 1;
+    s->rope_pos = p0;
+
+    const int nq = W + nh * vd;  /* the fused projection: q | k | v | gate */
+    float* nx = (float*)malloc(sizeof(float) * nc);
+    int8_t* nx8 = (int8_t*)malloc(nc);
+    float *u = (float*)malloc(sizeof(float) * d), *x1 = (float*)malloc(sizeof(float) * d);
+    float *hloc = (float*)malloc(sizeof(float) * d), *proj = (float*)malloc(sizeof(float) * nq);
+    float *qbuf = (float*)malloc(sizeof(float) * qd), *att = (float*)malloc(sizeof(float) * nh * vd);
+    float *o = (float*)malloc(sizeof(float) * d), *on = (float*)malloc(sizeof(float) * d);
+    float *x2 = (float*)malloc(sizeof(float) * d), *h2 = (float*)malloc(sizeof(float) * d);
+    float *ea = (float*)malloc(sizeof(float) * d), *eb = (float*)malloc(sizeof(float) * d);
+    float *z = (float*)malloc(sizeof(float) * HN), *mt = (float*)malloc(sizeof(float) * HN);
+    float *bt = (float*)malloc(sizeof(float) * HN), *cond = (float*)malloc(sizeof(float) * HN);
+    float *zs = (float*)malloc(sizeof(float) * HN), *t3 = (float*)malloc(sizeof(float) * HN);
+    float* newh = (float*)malloc(sizeof(float) * W);
+    const int ncols = 2 * n + n * n;
+    float p[24];
+
+    for (int l = 0; l < L; ++l) {
+        const struct nf_layer16* Lw = &m->L[l];
+        const int lane = l % n;
+        /* (a) mHC read */
+        {
+            const float r = cq_rinv(cq_dot16(xs, xs, nc), nc);
+            for (int i = 0; i < nc; ++i) nx[i] = xs[i] * r;
+            const float sx = cq_quant_scale(nx, nc);
+            cq_quant_with(nx, nc, 1.0f / sx, nx8);
+            for (int k = 0; k < ncols; ++k) p[k] = (sx * Lw->phi_s[k]) * (float)idot(Lw->phi_q + (size_t)k * nc, nx8, nc);
+            float hp[4];
+            for (int j = 0; j < 4; ++j) {
+                const float off = j == lane ? 4.0f : -4.0f;
+                const float zz = ((p[j] * Lw->a_pre) + off) + Lw->b_pre[j];
+                hp[j] = 1.0f / (expf(-zz) + 1.0f);
+            }
+            for (int i = 0; i < d; ++i) u[i] = xs[i] * hp[0];
+            for (int b = 1; b < 4; ++b)
+                for (int i = 0; i < d; ++i) u[i] = fmaf(xs[b * d + i], hp[b], u[i]);
+        }
+        /* (b) engram gate */
+        memcpy(x1, u, sizeof(float) * d);
+        const int site = l < 64 ? m->site_of_layer[l] : -1;
+        if (site >= 0) {
+            const float* kr = ekv + (size_t)site * 2 * d;
+            const float rx = cq_rinv(cq_dot16(x1, x1, d), d), rkk = cq_rinv(cq_dot16(kr, kr, d), d);
+            for (int i = 0; i < d; ++i) ea[i] = x1[i] * rx, eb[i] = kr[i] * rkk;
+            const float alpha = 1.0f / (expf((-cq_dot16(ea, eb, d)) / sqrtf((float)d)) + 1.0f);
+            for (int i = 0; i < d; ++i) x1[i] = fmaf(evals[(size_t)site * d + i], alpha, x1[i]);
+        }
+        /* (c)-(d) input norm, A8, q|k|v|gate */
+        {
+            const float rh = cq_rinv(cq_dot16(x1, x1, d), d);
+            cq_norm_apply16(hloc, x1, rh, Lw->norm_in, d);
+            cq_qact* a = cq_qact_new(hloc, 1, d, m->qkvg[l]->parts[0]->bits, 1);
+            cq_qlinear_matmul(m->qkvg[l], a, proj, nthreads);
+            cq_qact_free(a);
+        }
+        /* (e)-(g) taps, head norms, RoPE, the KV cache and the history */
+        const size_t hrows = s->hrows;
+        float* hist = s->hist[l];
+        const int keep = taps > 1 ? taps - 1 : 1;
+        for (int unit = 0; unit < nh + 2 * nkv; ++unit) {
+            int start, cw, cc, len;
+            const uint16_t* w;
+            if (unit < nh) {
+                start = unit * qk, cw = qd, cc = unit * qk, w = Lw->q_taps, len = qk;
+            } else if (unit < nh + nkv) {
+                const int kh = unit - nh;
+                start = qd + kh * qk, cw = kd, cc = kh * qk, w = Lw->k_taps, len = qk;
+            } else {
+                const int vh = unit - nh - nkv;
+                start = qd + kd + vh * vd, cw = vdim, cc = vh * vd, w = Lw->v_taps, len = vd;
+            }
+            const float* cur = proj + start;
+            memcpy(newh + start, cur, sizeof(float) * len);
+            float v[64];
+            for (int i = 0; i < len; ++i) v[i] = cq_f16_to_f32(w[cc + i]) * cur[i];
+            for (int j = 1; j < taps; ++j) {
+                const uint16_t* wj = w + (size_t)j * cw + cc;
+                if (hrows >= (size_t)j) {
+                    /* history row hrows - j: slot keep - j of the kept rows */
+                    const float* rr = hist + (size_t)(keep - j) * W + start;
+                    for (int i = 0; i < len; ++i) v[i] = fmaf(cq_f16_to_f32(wj[i]), rr[i], v[i]);
+                } else {
+                    for (int i = 0; i < len; ++i) v[i] = fmaf(cq_f16_to_f32(wj[i]), 0.0f, v[i]);
+                }
+            }
+            if (unit < nh + nkv) {
+                zcn16_inplace(v, unit < nh ? Lw->q_norm : Lw->k_norm, qk);
+                nf_rope_rotate(v, qk, cs, sn);
+            }
+            if (unit < nh) {
+                memcpy(qbuf + start, v, sizeof(float) * qk);
+            } else if (unit < nh + nkv) {
+                const int kh = unit - nh;
+                s->ks[l][p0 * nkv + kh] = cq_quant_i8(v, qk, s->k8[l] + (p0 * nkv + kh) * qk);
+            } else {
+                const int vh = unit - nh - nkv;
+                int8_t vq[64];
+                s->vs[l][p0 * nkv + vh] = cq_quant_i8(v, vd, vq);
+                for (int dm = 0; dm < vd; ++dm) s->v8t[l][((size_t)vh * vd + dm) * s->cap + p0] = vq[dm];
+            }
+        }
+        /* the history keeps its last taps - 1 rows, newest last */
+        if (keep > 1) memmove(hist, hist + W, sizeof(float) * (size_t)(keep - 1) * W);
+        memcpy(hist + (size_t)(keep - 1) * W, newh, sizeof(float) * W);
+        /* (h) attention per head, (i) its gate, A8 of the heads */
+        {
+            const int window = (c->sliding_window > 0 && !((c->global_mask >> l) & 1)) ? c->sliding_window : 0;
+            const size_t lo = window ? (p0 + 1 > (size_t)window ? p0 + 1 - (size_t)window : 0) : 0;
+            for (int hh = 0; hh < nh; ++hh) attend_head(m, s, l, qbuf + hh * qk, hh / group, lo, p0, att + hh * vd);
+            for (int hh = 0; hh < nh; ++hh)
+                for (int i = 0; i < vd; ++i) att[hh * vd + i] /= nf_nexp(-proj[W + hh * vd + i]) + 1.0f;
+            cq_qact* a = cq_qact_new(att, 1, nh * vd, m->out[l]->parts[0]->bits, 1);
+            cq_qlinear_matmul(m->out[l], a, o, nthreads);
+            cq_qact_free(a);
+        }
+        /* (k) post block and the Hadamard MLP */
+        const float ga = 1.0f / (expf(-Lw->attn_gate) + 1.0f);
+        cq_zcn16(o, Lw->post_norm, d, on);
+        for (int i = 0; i < d; ++i) x2[i] = fmaf(on[i], ga, x1[i]);
+        cq_zcn16(x2, Lw->pre_hada, d, h2);
+        float wk[8];
+        nf_cond_weights(h2, d, Lw->cond_v, wk);
+        for (int i = 0; i < d; ++i) z[i] = h2[i] * cq_f16_to_f32(Lw->d1[i]);
+        for (int i = d; i < HN; ++i) z[i] = 0.0f;
+        nf_mix8(1, Lw->kron[0], 1, z, 0, mt, 16);
+        nf_mix8(0, mt, 0, Lw->kron[1], 1, bt, 16);
+        for (int j = 0; j < HN; ++j) cond[j] = 1.0f;
+        for (int k = 0; k < HADA_COND_RANK; ++k)
+            for (int j = 0; j < HN; ++j) cond[j] = fmaf(cq_f16_to_f32(Lw->cond_u[(size_t)k * HN + j]), wk[k], cond[j]);
+        for (int j = 0; j < HN; ++j)
+            zs[j] = fmaf(bt[m->perm1[j]], cond[j] * cq_f16_to_f32(Lw->d2[j]), cq_f16_to_f32(Lw->b2[j]));
+        for (int j = 0; j < HN; ++j) zs[j] /= nf_nexp(-zs[j]) + 1.0f;
+        nf_mix8(1, Lw->kron[2], 1, zs, 0, mt, 16);
+        nf_mix8(0, mt, 0, Lw->kron[3], 1, bt, 16);
+        for (int j = 0; j < HN; ++j) zs[j] = bt[m->perm2[j]] * cq_f16_to_f32(Lw->d3[j]);
+        nf_mix8(1, Lw->kron[4], 1, zs, 0, mt, 16);
+        nf_mix8(0, mt, 0, Lw->kron[5], 1, t3, d / NB / 8 * 4);
+        /* the post and residual gates, then the mHC write */
+        float hpost[4], zres[16], hres[16];
+        for (int j = 0; j < 4; ++j) {
+            const float off = j == lane ? 0.0f : -4.0f;
+            const float zz = ((p[n + j] * Lw->a_post) + off) + Lw->b_post[j];
+            hpost[j] = 2.0f / (expf(-zz) + 1.0f);
+        }
+        for (int k = 0; k < 16; ++k) zres[k] = fmaf(p[2 * n + k], Lw->a_res, Lw->b_res[k]);
+        nf_sinkhorn64(zres, hres);
+        for (int ch = 0; ch < d; ++ch) {
+            const float y = (x2[ch] + t3[ch] * cq_f16_to_f32(Lw->d4[ch])) - u[ch];
+            float old[4];
+            for (int b = 0; b < 4; ++b) old[b] = xs[b * d + ch];
+            for (int a2 = 0; a2 < n; ++a2) {
+                float v = y * hpost[a2];
+                for (int b = 0; b < 4; ++b) v = fmaf(old[b], hres[a2 * n + b], v);
+                xs[a2 * d + ch] = v;
+            }
+        }
+    }
+    s->hrows += 1;
+
+    /* head: lane mean, final norm, tied embedding (step.rs:706-728) */
+    float* mean = (float*)malloc(sizeof(float) * d);
+    for (int ch = 0; ch < d; ++ch) mean[ch] = (((xs[ch] + xs[d + ch]) + xs[2 * d + ch]) + xs[3 * d + ch]) * 0.25f;
+    zcn(mean, m->final_norm, d, hloc);
+    if (logits) {
+        cq_qact* a = cq_qact_new(hloc, 1, d, m->embedding->bits, 1);
+        float* full = (float*)malloc(sizeof(float) * m->embedding->out);
+        cq_matmul_into(m->embedding, a, full, m->embedding->out, 0, nthreads);
+        memcpy(logits, full, sizeof(float) * c->out_rows);
+        free(full);
+        cq_qact_free(a);
+    }
+    free(mean), free(row), free(ekv), free(evals), free(nx), free(nx8), free(u), free(x1), free(hloc), free(proj);
+    free(qbuf), free(att), free(o), free(on), free(x2), free(h2), free(ea), free(eb), free(z), free(mt), free(bt);
+    free(cond), free(zs), free(t3), free(newh);
+    return 0;
+}

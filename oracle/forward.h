@@ -1,0 +1,65 @@
+/* The Needle-3 decode step on the CPU (forward.c): test infrastructure. */
+#ifndef NEEDLE_FORWARD_ORACLE_H
+#define NEEDLE_FORWARD_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "cq_oracle.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The geometry step_native reads (crates/needle-core/src/config.rs). */
+typedef struct nf_config {
+    int d, nh, nkv, qk, vd, layers, lanes, taps;
+    int out_rows;
+    int sliding_window;
+    uint64_t global_mask;
+    int sites, site_layers[16];
+    int norders, orders[4], eheads, seed_heads, engram_slots, engram_sub, dilation;
+    float rope_theta;
+} nf_config;
+
+/* Small per-layer tensors (f16 as the archive stores them). */
+enum {
+    NF_KRON0 = 0, NF_KRON1, NF_KRON2, NF_KRON3, NF_KRON4, NF_KRON5,
+    NF_COND_V, NF_COND_U, NF_D1, NF_D2, NF_B2, NF_D3, NF_D4,
+    NF_NORM_IN, NF_POST_NORM, NF_PRE_HADA, NF_Q_TAPS, NF_K_TAPS, NF_V_TAPS, NF_Q_NORM, NF_K_NORM
+};
+
+typedef struct nf_model nf_model;
+typedef struct nf_session nf_session;
+
+nf_model* nf_model_new(const nf_config* c);
+void nf_model_free(nf_model* m);
+void nf_set_layer_f16(nf_model* m, int l, int which, const uint16_t* v, size_t n);
+void nf_set_layer_scalars(nf_model* m, int l, float a_pre, float a_post, float a_res, float attn_gate,
+                          const float* b_pre, const float* b_post, const float* b_res);
+void nf_set_phi(nf_model* m, int l, const float* w, size_t rows, size_t width);
+void nf_set_matrices(nf_model* m, const cq_qmat* embedding, const cq_qlinear* const* qkvg, const cq_qlinear* const* out,
+                     const cq_qmat* const* etables, const cq_qlinear* const* ekv);
+void nf_set_engram_taps(nf_model* m, int site, const float* taps, size_t n);
+void nf_set_globals(nf_model* m, const float* final_norm, const int32_t* perm1, const int32_t* perm2);
+
+nf_session* nf_session_new(const nf_model* m, size_t cap);
+void nf_session_free(const nf_model* m, nf_session* s);
+size_t nf_session_len(const nf_session* s);
+/* One decode step; logits [out_rows] (NULL: none).  0 or -1. */
+int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int nthreads);
+
+/* Helpers, exposed for their own checks. */
+float nf_nexp(float x);
+void nf_rope_rotate(float* x, size_t n, const float* cs, const float* sn);
+void nf_cond_weights(const float* h2, size_t d, const uint16_t* cond_v, float out[8]);
+void nf_mix8(int transpose, const void* ct, int ct_half, const void* rows, int rows_half, float* out, int tiles);
+void nf_sinkhorn64(const float z[16], float out[16]);
+float nf_chunk_exp(float* s, size_t l, float m);
+void nf_digits21(const float* w, size_t n, float qw, int8_t* hi, int8_t* mid, int8_t* lo);
+void nf_key_chunks(size_t n, size_t nkv, size_t* count, size_t* size);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,240 @@
+"""The Needle-3 decode step on the CPU (oracle/forward.c), loaded from a
+.cact archive the way Weights::from_archive_mode(fast = true) reads one
+(crates/needle-engine/src/weights.rs:314-467) plus the native tables
+(Tables::new, crates/needle-engine/src/infer.rs:935-960: Phi8 of the
+dequantized mHC rows, the small weights in f16).
+
+TEST INFRASTRUCTURE: only tests/ (and a CPU baseline) may use it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import OQLinear, OQMat, _p, default_threads, f16_to_f32, lib
+from .cact import CQ, F16, F32, Archive, hada_blocks
+
+P = C.c_void_p
+
+(KRON0, KRON1, KRON2, KRON3, KRON4, KRON5, COND_V, COND_U, D1, D2, B2, D3, D4, NORM_IN, POST_NORM, PRE_HADA, Q_TAPS,
+ K_TAPS, V_TAPS, Q_NORM, K_NORM) = range(21)
+
+
+class Config(C.Structure):
+    """nf_config (oracle/forward.h)."""
+    _fields_ = [("d", C.c_int), ("nh", C.c_int), ("nkv", C.c_int), ("qk", C.c_int), ("vd", C.c_int),
+                ("layers", C.c_int), ("lanes", C.c_int), ("taps", C.c_int), ("out_rows", C.c_int),
+                ("sliding_window", C.c_int), ("global_mask", C.c_uint64), ("sites", C.c_int),
+                ("site_layers", C.c_int * 16), ("norders", C.c_int), ("orders", C.c_int * 4), ("eheads", C.c_int),
+                ("seed_heads", C.c_int), ("engram_slots", C.c_int), ("engram_sub", C.c_int),
+                ("dilation", C.c_int), ("rope_theta", C.c_float)]
+
+
+_declared = False
+
+
+def _lib():
+    global _declared
+    l = lib()
+    if not _declared:
+        sig = {
+            "nf_model_new": (P, [P]),
+            "nf_model_free": (None, [P]),
+            "nf_set_layer_f16": (None, [P, C.c_int, C.c_int, P, C.c_size_t]),
+            "nf_set_layer_scalars": (None, [P, C.c_int, C.c_float, C.c_float, C.c_float, C.c_float, P, P, P]),
+            "nf_set_phi": (None, [P, C.c_int, P, C.c_size_t, C.c_size_t]),
+            "nf_set_matrices": (None, [P, P, P, P, P, P]),
+            "nf_set_engram_taps": (None, [P, C.c_int, P, C.c_size_t]),
+            "nf_set_globals": (None, [P, P, P, P]),
+            "nf_session_new": (P, [P, C.c_size_t]),
+            "nf_session_free": (None, [P, P]),
+            "nf_session_len": (C.c_size_t, [P]),
+            "nf_step": (C.c_int, [P, P, C.c_uint32, P, C.c_int]),
+            "nf_nexp": (C.c_float, [C.c_float]),
+            "nf_rope_rotate": (None, [P, C.c_size_t, P, P]),
+            "nf_cond_weights": (None, [P, C.c_size_t, P, P]),
+            "nf_mix8": (None, [C.c_int, P, C.c_int, P, C.c_int, P, C.c_int]),
+            "nf_sinkhorn64": (None, [P, P]),
+            "nf_chunk_exp": (C.c_float, [P, C.c_size_t, C.c_float]),
+            "nf_digits21": (None, [P, C.c_size_t, C.c_float, P, P, P]),
+            "nf_key_chunks": (None, [C.c_size_t, C.c_size_t, P, P]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(l, name)
+            fn.restype = res
+            fn.argtypes = args
+        _declared = True
+    return l
+
+
+def _f16(a: Archive, i: int) -> np.ndarray:
+    r = a.records[i]
+    if r.dtype != F16:
+        raise ValueError(f"tensor {i} is not f16")
+    return np.frombuffer(a.bytes(i), dtype=np.uint16).copy()
+
+
+def _f32(a: Archive, i: int) -> np.ndarray:
+    r = a.records[i]
+    if r.dtype == F16:
+        return f16_to_f32(_f16(a, i))
+    if r.dtype == F32:
+        return np.frombuffer(a.bytes(i), dtype=np.float32).copy()
+    raise ValueError(f"tensor {i} is neither f16 nor f32")
+
+
+def _mat(a: Archive, i: int) -> OQMat:
+    """Cursor::big (weights.rs:113-128): CQ records as stored, others packed."""
+    r = a.records[i]
+    if r.dtype == CQ:
+        packed, norms, out, in_dim, bits = a.cq(i)
+        return OQMat.from_cq(packed, norms, out, in_dim, bits)
+    w = _f32(a, i)
+    return OQMat.from_f32(w[:r.shape[0] * r.shape[1]], r.shape[0], r.shape[1])
+
+
+class Forward:
+    """A Needle-3 model on the oracle's decode step (step_native)."""
+
+    def __init__(self, data: bytes, threads: int | None = None):
+        l = _lib()
+        a = Archive(data)
+        h = a.header
+        self.threads = threads or default_threads()
+        orders = list(h.engram_orders)
+        eheads = h.num_engram_tables // len(orders) if orders else 0
+        cfg = Config()
+        cfg.d, cfg.nh, cfg.nkv = h.d_model, h.num_heads, h.num_kv_heads
+        cfg.qk, cfg.vd, cfg.layers, cfg.lanes, cfg.taps = h.qk_head_dim, h.v_head_dim, h.num_layers, h.mhc_lanes, \
+            h.qkv_conv_taps
+        cfg.out_rows = h.out_vocab if h.out_vocab > 0 else h.vocab
+        cfg.sliding_window, cfg.global_mask = h.sliding_window, h.global_mask
+        cfg.sites = len(h.engram_sites)
+        for i, s in enumerate(h.engram_sites):
+            cfg.site_layers[i] = s
+        cfg.norders = len(orders)
+        for i, o in enumerate(orders):
+            cfg.orders[i] = o
+        cfg.eheads, cfg.seed_heads = eheads, h.engram_seed_heads
+        cfg.engram_slots, cfg.engram_sub = h.engram_slots, h.engram_sub_dim
+        cfg.dilation = max(orders) if orders else 1
+        cfg.rope_theta = h.rope_theta
+        self.cfg = cfg
+        self.vocab = h.vocab
+        m = l.nf_model_new(C.byref(cfg))
+        self.m = m
+        keep = []  # the oracle matrices the model points at
+
+        # The canonical order (weights.rs:318-420).
+        i = 0
+
+        def take():
+            nonlocal i
+            i += 1
+            return i - 1
+
+        emb = _mat(a, take())
+        keep.append(emb)
+        qkvg, outs, scal = [], [], []
+        for layer in range(h.num_layers):
+            def f16(which, idx=None):
+                t = _f16(a, take() if idx is None else idx)
+                l.nf_set_layer_f16(m, layer, which, _p(t), t.size)
+
+            f16(NORM_IN)
+            q, k, v = _mat(a, take()), _mat(a, take()), _mat(a, take())
+            if h.qkv_conv_taps > 0:
+                f16(Q_TAPS)
+                f16(K_TAPS)
+                f16(V_TAPS)
+            f16(Q_NORM)
+            f16(K_NORM)
+            g, o = _mat(a, take()), _mat(a, take())
+            keep += [q, k, v, g, o]
+            qkvg.append(OQLinear([q, k, v, g]))
+            outs.append(OQLinear([o]))
+            f16(POST_NORM)
+            attn_gate = float(_f32(a, take())[0])
+            f16(PRE_HADA)
+            for which in (D1, D2, B2, D3, D4):
+                f16(which)
+            for which in (KRON0, KRON1, KRON2, KRON3, KRON4, KRON5):
+                f16(which)
+            f16(COND_V)
+            f16(COND_U)
+            scal.append(attn_gate)
+        a_pre, a_post, a_res = _f32(a, take()), _f32(a, take()), _f32(a, take())
+        b_pre, b_post, b_res = _f32(a, take()), _f32(a, take()), _f32(a, take())
+        phi_pre, phi_post, phi_res = _mat(a, take()), _mat(a, take()), _mat(a, take())
+        n = h.mhc_lanes
+        nc = n * h.d_model
+        for layer in range(h.num_layers):
+            bp = np.ascontiguousarray(b_pre[layer * n:(layer + 1) * n], dtype=np.float32)
+            bq = np.ascontiguousarray(b_post[layer * n:(layer + 1) * n], dtype=np.float32)
+            br = np.ascontiguousarray(b_res[layer * n * n:(layer + 1) * n * n], dtype=np.float32)
+            l.nf_set_layer_scalars(m, layer, float(a_pre[layer]), float(a_post[layer]), float(a_res[layer]),
+                                   scal[layer], _p(bp), _p(bq), _p(br))
+            # QLinear::new(pre | post | res slices).dequantize() (weights.rs:380-389,492)
+            rows = [phi_pre.row(r) for r in range(layer * n, (layer + 1) * n)]
+            rows += [phi_post.row(r) for r in range(layer * n, (layer + 1) * n)]
+            rows += [phi_res.row(r) for r in range(layer * n * n, (layer + 1) * n * n)]
+            w = np.ascontiguousarray(np.stack(rows), dtype=np.float32)
+            l.nf_set_phi(m, layer, _p(w), w.shape[0], nc)
+        perm1 = _f32(a, take()).astype(np.int32)
+        perm2 = _f32(a, take()).astype(np.int32)
+        hn = 1
+        while hn < h.d_model:
+            hn *= 2
+        if perm1.size != hn or perm2.size != hn or hada_blocks(hn) != (32, 32):
+            raise ValueError("the decode step covers the shipped geometry (hada_n 1024)")
+        etables, ekv = [], []
+        for s in range(len(h.engram_sites)):
+            t, kk, vv = _mat(a, take()), _mat(a, take()), _mat(a, take())
+            keep += [t, kk, vv]
+            etables.append(t)
+            ekv.append(OQLinear([kk, vv]))
+            taps = np.ascontiguousarray(_f32(a, take()), dtype=np.float32)
+            l.nf_set_engram_taps(m, s, _p(taps), taps.size)
+        final_norm = np.ascontiguousarray(_f32(a, take()), dtype=np.float32)
+        l.nf_set_globals(m, _p(final_norm), _p(perm1), _p(perm2))
+
+        def arr(objs):
+            return (C.c_void_p * max(1, len(objs)))(*[C.cast(x.ptr, C.c_void_p).value for x in objs])
+
+        self._arrs = (arr(qkvg), arr(outs), arr(etables), arr(ekv))
+        l.nf_set_matrices(m, C.cast(emb.ptr, C.c_void_p), *[C.cast(x, C.c_void_p) for x in self._arrs])
+        self._keep = (keep, qkvg, outs, etables, ekv, emb)
+
+    def session(self, cap: int = 256) -> "Session":
+        return Session(self, cap)
+
+    def __del__(self):
+        if getattr(self, "m", None) and lib is not None:
+            _lib().nf_model_free(self.m)
+            self.m = None
+
+
+class Session:
+    """The decoding state of one sequence (NatState, infer.rs:1008-1071)."""
+
+    def __init__(self, f: Forward, cap: int):
+        self.f = f
+        self.s = _lib().nf_session_new(f.m, cap)
+        self.cap = cap
+
+    def step(self, tok: int) -> np.ndarray:
+        """step_native for one token: the logits [out_rows]."""
+        out = np.zeros(self.f.cfg.out_rows, dtype=np.float32)
+        rc = _lib().nf_step(self.f.m, self.s, int(tok), _p(out), self.f.threads)
+        if rc != 0:
+            raise ValueError("step outside the session's capacity or geometry")
+        return out
+
+    def __len__(self):
+        return _lib().nf_session_len(self.s)
+
+    def __del__(self):
+        if getattr(self, "s", None) and lib is not None:
+            _lib().nf_session_free(self.f.m, self.s)
+            self.s = None
