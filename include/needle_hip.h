@@ -38,6 +38,8 @@ extern "C" {
 typedef struct nh_qmat nh_qmat; /* a CQ matrix resident in HBM (QMat / fused QLinear) */
 typedef struct nh_qact nh_qact; /* rotated int8 activations resident in HBM (QAct) */
 typedef struct nh_weights nh_weights; /* every matmul weight of a .cact archive in HBM (QWeights) */
+typedef struct nh_model nh_model;     /* a loaded model for the decode step (Model) */
+typedef struct nh_session nh_session; /* one sequence's decoding state in HBM (Session) */
 
 /* ---- runtime ----------------------------------------------------------- */
 /* Select the device and prepare the code tables.  No reference counterpart
@@ -154,6 +156,47 @@ int nh_weights_count(const nh_weights* w, int kind);
 int nh_weights_get(const nh_weights* w, int kind, int index, const nh_qmat** m);
 /* QWeights::bytes (weights.rs:151-155): packed codes + f16 norms of every matrix. */
 int64_t nh_weights_bytes(const nh_weights* w);
+
+/* ---- the model and its sessions (crates/needle-engine/src/model.rs) ---- */
+/* Model::quantized over Weights::from_archive_mode(fast = true)
+ * (model.rs:248-262) with the native tables (Tables::new,
+ * crates/needle-engine/src/infer.rs:869-960): the archive as nh_weights_load
+ * reads it, plus its small per-layer weights narrowed to f16
+ * (LayerF16::new, infer.rs:905-938), the mHC rows requantized per row
+ * (Phi8, infer.rs:850-867), the RoPE tables and gate constants, all in HBM.
+ * Bytes are borrowed for the call only (needle_load, crates/needle-ffi/src/
+ * lib.rs:57-77).  The decode step covers the Needle-3 geometry family
+ * (4 mHC lanes, d_model in (512, 1024], head dims <= 64, engram sub-tables
+ * of 128); anything else is NH_EINVAL naming the property. */
+int nh_model_load(const uint8_t* bytes, uint64_t n, nh_model** m);
+int nh_model_free(nh_model* m);
+/* The model's matmul weights (owned by m). */
+int nh_model_weights(const nh_model* m, const nh_weights** w);
+/* Config::out_rows (crates/needle-core/src/config.rs:299-301): logits per step. */
+int nh_model_out_rows(const nh_model* m);
+/* Model::session (model.rs:264-280) with room for `cap` positions: the KV
+ * caches, tap and engram histories and every activation in one HBM
+ * allocation. */
+int nh_session_new(const nh_model* m, int cap, nh_session** s);
+int nh_session_free(nh_session* s);
+/* Session::len (model.rs:72-74). */
+int nh_session_len(const nh_session* s);
+/* Back to an empty session (Model::session again, without reallocating). */
+int nh_session_reset(nh_session* s);
+/* Model::forward (model.rs:304-306) with Outputs::LastLogits for HOST token
+ * ids, one step_native (crates/needle-engine/src/infer/step.rs:171-760) per
+ * token; `logits` (DEVICE, out_rows floats, or NULL) receives the last
+ * token's.  The reference feeds multi-token input in chunks of 32 through
+ * its prefill path (infer.rs:1105-1132); one step per token is the same
+ * arithmetic in decode order. */
+int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* stream);
+/* The greedy loop of generate (crates/needle-engine/src/generate.rs:87-139)
+ * at temperature 0, on the device: `steps` times argmax of the current
+ * logits (generate.rs:42-50, the first maximum), then a step on that token.
+ * The picked ids land in HOST `out` at the end (one synchronization); the
+ * last step's logits in `logits` (DEVICE, or NULL).  No stop token: the
+ * caller cuts at EOS. */
+int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, void* stream);
 
 /* ---- seeded inputs (host) ---------------------------------------------- */
 /* jax.random.normal for float32 from a threefry key, as

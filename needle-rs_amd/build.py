@@ -20,7 +20,8 @@ OUT_DIR = os.path.join(HERE, "needle_hip")
 LIB = os.path.join(OUT_DIR, "libneedle_hip.so")
 OBJ_DIR = os.path.join(HERE, "_build")
 
-SOURCES = ["nh_api.hip", "nh_act.hip", "nh_gemv.hip", "nh_gemm.hip", "nh_misc.hip", "nh_archive.cpp"]
+SOURCES = ["nh_api.hip", "nh_act.hip", "nh_gemv.hip", "nh_gemm.hip", "nh_misc.hip", "nh_forward.hip", "nh_archive.cpp",
+           "nh_model.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

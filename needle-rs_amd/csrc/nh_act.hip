@@ -60,8 +60,6 @@ __global__ __launch_bounds__(ACT_THREADS) void k_act_prep(const float* __restric
         r = s_r;
     }
 
-    const float hs = bits_f32(0x3db504f3u);  // hadamard_scale(128), quant.rs:71-73
-    const float k127 = bits_f32(0x3c010204u);
     for (int g = wave; g < groups; g += ACT_THREADS / 64) {
         int p0 = g * GROUP + lane, p1 = p0 + 64;
         float v0 = p0 < in_dim ? xr[p0] : 0.0f;
@@ -76,16 +74,7 @@ __global__ __launch_bounds__(ACT_THREADS) void k_act_prep(const float* __restric
                 v1 = __builtin_fmaf(t, f16_bits_to_f32(norm_scale[p1]), t);
             }
         }
-        fwht128(v0, v1, lane);
-        v0 *= hs;
-        v1 *= hs;
-        float m = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
-        float s = m > 0.0f ? m * k127 : 1.0f;
-        float inv = 1.0f / s;
-        int8_t* q = xq + ((size_t)row * groups + g) * GROUP;
-        q[act_offset(lane, bits)] = quant_one(v0, inv);
-        q[act_offset(lane + 64, bits)] = quant_one(v1, inv);
-        if (lane == 0) sx[(size_t)row * groups + g] = s;
+        a8_group(v0, v1, lane, bits, xq + ((size_t)row * groups + g) * GROUP, sx + (size_t)row * groups + g);
     }
 }
 

@@ -70,7 +70,8 @@ struct Fail {
     std::string msg;
 };
 
-// What the upload pass does: record indices of every matmul weight.
+// What the upload pass does: record indices of every matmul weight, and of
+// the small tensors (Cursor::next) the decode step reads.
 struct Plan {
     uint32_t header[49];
     std::vector<Rec> recs;
@@ -78,6 +79,10 @@ struct Plan {
     std::vector<std::array<size_t, 5>> layers;  // q, k, v, gate, out
     std::array<size_t, 3> phi{};                // pre, post, res
     std::vector<std::array<size_t, 3>> engrams; // tables, key, value
+    std::vector<std::array<long, nh::SMALL_KINDS>> small;  // per layer (-1: absent)
+    std::array<size_t, 6> mhc{};                // a_pre, a_post, a_res, b_pre, b_post, b_res
+    size_t perm1 = 0, perm2 = 0, final_norm = 0;
+    std::vector<size_t> etaps;
 };
 
 const char* dtype_name(uint8_t d) {
@@ -148,30 +153,46 @@ public:
         std::vector<uint64_t> cond_u;
         p_.embedding = big();
         for (uint64_t l = 0; l < layers; ++l) {
-            next();  // norm_in
+            std::array<long, nh::SMALL_KINDS> sm;
+            sm.fill(-1);
+            auto take = [&](int kind) {
+                sm[kind] = (long)i_;
+                return next();
+            };
+            take(nh::S_NORM_IN);
             const size_t q = big(), k = big(), v = big();
-            if (taps) next(), next(), next();  // q, k, v taps
-            next(), next();                     // q_norm, k_norm
+            if (taps) take(nh::S_Q_TAPS), take(nh::S_K_TAPS), take(nh::S_V_TAPS);
+            take(nh::S_Q_NORM), take(nh::S_K_NORM);
             const size_t g = big(), o = big();
             p_.layers.push_back({q, k, v, g, o});
-            next();  // post_attn_norm
-            if (next() < 1) throw Fail{"archive tensor " + std::to_string(i_ - 1) + ": attn_gate is empty"};
-            next();  // pre_hada_norm
-            for (int j = 0; j < 5; ++j) next();  // d1, d2, b2, d3, d4
+            take(nh::S_POST_NORM);
+            if (take(nh::S_ATTN_GATE) < 1)
+                throw Fail{"archive tensor " + std::to_string(i_ - 1) + ": attn_gate is empty"};
+            take(nh::S_PRE_HADA);
+            for (int j = 0; j < 5; ++j) take(nh::S_D1 + j);  // d1, d2, b2, d3, d4
             uint64_t kl[6];
-            for (int j = 0; j < 6; ++j) kl[j] = next();
+            for (int j = 0; j < 6; ++j) kl[j] = take(nh::S_KRON0 + j);
             kron.push_back({kl[0], kl[1]});
-            next();  // cond_v
-            cond_u.push_back(next());
+            take(nh::S_COND_V);
+            cond_u.push_back(take(nh::S_COND_U));
+            p_.small.push_back(sm);
         }
-        for (int j = 0; j < 6; ++j) next();  // mhc a_pre, a_post, a_res, b_pre, b_post, b_res
+        for (int j = 0; j < 6; ++j) {  // mhc a_pre, a_post, a_res, b_pre, b_post, b_res
+            p_.mhc[j] = i_;
+            next();
+        }
         p_.phi = {big(), big(), big()};
-        const uint64_t perm1 = next(), perm2 = next();
+        p_.perm1 = i_;
+        const uint64_t perm1 = next();
+        p_.perm2 = i_;
+        const uint64_t perm2 = next();
         for (uint64_t s = 0; s < sites; ++s) {
             const size_t t = big(), k = big(), v = big();
+            p_.etaps.push_back(i_);
             next();  // taps
             p_.engrams.push_back({t, k, v});
         }
+        p_.final_norm = i_;
         next();  // final_norm
         // The fast-path checks (weights.rs:460-464), on the lengths the
         // records hold.
@@ -375,9 +396,49 @@ int fuse(std::initializer_list<nh_qmat*> parts, nh_qmat** h) {
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-int nh_weights_load(const uint8_t* bytes, uint64_t n, nh_weights** out) {
+// One small tensor widened to f32.
+std::vector<float> small_f32(const uint8_t* data, const Plan& plan, size_t i) {
+    const Rec& r = plan.recs[i];
+    const uint8_t* blob = data + r.offset;
+    std::vector<float> v;
+    if (r.dtype == kF32) {
+        v.resize(r.nbytes / 4);
+        memcpy(v.data(), blob, v.size() * 4);
+    } else if (r.dtype == kF16) {
+        v.resize(r.nbytes / 2);
+        for (size_t j = 0; j < v.size(); ++j) {
+            uint16_t h;
+            memcpy(&h, blob + 2 * j, 2);
+            v[j] = half_to_float(h);
+        }
+    } else {
+        throw Fail{"archive tensor " + std::to_string(i) + ": a CQ record where the decode step reads a small tensor"};
+    }
+    return v;
+}
+
+void read_small(const uint8_t* data, const Plan& plan, nh::ArchiveSmall& sm) {
+    sm.layer.clear();
+    for (const auto& ly : plan.small) {
+        std::vector<std::vector<float>> kinds(nh::SMALL_KINDS);
+        for (int k = 0; k < nh::SMALL_KINDS; ++k)
+            if (ly[k] >= 0) kinds[k] = small_f32(data, plan, (size_t)ly[k]);
+        sm.layer.push_back(std::move(kinds));
+    }
+    sm.mhc.clear();
+    for (size_t i : plan.mhc) sm.mhc.push_back(small_f32(data, plan, i));
+    sm.perm1 = small_f32(data, plan, plan.perm1);
+    sm.perm2 = small_f32(data, plan, plan.perm2);
+    sm.final_norm = small_f32(data, plan, plan.final_norm);
+    sm.etaps.clear();
+    for (size_t i : plan.etaps) sm.etaps.push_back(small_f32(data, plan, i));
+}
+
+}  // namespace
+
+int nh::load_archive(const uint8_t* bytes, uint64_t n, nh_weights** out, nh::ArchiveSmall* small) {
     if (!out) {
         nh::set_error("null argument");
         return NH_EINVAL;
@@ -392,6 +453,7 @@ int nh_weights_load(const uint8_t* bytes, uint64_t n, nh_weights** out) {
         Walker w(bytes, n, plan);
         w.parse();
         w.walk();
+        if (small) read_small(bytes, plan, *small);
     } catch (const Fail& f) {
         nh::set_error(f.msg);
         return NH_EINVAL;
@@ -472,6 +534,12 @@ int nh_weights_load(const uint8_t* bytes, uint64_t n, nh_weights** out) {
     }
     *out = wts;
     return NH_OK;
+}
+
+extern "C" {
+
+int nh_weights_load(const uint8_t* bytes, uint64_t n, nh_weights** out) {
+    return nh::load_archive(bytes, n, out, nullptr);
 }
 
 int nh_weights_free(nh_weights* w) {

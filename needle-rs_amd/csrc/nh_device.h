@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "nh_internal.h"
+
 namespace nh {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -125,5 +127,56 @@ __device__ __forceinline__ int8_t quant_one(float v, float inv) {
 }
 
 __device__ __forceinline__ float bits_f32(uint32_t b) { return __builtin_bit_cast(float, b); }
+
+// The stored selector of natural position p: 4-bit dword d = p / 8 is
+// dword d / 4 of lane d % 4's 16-byte chunk; 2-bit dword d = p / 16 is
+// dword d / 4 of lane d % 4's 8-byte chunk, field p % 4 of byte (p / 4) % 4.
+template <int BITS>
+__device__ __forceinline__ uint32_t code_sel_at(const void* codes, int tile, int G, int g, int rt, int p) {
+    const size_t ci = ((size_t)tile * G + g) * 64 + rt * 4;
+    if constexpr (BITS == 4) {
+        const int d = p >> 3;
+        const uint32_t* chunk = (const uint32_t*)(reinterpret_cast<const uint4*>(codes) + ci + (d & 3));
+        return (chunk[d >> 2] >> (4 * (p & 7))) & 15u;
+    } else {
+        const int d = p >> 4;
+        const uint32_t* chunk = (const uint32_t*)(reinterpret_cast<const uint2*>(codes) + ci + (d & 3));
+        return (chunk[d >> 2] >> (8 * ((p >> 2) & 3) + 2 * (p & 3))) & 3u;
+    }
+}
+
+// The dequantized values of positions lane and lane + 64 of (row, group g)
+// of a tiled matrix: QMat::row (crates/needle-engine/src/qlinear.rs:309-323),
+// cb[code] * norm, then the normalised rotation (quant.rs:109-115).
+template <int BITS>
+__device__ __forceinline__ void row_group(const void* codes, const uint16_t* norms, const float* fsel, int G,
+                                          uint32_t row, int g, int lane, float& v0, float& v1) {
+    const int tile = row / TILE_ROWS, rt = row % TILE_ROWS;
+    const float norm = f16_bits_to_f32(norms[(size_t)row * G + g]);
+    v0 = fsel[code_sel_at<BITS>(codes, tile, G, g, rt, lane)] * norm;
+    v1 = fsel[code_sel_at<BITS>(codes, tile, G, g, rt, lane + 64)] * norm;
+    fwht128(v0, v1, lane);
+    const float hs = bits_f32(0x3db504f3u);
+    v0 *= hs;
+    v1 *= hs;
+}
+
+// prep_group (crates/needle-engine/src/qlinear.rs:149-164) for one group
+// held by one wavefront (positions lane, lane + 64): rotate, scale
+// (quant.rs:109-115), quantize with the group's amax scale (qlinear.rs:77-88)
+// and store the int8 codes at act_offset(p, bits) of the group's 128-byte
+// block `q`, the scale at `s_out`.
+__device__ __forceinline__ void a8_group(float v0, float v1, int lane, int bits, int8_t* q, float* s_out) {
+    fwht128(v0, v1, lane);
+    const float hs = bits_f32(0x3db504f3u);
+    v0 *= hs;
+    v1 *= hs;
+    const float m = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+    const float s = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
+    const float inv = 1.0f / s;
+    q[act_offset(lane, bits)] = quant_one(v0, inv);
+    q[act_offset(lane + 64, bits)] = quant_one(v1, inv);
+    if (lane == 0) *s_out = s;
+}
 
 }  // namespace nh

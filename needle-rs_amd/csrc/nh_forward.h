@@ -1,0 +1,130 @@
+// The Needle-3 decode step on the GPU: the geometry, per-layer weights and
+// per-session state the forward kernels (nh_forward.hip) take by value,
+// shared with the host side that builds them (nh_model.cpp).
+//
+// Every pointer is device memory.  Small per-layer weights are f16 bits as
+// the reference's LayerF16 keeps them (crates/needle-engine/src/infer.rs:
+// 887-938); Phi8 is the int8 requantization of the dequantized mHC rows
+// (infer.rs:850-867).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nh {
+
+constexpr int FWD_MAX_D = 1024;     // d_model (the Hadamard MLP pads to 1024)
+constexpr int HADA_NB = 32;         // Kronecker factor side (hada_n = 1024)
+constexpr int HADA_N = HADA_NB * HADA_NB;
+constexpr int COND_RANK = 8;        // HADA_COND_RANK (crates/needle-core/src/config.rs:13)
+constexpr int MHC_LANES = 4;        // the step is written for 4 residual lanes
+constexpr int MHC_COLS = 2 * MHC_LANES + MHC_LANES * MHC_LANES;  // pre | post | res = 24
+constexpr int MAX_UNITS = 16;       // q heads + k heads + v heads (one wavefront each)
+constexpr int MAX_HEAD_DIM = 64;
+constexpr int MAX_SITES = 16;
+constexpr int MAX_TABLES = 16;
+constexpr int ENGRAM_TAPS = 4;      // ENGRAM_CONV_TAPS (config.rs:10)
+constexpr int ATT_CHUNK_MAX = 256;  // key_chunks never makes a chunk longer
+constexpr int ATT_THREADS = 256;
+
+struct Dims {
+    int d, nh, nkv, qk, vd, lanes, taps, layers;
+    int W;      // (nh + nkv) * qk + nkv * vd: the pre-tap q | k | v width
+    int nq;     // W + nh * vd: the fused q | k | v | gate rows
+    int keep;   // history rows kept: taps - 1 (at least 1)
+    int vocab, out_rows;
+    int sites, ntab, eheads, seed_stride, slots, sub, dilation;
+    int orders[4];
+    int cap;    // session positions
+    int max_chunks;  // attention chunks a position can need
+};
+
+struct LayerDev {
+    const uint16_t* kron[6];
+    const uint16_t *cond_v, *cond_u, *d1, *d2, *b2, *d3, *d4;
+    const uint16_t *norm_in, *post_norm, *pre_hada, *q_taps, *k_taps, *v_taps, *q_norm, *k_norm;
+    const int8_t* phi_q;  // [24][lanes * d]
+    const float* phi_s;   // [24]
+    float a_pre, a_post, a_res;
+    float ga;             // sigmoid(attn_gate), f32 expf on the host
+    float b_pre[4], b_post[4], b_res[16];
+    int site;             // engram site gating this layer, or -1
+    int lane;             // l % lanes
+    int window;           // sliding window (0: attends to every position)
+};
+
+struct Globals {
+    const float* final_norm;  // [d] f32
+    const int32_t *perm1, *perm2;
+    const float *sd, *cd;     // RoPE: sincosf(freq)
+    const float* etaps;       // [sites][4][d] f32
+};
+
+// One session's state, all device memory.
+struct SessDev {
+    float* xs;        // [4][d] residual lanes
+    float* u;         // [d] mHC read of the layer
+    float* x1;        // [d] after the engram gate
+    float* p;         // [64]: the 24 mHC gate projections, then hpost [4]
+                      // at 24 and the Sinkhorn mixing hres [16] at 28
+    float* proj;      // [nq] q | k | v | gate
+    float* qbuf;      // [nh][qk] rotated queries
+    float* o;         // [d] attention output projection
+    float* ekv;       // [sites][2d] engram key | value
+    float* evals;     // [sites][d] engram conv
+    float* logits;    // [out_rows]
+    float* rope_c;    // [qk/2]
+    float* rope_s;
+    uint32_t* tokens; // [cap]
+    float* po;        // [nh][max_chunks][vd] attention chunk partials
+    float* pm;        // [nh][max_chunks]
+    float* psum;      // [nh][max_chunks]
+    float* hist;      // [layers][keep][W] ring: position p in slot p % keep
+    int8_t* k8;       // [layers][cap][nkv][qk]
+    float* ks;        // [layers][cap][nkv]
+    int8_t* v8t;      // [layers][nkv][vd][cap]
+    float* vs;        // [layers][cap][nkv]
+    int8_t* ev8;      // [sites][cap][d]
+    float* evs;       // [sites][cap][d / 32]
+    int8_t* xq_in;    // A8 activations: the layer input (K = d), rows 0
+    float* sx_in;
+    int8_t* xq_att;   // the gated heads (K = nh * vd)
+    float* sx_att;
+    int8_t* xq_eng;   // the engram rows, one row per site (K = d)
+    float* sx_eng;
+    int32_t* argmax;  // scratch of the greedy pick
+};
+
+// A CQ matrix read by rows (the embedding, the engram tables).
+struct RowSrc {
+    const void* codes;
+    const uint16_t* norms;
+    const float* fsel;
+    int out, groups, bits;
+};
+
+struct BeginArgs {
+    RowSrc emb;
+    RowSrc tab[MAX_SITES];
+    int eng_bits[MAX_SITES];  // code width of each site's key | value matrix
+};
+
+// Launchers (nh_forward.hip).
+// The start of a step: the embedding row into the lanes, the RoPE rows of
+// the position, and per engram site the hashed table rows as A8 rows.
+hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const BeginArgs& B, int p0, hipStream_t s);
+hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, int p0, hipStream_t s);
+// The per-layer boundary: the Hadamard MLP and mHC write of layer `prev`
+// (null: none, the lanes hold the embedding row), then the mHC read, engram
+// gate, input norm and A8 of layer `next` (null: the head's lane mean,
+// final norm and A8 instead).
+hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
+                     int in_bits, int head_bits, hipStream_t s);
+hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, hipStream_t s);
+hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, hipStream_t s);
+hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
+                        hipStream_t s);
+hipError_t fwd_argmax(const float* logits, int n, uint32_t* dst, hipStream_t s);
+hipError_t fwd_phi8(const float* rows, int nrows, int width, int8_t* q, float* scale, hipStream_t s);
+
+}  // namespace nh

@@ -1,0 +1,877 @@
+// The Needle-3 decode step (Model::step_native,
+// crates/needle-engine/src/infer/step.rs:171-760) on gfx950, one token per
+// step, the KV cache and every activation resident in HBM.
+//
+// Per step: fwd_begin (embedding row, RoPE rows, hashed engram rows as A8),
+// one key | value GEMV per engram site, fwd_engram_hist (int8 value history
+// and its dilated conv), then per layer
+//   fwd_layer   one workgroup: the previous layer's Hadamard MLP and mHC
+//               write, then this layer's mHC read, engram gate, input norm
+//               and A8;
+//   GEMV        q | k | v | gate;
+//   fwd_units   one wavefront per head unit: conv taps, head norm, RoPE,
+//               int8 KV append, the tap history;
+//   fwd_attend  one workgroup per (query head, key chunk): int8 scores,
+//               chunk softmax, 21-bit digit P.V;
+//   fwd_attn_out one workgroup: chunk merge, head gate, A8;
+//   GEMV        out;
+// and a last fwd_layer (lane mean, final norm, A8) before the head GEMV.
+//
+// Every floating-point operation follows the reference's portable branch in
+// order and rounding (fma where it has mul_add, no contraction elsewhere):
+// the serial dot16 chains, the cond_weights chains and the mix8 fma chains
+// run in their reference order; integer sums (idot, P.V digits) are exact
+// and order-free.  The reference's f32 exponential off Apple targets is the
+// f64 exp rounded once (lexpf, crates/needle-engine/src/infer.rs:84-101);
+// here too, with the device library's f64 exp: two f64 exps accurate to an
+// ulp give the same f32 unless an f32 rounding boundary falls between them.
+#include "nh_device.h"
+#include "nh_forward.h"
+#include "nh_internal.h"
+
+namespace nh {
+
+namespace {
+
+constexpr int LT = 1024;  // fwd_layer / fwd_attn_out threads
+constexpr uint32_t ENGRAM_SEED = 0x9E3779B9u;   // crates/needle-core/src/config.rs:11
+constexpr uint32_t ENGRAM_PRIME = 0x01000193u;  // config.rs:12
+constexpr int NATIVE_TEAM = 4;                  // infer.rs:38
+
+__device__ __forceinline__ float h2f(uint16_t h) { return f16_bits_to_f32(h); }
+
+// nexp (crates/needle-engine/src/infer.rs:353-367).
+__device__ __forceinline__ float nexp(float x) {
+    x = fminf(fmaxf(x, bits_f32(0xc2b0c0a5u)), bits_f32(0x42b0c0a5u));
+    const float k = __builtin_rintf(x * bits_f32(0x3fb8aa3bu));
+    float r = __builtin_fmaf(k, bits_f32(0xbf318000u), x);
+    r = __builtin_fmaf(k, bits_f32(0x395e8083u), r);
+    float p = __builtin_fmaf(bits_f32(0x39506967u), r, bits_f32(0x3ab743ceu));
+    p = __builtin_fmaf(r, p, bits_f32(0x3c088908u));
+    p = __builtin_fmaf(r, p, bits_f32(0x3d2aa9c1u));
+    p = __builtin_fmaf(r, p, bits_f32(0x3e2aaaaau));
+    p = __builtin_fmaf(r, p, 0.5f);
+    const float y = __builtin_fmaf(r * r, p, r);
+    const float s = __builtin_bit_cast(float, (uint32_t)((int32_t)k << 23) + 0x3f800000u);
+    return __builtin_fmaf(s, y, s);
+}
+
+// lexpf (infer.rs:84-88): exp in f64, rounded once.
+__device__ __forceinline__ float lexpf(float x) { return (float)exp((double)x); }
+
+// rinv (infer.rs:422-424).
+__device__ __forceinline__ float rinv(float ss, int n) {
+    const float v = ss / (float)n + 1e-6f;
+    return 1.0f / __builtin_sqrtf(v);
+}
+
+// dot16 (infer.rs:369-419, portable branch), by one wavefront: lane
+// i16 = 4 j + l carries accumulator a[j][l] over 16-element chunks in
+// order; t[l] = ((a[2][l] + a[3][l]) + a[1][l]) + a[0][l]; the result
+// (t0 + t1) + (t2 + t3) reaches every lane.
+__device__ __forceinline__ float dot16_wave(const float* x, const float* y, int n, int lane) {
+    float a = 0.0f;
+    if (lane < 16) {
+        const int chunks = n / 16;
+        for (int c = 0; c < chunks; ++c) a = __builtin_fmaf(x[c * 16 + lane], y[c * 16 + lane], a);
+    }
+    const int l = lane & 3;
+    const float a0 = __shfl(a, l, 64), a1 = __shfl(a, 4 + l, 64), a2 = __shfl(a, 8 + l, 64),
+                a3 = __shfl(a, 12 + l, 64);
+    const float t = ((a2 + a3) + a1) + a0;
+    const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
+    return (t0 + t1) + (t2 + t3);
+}
+
+// The same over a vector held one element per lane (n <= 64).
+__device__ __forceinline__ float dot16_lanes(float v, int n, int lane) {
+    float a = 0.0f;
+    const int chunks = n / 16;
+    for (int c = 0; c < chunks; ++c) {
+        const float x = __shfl(v, c * 16 + (lane & 15), 64);
+        a = __builtin_fmaf(x, x, a);
+    }
+    const int l = lane & 3;
+    const float a0 = __shfl(a, l, 64), a1 = __shfl(a, 4 + l, 64), a2 = __shfl(a, 8 + l, 64),
+                a3 = __shfl(a, 12 + l, 64);
+    const float t = ((a2 + a3) + a1) + a0;
+    const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
+    return (t0 + t1) + (t2 + t3);
+}
+
+// quant_i8's scale (qlinear.rs:92-108) of a value per lane, max over the
+// whole wavefront (lanes outside the vector hold 0).
+__device__ __forceinline__ float wave_quant_scale(float v) {
+    const float m = wave_max(fabsf(v));
+    return m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
+}
+
+// key_chunks (infer.rs:2093-2101): the chunk count and length of n keys.
+__device__ __forceinline__ void key_chunks(int n, int nkv, int& count, int& size) {
+    int k = 2 * NATIVE_TEAM / nkv;
+    if (k < 1) k = 1;
+    int c = (n + 255) / 256;
+    if (k * 64 <= n && c < k) c = k;
+    if (c < 1) c = 1;
+    const int chunk = ((n + c - 1) / c + 15) / 16 * 16;
+    size = chunk;
+    count = chunk ? (n + chunk - 1) / chunk : 0;
+}
+
+// The attended range of position p0: keys lo..p0.
+__device__ __forceinline__ int window_lo(int window, int p0) {
+    return (window > 0 && p0 + 1 > window) ? p0 + 1 - window : 0;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ begin
+// Waves 0 .. Gd-1: embedding row groups (step.rs:228-235: row * sqrt(d)
+// into every lane).  Then per site e and group g: the hashed row of table
+// g (step.rs:245-269 with the hash of infer.rs engram rows) dequantized and
+// rotated (QMat::row), A8-prepared as group g of the site's row
+// (QAct::new over the concatenated rows); missing rows are zeros.  The last
+// wave: the RoPE rows of p0 (rope_rows, infer.rs:1716-1747), by the
+// angle-addition recurrence from the previous position, exact (cos 0, sin 0)
+// = (1, 0) at position 0.
+__global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, BeginArgs B, int p0) {
+    const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    const int Gd = (D.d + GROUP - 1) / GROUP;
+    const int eng_waves = D.sites * Gd;
+    if (wave < Gd) {
+        const uint32_t tok = S.tokens[p0];
+        float v0, v1;
+        if (B.emb.bits == 2)
+            row_group<2>(B.emb.codes, B.emb.norms, B.emb.fsel, B.emb.groups, tok, wave, lane, v0, v1);
+        else
+            row_group<4>(B.emb.codes, B.emb.norms, B.emb.fsel, B.emb.groups, tok, wave, lane, v0, v1);
+        const float scale = __builtin_sqrtf((float)D.d);
+        const int i0 = wave * GROUP + lane, i1 = i0 + 64;
+        for (int b = 0; b < MHC_LANES; ++b) {
+            if (i0 < D.d) S.xs[b * D.d + i0] = v0 * scale;
+            if (i1 < D.d) S.xs[b * D.d + i1] = v1 * scale;
+        }
+    } else if (wave < Gd + eng_waves) {
+        const int e = (wave - Gd) / Gd, g = (wave - Gd) % Gd;
+        float v0 = 0.0f, v1 = 0.0f;
+        if (g < D.ntab) {
+            const int oi = g / D.eheads, h = g % D.eheads, order = D.orders[oi];
+            if (p0 + 1 >= order) {
+                uint32_t acc = ENGRAM_SEED * (uint32_t)(oi * D.seed_stride + h + 1);
+                for (int j = 0; j < order; ++j) acc = (acc ^ S.tokens[p0 - j]) * ENGRAM_PRIME;
+                acc ^= acc >> 15;
+                const uint32_t row = (uint32_t)g * (uint32_t)D.slots + acc % (uint32_t)D.slots;
+                const RowSrc& t = B.tab[e];
+                if (t.bits == 2)
+                    row_group<2>(t.codes, t.norms, t.fsel, t.groups, row, 0, lane, v0, v1);
+                else
+                    row_group<4>(t.codes, t.norms, t.fsel, t.groups, row, 0, lane, v0, v1);
+            }
+        }
+        a8_group(v0, v1, lane, B.eng_bits[e], S.xq_eng + ((size_t)e * Gd + g) * GROUP, S.sx_eng + e * Gd + g);
+    } else if (wave == Gd + eng_waves) {
+        const int half = D.qk / 2;
+        if (lane < half) {
+            float c = 1.0f, s = 0.0f;
+            if (p0 > 0) {
+                const float oc = S.rope_c[lane], os = S.rope_s[lane];
+                c = __builtin_fmaf(-G.sd[lane], os, G.cd[lane] * oc);
+                s = __builtin_fmaf(G.sd[lane], oc, G.cd[lane] * os);
+            }
+            S.rope_c[lane] = c;
+            S.rope_s[lane] = s;
+        }
+    }
+}
+
+hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const BeginArgs& B, int p0, hipStream_t s) {
+    const int Gd = (D.d + GROUP - 1) / GROUP;
+    const int waves = Gd + D.sites * Gd + 1;
+    hipLaunchKernelGGL(k_begin, dim3((waves + 3) / 4), dim3(256), 0, s, D, G, S, B, p0);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------- engram history
+// Per site: the value half of key | value as int8 groups of 32 appended to
+// the site's history, then the dilated causal conv over the last
+// ENGRAM_TAPS history rows (step.rs:346-391): dst = fma(tap, s * q, dst)
+// from the newest row back, stopping at position 0.
+__global__ __launch_bounds__(1024) void k_engram_hist(Dims D, Globals G, SessDev S, int p0) {
+    const int e = blockIdx.x, k = threadIdx.x, d = D.d;
+    const bool on = k < d;
+    const float v = on ? S.ekv[(size_t)e * 2 * d + d + k] : 0.0f;
+    float m = fabsf(v);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    const float s = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
+    const int8_t q = quant_one(v, 1.0f / s);
+    if (!on) return;
+    const int gs = d / 32;
+    int8_t* ev8 = S.ev8 + (size_t)e * D.cap * d;
+    float* evs = S.evs + (size_t)e * D.cap * gs;
+    ev8[(size_t)p0 * d + k] = q;
+    if ((k & 31) == 0) evs[(size_t)p0 * gs + k / 32] = s;
+    float dst = 0.0f;
+    for (int j = 0; j < ENGRAM_TAPS; ++j) {
+        if (p0 < j * D.dilation) break;
+        const int pj = p0 - j * D.dilation;
+        const float qs = j == 0 ? s : evs[(size_t)pj * gs + k / 32];
+        const int8_t q8 = j == 0 ? q : ev8[(size_t)pj * d + k];
+        const float tw = G.etaps[((size_t)e * ENGRAM_TAPS + j) * d + k];
+        dst = __builtin_fmaf(tw, qs * (float)q8, dst);
+    }
+    S.evals[(size_t)e * d + k] = dst;
+}
+
+hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, int p0, hipStream_t s) {
+    if (D.sites <= 0) return hipSuccess;
+    const int threads = (D.d + 63) / 64 * 64;
+    hipLaunchKernelGGL(k_engram_hist, dim3(D.sites), dim3(threads), 0, s, D, G, S, p0);
+    return hipGetLastError();
+}
+
+// -------------------------------------------------------------- the layer
+namespace {
+
+struct LayerShared {
+    float xs[MHC_LANES * FWD_MAX_D];
+    float o[FWD_MAX_D];
+    float x1[FWD_MAX_D];
+    float u[FWD_MAX_D];
+    float x2[FWD_MAX_D];
+    float h[FWD_MAX_D];
+    float A[HADA_N], B[HADA_N], C[HADA_N];
+    alignas(16) int8_t nx8[MHC_LANES * FWD_MAX_D];
+    float red[LT / 64];
+    float p[64];
+    float wk[COND_RANK];
+    float hp[MHC_LANES];
+    float r, r2;
+};
+
+__device__ __forceinline__ float block_max(float v, float* red) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    v = wave_max(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) m = fmaxf(m, red[i]);
+    return m;
+}
+
+// mix8 (infer.rs:2343-2380), portable branch: out[r][c] =
+// sum_j ct[j][r] * rows[j][c] as an fma chain from j = 0 (transposed: stored
+// at out[c][r]); rows r < rows_limit (a tile prefix).  One output per thread.
+template <bool CT_HALF, bool ROWS_HALF>
+__device__ __forceinline__ void mix8(bool transpose, const void* ct, const void* rows, float* out, int rows_limit) {
+    const int t = threadIdx.x, r = t >> 5, c = t & 31;
+    if (r >= rows_limit) return;
+    float o = 0.0f;
+#pragma unroll 8
+    for (int j = 0; j < HADA_NB; ++j) {
+        const float a = CT_HALF ? h2f(((const uint16_t*)ct)[j * HADA_NB + r]) : ((const float*)ct)[j * HADA_NB + r];
+        const float b = ROWS_HALF ? h2f(((const uint16_t*)rows)[j * HADA_NB + c])
+                                  : ((const float*)rows)[j * HADA_NB + c];
+        o = __builtin_fmaf(a, b, o);
+    }
+    out[transpose ? c * HADA_NB + r : r * HADA_NB + c] = o;
+}
+
+// sinkhorn64 (infer.rs:2501-2528) by 16 lanes, lane = 4 r + c holding
+// e[r][c]: row sums ((e0 + e1) + (e2 + e3)), column sums
+// ((e[c] + e[4 + c]) + (e[8 + c] + e[12 + c])), 20 rounds, in f64.
+__device__ __forceinline__ float sinkhorn_lane(float z, int lane) {
+    const int r = (lane >> 2) & 3, c = lane & 3;
+    const float z0 = __shfl(z, 4 * r, 64), z1 = __shfl(z, 4 * r + 1, 64), z2 = __shfl(z, 4 * r + 2, 64),
+                z3 = __shfl(z, 4 * r + 3, 64);
+    const double m = (double)fmaxf(fmaxf(z0, z1), fmaxf(z2, z3));
+    double e = exp((double)z - m);
+    for (int it = 0; it < 20; ++it) {
+        {
+            const double a0 = __shfl(e, 4 * r, 64), a1 = __shfl(e, 4 * r + 1, 64), a2 = __shfl(e, 4 * r + 2, 64),
+                         a3 = __shfl(e, 4 * r + 3, 64);
+            const double inv = 1.0 / ((a0 + a1) + (a2 + a3));
+            e *= inv;
+        }
+        {
+            const double a0 = __shfl(e, c, 64), a1 = __shfl(e, 4 + c, 64), a2 = __shfl(e, 8 + c, 64),
+                         a3 = __shfl(e, 12 + c, 64);
+            const double inv = 1.0 / ((a0 + a1) + (a2 + a3));
+            e *= inv;
+        }
+    }
+    return (float)e;
+}
+
+// The Hadamard MLP and mHC write of layer P (step.rs:600-705).
+__device__ void layer_out(const Dims& D, const Globals& G, const LayerDev& P, LayerShared& sh) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
+    // on = zcn16(o, post_norm); x2 = fma(on, sigmoid(attn_gate), x1)
+    if (wave == 0) {
+        const float ss = dot16_wave(sh.o, sh.o, d, lane);
+        if (lane == 0) sh.r = rinv(ss, d);
+    }
+    __syncthreads();
+    for (int i = t; i < d; i += LT) {
+        const float tt = sh.o[i] * sh.r;
+        const float on = __builtin_fmaf(tt, h2f(P.post_norm[i]), tt);
+        sh.x2[i] = __builtin_fmaf(on, P.ga, sh.x1[i]);
+    }
+    __syncthreads();
+    // h2 = zcn16(x2, pre_hada)
+    if (wave == 0) {
+        const float ss = dot16_wave(sh.x2, sh.x2, d, lane);
+        if (lane == 0) sh.r = rinv(ss, d);
+    }
+    __syncthreads();
+    for (int i = t; i < d; i += LT) {
+        const float tt = sh.x2[i] * sh.r;
+        sh.h[i] = __builtin_fmaf(tt, h2f(P.pre_hada[i]), tt);
+    }
+    __syncthreads();
+    // cond_weights (infer.rs:1640-1656): lane 8 jm + k chains
+    // acc[jm][k] = fma(h2[j], cond_v[j][k], .) over j = jm, jm + 4, ...
+    if (wave == 0) {
+        const int k = lane & 7;
+        float a = 0.0f;
+        if (lane < 32)
+            for (int j = lane >> 3; j < d; j += 4) a = __builtin_fmaf(sh.h[j], h2f(P.cond_v[j * 8 + k]), a);
+        const float a0 = __shfl(a, k, 64), a1 = __shfl(a, 8 + k, 64), a2 = __shfl(a, 16 + k, 64),
+                    a3 = __shfl(a, 24 + k, 64);
+        const float lg = ((a2 + a3) + a1) + a0;
+        float m = lg;
+        m = fmaxf(m, __shfl_xor(m, 1, 64));
+        m = fmaxf(m, __shfl_xor(m, 2, 64));
+        m = fmaxf(m, __shfl_xor(m, 4, 64));
+        const float e = lexpf(lg - m);
+        float ev[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ev[i] = __shfl(e, i, 64);
+        const float sum = ev[7] + ((ev[6] + (ev[5] + ev[4])) + ((ev[3] + ev[2]) + (ev[1] + ev[0])));
+        const float inv = 1.0f / sum;
+        if (lane < 8) sh.wk[lane] = e * inv;
+    }
+    // z = h2 * d1, zero-padded to hada_n
+    for (int j = t; j < HADA_N; j += LT) sh.A[j] = j < d ? sh.h[j] * h2f(P.d1[j]) : 0.0f;
+    __syncthreads();
+    mix8<true, false>(true, P.kron[0], sh.A, sh.B, HADA_NB);
+    __syncthreads();
+    mix8<false, true>(false, sh.B, P.kron[1], sh.C, HADA_NB);
+    __syncthreads();
+    for (int j = t; j < HADA_N; j += LT) {
+        float cond = 1.0f;
+#pragma unroll
+        for (int k = 0; k < COND_RANK; ++k) cond = __builtin_fmaf(h2f(P.cond_u[k * HADA_N + j]), sh.wk[k], cond);
+        float zs = __builtin_fmaf(sh.C[G.perm1[j]], cond * h2f(P.d2[j]), h2f(P.b2[j]));
+        zs = zs / (nexp(-zs) + 1.0f);
+        sh.A[j] = zs;
+    }
+    __syncthreads();
+    mix8<true, false>(true, P.kron[2], sh.A, sh.B, HADA_NB);
+    __syncthreads();
+    mix8<false, true>(false, sh.B, P.kron[3], sh.C, HADA_NB);
+    __syncthreads();
+    for (int j = t; j < HADA_N; j += LT) sh.A[j] = sh.C[G.perm2[j]] * h2f(P.d3[j]);
+    __syncthreads();
+    mix8<true, false>(true, P.kron[4], sh.A, sh.B, HADA_NB);
+    __syncthreads();
+    mix8<false, true>(false, sh.B, P.kron[5], sh.C, d / HADA_NB / 8 * 8);
+    __syncthreads();
+    // The mHC write: y = (x2 + t3 * d4) - u; lane a = y hpost[a] + sum_b
+    // hres[a][b] old[b] as an fma chain over b.
+    const float* hpost = sh.p + MHC_COLS;
+    const float* hres = sh.p + MHC_COLS + MHC_LANES;
+    for (int ch = t; ch < d; ch += LT) {
+        const float y = (sh.x2[ch] + sh.C[ch] * h2f(P.d4[ch])) - sh.u[ch];
+        float old[MHC_LANES];
+#pragma unroll
+        for (int b = 0; b < MHC_LANES; ++b) old[b] = sh.xs[b * d + ch];
+#pragma unroll
+        for (int a = 0; a < MHC_LANES; ++a) {
+            float v = y * hpost[a];
+#pragma unroll
+            for (int b = 0; b < MHC_LANES; ++b) v = __builtin_fmaf(old[b], hres[a * MHC_LANES + b], v);
+            sh.xs[a * d + ch] = v;
+        }
+    }
+    __syncthreads();
+}
+
+// The mHC read, engram gate, input norm and A8 of layer N
+// (step.rs:400-479).
+__device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, int in_bits, LayerShared& sh) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d, nc = MHC_LANES * d;
+    if (wave == 0) {
+        const float ss = dot16_wave(sh.xs, sh.xs, nc, lane);
+        if (lane == 0) sh.r = rinv(ss, nc);
+    }
+    __syncthreads();
+    const float r = sh.r;
+    float m = 0.0f;
+    for (int i = t; i < nc; i += LT) m = fmaxf(m, fabsf(sh.xs[i] * r));
+    m = block_max(m, sh.red);
+    const float sx = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
+    const float inv = 1.0f / sx;
+    for (int i = t; i < nc; i += LT) sh.nx8[i] = quant_one(sh.xs[i] * r, inv);
+    __syncthreads();
+    // Phi8 rows: p[k] = (sx * s_k) * idot(phi_q[k], nx8)
+    for (int k = wave; k < MHC_COLS; k += LT / 64) {
+        const uint4* row = reinterpret_cast<const uint4*>(N.phi_q + (size_t)k * nc);
+        const uint4* xv = reinterpret_cast<const uint4*>(sh.nx8);
+        int acc = 0;
+        for (int i = lane; i < nc / 16; i += 64) {
+            const uint4 a = row[i], b = xv[i];
+            acc = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, acc, false);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        if (lane == 0) sh.p[k] = (sx * N.phi_s[k]) * (float)acc;
+    }
+    __syncthreads();
+    // Gates: hp (pre, sigmoid), hpost (2 sigmoid), hres (Sinkhorn).
+    if (wave == 0) {
+        if (lane < MHC_LANES) {
+            const float off = lane == N.lane ? 4.0f : -4.0f;
+            const float zz = ((sh.p[lane] * N.a_pre) + off) + N.b_pre[lane];
+            sh.hp[lane] = 1.0f / (lexpf(-zz) + 1.0f);
+        } else if (lane >= 32 && lane < 32 + MHC_LANES) {
+            const int j = lane - 32;
+            const float off = j == N.lane ? 0.0f : -4.0f;
+            const float zz = ((sh.p[MHC_LANES + j] * N.a_post) + off) + N.b_post[j];
+            sh.p[MHC_COLS + j] = 2.0f / (lexpf(-zz) + 1.0f);
+        }
+    } else if (wave == 1) {
+        const int k = lane & 15;
+        const float z = __builtin_fmaf(sh.p[2 * MHC_LANES + k], N.a_res, N.b_res[k]);
+        const float hr = sinkhorn_lane(z, lane);
+        if (lane < 16) sh.p[MHC_COLS + MHC_LANES + lane] = hr;
+    }
+    __syncthreads();
+    for (int i = t; i < d; i += LT) {
+        float u = sh.xs[i] * sh.hp[0];
+#pragma unroll
+        for (int b = 1; b < MHC_LANES; ++b) u = __builtin_fmaf(sh.xs[b * d + i], sh.hp[b], u);
+        sh.u[i] = u;
+        sh.x1[i] = u;
+        if (N.site >= 0) sh.o[i] = S.ekv[(size_t)N.site * 2 * d + i];
+    }
+    __syncthreads();
+    if (N.site >= 0) {
+        // alpha = sigmoid(dot16(x1 / |x1|, k / |k|) / sqrt(d)); x1 += alpha * conv
+        if (wave == 0) {
+            const float ss = dot16_wave(sh.x1, sh.x1, d, lane);
+            if (lane == 0) sh.r = rinv(ss, d);
+        } else if (wave == 1) {
+            const float ss = dot16_wave(sh.o, sh.o, d, lane);
+            if (lane == 0) sh.r2 = rinv(ss, d);
+        }
+        __syncthreads();
+        for (int i = t; i < d; i += LT) {
+            sh.x2[i] = sh.x1[i] * sh.r;
+            sh.h[i] = sh.o[i] * sh.r2;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const float dd = dot16_wave(sh.x2, sh.h, d, lane);
+            if (lane == 0) sh.r = 1.0f / (lexpf((-dd) / __builtin_sqrtf((float)d)) + 1.0f);
+        }
+        __syncthreads();
+        const float alpha = sh.r;
+        for (int i = t; i < d; i += LT) sh.x1[i] = __builtin_fmaf(S.evals[(size_t)N.site * d + i], alpha, sh.x1[i]);
+        __syncthreads();
+    }
+    // hloc = norm_apply16(x1, rinv(dot16(x1)), norm_in), then A8.
+    if (wave == 0) {
+        const float ss = dot16_wave(sh.x1, sh.x1, d, lane);
+        if (lane == 0) sh.r = rinv(ss, d);
+    }
+    __syncthreads();
+    for (int i = t; i < d; i += LT) {
+        const float tt = sh.x1[i] * sh.r;
+        sh.h[i] = __builtin_fmaf(tt, h2f(N.norm_in[i]), tt);
+    }
+    __syncthreads();
+    const int groups = (d + GROUP - 1) / GROUP;
+    for (int g = wave; g < groups; g += LT / 64) {
+        const int p0 = g * GROUP + lane, p1 = p0 + 64;
+        a8_group(p0 < d ? sh.h[p0] : 0.0f, p1 < d ? sh.h[p1] : 0.0f, lane, in_bits, S.xq_in + (size_t)g * GROUP,
+                 S.sx_in + g);
+    }
+    for (int i = t; i < d; i += LT) {
+        S.u[i] = sh.u[i];
+        S.x1[i] = sh.x1[i];
+    }
+    if (t < MHC_COLS + MHC_LANES + MHC_LANES * MHC_LANES) S.p[t] = sh.p[t];
+}
+
+// The head's input (step.rs:706-728): lane mean, zcn with the f32 final
+// norm, A8.
+__device__ void head_in(const Dims& D, const Globals& G, const SessDev& S, int head_bits, LayerShared& sh) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
+    for (int ch = t; ch < d; ch += LT)
+        sh.h[ch] = (((sh.xs[ch] + sh.xs[d + ch]) + sh.xs[2 * d + ch]) + sh.xs[3 * d + ch]) * 0.25f;
+    __syncthreads();
+    if (wave == 0) {
+        const float ss = dot16_wave(sh.h, sh.h, d, lane);
+        if (lane == 0) sh.r = rinv(ss, d);
+    }
+    __syncthreads();
+    for (int i = t; i < d; i += LT) {
+        const float tt = sh.h[i] * sh.r;
+        sh.x2[i] = __builtin_fmaf(tt, G.final_norm[i], tt);
+    }
+    __syncthreads();
+    const int groups = (d + GROUP - 1) / GROUP;
+    for (int g = wave; g < groups; g += LT / 64) {
+        const int p0 = g * GROUP + lane, p1 = p0 + 64;
+        a8_group(p0 < d ? sh.x2[p0] : 0.0f, p1 < d ? sh.x2[p1] : 0.0f, lane, head_bits, S.xq_in + (size_t)g * GROUP,
+                 S.sx_in + g);
+    }
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int has_prev,
+                                              int has_next, int in_bits, int head_bits) {
+    __shared__ LayerShared sh;
+    const int t = threadIdx.x, d = D.d, nc = MHC_LANES * d;
+    for (int i = t; i < nc; i += LT) sh.xs[i] = S.xs[i];
+    if (has_prev) {
+        for (int i = t; i < d; i += LT) {
+            sh.o[i] = S.o[i];
+            sh.x1[i] = S.x1[i];
+            sh.u[i] = S.u[i];
+        }
+        if (t < 64) sh.p[t] = S.p[t];
+    }
+    __syncthreads();
+    if (has_prev) {
+        layer_out(D, G, P, sh);
+        for (int i = t; i < nc; i += LT) S.xs[i] = sh.xs[i];
+    }
+    if (has_next)
+        layer_in(D, S, N, in_bits, sh);
+    else
+        head_in(D, G, S, head_bits, sh);
+}
+
+hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
+                     int in_bits, int head_bits, hipStream_t s) {
+    const LayerDev none{};
+    hipLaunchKernelGGL(k_layer, dim3(1), dim3(LT), 0, s, D, G, S, prev ? *prev : none, next ? *next : none,
+                       prev ? 1 : 0, next ? 1 : 0, in_bits, head_bits);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ units
+// One wavefront per unit (q heads, k heads, v heads; step.rs:481-556), lane
+// i = element: the causal conv over the current row and the kept history
+// rows (fma from the newest back; a row before position 0 contributes
+// fma(w, 0, v)), the current pre-tap row into the history ring, then for q
+// and k the head zcn16 and RoPE, and for k and v the int8 cache append.
+__global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, LayerDev L, int layer, int p0) {
+    const int unit = threadIdx.x >> 6, i = threadIdx.x & 63;
+    const int nh = D.nh, nkv = D.nkv, qk = D.qk, vd = D.vd;
+    const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd, W = D.W;
+    int start, cw, cc, len;
+    const uint16_t* w;
+    if (unit < nh) {
+        start = unit * qk, cw = qd, cc = unit * qk, w = L.q_taps, len = qk;
+    } else if (unit < nh + nkv) {
+        const int kh = unit - nh;
+        start = qd + kh * qk, cw = kd, cc = kh * qk, w = L.k_taps, len = qk;
+    } else {
+        const int vh = unit - nh - nkv;
+        start = qd + kd + vh * vd, cw = vdim, cc = vh * vd, w = L.v_taps, len = vd;
+    }
+    float* hist = S.hist + (size_t)layer * D.keep * W;
+    float v = 0.0f;
+    if (i < len) {
+        const float cur = S.proj[start + i];
+        v = h2f(w[cc + i]) * cur;
+        for (int j = 1; j < D.taps; ++j) {
+            const float wj = h2f(w[(size_t)j * cw + cc + i]);
+            const float rr = p0 >= j ? hist[(size_t)((p0 - j) % D.keep) * W + start + i] : 0.0f;
+            v = __builtin_fmaf(wj, rr, v);
+        }
+        hist[(size_t)(p0 % D.keep) * W + start + i] = cur;
+    }
+    if (unit < nh + nkv) {
+        const float ss = dot16_lanes(v, qk, i);
+        const float r = rinv(ss, qk);
+        if (i < qk) {
+            const float tt = v * r;
+            v = __builtin_fmaf(tt, h2f((unit < nh ? L.q_norm : L.k_norm)[i]), tt);
+        }
+        const int half = qk / 2, f = i < half ? i : i - half;
+        const float a = __shfl(v, f, 64), b = __shfl(v, f + half, 64);
+        if (i < qk) {
+            const float cs = S.rope_c[f], sn = S.rope_s[f];
+            v = i < half ? __builtin_fmaf(-sn, b, cs * a) : __builtin_fmaf(sn, a, cs * b);
+        }
+    }
+    if (unit < nh) {
+        if (i < qk) S.qbuf[start + i] = v;
+    } else {
+        const float s = wave_quant_scale(i < len ? v : 0.0f);
+        const int8_t q = quant_one(v, 1.0f / s);
+        const size_t lc = (size_t)layer * D.cap;
+        if (unit < nh + nkv) {
+            const int kh = unit - nh;
+            if (i < qk) S.k8[((lc + p0) * nkv + kh) * qk + i] = q;
+            if (i == 0) S.ks[(lc + p0) * nkv + kh] = s;
+        } else {
+            const int vh = unit - nh - nkv;
+            if (i < vd) S.v8t[(((size_t)layer * nkv + vh) * vd + i) * D.cap + p0] = q;
+            if (i == 0) S.vs[(lc + p0) * nkv + vh] = s;
+        }
+    }
+}
+
+hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, hipStream_t s) {
+    const int units = D.nh + 2 * D.nkv;
+    hipLaunchKernelGGL(k_units, dim3(1), dim3(units * 64), 0, s, D, S, L, layer, p0);
+    return hipGetLastError();
+}
+
+// -------------------------------------------------------------- attention
+// attend_head_ref (infer.rs:1871-2007), one workgroup per (query head,
+// key chunk): q as int8 (scale x INV_SQRT_QK), int8 scores
+// (k-scale x dot) x qs for the 4-blocked prefix and (k-scale x qs) x dot
+// for the rest, the chunk max, chunk_exp (nexp over the 4-blocked prefix
+// summed in 8 lane classes, lexpf over the tail, infer.rs:2222-2279), the
+// weights times v-scales as 21-bit digits (digits21, infer.rs:2171-2220)
+// and their exact integer P.V with the int8 values.
+__global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, LayerDev L, int layer, int p0) {
+    const int hh = blockIdx.x, ci = blockIdx.y, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int nkv = D.nkv, qk = D.qk, vd = D.vd, kvh = hh / (D.nh / nkv);
+    const int lo = window_lo(L.window, p0), n = p0 + 1 - lo;
+    int count, chunk;
+    key_chunks(n, nkv, count, chunk);
+    if (ci >= count) return;
+    const int c0 = ci * chunk, len = min(chunk, n - c0), blocked = len / 4 * 4, slot0 = lo + c0;
+    __shared__ alignas(16) int8_t q8[MAX_HEAD_DIM];
+    __shared__ float sc[ATT_CHUNK_MAX];
+    __shared__ int8_t dig[3][ATT_CHUNK_MAX];
+    __shared__ float red[ATT_THREADS / 64];
+    __shared__ float s_qs, s_sum;
+    if (wave == 0) {
+        const float v = lane < qk ? S.qbuf[hh * qk + lane] : 0.0f;
+        const float s = wave_quant_scale(v);
+        if (lane < qk) q8[lane] = quant_one(v, 1.0f / s);
+        if (lane == 0) s_qs = s * bits_f32(0x3e13cd3au);
+    }
+    __syncthreads();
+    const size_t lc = (size_t)layer * D.cap;
+    const float qs = s_qs;
+    float mx = -__builtin_inff();
+    for (int i = t; i < len; i += ATT_THREADS) {
+        const size_t slot = lc + slot0 + i;
+        const int8_t* kr = S.k8 + (slot * nkv + kvh) * qk;
+        int dot = 0;
+        for (int j = 0; j < qk; j += 4)
+            dot = __builtin_amdgcn_sdot4(*(const int*)(kr + j), *(const int*)(q8 + j), dot, false);
+        const float ksc = S.ks[slot * nkv + kvh];
+        const float s = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
+        sc[i] = s;
+        mx = fmaxf(mx, s);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (int i = t; i < len; i += ATT_THREADS) sc[i] = i < blocked ? nexp(sc[i] - mx) : lexpf(sc[i] - mx);
+    __syncthreads();
+    if (wave == 0) {
+        // a[k] over the 8-blocks' first halves plus a trailing 4-block,
+        // b[k] over their second halves; t = a + b; (t0 + t1) + (t2 + t3).
+        float acc = 0.0f;
+        const int nb8 = len / 8;
+        if (lane < 8) {
+            const int k = lane & 3, hi = lane >> 2;
+            for (int b = 0; b < nb8; ++b) acc += sc[b * 8 + hi * 4 + k];
+            if (hi == 0 && len - nb8 * 8 >= 4) acc += sc[nb8 * 8 + k];
+        }
+        const int k = lane & 3;
+        const float tk = __shfl(acc, k, 64) + __shfl(acc, 4 + k, 64);
+        float sum = (__shfl(tk, 0, 64) + __shfl(tk, 1, 64)) + (__shfl(tk, 2, 64) + __shfl(tk, 3, 64));
+        int i = blocked;
+        if (len - i >= 2) {
+            sum = (sc[i] + sum) + sc[i + 1];
+            i += 2;
+        }
+        if (len - i == 1) sum += sc[i];
+        if (lane == 0) s_sum = sum;
+    }
+    __syncthreads();
+    float wmax = 0.0f;
+    for (int i = t; i < len; i += ATT_THREADS) {
+        const float w = sc[i] * S.vs[(lc + slot0 + i) * nkv + kvh];
+        sc[i] = w;
+        wmax = fmaxf(wmax, w);
+    }
+    wmax = wave_max(wmax);
+    __syncthreads();
+    if (lane == 0) red[wave] = wmax;
+    __syncthreads();
+    wmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float qw = bits_f32(0x49fffff8u) / wmax;
+    for (int i = t; i < len; i += ATT_THREADS) {
+        const int32_t wq = (int32_t)roundf(sc[i] * qw);
+        dig[0][i] = (int8_t)(wq >> 14);
+        dig[1][i] = (int8_t)((wq >> 7) & 127);
+        dig[2][i] = (int8_t)(wq & 127);
+    }
+    __syncthreads();
+    const float cw = wmax * bits_f32(0x35000004u);
+    const int dm = t >> 2, part = t & 3;
+    int a = 0, b = 0, c = 0;
+    if (dm < vd) {
+        const int8_t* row = S.v8t + (((size_t)layer * nkv + kvh) * vd + dm) * D.cap + slot0;
+        for (int i = part; i < len; i += 4) {
+            const int v = row[i];
+            a += dig[0][i] * v;
+            b += dig[1][i] * v;
+            c += dig[2][i] * v;
+        }
+    }
+    a += __shfl_xor(a, 1, 64);
+    a += __shfl_xor(a, 2, 64);
+    b += __shfl_xor(b, 1, 64);
+    b += __shfl_xor(b, 2, 64);
+    c += __shfl_xor(c, 1, 64);
+    c += __shfl_xor(c, 2, 64);
+    const size_t pi = (size_t)hh * D.max_chunks + ci;
+    if (dm < vd && part == 0)
+        S.po[pi * vd + dm] = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
+    if (t == 0) {
+        S.pm[pi] = mx;
+        S.psum[pi] = s_sum;
+    }
+}
+
+hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, hipStream_t s) {
+    hipLaunchKernelGGL(k_attend, dim3(D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer, p0);
+    return hipGetLastError();
+}
+
+// The chunk merge (infer.rs:1990-2006), the head gate
+// (att / (nexp(-gate) + 1), step.rs:558-572) and A8 of the heads.
+__global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, int p0, int out_bits) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, vd = D.vd, K = D.nh * vd;
+    __shared__ float att[FWD_MAX_D];
+    const int lo = window_lo(L.window, p0), n = p0 + 1 - lo;
+    int count, chunk;
+    key_chunks(n, D.nkv, count, chunk);
+    if (t < K) {
+        const int hh = t / vd, i = t % vd;
+        const size_t base = (size_t)hh * D.max_chunks;
+        float out;
+        if (count == 1) {
+            const float inv = 1.0f / S.psum[base];
+            out = S.po[base * vd + i] * inv;
+        } else {
+            float big = -1e30f;
+            for (int p = 0; p < count; ++p) big = fmaxf(big, S.pm[base + p]);
+            float acc = 0.0f, total = 0.0f;
+            for (int p = 0; p < count; ++p) {
+                const float w = lexpf(S.pm[base + p] - big);
+                acc = __builtin_fmaf(S.po[(base + p) * vd + i], w, acc);
+                total = __builtin_fmaf(w, S.psum[base + p], total);
+            }
+            const float inv = 1.0f / total;
+            out = acc * inv;
+        }
+        att[t] = out / (nexp(-S.proj[D.W + t]) + 1.0f);
+    }
+    __syncthreads();
+    const int groups = (K + GROUP - 1) / GROUP;
+    for (int g = wave; g < groups; g += LT / 64) {
+        const int q0 = g * GROUP + lane, q1 = q0 + 64;
+        a8_group(q0 < K ? att[q0] : 0.0f, q1 < K ? att[q1] : 0.0f, lane, out_bits, S.xq_att + (size_t)g * GROUP,
+                 S.sx_att + g);
+    }
+}
+
+hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
+                        hipStream_t s) {
+    (void)layer;
+    hipLaunchKernelGGL(k_attn_out, dim3(1), dim3(LT), 0, s, D, S, L, p0, out_bits);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------- argmax
+// argmax (crates/needle-engine/src/generate.rs:42-50): the first maximum.
+__global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, uint32_t* __restrict__ dst) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    float best = -__builtin_inff();
+    int bi = n;
+    for (int i = t; i < n; i += 1024) {
+        const float v = x[i];
+        if (bi == n || v > best) {
+            best = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (oi < n && (bi == n || ov > best || (ov == best && oi < bi))) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    if (lane == 0) {
+        sv[wave] = best;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (si[w] < n && (bi == n || sv[w] > best || (sv[w] == best && si[w] < bi))) {
+                best = sv[w];
+                bi = si[w];
+            }
+        dst[0] = (uint32_t)(bi < n ? bi : 0);
+    }
+}
+
+hipError_t fwd_argmax(const float* logits, int n, uint32_t* dst, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, logits, n, dst);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------- Phi8
+// Phi8::new (infer.rs:850-867): each row requantized to int8 with its own
+// quant_i8 scale.  One workgroup per row.
+__global__ __launch_bounds__(256) void k_phi8(const float* __restrict__ rows, int width, int8_t* __restrict__ q,
+                                              float* __restrict__ scale) {
+    const int r = blockIdx.x, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const float* x = rows + (size_t)r * width;
+    float m = 0.0f;
+    for (int i = t; i < width; i += 256) m = fmaxf(m, fabsf(x[i]));
+    m = wave_max(m);
+    __shared__ float red[4];
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
+    const float inv = 1.0f / s;
+    for (int i = t; i < width; i += 256) q[(size_t)r * width + i] = quant_one(x[i], inv);
+    if (t == 0) scale[r] = s;
+}
+
+hipError_t fwd_phi8(const float* rows, int nrows, int width, int8_t* q, float* scale, hipStream_t s) {
+    if (nrows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(k_phi8, dim3(nrows), dim3(256), 0, s, rows, width, q, scale);
+    return hipGetLastError();
+}
+
+}  // namespace nh

@@ -63,6 +63,8 @@ struct nh_qmat {
     std::vector<uint16_t> h_norms;   // out x groups
 };
 
+struct nh_weights;
+
 struct nh_qact {
     int cap_rows;   // allocated rows (multiple of ACT_PAD)
     int rows;       // rows of the last prep
@@ -100,6 +102,27 @@ __host__ __device__ inline int act_offset(int p, int bits) {
     const int l = d & 3, k = d >> 2;
     return ((l * 4 + k) << 3) + ((j & 1) ? 4 + (j >> 1) : (j >> 1));
 }
+
+// The small per-layer tensors of a .cact layer in their canonical walk
+// order (crates/needle-engine/src/weights.rs:322-371).
+enum SmallKind {
+    S_NORM_IN = 0, S_Q_TAPS, S_K_TAPS, S_V_TAPS, S_Q_NORM, S_K_NORM, S_POST_NORM, S_ATTN_GATE, S_PRE_HADA,
+    S_D1, S_D2, S_B2, S_D3, S_D4, S_KRON0, S_KRON1, S_KRON2, S_KRON3, S_KRON4, S_KRON5, S_COND_V, S_COND_U,
+    SMALL_KINDS
+};
+
+// The non-matmul tensors of an archive widened to f32 (f16 records exactly),
+// as Cursor::next yields them (weights.rs:106-110).
+struct ArchiveSmall {
+    std::vector<std::vector<std::vector<float>>> layer;  // [layer][SmallKind] (empty: absent)
+    std::vector<std::vector<float>> mhc;                  // a_pre, a_post, a_res, b_pre, b_post, b_res
+    std::vector<float> perm1, perm2, final_norm;
+    std::vector<std::vector<float>> etaps;                // per engram site
+};
+
+// nh_weights_load, and with `small` set the small tensors too (an error if
+// one of them is a CQ record).
+int load_archive(const uint8_t* bytes, uint64_t n, nh_weights** w, ArchiveSmall* small);
 
 // Launchers (one per kernel translation unit).
 hipError_t launch_act_prep(const float* x, int rows, int in_dim, int groups, int bits, const uint16_t* norm_scale,

@@ -88,23 +88,6 @@ hipError_t launch_fill(float* p, float v, int n, hipStream_t s) {
 // QMat::row (crates/needle-engine/src/qlinear.rs:309-323): per group
 // cb[code] * norm, then the normalised rotation.  One wavefront per
 // (id, group), two positions per lane.
-// The stored selector of natural position p: 4-bit dword d = p / 8 is
-// dword d / 4 of lane d % 4's 16-byte chunk; 2-bit dword d = p / 16 is
-// dword d / 4 of lane d % 4's 8-byte chunk, field p % 4 of byte (p / 4) % 4.
-template <int BITS>
-__device__ __forceinline__ uint32_t code_sel_at(const void* codes, int tile, int G, int g, int rt, int p) {
-    const size_t ci = ((size_t)tile * G + g) * 64 + rt * 4;
-    if constexpr (BITS == 4) {
-        const int d = p >> 3;
-        const uint32_t* chunk = (const uint32_t*)(reinterpret_cast<const uint4*>(codes) + ci + (d & 3));
-        return (chunk[d >> 2] >> (4 * (p & 7))) & 15u;
-    } else {
-        const int d = p >> 4;
-        const uint32_t* chunk = (const uint32_t*)(reinterpret_cast<const uint2*>(codes) + ci + (d & 3));
-        return (chunk[d >> 2] >> (8 * ((p >> 2) & 3) + 2 * (p & 3))) & 3u;
-    }
-}
-
 template <int BITS>
 __global__ __launch_bounds__(256) void k_rows(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
                                               const float* __restrict__ fsel, const uint32_t* __restrict__ ids,
@@ -115,15 +98,8 @@ __global__ __launch_bounds__(256) void k_rows(const void* __restrict__ codes, co
     const int i = unit / G, g = unit % G;
     const uint32_t row = ids[i];
     const bool ok = row < (uint32_t)out;
-    const uint32_t rr = ok ? row : 0u;
-    const int tile = rr / TILE_ROWS, rt = rr % TILE_ROWS;
-    const float norm = f16_bits_to_f32(norms[(size_t)rr * G + g]);
-    float v0 = fsel[code_sel_at<BITS>(codes, tile, G, g, rt, lane)] * norm;
-    float v1 = fsel[code_sel_at<BITS>(codes, tile, G, g, rt, lane + 64)] * norm;
-    fwht128(v0, v1, lane);
-    const float hs = bits_f32(0x3db504f3u);
-    v0 *= hs;
-    v1 *= hs;
+    float v0, v1;
+    row_group<BITS>(codes, norms, fsel, G, ok ? row : 0u, g, lane, v0, v1);
     if (!ok) v0 = v1 = __builtin_nanf("");
     const int p0 = g * GROUP + lane, p1 = p0 + 64;
     float* o = dst + (size_t)i * in_dim;

@@ -1,0 +1,588 @@
+// The Needle-3 model and its decoding sessions on the GPU: Model::quantized
+// plus the native tables (crates/needle-engine/src/model.rs:248-262,
+// crates/needle-engine/src/infer.rs:869-960), Model::session
+// (model.rs:264-280) with the native state in HBM (NatState,
+// infer.rs:966-1071), and Model::forward over single-token steps
+// (step_native, crates/needle-engine/src/infer/step.rs:171-760).
+//
+// nh_model_load reads the archive with the matmul loader, then uploads the
+// small per-layer weights narrowed to f16 as LayerF16::new does
+// (infer.rs:905-938), the mHC rows requantized per row (Phi8,
+// infer.rs:850-867, dequantized on the device with QMat::row), the RoPE
+// tables powf / sincosf (Tables::new, infer.rs:942-947) and the gate
+// constants.  A session is one HBM arena: residual lanes, KV caches, tap
+// and engram histories, activation buffers and logits.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "../../include/needle_hip.h"
+#include "nh_forward.h"
+#include "nh_internal.h"
+
+namespace {
+
+constexpr size_t ALIGN = 256;
+
+size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int fail(int code, const std::string& msg) {
+    nh::set_error(msg);
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(NH_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define NH_TRY(call, what)                                   \
+    do {                                                     \
+        hipError_t e_ = (call);                              \
+        if (e_ != hipSuccess) return hip_fail(e_, what);     \
+    } while (0)
+
+// f16::from_f32 of the `half` crate: round to nearest even, overflow to
+// infinity, subnormals kept, NaN stays NaN.
+uint16_t f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (exp == 0xff) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u | (man >> 13) : 0u));
+    const int e = (int)exp - 127 + 15;
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        man |= 0x800000u;
+        const int shift = 14 - e;
+        const uint32_t half = 1u << (shift - 1);
+        uint32_t r = man >> shift;
+        const uint32_t rem = man & ((1u << shift) - 1);
+        if (rem > half || (rem == half && (r & 1))) ++r;
+        return (uint16_t)(sign | r);
+    }
+    uint32_t r = ((uint32_t)e << 10) | (man >> 13);
+    const uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (r & 1))) ++r;
+    return (uint16_t)(sign | r);
+}
+
+// Host staging of one device buffer: 256-byte aligned sections.
+struct Arena {
+    std::vector<uint8_t> host;
+    size_t put(const void* p, size_t bytes) {
+        const size_t off = round_up(host.size(), ALIGN);
+        host.resize(off + bytes, 0);
+        if (bytes && p) memcpy(host.data() + off, p, bytes);
+        return off;
+    }
+    size_t reserve(size_t bytes) { return put(nullptr, bytes); }
+};
+
+// A device arena of zeroed sections, laid out before allocation.
+struct Layout {
+    size_t size = 0;
+    size_t take(size_t bytes) {
+        const size_t off = round_up(size, ALIGN);
+        size = off + std::max<size_t>(bytes, 1);
+        return off;
+    }
+};
+
+int key_chunk_count(int n, int nkv) {
+    // key_chunks (infer.rs:2093-2101)
+    int k = std::max(1, 2 * 4 / nkv);
+    int c = (n + 255) / 256;
+    if (k * 64 <= n && c < k) c = k;
+    c = std::max(c, 1);
+    const int chunk = ((n + c - 1) / c + 15) / 16 * 16;
+    return chunk ? (n + chunk - 1) / chunk : 0;
+}
+
+}  // namespace
+
+struct nh_model {
+    nh_weights* w = nullptr;
+    uint32_t header[49];
+    nh::Dims dims{};
+    nh::Globals glob{};
+    nh::BeginArgs begin{};
+    std::vector<nh::LayerDev> layers;
+    std::vector<const nh_qmat*> qkvg, out, ekv;
+    nh_qmat* head = nullptr;  // the embedding's first out_rows rows (shares its memory)
+    int head_bits = 4;
+    void* d_small = nullptr;
+
+    ~nh_model() {
+        if (d_small) hipFree(d_small);
+        delete head;
+        nh_weights_free(w);
+    }
+};
+
+struct nh_session {
+    const nh_model* m = nullptr;
+    nh::Dims dims{};
+    nh::SessDev S{};
+    void* d_buf = nullptr;
+    int len = 0;
+    bool have_logits = false;
+    nh_qact a_in{}, a_att{};
+    std::vector<nh_qact> a_eng;
+
+    ~nh_session() {
+        if (d_buf) hipFree(d_buf);
+    }
+};
+
+namespace {
+
+// The geometry the decode step is written for, from the header and the
+// loaded matrices; an error names the first unsupported property.
+int check_geometry(nh_model* m, const nh::ArchiveSmall& sm) {
+    const uint32_t* h = m->header;
+    nh::Dims& D = m->dims;
+    D.vocab = (int)h[5];
+    D.out_rows = h[6] > 0 ? (int)h[6] : (int)h[5];  // Config::out_rows (config.rs:299-301)
+    D.d = (int)h[7];
+    D.nh = (int)h[8];
+    D.nkv = (int)h[9];
+    D.layers = (int)h[10];
+    D.qk = (int)h[11];
+    D.vd = (int)h[12];
+    D.lanes = (int)h[15];
+    D.taps = (int)h[19];
+    const int window = (int)h[16];
+    const uint64_t gmask = (uint64_t)h[17] | ((uint64_t)h[18] << 32);
+    const int norders = (int)h[26];
+    const int tables = (int)h[22];
+    D.sites = (int)h[31];
+    if (D.lanes != nh::MHC_LANES) return fail(NH_EINVAL, "the decode step is written for 4 mHC lanes");
+    if (D.d <= nh::FWD_MAX_D / 2 || D.d > nh::FWD_MAX_D || D.d % 32 != 0)
+        return fail(NH_EINVAL, "the decode step needs d_model in (512, 1024], a multiple of 32 (hada_n 1024)");
+    if (D.nh <= 0 || D.nkv <= 0 || D.nh % D.nkv != 0 || D.nh + 2 * D.nkv > nh::MAX_UNITS)
+        return fail(NH_EINVAL, "the decode step needs heads + 2 kv heads <= 16, heads a multiple of kv heads");
+    if (D.qk <= 0 || D.qk % 16 != 0 || D.qk > nh::MAX_HEAD_DIM || D.vd <= 0 || D.vd % 4 != 0 ||
+        D.vd > nh::MAX_HEAD_DIM)
+        return fail(NH_EINVAL, "the decode step needs qk a multiple of 16 and vd a multiple of 4, both <= 64");
+    if (D.nh * D.vd > nh::FWD_MAX_D) return fail(NH_EINVAL, "heads x vd above 1024");
+    if (D.layers > 64) return fail(NH_EINVAL, "more than 64 layers");
+    if (D.out_rows <= 0 || D.out_rows > D.vocab) return fail(NH_EINVAL, "out_vocab above the vocabulary");
+    const int qd = D.nh * D.qk, kd = D.nkv * D.qk, vdim = D.nkv * D.vd;
+    D.W = qd + kd + vdim;
+    D.nq = D.W + D.nh * D.vd;
+    D.keep = D.taps > 1 ? D.taps - 1 : 1;
+    if (D.taps <= 0) return fail(NH_EINVAL, "the decode step needs qkv conv taps");
+    // engram geometry (config.rs:273-288 with heads = tables / orders, cact.rs:191)
+    if (D.sites > nh::MAX_SITES || norders > 4) return fail(NH_EINVAL, "corrupt engram geometry");
+    if (D.sites > 0) {
+        if (norders <= 0 || tables <= 0 || tables % norders != 0 || tables > nh::MAX_TABLES)
+            return fail(NH_EINVAL, "engram tables do not split over the orders");
+        D.eheads = tables / norders;
+        D.ntab = tables;
+        D.sub = D.d / (norders * D.eheads);
+        if (D.sub != nh::GROUP || D.ntab * D.sub > D.d)
+            return fail(NH_EINVAL, "the decode step needs engram sub-tables of 128");
+        D.seed_stride = h[25] > 0 ? (int)h[25] : D.eheads;
+        D.slots = (int)h[20];
+        if (D.slots <= 0) return fail(NH_EINVAL, "engram_slots is zero");
+        int dil = 1;
+        for (int i = 0; i < norders; ++i) {
+            D.orders[i] = (int)h[27 + i];
+            if (D.orders[i] <= 0 || D.orders[i] > 64) return fail(NH_EINVAL, "engram order out of range");
+            dil = std::max(dil, D.orders[i]);
+        }
+        D.dilation = dil;  // Config::engram_dilation (config.rs:286-288)
+    }
+    // matrices
+    const nh_qmat* emb = nullptr;
+    nh_weights_get(m->w, NH_W_EMBEDDING, 0, &emb);
+    if (emb->m.in_dim != D.d || emb->m.out != D.vocab) return fail(NH_EINVAL, "embedding shape");
+    for (int l = 0; l < D.layers; ++l) {
+        const nh_qmat *q = nullptr, *o = nullptr, *p = nullptr;
+        nh_weights_get(m->w, NH_W_QKVG, l, &q);
+        nh_weights_get(m->w, NH_W_OUT, l, &o);
+        nh_weights_get(m->w, NH_W_PHI, l, &p);
+        if (q->m.out != D.nq || q->m.in_dim != D.d) return fail(NH_EINVAL, "q|k|v|gate shape");
+        if (o->m.out != D.d || o->m.in_dim != D.nh * D.vd) return fail(NH_EINVAL, "out projection shape");
+        if (p->m.out != nh::MHC_COLS || p->m.in_dim != nh::MHC_LANES * D.d) return fail(NH_EINVAL, "mHC phi shape");
+        m->qkvg.push_back(q);
+        m->out.push_back(o);
+    }
+    for (int s = 0; s < D.sites; ++s) {
+        const nh_qmat *t = nullptr, *kv = nullptr;
+        nh_weights_get(m->w, NH_W_ENGRAM_TABLE, s, &t);
+        nh_weights_get(m->w, NH_W_ENGRAM_KV, s, &kv);
+        if (t->m.in_dim != D.sub || t->m.out != D.ntab * D.slots) return fail(NH_EINVAL, "engram table shape");
+        if (kv->m.in_dim != D.d || kv->m.out != 2 * D.d) return fail(NH_EINVAL, "engram key|value shape");
+        const int site = (int)h[32 + s];
+        if (site < 0 || site >= D.layers) return fail(NH_EINVAL, "engram site past the last layer");
+        m->ekv.push_back(kv);
+    }
+    // small tensors: the lengths the step reads
+    const size_t d = D.d;
+    auto need = [&](const std::vector<float>& v, size_t n, const char* what) -> int {
+        if (v.size() < n) return fail(NH_EINVAL, std::string(what) + " is shorter than the step reads");
+        return NH_OK;
+    };
+    for (int l = 0; l < D.layers; ++l) {
+        const auto& L = sm.layer[l];
+        int rc = NH_OK;
+        if (!rc) rc = need(L[nh::S_NORM_IN], d, "norm_in");
+        if (!rc && D.taps > 0) rc = need(L[nh::S_Q_TAPS], (size_t)D.taps * qd, "q taps");
+        if (!rc && D.taps > 0) rc = need(L[nh::S_K_TAPS], (size_t)D.taps * kd, "k taps");
+        if (!rc && D.taps > 0) rc = need(L[nh::S_V_TAPS], (size_t)D.taps * vdim, "v taps");
+        if (!rc) rc = need(L[nh::S_Q_NORM], D.qk, "q_norm");
+        if (!rc) rc = need(L[nh::S_K_NORM], D.qk, "k_norm");
+        if (!rc) rc = need(L[nh::S_POST_NORM], d, "post_attn_norm");
+        if (!rc) rc = need(L[nh::S_PRE_HADA], d, "pre_hada_norm");
+        if (!rc) rc = need(L[nh::S_D1], d, "d1");
+        if (!rc) rc = need(L[nh::S_D2], nh::HADA_N, "d2");
+        if (!rc) rc = need(L[nh::S_B2], nh::HADA_N, "b2");
+        if (!rc) rc = need(L[nh::S_D3], nh::HADA_N, "d3");
+        if (!rc) rc = need(L[nh::S_D4], d, "d4");
+        if (!rc) rc = need(L[nh::S_COND_V], d * nh::COND_RANK, "cond_v");
+        if (rc) return rc;
+    }
+    const size_t L = D.layers;
+    if (need(sm.mhc[0], L, "mhc a_pre") || need(sm.mhc[1], L, "mhc a_post") || need(sm.mhc[2], L, "mhc a_res") ||
+        need(sm.mhc[3], L * 4, "mhc b_pre") || need(sm.mhc[4], L * 4, "mhc b_post") ||
+        need(sm.mhc[5], L * 16, "mhc b_res") || need(sm.final_norm, d, "final_norm"))
+        return NH_EINVAL;
+    for (const auto* perm : {&sm.perm1, &sm.perm2})
+        for (float v : *perm)
+            if (!(v >= 0.0f && v < (float)nh::HADA_N) || v != floorf(v))
+                return fail(NH_EINVAL, "Hadamard permutation entry out of range");
+    for (int s = 0; s < D.sites; ++s)
+        if (need(sm.etaps[s], (size_t)nh::ENGRAM_TAPS * d, "engram taps")) return NH_EINVAL;
+    (void)window;
+    (void)gmask;
+    return NH_OK;
+}
+
+int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
+    nh::Dims& D = m->dims;
+    const uint32_t* h = m->header;
+    const int window = (int)h[16];
+    const uint64_t gmask = (uint64_t)h[17] | ((uint64_t)h[18] << 32);
+    const int nc = nh::MHC_LANES * D.d;
+    Arena A;
+    struct LayerOff {
+        size_t t[nh::SMALL_KINDS];
+        size_t phi_q, phi_s;
+    };
+    std::vector<LayerOff> off(D.layers);
+    auto put16 = [&](const std::vector<float>& v) {
+        std::vector<uint16_t> b(v.size());
+        for (size_t i = 0; i < v.size(); ++i) b[i] = f32_to_f16(v[i]);
+        return A.put(b.data(), b.size() * 2);
+    };
+    for (int l = 0; l < D.layers; ++l) {
+        for (int k = 0; k < nh::SMALL_KINDS; ++k) off[l].t[k] = put16(sm.layer[l][k]);
+        off[l].phi_q = A.reserve((size_t)nh::MHC_COLS * nc);
+        off[l].phi_s = A.reserve(nh::MHC_COLS * 4);
+    }
+    const size_t o_final = A.put(sm.final_norm.data(), (size_t)D.d * 4);
+    std::vector<int32_t> p1(nh::HADA_N), p2(nh::HADA_N);
+    for (int i = 0; i < nh::HADA_N; ++i) p1[i] = (int32_t)sm.perm1[i], p2[i] = (int32_t)sm.perm2[i];
+    const size_t o_p1 = A.put(p1.data(), p1.size() * 4), o_p2 = A.put(p2.data(), p2.size() * 4);
+    // Tables::new (infer.rs:942-947): freq = lpowf(theta, i * (-2 / qk)),
+    // (sd, cd) = sincosf(freq), both f64 libm results rounded once as the
+    // reference computes them off Apple targets (infer.rs:84-101).
+    float theta;
+    memcpy(&theta, &h[48], 4);
+    const int half = D.qk / 2;
+    std::vector<float> sd(half), cd(half);
+    const float coef = -2.0f / (float)D.qk;
+    for (int i = 0; i < half; ++i) {
+        const float f = (float)pow((double)theta, (double)((float)i * coef));
+        double sv, cv;
+        sincos((double)f, &sv, &cv);
+        sd[i] = (float)sv;
+        cd[i] = (float)cv;
+    }
+    const size_t o_sd = A.put(sd.data(), half * 4), o_cd = A.put(cd.data(), half * 4);
+    std::vector<float> etaps;
+    for (int s = 0; s < D.sites; ++s)
+        etaps.insert(etaps.end(), sm.etaps[s].begin(), sm.etaps[s].begin() + (size_t)nh::ENGRAM_TAPS * D.d);
+    const size_t o_et = A.put(etaps.data(), etaps.size() * 4);
+    const size_t o_ids = A.reserve(nh::MHC_COLS * 4);
+
+    NH_TRY(hipMalloc(&m->d_small, A.host.size()), "model tables allocation");
+    NH_TRY(hipMemcpy(m->d_small, A.host.data(), A.host.size(), hipMemcpyHostToDevice), "model tables upload");
+    uint8_t* base = (uint8_t*)m->d_small;
+
+    // Phi8 per layer: QMat::row of the fused pre|post|res rows, then quant_i8.
+    {
+        std::vector<uint32_t> ids(nh::MHC_COLS);
+        for (int i = 0; i < nh::MHC_COLS; ++i) ids[i] = i;
+        NH_TRY(hipMemcpy(base + o_ids, ids.data(), ids.size() * 4, hipMemcpyHostToDevice), "phi ids");
+        float* rows = nullptr;
+        NH_TRY(hipMalloc(&rows, (size_t)nh::MHC_COLS * nc * 4), "phi rows");
+        hipError_t e = hipSuccess;
+        for (int l = 0; l < D.layers && e == hipSuccess; ++l) {
+            const nh_qmat* phi = nullptr;
+            nh_weights_get(m->w, NH_W_PHI, l, &phi);
+            e = nh::launch_rows(phi, (const uint32_t*)(base + o_ids), nh::MHC_COLS, rows, nullptr);
+            if (e == hipSuccess)
+                e = nh::fwd_phi8(rows, nh::MHC_COLS, nc, (int8_t*)(base + off[l].phi_q), (float*)(base + off[l].phi_s),
+                                 nullptr);
+        }
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        hipFree(rows);
+        NH_TRY(e, "Phi8");
+    }
+
+    m->glob.final_norm = (const float*)(base + o_final);
+    m->glob.perm1 = (const int32_t*)(base + o_p1);
+    m->glob.perm2 = (const int32_t*)(base + o_p2);
+    m->glob.sd = (const float*)(base + o_sd);
+    m->glob.cd = (const float*)(base + o_cd);
+    m->glob.etaps = (const float*)(base + o_et);
+
+    std::vector<int> site_of(D.layers, -1);
+    for (int s = 0; s < D.sites; ++s) site_of[h[32 + s]] = s;
+    for (int l = 0; l < D.layers; ++l) {
+        nh::LayerDev L{};
+        auto p16 = [&](int k) { return (const uint16_t*)(base + off[l].t[k]); };
+        for (int k = 0; k < 6; ++k) L.kron[k] = p16(nh::S_KRON0 + k);
+        L.cond_v = p16(nh::S_COND_V), L.cond_u = p16(nh::S_COND_U);
+        L.d1 = p16(nh::S_D1), L.d2 = p16(nh::S_D2), L.b2 = p16(nh::S_B2), L.d3 = p16(nh::S_D3), L.d4 = p16(nh::S_D4);
+        L.norm_in = p16(nh::S_NORM_IN), L.post_norm = p16(nh::S_POST_NORM), L.pre_hada = p16(nh::S_PRE_HADA);
+        L.q_taps = p16(nh::S_Q_TAPS), L.k_taps = p16(nh::S_K_TAPS), L.v_taps = p16(nh::S_V_TAPS);
+        L.q_norm = p16(nh::S_Q_NORM), L.k_norm = p16(nh::S_K_NORM);
+        L.phi_q = (const int8_t*)(base + off[l].phi_q);
+        L.phi_s = (const float*)(base + off[l].phi_s);
+        L.a_pre = sm.mhc[0][l], L.a_post = sm.mhc[1][l], L.a_res = sm.mhc[2][l];
+        // The attention output gate 1 / (lexpf(-attn_gate) + 1) (step.rs:582).
+        const float g = sm.layer[l][nh::S_ATTN_GATE][0];
+        L.ga = 1.0f / ((float)exp((double)-g) + 1.0f);
+        for (int j = 0; j < 4; ++j) L.b_pre[j] = sm.mhc[3][l * 4 + j], L.b_post[j] = sm.mhc[4][l * 4 + j];
+        for (int j = 0; j < 16; ++j) L.b_res[j] = sm.mhc[5][l * 16 + j];
+        L.site = site_of[l];
+        L.lane = l % D.lanes;
+        L.window = (window > 0 && !((gmask >> l) & 1)) ? window : 0;
+        m->layers.push_back(L);
+    }
+
+    const nh_qmat* emb = nullptr;
+    nh_weights_get(m->w, NH_W_EMBEDDING, 0, &emb);
+    m->begin.emb = {emb->d_codes, emb->d_norms, emb->d_fsel, emb->m.out, emb->m.groups, emb->m.bits};
+    for (int s = 0; s < D.sites; ++s) {
+        const nh_qmat* t = nullptr;
+        nh_weights_get(m->w, NH_W_ENGRAM_TABLE, s, &t);
+        m->begin.tab[s] = {t->d_codes, t->d_norms, t->d_fsel, t->m.out, t->m.groups, t->m.bits};
+        m->begin.eng_bits[s] = m->ekv[s]->m.bits;
+    }
+    m->head = new nh_qmat();
+    m->head->m = emb->m;
+    m->head->m.out = D.out_rows;
+    m->head->m.out_pad = (int)round_up(D.out_rows, nh::TILE_ROWS);
+    m->head->d_codes = emb->d_codes;
+    m->head->d_norms = emb->d_norms;
+    m->head->d_fsel = emb->d_fsel;
+    m->head_bits = emb->m.bits;
+    return NH_OK;
+}
+
+// One decode step at position s->len; the head when `logits`.
+int step(nh_session* s, bool logits, hipStream_t st) {
+    const nh_model* m = s->m;
+    const nh::Dims& D = s->dims;
+    const nh::SessDev& S = s->S;
+    const int p0 = s->len;
+    NH_TRY(nh::fwd_begin(D, m->glob, S, m->begin, p0, st), "step begin");
+    for (int e = 0; e < D.sites; ++e)
+        NH_TRY(nh::launch_gemv(m->ekv[e], &s->a_eng[e], S.ekv + (size_t)e * 2 * D.d, 0, nullptr, st), "engram kv");
+    NH_TRY(nh::fwd_engram_hist(D, m->glob, S, p0, st), "engram history");
+    for (int l = 0; l < D.layers; ++l) {
+        const nh::LayerDev* prev = l > 0 ? &m->layers[l - 1] : nullptr;
+        NH_TRY(nh::fwd_layer(D, m->glob, S, prev, &m->layers[l], m->qkvg[l]->m.bits, 0, st), "layer");
+        NH_TRY(nh::launch_gemv(m->qkvg[l], &s->a_in, S.proj, 0, nullptr, st), "q|k|v|gate");
+        NH_TRY(nh::fwd_units(D, S, m->layers[l], l, p0, st), "units");
+        NH_TRY(nh::fwd_attend(D, S, m->layers[l], l, p0, st), "attend");
+        NH_TRY(nh::fwd_attn_out(D, S, m->layers[l], l, p0, m->out[l]->m.bits, st), "attention out");
+        NH_TRY(nh::launch_gemv(m->out[l], &s->a_att, S.o, 0, nullptr, st), "out");
+    }
+    const nh::LayerDev* last = D.layers > 0 ? &m->layers[D.layers - 1] : nullptr;
+    NH_TRY(nh::fwd_layer(D, m->glob, S, last, nullptr, 0, m->head_bits, st), "head input");
+    if (logits) NH_TRY(nh::launch_gemv(m->head, &s->a_in, S.logits, 0, nullptr, st), "head");
+    s->len = p0 + 1;
+    s->have_logits = logits;
+    return NH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nh_model_load(const uint8_t* bytes, uint64_t n, nh_model** out) {
+    if (!out) return fail(NH_EINVAL, "null argument");
+    *out = nullptr;
+    nh::ArchiveSmall sm;
+    nh_weights* w = nullptr;
+    int rc = nh::load_archive(bytes, n, &w, &sm);
+    if (rc != NH_OK) return rc;
+    auto* m = new (std::nothrow) nh_model;
+    if (!m) {
+        nh_weights_free(w);
+        return fail(NH_ENOMEM, "out of host memory");
+    }
+    m->w = w;
+    nh_weights_header(w, m->header, 49);
+    rc = check_geometry(m, sm);
+    if (rc == NH_OK) rc = build_model(m, sm);
+    if (rc != NH_OK) {
+        delete m;
+        return rc;
+    }
+    *out = m;
+    return NH_OK;
+}
+
+int nh_model_free(nh_model* m) {
+    delete m;
+    return NH_OK;
+}
+
+int nh_model_weights(const nh_model* m, const nh_weights** w) {
+    if (!m || !w) return fail(NH_EINVAL, "null argument");
+    *w = m->w;
+    return NH_OK;
+}
+
+int nh_model_out_rows(const nh_model* m) {
+    if (!m) return fail(NH_EINVAL, "null model");
+    return m->dims.out_rows;
+}
+
+int nh_session_new(const nh_model* m, int cap, nh_session** out) {
+    if (!m || !out) return fail(NH_EINVAL, "null argument");
+    *out = nullptr;
+    if (cap <= 0 || cap > (1 << 20)) return fail(NH_EINVAL, "session capacity out of range");
+    auto* s = new (std::nothrow) nh_session;
+    if (!s) return fail(NH_ENOMEM, "out of host memory");
+    s->m = m;
+    nh::Dims& D = s->dims;
+    D = m->dims;
+    D.cap = cap;
+    int mc = 1;
+    for (int n = 1; n <= cap; ++n) mc = std::max(mc, key_chunk_count(n, D.nkv));
+    D.max_chunks = mc;
+    const size_t d = D.d, L = D.layers, c = cap, E = D.sites;
+    const int Gd = (D.d + nh::GROUP - 1) / nh::GROUP, Ga = (D.nh * D.vd + nh::GROUP - 1) / nh::GROUP;
+    Layout Y;
+    const size_t o_xs = Y.take(4 * d * 4), o_u = Y.take(d * 4), o_x1 = Y.take(d * 4), o_p = Y.take(64 * 4);
+    const size_t o_proj = Y.take((size_t)D.nq * 4), o_q = Y.take((size_t)D.nh * D.qk * 4), o_o = Y.take(d * 4);
+    const size_t o_ekv = Y.take(E * 2 * d * 4), o_ev = Y.take(E * d * 4);
+    const size_t o_lg = Y.take(round_up(D.out_rows, nh::PANEL_ROWS) * 4);
+    const size_t o_rc = Y.take(D.qk / 2 * 4), o_rs = Y.take(D.qk / 2 * 4), o_tok = Y.take(c * 4);
+    const size_t o_po = Y.take((size_t)D.nh * mc * D.vd * 4), o_pm = Y.take((size_t)D.nh * mc * 4),
+                 o_ps = Y.take((size_t)D.nh * mc * 4);
+    const size_t o_hist = Y.take(L * D.keep * D.W * 4);
+    const size_t o_k8 = Y.take(L * c * D.nkv * D.qk), o_ks = Y.take(L * c * D.nkv * 4);
+    const size_t o_v8 = Y.take(L * D.nkv * D.vd * c), o_vs = Y.take(L * c * D.nkv * 4);
+    const size_t o_e8 = Y.take(E * c * d), o_es = Y.take(E * c * (d / 32) * 4);
+    const size_t o_xi = Y.take((size_t)Gd * nh::GROUP), o_si = Y.take((size_t)Gd * 4);
+    const size_t o_xa = Y.take((size_t)Ga * nh::GROUP), o_sa = Y.take((size_t)Ga * 4);
+    const size_t o_xe = Y.take(E * Gd * nh::GROUP), o_se = Y.take(E * Gd * 4);
+    const size_t o_am = Y.take(16);
+    hipError_t e = hipMalloc(&s->d_buf, Y.size);
+    if (e == hipSuccess) e = hipMemset(s->d_buf, 0, Y.size);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        delete s;
+        return fail(NH_ENOMEM, std::string("session allocation: ") + hipGetErrorString(e));
+    }
+    uint8_t* b = (uint8_t*)s->d_buf;
+    nh::SessDev& S = s->S;
+    S.xs = (float*)(b + o_xs), S.u = (float*)(b + o_u), S.x1 = (float*)(b + o_x1), S.p = (float*)(b + o_p);
+    S.proj = (float*)(b + o_proj), S.qbuf = (float*)(b + o_q), S.o = (float*)(b + o_o);
+    S.ekv = (float*)(b + o_ekv), S.evals = (float*)(b + o_ev), S.logits = (float*)(b + o_lg);
+    S.rope_c = (float*)(b + o_rc), S.rope_s = (float*)(b + o_rs), S.tokens = (uint32_t*)(b + o_tok);
+    S.po = (float*)(b + o_po), S.pm = (float*)(b + o_pm), S.psum = (float*)(b + o_ps);
+    S.hist = (float*)(b + o_hist), S.k8 = (int8_t*)(b + o_k8), S.ks = (float*)(b + o_ks);
+    S.v8t = (int8_t*)(b + o_v8), S.vs = (float*)(b + o_vs), S.ev8 = (int8_t*)(b + o_e8), S.evs = (float*)(b + o_es);
+    S.xq_in = (int8_t*)(b + o_xi), S.sx_in = (float*)(b + o_si);
+    S.xq_att = (int8_t*)(b + o_xa), S.sx_att = (float*)(b + o_sa);
+    S.xq_eng = (int8_t*)(b + o_xe), S.sx_eng = (float*)(b + o_se);
+    S.argmax = (int32_t*)(b + o_am);
+    auto view = [](int8_t* xq, float* sx, int in_dim, int groups) {
+        nh_qact a{};
+        a.cap_rows = 1;
+        a.rows = 1;
+        a.in_dim = in_dim;
+        a.groups = groups;
+        a.d_xq = xq;
+        a.d_sx = sx;
+        return a;
+    };
+    s->a_in = view(S.xq_in, S.sx_in, D.d, Gd);
+    s->a_att = view(S.xq_att, S.sx_att, D.nh * D.vd, Ga);
+    for (int i = 0; i < D.sites; ++i)
+        s->a_eng.push_back(view(S.xq_eng + (size_t)i * Gd * nh::GROUP, S.sx_eng + (size_t)i * Gd, D.d, Gd));
+    *out = s;
+    return NH_OK;
+}
+
+int nh_session_free(nh_session* s) {
+    delete s;
+    return NH_OK;
+}
+
+int nh_session_len(const nh_session* s) {
+    if (!s) return fail(NH_EINVAL, "null session");
+    return s->len;
+}
+
+int nh_session_reset(nh_session* s) {
+    if (!s) return fail(NH_EINVAL, "null session");
+    s->len = 0;
+    s->have_logits = false;
+    return NH_OK;
+}
+
+int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* stream) {
+    if (!s || (n > 0 && !toks) || n < 0) return fail(NH_EINVAL, "bad arguments");
+    if (!nh::ready()) return fail(NH_ESTATE, "nh_init has not been called");
+    if (s->len + n > s->dims.cap) return fail(NH_EINVAL, "the tokens do not fit the session's capacity");
+    for (int i = 0; i < n; ++i)
+        if (toks[i] >= (uint32_t)s->dims.vocab) return fail(NH_EINVAL, "token id outside the vocabulary");
+    if (n == 0) return NH_OK;
+    hipStream_t st = (hipStream_t)stream;
+    NH_TRY(hipMemcpyAsync(s->S.tokens + s->len, toks, (size_t)n * 4, hipMemcpyHostToDevice, st), "tokens");
+    NH_TRY(hipStreamSynchronize(st), "tokens");
+    for (int i = 0; i < n; ++i)
+        if (int rc = step(s, i + 1 == n, st)) return rc;
+    if (logits)
+        NH_TRY(hipMemcpyAsync(logits, s->S.logits, (size_t)s->dims.out_rows * 4, hipMemcpyDeviceToDevice, st),
+               "logits");
+    return NH_OK;
+}
+
+int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, void* stream) {
+    if (!s || steps < 0 || (steps > 0 && !out)) return fail(NH_EINVAL, "bad arguments");
+    if (!nh::ready()) return fail(NH_ESTATE, "nh_init has not been called");
+    if (!s->have_logits) return fail(NH_EINVAL, "no logits to pick from (nh_forward a prompt first)");
+    if (s->len + steps > s->dims.cap) return fail(NH_EINVAL, "the steps do not fit the session's capacity");
+    hipStream_t st = (hipStream_t)stream;
+    const int len0 = s->len;
+    for (int i = 0; i < steps; ++i) {
+        NH_TRY(nh::fwd_argmax(s->S.logits, s->dims.out_rows, s->S.tokens + s->len, st), "argmax");
+        if (int rc = step(s, true, st)) return rc;
+    }
+    if (logits)
+        NH_TRY(hipMemcpyAsync(logits, s->S.logits, (size_t)s->dims.out_rows * 4, hipMemcpyDeviceToDevice, st),
+               "logits");
+    if (steps > 0) {
+        NH_TRY(hipMemcpyAsync(out, s->S.tokens + len0, (size_t)steps * 4, hipMemcpyDeviceToHost, st), "tokens");
+        NH_TRY(hipStreamSynchronize(st), "tokens");
+    }
+    return NH_OK;
+}
+
+}  // extern "C"

@@ -52,6 +52,16 @@ SIGNATURES = {
     "nh_weights_count": (I, [P, I]),
     "nh_weights_get": (I, [P, I, I, P]),
     "nh_weights_bytes": (C.c_int64, [P]),
+    "nh_model_load": (I, [P, C.c_uint64, P]),
+    "nh_model_free": (I, [P]),
+    "nh_model_weights": (I, [P, P]),
+    "nh_model_out_rows": (I, [P]),
+    "nh_session_new": (I, [P, I, P]),
+    "nh_session_free": (I, [P]),
+    "nh_session_len": (I, [P]),
+    "nh_session_reset": (I, [P]),
+    "nh_forward": (I, [P, P, I, P, P]),
+    "nh_generate_greedy": (I, [P, I, P, P, P]),
     "nh_normal": (I, [C.c_uint32, C.c_uint32, C.c_uint64, P]),
     "nh_split": (I, [C.c_uint32, C.c_uint32, P]),
 }
@@ -318,8 +328,9 @@ class QWeights:
     pre|post|res rows fused); engram_tables and engram_kv (key|value fused)
     per site."""
 
-    def __init__(self, h):
+    def __init__(self, h, owner=None):
         self.h = h
+        self._owner = owner  # a Model that owns these weights (not freed here)
         words = (C.c_uint32 * 49)()
         _check(_lib.nh_weights_header(h, C.cast(words, C.c_void_p), 49))
         self.header_words = list(words)
@@ -361,8 +372,82 @@ class QWeights:
         return int(n)
 
     def __del__(self):
-        if getattr(self, "h", None) and _lib is not None:
+        if getattr(self, "h", None) and _lib is not None and getattr(self, "_owner", None) is None:
             _lib.nh_weights_free(self.h)
+        self.h = None
+
+
+class Model:
+    """Model::quantized with the native tables (crates/needle-engine/src/model.rs:248-262,
+    crates/needle-engine/src/infer.rs:869-960) for the decode step, in HBM."""
+
+    def __init__(self, h):
+        self.h = h
+        self.out_rows = _check(_lib.nh_model_out_rows(h))
+
+    @property
+    def weights(self) -> "QWeights":
+        """The model's matmul weights (they keep the model alive)."""
+        w = C.c_void_p()
+        _check(_lib.nh_model_weights(self.h, C.byref(w)))
+        return QWeights(w.value, owner=self)
+
+    @classmethod
+    def from_archive(cls, data) -> "Model":
+        """nh_model_load over archive bytes, borrowed for the call only."""
+        lib = init()
+        buf = np.frombuffer(data, dtype=np.uint8) if isinstance(data, (bytes, bytearray)) else \
+            np.ascontiguousarray(data, dtype=np.uint8)
+        h = C.c_void_p()
+        _check(lib.nh_model_load(_hptr(buf), buf.nbytes, C.byref(h)))
+        return cls(h.value)
+
+    def session(self, cap: int = 4096) -> "Session":
+        """Model::session (model.rs:264-280) with room for `cap` positions."""
+        return Session(self, cap)
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.nh_model_free(self.h)
+        self.h = None
+
+
+class Session:
+    """Session (crates/needle-engine/src/model.rs:55-69): one sequence's
+    decoding state (KV caches, tap and engram histories) in HBM."""
+
+    def __init__(self, model: Model, cap: int):
+        self.model = model
+        h = C.c_void_p()
+        _check(_lib.nh_session_new(model.h, int(cap), C.byref(h)))
+        self.h = h.value
+        self.cap = cap
+
+    def __len__(self):
+        return _check(_lib.nh_session_len(self.h))
+
+    def reset(self):
+        _check(_lib.nh_session_reset(self.h))
+
+    def forward(self, tokens, stream=None) -> torch.Tensor:
+        """Model::forward with Outputs::LastLogits (model.rs:304-306), one
+        step_native per token: the last token's logits [out_rows] (device)."""
+        toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(-1))
+        logits = torch.empty(self.model.out_rows, dtype=torch.float32, device="cuda")
+        _check(_lib.nh_forward(self.h, _hptr(toks), toks.size, _dptr(logits), _stream(stream)))
+        return logits
+
+    def generate_greedy(self, steps: int, stream=None):
+        """The greedy loop of generate (crates/needle-engine/src/generate.rs:87-139)
+        on the device: (token ids [steps], the last step's logits)."""
+        out = np.zeros(max(1, steps), dtype=np.uint32)
+        logits = torch.empty(self.model.out_rows, dtype=torch.float32, device="cuda")
+        _check(_lib.nh_generate_greedy(self.h, int(steps), _hptr(out), _dptr(logits), _stream(stream)))
+        return out[:steps].copy(), logits
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.nh_session_free(self.h)
         self.h = None
 
 

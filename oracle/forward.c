@@ -8,12 +8,17 @@
  *
  * Scope: Model::step_native for one token with attend = None (no attention
  * span: every position keeps its own KV slot, slot_of(p) = p), Outputs =
- * logits, no cells, no rollback.  The libm functions the reference takes
- * from the Rust `libm` crate (expf, exp, powf, sincosf) are glibc's here:
- * equal to them except for rare last-ulp differences, so results that
- * pass through them are parity unpinned at that boundary.
+ * logits, no cells, no rollback.
+ *
+ * libm: off Apple targets the reference computes its f32 functions in f64
+ * with the Rust `libm` crate (0.2.16, Cargo.lock:647-650) and rounds once
+ * (infer.rs:76-101): lexpf = (f32)exp((f64)x), lpowf = (f32)pow, sincosf =
+ * the f64 sincos rounded; lexp = exp.  Here the f64 functions are glibc's.
+ * Both are accurate to under an f64 ulp, so the f32 results agree unless an
+ * f32 rounding boundary falls between the two f64 results (about 2^-29 of
+ * calls): the step is parity unpinned at that boundary only.
  */
-#define _GNU_SOURCE /* sincosf */
+#define _GNU_SOURCE /* sincos */
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -42,6 +47,16 @@ static float bits_f(uint32_t b) {
 #define HN (NB * NB)
 
 /* ---------------------------------------------------------------- helpers */
+
+/* lexpf / lpowf / sincosf off Apple targets (infer.rs:84-101). */
+static float lexpf(float x) { return (float)exp((double)x); }
+static float lpowf(float x, float y) { return (float)pow((double)x, (double)y); }
+static void lsincosf(float x, float* s, float* c) {
+    double sd, cd;
+    sincos((double)x, &sd, &cd);
+    *s = (float)sd;
+    *c = (float)cd;
+}
 
 /* nexp (infer.rs:353-367). */
 float nf_nexp(float x) {
@@ -108,7 +123,7 @@ void nf_cond_weights(const float* h2, size_t d, const uint16_t* cond_v, float ou
         lg[k] = ((acc[2][k] + acc[3][k]) + acc[1][k]) + acc[0][k];
         m = fmaxf(m, lg[k]);
     }
-    for (int k = 0; k < 8; ++k) e[k] = expf(lg[k] - m);
+    for (int k = 0; k < 8; ++k) e[k] = lexpf(lg[k] - m);
     const float sum = e[7] + ((e[6] + (e[5] + e[4])) + ((e[3] + e[2]) + (e[1] + e[0])));
     const float inv = 1.0f / sum;
     for (int k = 0; k < 8; ++k) out[k] = e[k] * inv;
@@ -188,14 +203,14 @@ float nf_chunk_exp(float* s, size_t l, float m) {
     for (int k = 0; k < 4; ++k) t[k] = a[k] + b[k];
     float sum = (t[0] + t[1]) + (t[2] + t[3]);
     if (l - i >= 2) {
-        const float e0 = expf(s[i] - m), e1 = expf(s[i + 1] - m);
+        const float e0 = lexpf(s[i] - m), e1 = lexpf(s[i + 1] - m);
         s[i] = e0;
         s[i + 1] = e1;
         sum = (e0 + sum) + e1;
         i += 2;
     }
     if (l - i == 1) {
-        const float e = expf(s[i] - m);
+        const float e = lexpf(s[i] - m);
         s[i] = e;
         sum += e;
     }
@@ -287,15 +302,15 @@ nf_model* nf_model_new(const nf_config* c) {
     m->etaps = (float**)calloc((size_t)c->sites + 1, sizeof(float*));
     for (int l = 0; l < 64; ++l) m->site_of_layer[l] = -1;
     for (int s = 0; s < c->sites; ++s) m->site_of_layer[c->site_layers[s]] = s;
-    /* Tables::new: freq = powf(theta, i * (-2 / qk)), then sincosf. */
+    /* Tables::new (infer.rs:942-947): freq = lpowf(theta, i * (-2 / qk)), then sincosf. */
     const int half = c->qk / 2;
     m->freq = (float*)malloc(sizeof(float) * half);
     m->sd = (float*)malloc(sizeof(float) * half);
     m->cd = (float*)malloc(sizeof(float) * half);
     const float coef = -2.0f / (float)c->qk;
     for (int i = 0; i < half; ++i) {
-        m->freq[i] = powf(c->rope_theta, (float)i * coef);
-        sincosf(m->freq[i], &m->sd[i], &m->cd[i]);
+        m->freq[i] = lpowf(c->rope_theta, (float)i * coef);
+        lsincosf(m->freq[i], &m->sd[i], &m->cd[i]);
     }
     return m;
 }
@@ -486,7 +501,7 @@ static void attend_head(const nf_model* m, const nf_session* s, int l, const flo
         for (int p = 0; p < np; ++p) big = fmaxf(big, pm[p]);
         float acc[64] = {0}, total = 0.0f;
         for (int p = 0; p < np; ++p) {
-            const float w = expf(pm[p] - big);
+            const float w = lexpf(pm[p] - big);
             for (size_t i = 0; i < vd; ++i) acc[i] = fmaf(po[p][i], w, acc[i]);
             total = fmaf(w, psum[p], total);
         }
@@ -577,7 +592,7 @@ int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int n
             sn[f] = fmaf(m->sd[f], s->rope_c[f], m->cd[f] * s->rope_s[f]);
         }
     } else {
-        for (int f = 0; f < half; ++f) sincosf(m->freq[f] * (float)p0, &sn[f], &cs[f]);
+        for (int f = 0; f < half; ++f) lsincosf(m->freq[f] * (float)p0, &sn[f], &cs[f]);
     }
     memcpy(s->rope_c, cs, sizeof(float) * half);
     memcpy(s->rope_s, sn, sizeof(float) * half);
@@ -614,7 +629,7 @@ int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int n
             for (int j = 0; j < 4; ++j) {
                 const float off = j == lane ? 4.0f : -4.0f;
                 const float zz = ((p[j] * Lw->a_pre) + off) + Lw->b_pre[j];
-                hp[j] = 1.0f / (expf(-zz) + 1.0f);
+                hp[j] = 1.0f / (lexpf(-zz) + 1.0f);
             }
             for (int i = 0; i < d; ++i) u[i] = xs[i] * hp[0];
             for (int b = 1; b < 4; ++b)
@@ -627,7 +642,7 @@ int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int n
             const float* kr = ekv + (size_t)site * 2 * d;
             const float rx = cq_rinv(cq_dot16(x1, x1, d), d), rkk = cq_rinv(cq_dot16(kr, kr, d), d);
             for (int i = 0; i < d; ++i) ea[i] = x1[i] * rx, eb[i] = kr[i] * rkk;
-            const float alpha = 1.0f / (expf((-cq_dot16(ea, eb, d)) / sqrtf((float)d)) + 1.0f);
+            const float alpha = 1.0f / (lexpf((-cq_dot16(ea, eb, d)) / sqrtf((float)d)) + 1.0f);
             for (int i = 0; i < d; ++i) x1[i] = fmaf(evals[(size_t)site * d + i], alpha, x1[i]);
         }
         /* (c)-(d) input norm, A8, q|k|v|gate */
@@ -699,7 +714,7 @@ int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int n
             cq_qact_free(a);
         }
         /* (k) post block and the Hadamard MLP */
-        const float ga = 1.0f / (expf(-Lw->attn_gate) + 1.0f);
+        const float ga = 1.0f / (lexpf(-Lw->attn_gate) + 1.0f);
         cq_zcn16(o, Lw->post_norm, d, on);
         for (int i = 0; i < d; ++i) x2[i] = fmaf(on[i], ga, x1[i]);
         cq_zcn16(x2, Lw->pre_hada, d, h2);
@@ -725,7 +740,7 @@ int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int n
         for (int j = 0; j < 4; ++j) {
             const float off = j == lane ? 0.0f : -4.0f;
             const float zz = ((p[n + j] * Lw->a_post) + off) + Lw->b_post[j];
-            hpost[j] = 2.0f / (expf(-zz) + 1.0f);
+            hpost[j] = 2.0f / (lexpf(-zz) + 1.0f);
         }
         for (int k = 0; k < 16; ++k) zres[k] = fmaf(p[2 * n + k], Lw->a_res, Lw->b_res[k]);
         nf_sinkhorn64(zres, hres);

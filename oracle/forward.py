@@ -235,6 +235,8 @@ class Session:
         return _lib().nf_session_len(self.s)
 
     def __del__(self):
-        if getattr(self, "s", None) and lib is not None:
+        # At interpreter exit the model may be finalized first; its session
+        # memory then goes with the process.
+        if getattr(self, "s", None) and lib is not None and getattr(self.f, "m", None):
             _lib().nf_session_free(self.f.m, self.s)
-            self.s = None
+        self.s = None
