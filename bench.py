@@ -244,6 +244,88 @@ def needle3_products(nh, torch):
             "prefill_products_tok_s": round(seq * 1e3 / pre_ms, 1)}
 
 
+DECODE_PROMPT, DECODE_STEPS = 118, 64
+
+
+def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
+    """The full Needle-3 decode (crates/needle-core/src/config.rs:61-100:
+    20 layers, d 768, vocab 16384, 5 engram sites) from random-init weights
+    0.02*N(0,1) through CQ-W4 (needle_hip.archive.random_needle3, seed 0):
+    a prompt of 118 uniform random token ids fed one step_native per token,
+    then 64 greedy decode steps on the device (argmax, step, no host round
+    trip), the KV cache and every activation in HBM.  decode_tok_s counts
+    the 64 greedy steps over their HIP-event time on the launch stream.
+
+    The CPU leg runs the oracle's step_native (oracle/forward.c, OpenMP over
+    the products' rows) on the same archive and tokens, for as many steps
+    as fit the time bound, and checks its logits' argmax against every
+    device pick it reaches."""
+    import numpy as np
+
+    from needle_hip import archive
+
+    t0 = time.perf_counter()
+    data = archive.random_needle3(nh, seed=0)
+    build_s = time.perf_counter() - t0
+    model = nh.Model.from_archive(data)
+    vocab = model.out_rows
+    prompt = np.random.default_rng(0).integers(0, vocab, DECODE_PROMPT).astype(np.uint32)
+    sess = model.session(DECODE_PROMPT + DECODE_STEPS)
+    progress(f"Needle-3 archive built in {build_s:.1f} s ({len(data) / 2**20:.1f} MiB)")
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    runs = []
+    picks = None
+    for r in range(4):  # the first run warms up
+        sess.reset()
+        torch.cuda.synchronize()
+        ev[0].record(stream)
+        sess.forward(prompt)
+        ev[1].record(stream)
+        picks, _ = sess.generate_greedy(DECODE_STEPS)
+        ev[2].record(stream)
+        torch.cuda.synchronize()
+        if r > 0:
+            runs.append((ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])))
+    prompt_ms = min(a for a, _ in runs)
+    decode_ms = min(b for _, b in runs)
+    sites, layers = 5, 20
+    out = {"workload": "Needle-3 random-init decode: 118 random prompt tokens (one step each), then 64 greedy "
+                       "steps on the device",
+           "prompt_tokens": DECODE_PROMPT, "decode_steps": DECODE_STEPS,
+           "decode_tok_s": round(DECODE_STEPS * 1e3 / decode_ms, 1),
+           "decode_ms_per_token": round(decode_ms / DECODE_STEPS, 4),
+           "prompt_tok_s": round(DECODE_PROMPT * 1e3 / prompt_ms, 1),
+           "runs": len(runs), "launches_per_token": 2 + sites + 6 * layers + 3,
+           "first_picks": [int(t) for t in picks[:8]]}
+    progress(f"Needle-3 decode: {out['decode_ms_per_token'] * 1e3:.1f} us per token")
+    if with_cpu:
+        import oracle as o
+        from oracle import forward
+
+        f = forward.Forward(data)
+        ses = f.session(DECODE_PROMPT + DECODE_STEPS)
+        t1 = time.perf_counter()
+        for t in prompt:
+            last = ses.step(int(t))
+        t_prompt = time.perf_counter() - t1
+        agree, steps, t2 = 0, 0, time.perf_counter()
+        for t in picks:
+            agree += int(int(np.argmax(last)) == int(t))
+            last = ses.step(int(t))
+            steps += 1
+            if time.perf_counter() - t2 >= cpu_seconds:
+                break
+        t_dec = time.perf_counter() - t2
+        out["cpu_baseline"] = {"value": round(steps / t_dec, 2), "unit": "tok/s", "cores": o.default_threads(),
+                               "kind": "port",
+                               "sample": f"the oracle's step_native: the 118-token prompt ({t_prompt:.1f} s), then "
+                                         f"{steps} of the 64 decode steps fed the device's picks ({t_dec:.1f} s)"}
+        out["parity"] = {"greedy_picks_checked": steps, "oracle_argmax_agrees": agree}
+        out["gpu_over_cpu"] = round(out["decode_tok_s"] / out["cpu_baseline"]["value"], 1)
+    return out
+
+
 def gemm_shape(spec: str, launches: int, nh, torch):
     """One prefill product M x K x N (seeded as the sweep), `launches` eager
     launches timed with HIP events on the launch stream: the command the
@@ -365,6 +447,8 @@ def main():
         progress("GEMM sweep done")
         line["needle3_products"] = needle3_products(nh, torch)
         progress("Needle-3 products done")
+        line["needle3_decode"] = needle3_decode(nh, torch, args.cpu_seconds * 2, not args.no_cpu)
+        progress("Needle-3 decode done")
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(gpu, args.cpu_seconds)
         line["cpu_baseline"]["gpu_over_cpu"] = round(gpu["gbs"] / line["cpu_baseline"]["value"], 1)

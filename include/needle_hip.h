@@ -49,6 +49,10 @@ int nh_init(int device);
 const char* nh_last_error(void);
 /* Library ABI version (major*100 + minor). */
 int nh_version(void);
+/* quant::codebook(bits, 128) (crates/needle-core/src/quant.rs:52-68): the
+ * f32 centroids of a code width (2, 3, 4; 5 = ternary) into out[16];
+ * returns their count. */
+int nh_codebook(int bits, float* out);
 
 /* ---- matrices (QMat, qlinear.rs:43-61) --------------------------------- */
 /* QMat::from_cq (qlinear.rs:220-236) over a .cact CQ blob as CqView holds

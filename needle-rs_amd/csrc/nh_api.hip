@@ -99,6 +99,12 @@ static int codebook2(bool ternary, float* cb) {
     return 4;
 }
 
+// quant.rs:20-29 (LM3): the 3-bit centroids, only written into archive
+// codebook blocks (no 3-bit matmul records are read).
+static const uint64_t LM3_BITS[8] = {0xc00121468f3c6b81ull, 0xbff556e7125deacaull, 0xbfe7f2e0f9d592abull,
+                                     0xbfce6e4509e1aa2cull, 0x3fd000bb25e4dfa5ull, 0x3fe82dc469b936a5ull,
+                                     0x3ff568607ac227c5ull, 0x40012e5beccc8fdaull};
+
 // int8_codebook (qlinear.rs:211-216): scale = amax * K127, values
 // round-half-away(v * (1 / scale)) saturated.
 static void int8_codebook(const float* cb, int n, int8_t* cb8, float* scale) {
@@ -353,6 +359,25 @@ using namespace nh;
 extern "C" {
 
 int nh_version(void) { return 100; }
+
+int nh_codebook(int bits, float* out) {
+    if (!out) return fail(NH_EINVAL, "null output");
+    switch (bits) {
+        case 2: return codebook2(false, out);
+        case 3: {
+            const double s = std::sqrt(128.0);
+            for (int i = 0; i < 8; ++i) {
+                double c;
+                memcpy(&c, &LM3_BITS[i], 8);
+                out[i] = (float)(c / s);
+            }
+            return 8;
+        }
+        case 4: codebook4(out); return 16;
+        case 5: return codebook2(true, out);
+        default: return fail(NH_EINVAL, "no CQ codebook for this width");
+    }
+}
 
 const char* nh_last_error(void) { return g_err.c_str(); }
 

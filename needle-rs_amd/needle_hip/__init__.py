@@ -52,6 +52,7 @@ SIGNATURES = {
     "nh_weights_count": (I, [P, I]),
     "nh_weights_get": (I, [P, I, I, P]),
     "nh_weights_bytes": (C.c_int64, [P]),
+    "nh_codebook": (I, [I, P]),
     "nh_model_load": (I, [P, C.c_uint64, P]),
     "nh_model_free": (I, [P]),
     "nh_model_weights": (I, [P, P]),
@@ -463,6 +464,13 @@ def head_logits(embedding: QMat, h: torch.Tensor, out_rows: int) -> torch.Tensor
     """Model::head_logits (crates/needle-engine/src/infer.rs:1135-1141)."""
     a = QAct.new(h, 1, h.numel(), embedding.act_bits())
     return embedding.matmul(a)[0, :out_rows]
+
+
+def codebook(bits: int) -> np.ndarray:
+    """quant::codebook(bits, 128) (crates/needle-core/src/quant.rs:52-68)."""
+    out = np.zeros(16, dtype=np.float32)
+    n = _check(load_library().nh_codebook(int(bits), _hptr(out)))
+    return out[:n].copy()
 
 
 # ------------------------------------------------------------- seeded inputs

@@ -173,3 +173,11 @@ def test_session_errors(nh):
     with pytest.raises(nh.NeedleHipError, match="d_model"):
         nh.Model.from_archive(archive(small, seed=17))
     torch.cuda.synchronize()
+
+
+def test_product_archive_writer(nh):
+    say("the product's random-init archive writer, decoded against the oracle")
+    from needle_hip import archive as W
+    g = W.Needle3(vocab=300, num_layers=2, engram_slots=64, engram_sites=(1,), global_layers=(0,), sliding_window=16)
+    data = W.random_needle3(nh, g, seed=3)
+    run_pair(nh, data, o.random_tokens(12, g.vocab, seed=8), 16, "written")
