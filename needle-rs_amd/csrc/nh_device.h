@@ -6,6 +6,10 @@
 
 #include "nh_internal.h"
 
+// Wavefront reductions of the device library (DPP sequences).
+extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
+extern "C" __device__ __attribute__((const)) int __ockl_wfred_add_i32(int);
+
 namespace nh {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -113,11 +117,9 @@ __device__ __forceinline__ void fwht128(float& v0, float& v1, int lane) {
     v1 = a - b;
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
+// The maximum over the 64 lanes (v_max_f32 through the DPP reduction of
+// the device library; exact, order-free for non-NaN inputs).
+__device__ __forceinline__ float wave_max(float v) { return __ockl_wfred_max_f32(v); }
 
 // `(v * inv).round().clamp(-128, 127) as i8` (crates/needle-engine/src/qlinear.rs:137-139).
 __device__ __forceinline__ int8_t quant_one(float v, float inv) {

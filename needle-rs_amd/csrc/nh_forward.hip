@@ -73,7 +73,19 @@ __device__ __forceinline__ float dot16_wave(const float* x, const float* y, int 
     float a = 0.0f;
     if (lane < 16) {
         const int chunks = n / 16;
-        for (int c = 0; c < chunks; ++c) a = __builtin_fmaf(x[c * 16 + lane], y[c * 16 + lane], a);
+        int c = 0;
+        // batches of 16 chunks: the loads issue together, then the chain
+        for (; c + 16 <= chunks; c += 16) {
+            float xv[16], yv[16];
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                xv[u] = x[(c + u) * 16 + lane];
+                yv[u] = y[(c + u) * 16 + lane];
+            }
+#pragma unroll
+            for (int u = 0; u < 16; ++u) a = __builtin_fmaf(xv[u], yv[u], a);
+        }
+        for (; c < chunks; ++c) a = __builtin_fmaf(x[c * 16 + lane], y[c * 16 + lane], a);
     }
     const int l = lane & 3;
     const float a0 = __shfl(a, l, 64), a1 = __shfl(a, 4 + l, 64), a2 = __shfl(a, 8 + l, 64),
@@ -231,17 +243,30 @@ hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, in
 }
 
 // -------------------------------------------------------------- the layer
+// One workgroup of 1024 threads; thread t owns element t of every d- and
+// hada_n-long vector (d <= 1024 = hada_n) and elements t + 1024 k of the
+// 4 d residual lanes.  Every global read is issued at the start: the
+// Kronecker factors and the cond_v / cond_u tables land in LDS, the
+// elementwise weights and this wavefront's Phi8 rows in registers, so the
+// serial chains (dot16, cond_weights, mix8) wait on LDS only.
 namespace {
+
+constexpr int MIX_T = 256;             // threads of one mix8 (4 outputs each)
+constexpr int BT_STRIDE = HADA_NB + 1;  // padded row of a transposed mix8 output
 
 struct LayerShared {
     float xs[MHC_LANES * FWD_MAX_D];
-    float o[FWD_MAX_D];
+    float o[FWD_MAX_D];   // attention output, later the engram key row
     float x1[FWD_MAX_D];
-    float u[FWD_MAX_D];
     float x2[FWD_MAX_D];
     float h[FWD_MAX_D];
-    float A[HADA_N], B[HADA_N], C[HADA_N];
+    alignas(16) float A[HADA_N];
+    alignas(16) float B[HADA_NB * BT_STRIDE];
+    alignas(16) float C[HADA_N];
     alignas(16) int8_t nx8[MHC_LANES * FWD_MAX_D];
+    alignas(16) uint16_t kron[6][HADA_N];
+    alignas(16) uint16_t cond_v[FWD_MAX_D * COND_RANK];
+    alignas(16) uint16_t cond_u[COND_RANK * HADA_N];
     float red[LT / 64];
     float p[64];
     float wk[COND_RANK];
@@ -249,35 +274,428 @@ struct LayerShared {
     float r, r2;
 };
 
-__device__ __forceinline__ float block_max(float v, float* red) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    v = wave_max(v);
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float m = red[0];
-    for (int i = 1; i < (int)(blockDim.x >> 6); ++i) m = fmaxf(m, red[i]);
-    return m;
-}
-
 // mix8 (infer.rs:2343-2380), portable branch: out[r][c] =
-// sum_j ct[j][r] * rows[j][c] as an fma chain from j = 0 (transposed: stored
-// at out[c][r]); rows r < rows_limit (a tile prefix).  One output per thread.
-template <bool CT_HALF, bool ROWS_HALF>
-__device__ __forceinline__ void mix8(bool transpose, const void* ct, const void* rows, float* out, int rows_limit) {
-    const int t = threadIdx.x, r = t >> 5, c = t & 31;
-    if (r >= rows_limit) return;
-    float o = 0.0f;
-#pragma unroll 8
+// sum_j ct[j][r] * rows[j][c], each output an fma chain from j = 0.  Thread
+// u < 256 computes r = u / 8 and c = 4 (u % 8) .. + 3, so each step reads
+// one ct value and four row values.
+// Transposed (ct = an f16 factor, rows = f32 [32][32]): stored at
+// out[c * 33 + r].
+__device__ __forceinline__ void mix8_t(int u, const uint16_t* ct, const float* rows, float* out) {
+    const int r = u >> 3, c0 = (u & 7) * 4;
+    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+#pragma unroll
     for (int j = 0; j < HADA_NB; ++j) {
-        const float a = CT_HALF ? h2f(((const uint16_t*)ct)[j * HADA_NB + r]) : ((const float*)ct)[j * HADA_NB + r];
-        const float b = ROWS_HALF ? h2f(((const uint16_t*)rows)[j * HADA_NB + c])
-                                  : ((const float*)rows)[j * HADA_NB + c];
-        o = __builtin_fmaf(a, b, o);
+        const float a = h2f(ct[j * HADA_NB + r]);
+        const float4 b = *reinterpret_cast<const float4*>(rows + j * HADA_NB + c0);
+        o0 = __builtin_fmaf(a, b.x, o0);
+        o1 = __builtin_fmaf(a, b.y, o1);
+        o2 = __builtin_fmaf(a, b.z, o2);
+        o3 = __builtin_fmaf(a, b.w, o3);
     }
-    out[transpose ? c * HADA_NB + r : r * HADA_NB + c] = o;
+    out[(c0 + 0) * BT_STRIDE + r] = o0;
+    out[(c0 + 1) * BT_STRIDE + r] = o1;
+    out[(c0 + 2) * BT_STRIDE + r] = o2;
+    out[(c0 + 3) * BT_STRIDE + r] = o3;
 }
 
+// Plain (ct = the f32 output of mix8_t, rows = an f16 factor): out[r][c],
+// rows r < rows_limit.
+__device__ __forceinline__ void mix8_n(int u, const float* ct, const uint16_t* rows, float* out, int rows_limit) {
+    const int r = u >> 3, c0 = (u & 7) * 4;
+    if (r >= rows_limit) return;
+    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < HADA_NB; ++j) {
+        const float a = ct[j * BT_STRIDE + r];
+        const uint2 b = *reinterpret_cast<const uint2*>(rows + j * HADA_NB + c0);
+        o0 = __builtin_fmaf(a, h2f((uint16_t)(b.x & 0xffffu)), o0);
+        o1 = __builtin_fmaf(a, h2f((uint16_t)(b.x >> 16)), o1);
+        o2 = __builtin_fmaf(a, h2f((uint16_t)(b.y & 0xffffu)), o2);
+        o3 = __builtin_fmaf(a, h2f((uint16_t)(b.y >> 16)), o3);
+    }
+    *reinterpret_cast<float4*>(out + r * HADA_NB + c0) = make_float4(o0, o1, o2, o3);
+}
+
+// 16-byte copies of n bytes from global to LDS by the whole block (n a
+// multiple of 16, both ends 16-byte aligned).
+__device__ __forceinline__ void stage16(void* dst, const void* src, int n) {
+    for (int i = threadIdx.x; i < n / 16; i += LT)
+        reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+}
+
+// The previous layer's inputs and weights a thread needs, read up front.
+struct OutRegs {
+    float o, x1, u, pn, ph, d1, d2, b2, d3, d4;
+    int p1, p2;
+};
+
+__device__ __forceinline__ OutRegs load_out(const Dims& D, const Globals& G, const SessDev& S, const LayerDev& P,
+                                            LayerShared& sh) {
+    const int t = threadIdx.x, d = D.d;
+    OutRegs q{};
+    for (int k = 0; k < 6; ++k) stage16(sh.kron[k], P.kron[k], HADA_N * 2);
+    stage16(sh.cond_v, P.cond_v, d * COND_RANK * 2);
+    stage16(sh.cond_u, P.cond_u, COND_RANK * HADA_N * 2);
+    if (t < d) {
+        q.o = S.o[t];
+        q.x1 = S.x1[t];
+        q.u = S.u[t];
+        q.pn = h2f(P.post_norm[t]);
+        q.ph = h2f(P.pre_hada[t]);
+        q.d1 = h2f(P.d1[t]);
+        q.d4 = h2f(P.d4[t]);
+    }
+    q.d2 = h2f(P.d2[t]);
+    q.b2 = h2f(P.b2[t]);
+    q.d3 = h2f(P.d3[t]);
+    q.p1 = G.perm1[t];
+    q.p2 = G.perm2[t];
+    if (t < 64) sh.p[t] = S.p[t];
+    return q;
+}
+
+// cond_weights (infer.rs:1640-1656) by wavefront 0: lane 8 jm + k carries
+// acc[jm][k] = fma(h2[j], cond_v[j][k], .) over j = jm, jm + 4, ... in
+// batches of 32 steps; then the softmax of the combined logits.
+__device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int lane, float* wk) {
+    const int k = lane & 7, jm = lane >> 3;
+    float a = 0.0f;
+    if (lane < 32) {
+        int j = jm;
+        for (; j + 4 * 31 < d; j += 4 * 32) {
+            float hv[32], cv[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) {
+                hv[u] = sh.h[j + 4 * u];
+                cv[u] = h2f(sh.cond_v[(j + 4 * u) * 8 + k]);
+            }
+#pragma unroll
+            for (int u = 0; u < 32; ++u) a = __builtin_fmaf(hv[u], cv[u], a);
+        }
+        for (; j < d; j += 4) a = __builtin_fmaf(sh.h[j], h2f(sh.cond_v[j * 8 + k]), a);
+    }
+    const float a0 = __shfl(a, k, 64), a1 = __shfl(a, 8 + k, 64), a2 = __shfl(a, 16 + k, 64),
+                a3 = __shfl(a, 24 + k, 64);
+    const float lg = ((a2 + a3) + a1) + a0;
+    float m = lg;
+    m = fmaxf(m, quad_xor1(m));
+    m = fmaxf(m, quad_xor2(m));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    const float e = lexpf(lg - m);
+    float ev[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ev[i] = __shfl(e, i, 64);
+    const float sum = ev[7] + ((ev[6] + (ev[5] + ev[4])) + ((ev[3] + ev[2]) + (ev[1] + ev[0])));
+    const float inv = 1.0f / sum;
+    if (lane < 8) wk[lane] = e * inv;
+}
+
+// The Hadamard MLP and mHC write of layer P (step.rs:600-705).
+__device__ void layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, LayerShared& sh) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
+    // mix8 runs on waves 4..7 (threads 256..511), beside cond_weights on wave 0
+    const bool mixer = t >= MIX_T && t < 2 * MIX_T;
+    const int mu = t - MIX_T;
+    // on = zcn16(o, post_norm); x2 = fma(on, sigmoid(attn_gate), x1)
+    if (wave == 0) {
+        const float ss = dot16_wave(sh.o, sh.o, d, lane);
+        if (lane == 0) sh.r = rinv(ss, d);
+    }
+    __syncthreads();
+    float x2 = 0.0f;
+    if (t < d) {
+        const float tt = q.o * sh.r;
+        const float on = __builtin_fmaf(tt, q.pn, tt);
+        x2 = __builtin_fmaf(on, P.ga, q.x1);
+        sh.x2[t] = x2;
+    }
+    __syncthreads();
+    // h2 = zcn16(x2, pre_hada); z = h2 * d1 zero-padded to hada_n
+    if (wave == 0) {
+        const float ss = dot16_wave(sh.x2, sh.x2, d, lane);
+        if (lane == 0) sh.r = rinv(ss, d);
+    }
+    __syncthreads();
+    float h2 = 0.0f;
+    if (t < d) {
+        const float tt = x2 * sh.r;
+        h2 = __builtin_fmaf(tt, q.ph, tt);
+        sh.h[t] = h2;
+    }
+    sh.A[t] = t < d ? h2 * q.d1 : 0.0f;
+    __syncthreads();
+    if (wave == 0) cond_weights(sh, d, lane, sh.wk);
+    if (mixer) mix8_t(mu, sh.kron[0], sh.A, sh.B);
+    __syncthreads();
+    if (mixer) mix8_n(mu, sh.B, sh.kron[1], sh.C, HADA_NB);
+    __syncthreads();
+    {
+        float cond = 1.0f;
+#pragma unroll
+        for (int k = 0; k < COND_RANK; ++k) cond = __builtin_fmaf(h2f(sh.cond_u[k * HADA_N + t]), sh.wk[k], cond);
+        float zs = __builtin_fmaf(sh.C[q.p1], cond * q.d2, q.b2);
+        zs = zs / (nexp(-zs) + 1.0f);
+        sh.A[t] = zs;
+    }
+    __syncthreads();
+    if (mixer) mix8_t(mu, sh.kron[2], sh.A, sh.B);
+    __syncthreads();
+    if (mixer) mix8_n(mu, sh.B, sh.kron[3], sh.C, HADA_NB);
+    __syncthreads();
+    sh.A[t] = sh.C[q.p2] * q.d3;
+    __syncthreads();
+    if (mixer) mix8_t(mu, sh.kron[4], sh.A, sh.B);
+    __syncthreads();
+    if (mixer) mix8_n(mu, sh.B, sh.kron[5], sh.C, d / HADA_NB / 8 * 8);
+    __syncthreads();
+    // The mHC write: y = (x2 + t3 * d4) - u; lane a = y hpost[a] + sum_b
+    // hres[a][b] old[b] as an fma chain over b.
+    if (t < d) {
+        const float* hpost = sh.p + MHC_COLS;
+        const float* hres = sh.p + MHC_COLS + MHC_LANES;
+        const float y = (x2 + sh.C[t] * q.d4) - q.u;
+        float old[MHC_LANES];
+#pragma unroll
+        for (int b = 0; b < MHC_LANES; ++b) old[b] = sh.xs[b * d + t];
+#pragma unroll
+        for (int a = 0; a < MHC_LANES; ++a) {
+            float v = y * hpost[a];
+#pragma unroll
+            for (int b = 0; b < MHC_LANES; ++b) v = __builtin_fmaf(old[b], hres[a * MHC_LANES + b], v);
+            sh.xs[a * d + t] = v;
+        }
+    }
+    __syncthreads();
+}
+
+// The next layer's weights a thread needs, read up front: its norm scale,
+// engram key / conv element, and its wavefront's Phi8 rows (rows wave and
+// wave + 16, 16 bytes at lane + 64 j of each, j < 4: rows of up to 4096).
+constexpr int PHI_CHUNKS = MHC_LANES * FWD_MAX_D / 16 / 64;
+struct InRegs {
+    float norm, kr, ev, ps0, ps1;
+    uint4 r0[PHI_CHUNKS], r1[PHI_CHUNKS];
+};
+
+__device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const LayerDev& N) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d, nc = MHC_LANES * d;
+    InRegs q{};
+    if (t < d) {
+        q.norm = h2f(N.norm_in[t]);
+        if (N.site >= 0) {
+            q.kr = S.ekv[(size_t)N.site * 2 * d + t];
+            q.ev = S.evals[(size_t)N.site * d + t];
+        }
+    }
+    const int per = nc / 16;  // uint4 per row
+    if (wave < MHC_COLS) {
+        const uint4* row = reinterpret_cast<const uint4*>(N.phi_q + (size_t)wave * nc);
+#pragma unroll
+        for (int j = 0; j < PHI_CHUNKS; ++j)
+            if (lane + 64 * j < per) q.r0[j] = row[lane + 64 * j];
+        q.ps0 = N.phi_s[wave];
+    }
+    if (wave + LT / 64 < MHC_COLS) {
+        const uint4* row = reinterpret_cast<const uint4*>(N.phi_q + (size_t)(wave + LT / 64) * nc);
+#pragma unroll
+        for (int j = 0; j < PHI_CHUNKS; ++j)
+            if (lane + 64 * j < per) q.r1[j] = row[lane + 64 * j];
+        q.ps1 = N.phi_s[wave + LT / 64];
+    }
+    return q;
+}
+
+__device__ __forceinline__ int dot_row(const uint4* r, const int8_t* x8, int per, int lane) {
+    const uint4* xv = reinterpret_cast<const uint4*>(x8);
+    int acc = 0;
+#pragma unroll
+    for (int j = 0; j < PHI_CHUNKS; ++j) {
+        const int i = lane + 64 * j;
+        if (i < per) {
+            const uint4 b = xv[i];
+            acc = __builtin_amdgcn_sdot4((int)r[j].x, (int)b.x, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)r[j].y, (int)b.y, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)r[j].z, (int)b.z, acc, false);
+            acc = __builtin_amdgcn_sdot4((int)r[j].w, (int)b.w, acc, false);
+        }
+    }
+    return __ockl_wfred_add_i32(acc);
+}
+
+// The mHC read, engram gate, input norm and A8 of layer N
+// (step.rs:400-479).  The post and residual gates of the layer (hpost,
+// the Sinkhorn hres) are computed beside its units (fwd_units), off this
+// kernel's path.
+__device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, const InRegs& q, int in_bits,
+                         LayerShared& sh) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d, nc = MHC_LANES * d;
+    // max |xs| beside the dot16 chain: rounding is monotonic, so
+    // max_i |xs_i * r| = max_i |xs_i| * r for r > 0.
+    {
+        float m = 0.0f;
+        for (int i = t; i < nc; i += LT) m = fmaxf(m, fabsf(sh.xs[i]));
+        m = wave_max(m);
+        if (lane == 0) sh.red[wave] = m;
+    }
+    if (wave == 0) {
+        const float ss = dot16_wave(sh.xs, sh.xs, nc, lane);
+        if (lane == 0) sh.r = rinv(ss, nc);
+    }
+    __syncthreads();
+    const float r = sh.r;
+    float m = sh.red[0];
+#pragma unroll
+    for (int i = 1; i < LT / 64; ++i) m = fmaxf(m, sh.red[i]);
+    m = m * r;
+    const float sx = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
+    const float inv = 1.0f / sx;
+    for (int i = t; i < nc; i += LT) sh.nx8[i] = quant_one(sh.xs[i] * r, inv);
+    __syncthreads();
+    // Phi8 rows: p[k] = (sx * s_k) * idot(phi_q[k], nx8)
+    {
+        const int per = nc / 16;
+        if (wave < MHC_COLS) {
+            const int acc = dot_row(q.r0, sh.nx8, per, lane);
+            if (lane == 0) sh.p[wave] = (sx * q.ps0) * (float)acc;
+        }
+        if (wave + LT / 64 < MHC_COLS) {
+            const int acc = dot_row(q.r1, sh.nx8, per, lane);
+            if (lane == 0) sh.p[wave + LT / 64] = (sx * q.ps1) * (float)acc;
+        }
+    }
+    __syncthreads();
+    // The pre gate hp (sigmoid).
+    if (wave == 0 && lane < MHC_LANES) {
+        const float off = lane == N.lane ? 4.0f : -4.0f;
+        const float zz = ((sh.p[lane] * N.a_pre) + off) + N.b_pre[lane];
+        sh.hp[lane] = 1.0f / (lexpf(-zz) + 1.0f);
+    }
+    __syncthreads();
+    float u = 0.0f, x1 = 0.0f;
+    if (t < d) {
+        u = sh.xs[t] * sh.hp[0];
+#pragma unroll
+        for (int b = 1; b < MHC_LANES; ++b) u = __builtin_fmaf(sh.xs[b * d + t], sh.hp[b], u);
+        x1 = u;
+        sh.x1[t] = x1;
+        if (N.site >= 0) sh.o[t] = q.kr;
+    }
+    __syncthreads();
+    if (N.site >= 0) {
+        // alpha = sigmoid(dot16(x1 / |x1|, k / |k|) / sqrt(d)); x1 += alpha * conv
+        if (wave == 0) {
+            const float ss = dot16_wave(sh.x1, sh.x1, d, lane);
+            if (lane == 0) sh.r = rinv(ss, d);
+        } else if (wave == 1) {
+            const float ss = dot16_wave(sh.o, sh.o, d, lane);
+            if (lane == 0) sh.r2 = rinv(ss, d);
+        }
+        __syncthreads();
+        if (t < d) {
+            sh.x2[t] = x1 * sh.r;
+            sh.h[t] = q.kr * sh.r2;
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const float dd = dot16_wave(sh.x2, sh.h, d, lane);
+            if (lane == 0) sh.r = 1.0f / (lexpf((-dd) / __builtin_sqrtf((float)d)) + 1.0f);
+        }
+        __syncthreads();
+        if (t < d) {
+            x1 = __builtin_fmaf(q.ev, sh.r, x1);
+            sh.x1[t] = x1;
+        }
+        __syncthreads();
+    }
+    // hloc = norm_apply16(x1, rinv(dot16(x1)), norm_in), then A8.
+    if (wave == 0) {
+        const float ss = dot16_wave(sh.x1, sh.x1, d, lane);
+        if (lane == 0) sh.r = rinv(ss, d);
+    }
+    __syncthreads();
+    if (t < d) {
+        const float tt = x1 * sh.r;
+        sh.h[t] = __builtin_fmaf(tt, q.norm, tt);
+        S.u[t] = u;
+        S.x1[t] = x1;
+    }
+    if (t < MHC_COLS) S.p[t] = sh.p[t];
+    __syncthreads();
+    const int groups = (d + GROUP - 1) / GROUP;
+    for (int g = wave; g < groups; g += LT / 64) {
+        const int p0 = g * GROUP + lane, p1 = p0 + 64;
+        a8_group(p0 < d ? sh.h[p0] : 0.0f, p1 < d ? sh.h[p1] : 0.0f, lane, in_bits, S.xq_in + (size_t)g * GROUP,
+                 S.sx_in + g);
+    }
+}
+
+// The head's input (step.rs:706-728): lane mean, zcn with the f32 final
+// norm, A8.
+__device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_bits, LayerShared& sh) {
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
+    float mean = 0.0f;
+    if (t < d) {
+        mean = (((sh.xs[t] + sh.xs[d + t]) + sh.xs[2 * d + t]) + sh.xs[3 * d + t]) * 0.25f;
+        sh.h[t] = mean;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const float ss = dot16_wave(sh.h, sh.h, d, lane);
+        if (lane == 0) sh.r = rinv(ss, d);
+    }
+    __syncthreads();
+    if (t < d) {
+        const float tt = mean * sh.r;
+        sh.x2[t] = __builtin_fmaf(tt, fnorm, tt);
+    }
+    __syncthreads();
+    const int groups = (d + GROUP - 1) / GROUP;
+    for (int g = wave; g < groups; g += LT / 64) {
+        const int p0 = g * GROUP + lane, p1 = p0 + 64;
+        a8_group(p0 < d ? sh.x2[p0] : 0.0f, p1 < d ? sh.x2[p1] : 0.0f, lane, head_bits, S.xq_in + (size_t)g * GROUP,
+                 S.sx_in + g);
+    }
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int has_prev,
+                                              int has_next, int in_bits, int head_bits) {
+    __shared__ LayerShared sh;
+    const int t = threadIdx.x, d = D.d, nc = MHC_LANES * d;
+    // every global read first
+    for (int i = t; i < nc; i += LT) sh.xs[i] = S.xs[i];
+    OutRegs qo{};
+    if (has_prev) {
+        qo = load_out(D, G, S, P, sh);
+        if (t < d) sh.o[t] = qo.o;
+    }
+    InRegs qi{};
+    float fnorm = 0.0f;
+    if (has_next)
+        qi = load_in(D, S, N);
+    else if (t < d)
+        fnorm = G.final_norm[t];
+    __syncthreads();
+    if (has_prev) {
+        layer_out(D, P, qo, sh);
+        for (int i = t; i < nc; i += LT) S.xs[i] = sh.xs[i];
+    }
+    if (has_next)
+        layer_in(D, S, N, qi, in_bits, sh);
+    else
+        head_in(D, S, fnorm, head_bits, sh);
+}
+
+hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
+                     int in_bits, int head_bits, hipStream_t s) {
+    const LayerDev none{};
+    hipLaunchKernelGGL(k_layer, dim3(1), dim3(LT), 0, s, D, G, S, prev ? *prev : none, next ? *next : none,
+                       prev ? 1 : 0, next ? 1 : 0, in_bits, head_bits);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------ units
 // sinkhorn64 (infer.rs:2501-2528) by 16 lanes, lane = 4 r + c holding
 // e[r][c]: row sums ((e0 + e1) + (e2 + e3)), column sums
 // ((e[c] + e[4 + c]) + (e[8 + c] + e[12 + c])), 20 rounds, in f64.
@@ -304,277 +722,28 @@ __device__ __forceinline__ float sinkhorn_lane(float z, int lane) {
     return (float)e;
 }
 
-// The Hadamard MLP and mHC write of layer P (step.rs:600-705).
-__device__ void layer_out(const Dims& D, const Globals& G, const LayerDev& P, LayerShared& sh) {
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
-    // on = zcn16(o, post_norm); x2 = fma(on, sigmoid(attn_gate), x1)
-    if (wave == 0) {
-        const float ss = dot16_wave(sh.o, sh.o, d, lane);
-        if (lane == 0) sh.r = rinv(ss, d);
-    }
-    __syncthreads();
-    for (int i = t; i < d; i += LT) {
-        const float tt = sh.o[i] * sh.r;
-        const float on = __builtin_fmaf(tt, h2f(P.post_norm[i]), tt);
-        sh.x2[i] = __builtin_fmaf(on, P.ga, sh.x1[i]);
-    }
-    __syncthreads();
-    // h2 = zcn16(x2, pre_hada)
-    if (wave == 0) {
-        const float ss = dot16_wave(sh.x2, sh.x2, d, lane);
-        if (lane == 0) sh.r = rinv(ss, d);
-    }
-    __syncthreads();
-    for (int i = t; i < d; i += LT) {
-        const float tt = sh.x2[i] * sh.r;
-        sh.h[i] = __builtin_fmaf(tt, h2f(P.pre_hada[i]), tt);
-    }
-    __syncthreads();
-    // cond_weights (infer.rs:1640-1656): lane 8 jm + k chains
-    // acc[jm][k] = fma(h2[j], cond_v[j][k], .) over j = jm, jm + 4, ...
-    if (wave == 0) {
-        const int k = lane & 7;
-        float a = 0.0f;
-        if (lane < 32)
-            for (int j = lane >> 3; j < d; j += 4) a = __builtin_fmaf(sh.h[j], h2f(P.cond_v[j * 8 + k]), a);
-        const float a0 = __shfl(a, k, 64), a1 = __shfl(a, 8 + k, 64), a2 = __shfl(a, 16 + k, 64),
-                    a3 = __shfl(a, 24 + k, 64);
-        const float lg = ((a2 + a3) + a1) + a0;
-        float m = lg;
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        m = fmaxf(m, __shfl_xor(m, 2, 64));
-        m = fmaxf(m, __shfl_xor(m, 4, 64));
-        const float e = lexpf(lg - m);
-        float ev[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) ev[i] = __shfl(e, i, 64);
-        const float sum = ev[7] + ((ev[6] + (ev[5] + ev[4])) + ((ev[3] + ev[2]) + (ev[1] + ev[0])));
-        const float inv = 1.0f / sum;
-        if (lane < 8) sh.wk[lane] = e * inv;
-    }
-    // z = h2 * d1, zero-padded to hada_n
-    for (int j = t; j < HADA_N; j += LT) sh.A[j] = j < d ? sh.h[j] * h2f(P.d1[j]) : 0.0f;
-    __syncthreads();
-    mix8<true, false>(true, P.kron[0], sh.A, sh.B, HADA_NB);
-    __syncthreads();
-    mix8<false, true>(false, sh.B, P.kron[1], sh.C, HADA_NB);
-    __syncthreads();
-    for (int j = t; j < HADA_N; j += LT) {
-        float cond = 1.0f;
-#pragma unroll
-        for (int k = 0; k < COND_RANK; ++k) cond = __builtin_fmaf(h2f(P.cond_u[k * HADA_N + j]), sh.wk[k], cond);
-        float zs = __builtin_fmaf(sh.C[G.perm1[j]], cond * h2f(P.d2[j]), h2f(P.b2[j]));
-        zs = zs / (nexp(-zs) + 1.0f);
-        sh.A[j] = zs;
-    }
-    __syncthreads();
-    mix8<true, false>(true, P.kron[2], sh.A, sh.B, HADA_NB);
-    __syncthreads();
-    mix8<false, true>(false, sh.B, P.kron[3], sh.C, HADA_NB);
-    __syncthreads();
-    for (int j = t; j < HADA_N; j += LT) sh.A[j] = sh.C[G.perm2[j]] * h2f(P.d3[j]);
-    __syncthreads();
-    mix8<true, false>(true, P.kron[4], sh.A, sh.B, HADA_NB);
-    __syncthreads();
-    mix8<false, true>(false, sh.B, P.kron[5], sh.C, d / HADA_NB / 8 * 8);
-    __syncthreads();
-    // The mHC write: y = (x2 + t3 * d4) - u; lane a = y hpost[a] + sum_b
-    // hres[a][b] old[b] as an fma chain over b.
-    const float* hpost = sh.p + MHC_COLS;
-    const float* hres = sh.p + MHC_COLS + MHC_LANES;
-    for (int ch = t; ch < d; ch += LT) {
-        const float y = (sh.x2[ch] + sh.C[ch] * h2f(P.d4[ch])) - sh.u[ch];
-        float old[MHC_LANES];
-#pragma unroll
-        for (int b = 0; b < MHC_LANES; ++b) old[b] = sh.xs[b * d + ch];
-#pragma unroll
-        for (int a = 0; a < MHC_LANES; ++a) {
-            float v = y * hpost[a];
-#pragma unroll
-            for (int b = 0; b < MHC_LANES; ++b) v = __builtin_fmaf(old[b], hres[a * MHC_LANES + b], v);
-            sh.xs[a * d + ch] = v;
-        }
-    }
-    __syncthreads();
-}
-
-// The mHC read, engram gate, input norm and A8 of layer N
-// (step.rs:400-479).
-__device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, int in_bits, LayerShared& sh) {
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d, nc = MHC_LANES * d;
-    if (wave == 0) {
-        const float ss = dot16_wave(sh.xs, sh.xs, nc, lane);
-        if (lane == 0) sh.r = rinv(ss, nc);
-    }
-    __syncthreads();
-    const float r = sh.r;
-    float m = 0.0f;
-    for (int i = t; i < nc; i += LT) m = fmaxf(m, fabsf(sh.xs[i] * r));
-    m = block_max(m, sh.red);
-    const float sx = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
-    const float inv = 1.0f / sx;
-    for (int i = t; i < nc; i += LT) sh.nx8[i] = quant_one(sh.xs[i] * r, inv);
-    __syncthreads();
-    // Phi8 rows: p[k] = (sx * s_k) * idot(phi_q[k], nx8)
-    for (int k = wave; k < MHC_COLS; k += LT / 64) {
-        const uint4* row = reinterpret_cast<const uint4*>(N.phi_q + (size_t)k * nc);
-        const uint4* xv = reinterpret_cast<const uint4*>(sh.nx8);
-        int acc = 0;
-        for (int i = lane; i < nc / 16; i += 64) {
-            const uint4 a = row[i], b = xv[i];
-            acc = __builtin_amdgcn_sdot4((int)a.x, (int)b.x, acc, false);
-            acc = __builtin_amdgcn_sdot4((int)a.y, (int)b.y, acc, false);
-            acc = __builtin_amdgcn_sdot4((int)a.z, (int)b.z, acc, false);
-            acc = __builtin_amdgcn_sdot4((int)a.w, (int)b.w, acc, false);
-        }
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
-        if (lane == 0) sh.p[k] = (sx * N.phi_s[k]) * (float)acc;
-    }
-    __syncthreads();
-    // Gates: hp (pre, sigmoid), hpost (2 sigmoid), hres (Sinkhorn).
-    if (wave == 0) {
-        if (lane < MHC_LANES) {
-            const float off = lane == N.lane ? 4.0f : -4.0f;
-            const float zz = ((sh.p[lane] * N.a_pre) + off) + N.b_pre[lane];
-            sh.hp[lane] = 1.0f / (lexpf(-zz) + 1.0f);
-        } else if (lane >= 32 && lane < 32 + MHC_LANES) {
-            const int j = lane - 32;
-            const float off = j == N.lane ? 0.0f : -4.0f;
-            const float zz = ((sh.p[MHC_LANES + j] * N.a_post) + off) + N.b_post[j];
-            sh.p[MHC_COLS + j] = 2.0f / (lexpf(-zz) + 1.0f);
-        }
-    } else if (wave == 1) {
-        const int k = lane & 15;
-        const float z = __builtin_fmaf(sh.p[2 * MHC_LANES + k], N.a_res, N.b_res[k]);
-        const float hr = sinkhorn_lane(z, lane);
-        if (lane < 16) sh.p[MHC_COLS + MHC_LANES + lane] = hr;
-    }
-    __syncthreads();
-    for (int i = t; i < d; i += LT) {
-        float u = sh.xs[i] * sh.hp[0];
-#pragma unroll
-        for (int b = 1; b < MHC_LANES; ++b) u = __builtin_fmaf(sh.xs[b * d + i], sh.hp[b], u);
-        sh.u[i] = u;
-        sh.x1[i] = u;
-        if (N.site >= 0) sh.o[i] = S.ekv[(size_t)N.site * 2 * d + i];
-    }
-    __syncthreads();
-    if (N.site >= 0) {
-        // alpha = sigmoid(dot16(x1 / |x1|, k / |k|) / sqrt(d)); x1 += alpha * conv
-        if (wave == 0) {
-            const float ss = dot16_wave(sh.x1, sh.x1, d, lane);
-            if (lane == 0) sh.r = rinv(ss, d);
-        } else if (wave == 1) {
-            const float ss = dot16_wave(sh.o, sh.o, d, lane);
-            if (lane == 0) sh.r2 = rinv(ss, d);
-        }
-        __syncthreads();
-        for (int i = t; i < d; i += LT) {
-            sh.x2[i] = sh.x1[i] * sh.r;
-            sh.h[i] = sh.o[i] * sh.r2;
-        }
-        __syncthreads();
-        if (wave == 0) {
-            const float dd = dot16_wave(sh.x2, sh.h, d, lane);
-            if (lane == 0) sh.r = 1.0f / (lexpf((-dd) / __builtin_sqrtf((float)d)) + 1.0f);
-        }
-        __syncthreads();
-        const float alpha = sh.r;
-        for (int i = t; i < d; i += LT) sh.x1[i] = __builtin_fmaf(S.evals[(size_t)N.site * d + i], alpha, sh.x1[i]);
-        __syncthreads();
-    }
-    // hloc = norm_apply16(x1, rinv(dot16(x1)), norm_in), then A8.
-    if (wave == 0) {
-        const float ss = dot16_wave(sh.x1, sh.x1, d, lane);
-        if (lane == 0) sh.r = rinv(ss, d);
-    }
-    __syncthreads();
-    for (int i = t; i < d; i += LT) {
-        const float tt = sh.x1[i] * sh.r;
-        sh.h[i] = __builtin_fmaf(tt, h2f(N.norm_in[i]), tt);
-    }
-    __syncthreads();
-    const int groups = (d + GROUP - 1) / GROUP;
-    for (int g = wave; g < groups; g += LT / 64) {
-        const int p0 = g * GROUP + lane, p1 = p0 + 64;
-        a8_group(p0 < d ? sh.h[p0] : 0.0f, p1 < d ? sh.h[p1] : 0.0f, lane, in_bits, S.xq_in + (size_t)g * GROUP,
-                 S.sx_in + g);
-    }
-    for (int i = t; i < d; i += LT) {
-        S.u[i] = sh.u[i];
-        S.x1[i] = sh.x1[i];
-    }
-    if (t < MHC_COLS + MHC_LANES + MHC_LANES * MHC_LANES) S.p[t] = sh.p[t];
-}
-
-// The head's input (step.rs:706-728): lane mean, zcn with the f32 final
-// norm, A8.
-__device__ void head_in(const Dims& D, const Globals& G, const SessDev& S, int head_bits, LayerShared& sh) {
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
-    for (int ch = t; ch < d; ch += LT)
-        sh.h[ch] = (((sh.xs[ch] + sh.xs[d + ch]) + sh.xs[2 * d + ch]) + sh.xs[3 * d + ch]) * 0.25f;
-    __syncthreads();
-    if (wave == 0) {
-        const float ss = dot16_wave(sh.h, sh.h, d, lane);
-        if (lane == 0) sh.r = rinv(ss, d);
-    }
-    __syncthreads();
-    for (int i = t; i < d; i += LT) {
-        const float tt = sh.h[i] * sh.r;
-        sh.x2[i] = __builtin_fmaf(tt, G.final_norm[i], tt);
-    }
-    __syncthreads();
-    const int groups = (d + GROUP - 1) / GROUP;
-    for (int g = wave; g < groups; g += LT / 64) {
-        const int p0 = g * GROUP + lane, p1 = p0 + 64;
-        a8_group(p0 < d ? sh.x2[p0] : 0.0f, p1 < d ? sh.x2[p1] : 0.0f, lane, head_bits, S.xq_in + (size_t)g * GROUP,
-                 S.sx_in + g);
+// The post and residual gates of the layer (step.rs:636-660), written
+// after the 24 mHC projections: hpost[j] = 2 sigmoid(p_post[j] a_post +
+// off_j + b_post[j]) at 24, hres = sinkhorn64(fma(p_res, a_res, b_res)) at
+// 28.  One wavefront, beside the units.
+__device__ __forceinline__ void post_gates(const SessDev& S, const LayerDev& L, int lane) {
+    const int k = lane & 15;
+    const float z = __builtin_fmaf(S.p[2 * MHC_LANES + k], L.a_res, L.b_res[k]);
+    const float hr = sinkhorn_lane(z, lane);
+    if (lane < 16) S.p[MHC_COLS + MHC_LANES + lane] = hr;
+    if (lane < MHC_LANES) {
+        const float off = lane == L.lane ? 0.0f : -4.0f;
+        const float zz = ((S.p[MHC_LANES + lane] * L.a_post) + off) + L.b_post[lane];
+        S.p[MHC_COLS + lane] = 2.0f / (lexpf(-zz) + 1.0f);
     }
 }
 
-}  // namespace
-
-__global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int has_prev,
-                                              int has_next, int in_bits, int head_bits) {
-    __shared__ LayerShared sh;
-    const int t = threadIdx.x, d = D.d, nc = MHC_LANES * d;
-    for (int i = t; i < nc; i += LT) sh.xs[i] = S.xs[i];
-    if (has_prev) {
-        for (int i = t; i < d; i += LT) {
-            sh.o[i] = S.o[i];
-            sh.x1[i] = S.x1[i];
-            sh.u[i] = S.u[i];
-        }
-        if (t < 64) sh.p[t] = S.p[t];
-    }
-    __syncthreads();
-    if (has_prev) {
-        layer_out(D, G, P, sh);
-        for (int i = t; i < nc; i += LT) S.xs[i] = sh.xs[i];
-    }
-    if (has_next)
-        layer_in(D, S, N, in_bits, sh);
-    else
-        head_in(D, G, S, head_bits, sh);
-}
-
-hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
-                     int in_bits, int head_bits, hipStream_t s) {
-    const LayerDev none{};
-    hipLaunchKernelGGL(k_layer, dim3(1), dim3(LT), 0, s, D, G, S, prev ? *prev : none, next ? *next : none,
-                       prev ? 1 : 0, next ? 1 : 0, in_bits, head_bits);
-    return hipGetLastError();
-}
-
-// ------------------------------------------------------------------ units
-// One wavefront per unit (q heads, k heads, v heads; step.rs:481-556), lane
-// i = element: the causal conv over the current row and the kept history
-// rows (fma from the newest back; a row before position 0 contributes
-// fma(w, 0, v)), the current pre-tap row into the history ring, then for q
-// and k the head zcn16 and RoPE, and for k and v the int8 cache append.
 __global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, LayerDev L, int layer, int p0) {
     const int unit = threadIdx.x >> 6, i = threadIdx.x & 63;
+    if (blockIdx.x == 1) {
+        if (unit == 0) post_gates(S, L, i);
+        return;
+    }
     const int nh = D.nh, nkv = D.nkv, qk = D.qk, vd = D.vd;
     const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd, W = D.W;
     int start, cw, cc, len;
@@ -634,7 +803,7 @@ __global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, Lay
 
 hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, hipStream_t s) {
     const int units = D.nh + 2 * D.nkv;
-    hipLaunchKernelGGL(k_units, dim3(1), dim3(units * 64), 0, s, D, S, L, layer, p0);
+    hipLaunchKernelGGL(k_units, dim3(2), dim3(units * 64), 0, s, D, S, L, layer, p0);
     return hipGetLastError();
 }
 
