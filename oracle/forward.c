@@ -227,16 +227,22 @@ void nf_digits21(const float* w, size_t n, float qw, int8_t* hi, int8_t* mid, in
     }
 }
 
-/* key_chunks (infer.rs:2093-2101): (count, size). */
-void nf_key_chunks(size_t n, size_t nkv, size_t* count, size_t* size) {
-    size_t k = 2 * NATIVE_TEAM / nkv;
-    if (k < 1) k = 1;
+/* key_chunks (infer.rs:2093-2101) with the minimum chunk count k: (count,
+ * size).  attend_head_ref uses k = max(1, 2 NATIVE_TEAM / nkv), or 1 when
+ * nested (infer.rs:1888). */
+static void key_chunks_k(size_t n, size_t k, size_t* count, size_t* size) {
     size_t c = (n + 255) / 256;
     if (k * 64 <= n && c < k) c = k;
     if (c < 1) c = 1;
     const size_t chunk = ((n + c - 1) / c + 15) / 16 * 16;
     *size = chunk;
     *count = chunk ? (n + chunk - 1) / chunk : 0;
+}
+
+void nf_key_chunks(size_t n, size_t nkv, size_t* count, size_t* size) {
+    size_t k = 2 * NATIVE_TEAM / nkv;
+    if (k < 1) k = 1;
+    key_chunks_k(n, k, count, size);
 }
 
 /* ------------------------------------------------------------------ model */
@@ -268,13 +274,13 @@ struct nf_session {
     size_t cap;     /* positions */
     size_t len;     /* tokens fed */
     uint32_t* tokens;
-    /* per layer: k8 [pos][nkv][qk], ks [pos][nkv], v8t [nkv][vd][cap], vs [pos][nkv], hist (last taps-1 rows) */
+    /* per layer: k8 [pos][nkv][qk], ks [pos][nkv], v8t [nkv][vd][cap], vs [pos][nkv], hist [pos][width] (the
+     * pre-tap q|k|v row of every position) */
     int8_t** k8;
     float** ks;
     int8_t** v8t;
     float** vs;
-    float** hist;    /* [taps - 1][width], newest last */
-    size_t hrows;
+    float** hist;
     /* engram value history per site: [pos][d] int8 + [pos][d/32] */
     int8_t** ev8;
     float** evs;
@@ -282,7 +288,6 @@ struct nf_session {
     int rope_ok;
     size_t rope_pos;
     float *rope_c, *rope_s;
-    float* xs;       /* the residual lanes [n][d] */
 };
 
 static uint16_t* dup16(const uint16_t* p, size_t n) {
@@ -413,13 +418,13 @@ nf_session* nf_session_new(const nf_model* m, size_t cap) {
     s->v8t = (int8_t**)calloc((size_t)c->layers, sizeof(void*));
     s->vs = (float**)calloc((size_t)c->layers, sizeof(void*));
     s->hist = (float**)calloc((size_t)c->layers, sizeof(void*));
-    const int W = width_of(c), keep = c->taps > 1 ? c->taps - 1 : 1;
+    const int W = width_of(c);
     for (int l = 0; l < c->layers; ++l) {
         s->k8[l] = (int8_t*)calloc(cap * c->nkv * c->qk, 1);
         s->ks[l] = (float*)calloc(cap * c->nkv, sizeof(float));
         s->v8t[l] = (int8_t*)calloc((size_t)c->nkv * c->vd * cap, 1);
         s->vs[l] = (float*)calloc(cap * c->nkv, sizeof(float));
-        s->hist[l] = (float*)calloc((size_t)keep * W, sizeof(float));
+        s->hist[l] = (float*)calloc(cap * (size_t)W, sizeof(float));
     }
     s->ev8 = (int8_t**)calloc((size_t)c->sites + 1, sizeof(void*));
     s->evs = (float**)calloc((size_t)c->sites + 1, sizeof(void*));
@@ -429,7 +434,6 @@ nf_session* nf_session_new(const nf_model* m, size_t cap) {
     }
     s->rope_c = (float*)calloc((size_t)c->qk / 2, sizeof(float));
     s->rope_s = (float*)calloc((size_t)c->qk / 2, sizeof(float));
-    s->xs = (float*)calloc((size_t)c->lanes * c->d, sizeof(float));
     return s;
 }
 
@@ -438,23 +442,26 @@ void nf_session_free(const nf_model* m, nf_session* s) {
     for (int l = 0; l < m->c.layers; ++l) free(s->k8[l]), free(s->ks[l]), free(s->v8t[l]), free(s->vs[l]), free(s->hist[l]);
     for (int e = 0; e < m->c.sites; ++e) free(s->ev8[e]), free(s->evs[e]);
     free(s->k8), free(s->ks), free(s->v8t), free(s->vs), free(s->hist), free(s->ev8), free(s->evs);
-    free(s->tokens), free(s->rope_c), free(s->rope_s), free(s->xs);
+    free(s->tokens), free(s->rope_c), free(s->rope_s);
     free(s);
 }
 
 size_t nf_session_len(const nf_session* s) { return s->len; }
 
-/* attend_head_ref (infer.rs:1871-2007) with attend = None, nested = false:
- * keys are positions lo..pos (inclusive), slot = position. */
+/* attend_head_ref (infer.rs:1871-2007) with attend = None: keys are
+ * positions lo..pos (inclusive), slot = position.  `nested` (a chunk's rows,
+ * infer/chunk.rs:263) drops the minimum chunk count (infer.rs:1888). */
 static void attend_head(const nf_model* m, const nf_session* s, int l, const float* qh, int kvh, size_t lo, size_t pos,
-                        float* out) {
+                        int nested, float* out) {
     const nf_config* c = &m->c;
     const size_t qk = c->qk, vd = c->vd, nkv = c->nkv, cap = s->cap;
     int8_t q8[64];
     const float qs = cq_quant_i8(qh, qk, q8) * INV_SQRT_QK;
     const size_t n = pos + 1 - lo;
     size_t count, chunk;
-    nf_key_chunks(n, nkv, &count, &chunk);
+    size_t kmin = 2 * NATIVE_TEAM / nkv;
+    if (kmin < 1 || nested) kmin = 1;
+    key_chunks_k(n, kmin, &count, &chunk);
     float* sc = (float*)malloc(chunk * sizeof(float));
     float* scale = (float*)malloc(chunk * sizeof(float));
     int32_t* dots = (int32_t*)malloc(chunk * sizeof(int32_t));
@@ -511,266 +518,294 @@ static void attend_head(const nf_model* m, const nf_session* s, int l, const flo
     free(sc), free(scale), free(dots), free(dig);
 }
 
-/* Model::step_native (step.rs:171-760) for one token; logits [out_rows]. */
-int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int nthreads) {
+/* The rows p0 .. p0 + t - 1 of one feed: Model::step_native
+ * (infer/step.rs:171-760) for t = 1, Model::chunk_job (infer/chunk.rs:32-358)
+ * for a chunk of t > 1 tokens.  The two share the per-row arithmetic; a chunk
+ * differs in its projections (the prefill combine over its t rows), its RoPE
+ * rows (sincosf per position, rope_rows, infer.rs:1716-1747) and its
+ * attention chunking (nested, infer.rs:1888).  Logits of the last row
+ * [out_rows] when `logits` is set. */
+static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_t t, float* logits, int nthreads) {
     const nf_config* c = &m->c;
     const int n = c->lanes, d = c->d, nc = n * d, L = c->layers;
     const int qk = c->qk, vd = c->vd, nh = c->nh, nkv = c->nkv;
     const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd, W = qd + kd + vdim, taps = c->taps;
     const int half = qk / 2, group = nh / nkv, sites = c->sites;
     const size_t p0 = s->len;
-    if (p0 >= s->cap || n != 4 || qk > 64 || vd > 64 || c->norders * c->eheads > 16 || L > 64) return -1;
-    s->tokens[p0] = tok;
-    s->len = p0 + 1;
+    if (t == 0 || p0 + t > s->cap || n != 4 || qk > 64 || vd > 64 || c->norders * c->eheads > 16 || L > 64) return -1;
+    const int nested = t > 1;
+    for (size_t i = 0; i < t; ++i) s->tokens[p0 + i] = toks[i];
+    s->len = p0 + t;
 
-    /* embedding row * sqrt(d) into every lane (step.rs:228-235) */
-    float* xs = s->xs;
+    /* embedding row * sqrt(d) into every lane (step.rs:228-235, chunk.rs:58-66) */
+    float* xs = (float*)malloc(sizeof(float) * t * nc);
     float* row = (float*)malloc(sizeof(float) * d);
-    cq_qmat_row(m->embedding, tok, row);
     const float scale = sqrtf((float)d);
-    for (int lane = 0; lane < n; ++lane)
-        for (int i = 0; i < d; ++i) xs[lane * d + i] = row[i] * scale;
-
-    /* engram rows and their key|value products, value history and conv
-     * (step.rs:245-269, 346-391) */
-    const int norders = c->norders, eheads = c->eheads, ntab = norders * eheads, sub = c->engram_sub;
-    float* ekv = (float*)calloc((size_t)sites * 2 * d + 1, sizeof(float));
-    float* evals = (float*)calloc((size_t)sites * d + 1, sizeof(float));
-    if (sites > 0) {
-        long erow[16];
-        const int stride = c->seed_heads > 0 ? c->seed_heads : eheads;
-        for (int oi = 0; oi < norders; ++oi)
-            for (int h = 0; h < eheads; ++h) {
-                const int order = c->orders[oi], tbl = oi * eheads + h;
-                erow[tbl] = -1;
-                if (p0 + 1 < (size_t)order) continue;
-                uint32_t acc = ENGRAM_SEED * (uint32_t)(oi * stride + h + 1);
-                for (int j = 0; j < order; ++j) {
-                    const uint32_t t = p0 >= (size_t)j ? s->tokens[p0 - j] : 0;
-                    acc = (acc ^ t) * ENGRAM_PRIME;
-                }
-                acc ^= acc >> 15;
-                erow[tbl] = (long)tbl * c->engram_slots + (long)(acc % (uint32_t)c->engram_slots);
-            }
-        float* er = (float*)malloc(sizeof(float) * d);
-        float* trow = (float*)malloc(sizeof(float) * sub);
-        for (int e = 0; e < sites; ++e) {
-            memset(er, 0, sizeof(float) * d);
-            for (int tbl = 0; tbl < ntab; ++tbl)
-                if (erow[tbl] >= 0) {
-                    cq_qmat_row(m->etables[e], (size_t)erow[tbl], trow);
-                    memcpy(er + tbl * sub, trow, sizeof(float) * sub);
-                }
-            cq_qact* a = cq_qact_new(er, 1, d, m->ekv[e]->parts[0]->bits, 1);
-            cq_qlinear_matmul(m->ekv[e], a, ekv + (size_t)e * 2 * d, 1);
-            cq_qact_free(a);
-            /* int8 value history, groups of 32 */
-            for (int g = 0; g < d / 32; ++g)
-                s->evs[e][p0 * (d / 32) + g] =
-                    cq_quant_i8(ekv + (size_t)e * 2 * d + d + g * 32, 32, s->ev8[e] + p0 * d + g * 32);
-        }
-        free(er), free(trow);
-        const int dil = c->dilation;
-        for (int e = 0; e < sites; ++e) {
-            float* dst = evals + (size_t)e * d;
-            for (int j = 0; j < ENGRAM_CONV_TAPS; ++j) {
-                if (p0 < (size_t)(j * dil)) break;
-                const size_t pj = p0 - (size_t)j * dil;
-                const int8_t* q8 = s->ev8[e] + pj * d;
-                const float* qs = s->evs[e] + pj * (d / 32);
-                const float* tw = m->etaps[e] + (size_t)j * d;
-                for (int k = 0; k < d; ++k) dst[k] = fmaf(tw[k], qs[k / 32] * (float)q8[k], dst[k]);
-            }
-        }
+    for (size_t i = 0; i < t; ++i) {
+        cq_qmat_row(m->embedding, toks[i], row);
+        for (int lane = 0; lane < n; ++lane)
+            for (int k = 0; k < d; ++k) xs[i * nc + lane * d + k] = row[k] * scale;
     }
 
-    /* RoPE rows for this position (rope_rows, infer.rs:1716-1747) */
-    float cs[32], sn[32];
-    if (s->rope_ok && s->rope_pos + 1 == p0) {
+    /* engram rows and their key|value products over the t rows, value
+     * history and conv (engram_native, infer.rs:1244-1335) */
+    const int norders = c->norders, eheads = c->eheads, ntab = norders * eheads, sub = c->engram_sub;
+    float* ekv = (float*)calloc((size_t)sites * t * 2 * d + 1, sizeof(float));
+    float* evals = (float*)calloc((size_t)sites * t * d + 1, sizeof(float));
+    if (sites > 0) {
+        long* erow = (long*)malloc(sizeof(long) * t * 16);
+        const int stride = c->seed_heads > 0 ? c->seed_heads : eheads;
+        for (size_t i = 0; i < t; ++i) {
+            const size_t pos = p0 + i;
+            for (int oi = 0; oi < norders; ++oi)
+                for (int h = 0; h < eheads; ++h) {
+                    const int order = c->orders[oi], tbl = oi * eheads + h;
+                    erow[i * 16 + tbl] = -1;
+                    if (pos + 1 < (size_t)order) continue;
+                    uint32_t acc = ENGRAM_SEED * (uint32_t)(oi * stride + h + 1);
+                    for (int j = 0; j < order; ++j) {
+                        const uint32_t tk = pos >= (size_t)j ? s->tokens[pos - j] : 0;
+                        acc = (acc ^ tk) * ENGRAM_PRIME;
+                    }
+                    acc ^= acc >> 15;
+                    erow[i * 16 + tbl] = (long)tbl * c->engram_slots + (long)(acc % (uint32_t)c->engram_slots);
+                }
+        }
+        float* er = (float*)malloc(sizeof(float) * t * d);
+        float* trow = (float*)malloc(sizeof(float) * sub);
+        for (int e = 0; e < sites; ++e) {
+            memset(er, 0, sizeof(float) * t * d);
+            for (size_t i = 0; i < t; ++i)
+                for (int tbl = 0; tbl < ntab; ++tbl)
+                    if (erow[i * 16 + tbl] >= 0) {
+                        cq_qmat_row(m->etables[e], (size_t)erow[i * 16 + tbl], trow);
+                        memcpy(er + i * d + tbl * sub, trow, sizeof(float) * sub);
+                    }
+            cq_qact* a = cq_qact_new(er, t, d, m->ekv[e]->parts[0]->bits, 1);
+            float* kv = ekv + (size_t)e * t * 2 * d;
+            cq_qlinear_matmul(m->ekv[e], a, kv, nthreads);
+            cq_qact_free(a);
+            /* int8 value history, groups of 32 */
+            for (size_t i = 0; i < t; ++i)
+                for (int g = 0; g < d / 32; ++g)
+                    s->evs[e][(p0 + i) * (d / 32) + g] =
+                        cq_quant_i8(kv + i * 2 * d + d + g * 32, 32, s->ev8[e] + (p0 + i) * d + g * 32);
+        }
+        free(er), free(trow), free(erow);
+        const int dil = c->dilation;
+        for (int e = 0; e < sites; ++e)
+            for (size_t i = 0; i < t; ++i) {
+                const size_t pos = p0 + i;
+                float* dst = evals + ((size_t)e * t + i) * d;
+                for (int j = 0; j < ENGRAM_CONV_TAPS; ++j) {
+                    if (pos < (size_t)(j * dil)) break;
+                    const size_t pj = pos - (size_t)j * dil;
+                    const int8_t* q8 = s->ev8[e] + pj * d;
+                    const float* qs = s->evs[e] + pj * (d / 32);
+                    const float* tw = m->etaps[e] + (size_t)j * d;
+                    for (int k = 0; k < d; ++k) dst[k] = fmaf(tw[k], qs[k / 32] * (float)q8[k], dst[k]);
+                }
+            }
+    }
+
+    /* RoPE rows (rope_rows, infer.rs:1716-1747): the recurrence for a single
+     * token right after the newest known position, sincosf otherwise. */
+    float* cs = (float*)malloc(sizeof(float) * t * 32);
+    float* sn = (float*)malloc(sizeof(float) * t * 32);
+    if (t == 1 && s->rope_ok && s->rope_pos + 1 == p0) {
         for (int f = 0; f < half; ++f) {
             cs[f] = fmaf(-m->sd[f], s->rope_s[f], m->cd[f] * s->rope_c[f]);
             sn[f] = fmaf(m->sd[f], s->rope_c[f], m->cd[f] * s->rope_s[f]);
         }
     } else {
-        for (int f = 0; f < half; ++f) lsincosf(m->freq[f] * (float)p0, &sn[f], &cs[f]);
+        for (size_t i = 0; i < t; ++i)
+            for (int f = 0; f < half; ++f) lsincosf(m->freq[f] * (float)(p0 + i), &sn[i * 32 + f], &cs[i * 32 + f]);
     }
-    memcpy(s->rope_c, cs, sizeof(float) * half);
-    memcpy(s->rope_s, sn, sizeof(float) * half);
+    memcpy(s->rope_c, cs + (t - 1) * 32, sizeof(float) * half);
+    memcpy(s->rope_s, sn + (t - 1) * 32, sizeof(float) * half);
     s->rope_ok = 1;
-    s->rope_pos = p0;
+    s->rope_pos = p0 + t - 1;
 
     const int nq = W + nh * vd;  /* the fused projection: q | k | v | gate */
+    const int ncols = 2 * n + n * n;
     float* nx = (float*)malloc(sizeof(float) * nc);
     int8_t* nx8 = (int8_t*)malloc(nc);
-    float *u = (float*)malloc(sizeof(float) * d), *x1 = (float*)malloc(sizeof(float) * d);
-    float *hloc = (float*)malloc(sizeof(float) * d), *proj = (float*)malloc(sizeof(float) * nq);
-    float *qbuf = (float*)malloc(sizeof(float) * qd), *att = (float*)malloc(sizeof(float) * nh * vd);
-    float *o = (float*)malloc(sizeof(float) * d), *on = (float*)malloc(sizeof(float) * d);
+    float *u = (float*)malloc(sizeof(float) * t * d), *x1 = (float*)malloc(sizeof(float) * t * d);
+    float* p = (float*)malloc(sizeof(float) * t * ncols);
+    float *hloc = (float*)malloc(sizeof(float) * t * d), *proj = (float*)malloc(sizeof(float) * t * nq);
+    float *qkv = (float*)malloc(sizeof(float) * t * W), *att = (float*)malloc(sizeof(float) * t * nh * vd);
+    float *o = (float*)malloc(sizeof(float) * t * d), *on = (float*)malloc(sizeof(float) * d);
     float *x2 = (float*)malloc(sizeof(float) * d), *h2 = (float*)malloc(sizeof(float) * d);
     float *ea = (float*)malloc(sizeof(float) * d), *eb = (float*)malloc(sizeof(float) * d);
     float *z = (float*)malloc(sizeof(float) * HN), *mt = (float*)malloc(sizeof(float) * HN);
     float *bt = (float*)malloc(sizeof(float) * HN), *cond = (float*)malloc(sizeof(float) * HN);
     float *zs = (float*)malloc(sizeof(float) * HN), *t3 = (float*)malloc(sizeof(float) * HN);
-    float* newh = (float*)malloc(sizeof(float) * W);
-    const int ncols = 2 * n + n * n;
-    float p[24];
 
     for (int l = 0; l < L; ++l) {
         const struct nf_layer16* Lw = &m->L[l];
         const int lane = l % n;
-        /* (a) mHC read */
-        {
-            const float r = cq_rinv(cq_dot16(xs, xs, nc), nc);
-            for (int i = 0; i < nc; ++i) nx[i] = xs[i] * r;
+        const int site = l < 64 ? m->site_of_layer[l] : -1;
+        /* (a) mHC read, (b) engram gate, (c) input norm, per row */
+        for (size_t i = 0; i < t; ++i) {
+            const float* x = xs + i * nc;
+            float* pr = p + i * ncols;
+            float* ur = u + i * d;
+            float* xr = x1 + i * d;
+            const float r = cq_rinv(cq_dot16(x, x, nc), nc);
+            for (int k = 0; k < nc; ++k) nx[k] = x[k] * r;
             const float sx = cq_quant_scale(nx, nc);
             cq_quant_with(nx, nc, 1.0f / sx, nx8);
-            for (int k = 0; k < ncols; ++k) p[k] = (sx * Lw->phi_s[k]) * (float)idot(Lw->phi_q + (size_t)k * nc, nx8, nc);
+            for (int k = 0; k < ncols; ++k) pr[k] = (sx * Lw->phi_s[k]) * (float)idot(Lw->phi_q + (size_t)k * nc, nx8, nc);
             float hp[4];
             for (int j = 0; j < 4; ++j) {
                 const float off = j == lane ? 4.0f : -4.0f;
-                const float zz = ((p[j] * Lw->a_pre) + off) + Lw->b_pre[j];
+                const float zz = ((pr[j] * Lw->a_pre) + off) + Lw->b_pre[j];
                 hp[j] = 1.0f / (lexpf(-zz) + 1.0f);
             }
-            for (int i = 0; i < d; ++i) u[i] = xs[i] * hp[0];
+            for (int k = 0; k < d; ++k) ur[k] = x[k] * hp[0];
             for (int b = 1; b < 4; ++b)
-                for (int i = 0; i < d; ++i) u[i] = fmaf(xs[b * d + i], hp[b], u[i]);
+                for (int k = 0; k < d; ++k) ur[k] = fmaf(x[b * d + k], hp[b], ur[k]);
+            memcpy(xr, ur, sizeof(float) * d);
+            if (site >= 0) {
+                const float* kr = ekv + ((size_t)site * t + i) * 2 * d;
+                const float rx = cq_rinv(cq_dot16(xr, xr, d), d), rkk = cq_rinv(cq_dot16(kr, kr, d), d);
+                for (int k = 0; k < d; ++k) ea[k] = xr[k] * rx, eb[k] = kr[k] * rkk;
+                const float alpha = 1.0f / (lexpf((-cq_dot16(ea, eb, d)) / sqrtf((float)d)) + 1.0f);
+                const float* ev = evals + ((size_t)site * t + i) * d;
+                for (int k = 0; k < d; ++k) xr[k] = fmaf(ev[k], alpha, xr[k]);
+            }
+            const float rh = cq_rinv(cq_dot16(xr, xr, d), d);
+            cq_norm_apply16(hloc + i * d, xr, rh, Lw->norm_in, d);
         }
-        /* (b) engram gate */
-        memcpy(x1, u, sizeof(float) * d);
-        const int site = l < 64 ? m->site_of_layer[l] : -1;
-        if (site >= 0) {
-            const float* kr = ekv + (size_t)site * 2 * d;
-            const float rx = cq_rinv(cq_dot16(x1, x1, d), d), rkk = cq_rinv(cq_dot16(kr, kr, d), d);
-            for (int i = 0; i < d; ++i) ea[i] = x1[i] * rx, eb[i] = kr[i] * rkk;
-            const float alpha = 1.0f / (lexpf((-cq_dot16(ea, eb, d)) / sqrtf((float)d)) + 1.0f);
-            for (int i = 0; i < d; ++i) x1[i] = fmaf(evals[(size_t)site * d + i], alpha, x1[i]);
-        }
-        /* (c)-(d) input norm, A8, q|k|v|gate */
+        /* (d) A8 of the rows and q|k|v|gate over all of them */
         {
-            const float rh = cq_rinv(cq_dot16(x1, x1, d), d);
-            cq_norm_apply16(hloc, x1, rh, Lw->norm_in, d);
-            cq_qact* a = cq_qact_new(hloc, 1, d, m->qkvg[l]->parts[0]->bits, 1);
+            cq_qact* a = cq_qact_new(hloc, t, d, m->qkvg[l]->parts[0]->bits, 1);
             cq_qlinear_matmul(m->qkvg[l], a, proj, nthreads);
             cq_qact_free(a);
         }
-        /* (e)-(g) taps, head norms, RoPE, the KV cache and the history */
-        const size_t hrows = s->hrows;
+        /* (e)-(g) the rows' pre-tap history, then per row the conv taps,
+         * head norms, RoPE and the KV cache */
         float* hist = s->hist[l];
-        const int keep = taps > 1 ? taps - 1 : 1;
-        for (int unit = 0; unit < nh + 2 * nkv; ++unit) {
-            int start, cw, cc, len;
-            const uint16_t* w;
-            if (unit < nh) {
-                start = unit * qk, cw = qd, cc = unit * qk, w = Lw->q_taps, len = qk;
-            } else if (unit < nh + nkv) {
-                const int kh = unit - nh;
-                start = qd + kh * qk, cw = kd, cc = kh * qk, w = Lw->k_taps, len = qk;
-            } else {
-                const int vh = unit - nh - nkv;
-                start = qd + kd + vh * vd, cw = vdim, cc = vh * vd, w = Lw->v_taps, len = vd;
-            }
-            const float* cur = proj + start;
-            memcpy(newh + start, cur, sizeof(float) * len);
-            float v[64];
-            for (int i = 0; i < len; ++i) v[i] = cq_f16_to_f32(w[cc + i]) * cur[i];
-            for (int j = 1; j < taps; ++j) {
-                const uint16_t* wj = w + (size_t)j * cw + cc;
-                if (hrows >= (size_t)j) {
-                    /* history row hrows - j: slot keep - j of the kept rows */
-                    const float* rr = hist + (size_t)(keep - j) * W + start;
-                    for (int i = 0; i < len; ++i) v[i] = fmaf(cq_f16_to_f32(wj[i]), rr[i], v[i]);
-                } else {
-                    for (int i = 0; i < len; ++i) v[i] = fmaf(cq_f16_to_f32(wj[i]), 0.0f, v[i]);
+        for (size_t i = 0; i < t; ++i) memcpy(hist + (p0 + i) * (size_t)W, proj + i * nq, sizeof(float) * W);
+        for (size_t i = 0; i < t; ++i) {
+            const size_t pos = p0 + i;
+            float* out = qkv + i * W;
+            for (int part = 0; part < 3; ++part) {
+                const int start = part == 0 ? 0 : part == 1 ? qd : qd + kd;
+                const int cw = part == 0 ? qd : part == 1 ? kd : vdim;
+                const uint16_t* w = part == 0 ? Lw->q_taps : part == 1 ? Lw->k_taps : Lw->v_taps;
+                const float* cur = hist + pos * (size_t)W + start;
+                for (int k = 0; k < cw; ++k) out[start + k] = cq_f16_to_f32(w[k]) * cur[k];
+                for (int j = 1; j < taps; ++j) {
+                    const uint16_t* wj = w + (size_t)j * cw;
+                    if (pos >= (size_t)j) {
+                        const float* rr = hist + (pos - j) * (size_t)W + start;
+                        for (int k = 0; k < cw; ++k) out[start + k] = fmaf(cq_f16_to_f32(wj[k]), rr[k], out[start + k]);
+                    } else {
+                        for (int k = 0; k < cw; ++k) out[start + k] = fmaf(cq_f16_to_f32(wj[k]), 0.0f, out[start + k]);
+                    }
                 }
             }
-            if (unit < nh + nkv) {
-                zcn16_inplace(v, unit < nh ? Lw->q_norm : Lw->k_norm, qk);
-                nf_rope_rotate(v, qk, cs, sn);
+            for (int hh = 0; hh < nh + nkv; ++hh) {
+                float* v = out + (hh < nh ? hh * qk : qd + (hh - nh) * qk);
+                zcn16_inplace(v, hh < nh ? Lw->q_norm : Lw->k_norm, qk);
+                nf_rope_rotate(v, qk, cs + i * 32, sn + i * 32);
             }
-            if (unit < nh) {
-                memcpy(qbuf + start, v, sizeof(float) * qk);
-            } else if (unit < nh + nkv) {
-                const int kh = unit - nh;
-                s->ks[l][p0 * nkv + kh] = cq_quant_i8(v, qk, s->k8[l] + (p0 * nkv + kh) * qk);
-            } else {
-                const int vh = unit - nh - nkv;
+            for (int kvh = 0; kvh < nkv; ++kvh) {
+                s->ks[l][pos * nkv + kvh] = cq_quant_i8(out + qd + kvh * qk, qk, s->k8[l] + (pos * nkv + kvh) * qk);
                 int8_t vq[64];
-                s->vs[l][p0 * nkv + vh] = cq_quant_i8(v, vd, vq);
-                for (int dm = 0; dm < vd; ++dm) s->v8t[l][((size_t)vh * vd + dm) * s->cap + p0] = vq[dm];
+                s->vs[l][pos * nkv + kvh] = cq_quant_i8(out + qd + kd + kvh * vd, vd, vq);
+                for (int dm = 0; dm < vd; ++dm) s->v8t[l][((size_t)kvh * vd + dm) * s->cap + pos] = vq[dm];
             }
         }
-        /* the history keeps its last taps - 1 rows, newest last */
-        if (keep > 1) memmove(hist, hist + W, sizeof(float) * (size_t)(keep - 1) * W);
-        memcpy(hist + (size_t)(keep - 1) * W, newh, sizeof(float) * W);
-        /* (h) attention per head, (i) its gate, A8 of the heads */
+        /* (h) attention per (row, head), (i) its gate, (j) A8 and out */
         {
             const int window = (c->sliding_window > 0 && !((c->global_mask >> l) & 1)) ? c->sliding_window : 0;
-            const size_t lo = window ? (p0 + 1 > (size_t)window ? p0 + 1 - (size_t)window : 0) : 0;
-            for (int hh = 0; hh < nh; ++hh) attend_head(m, s, l, qbuf + hh * qk, hh / group, lo, p0, att + hh * vd);
-            for (int hh = 0; hh < nh; ++hh)
-                for (int i = 0; i < vd; ++i) att[hh * vd + i] /= nf_nexp(-proj[W + hh * vd + i]) + 1.0f;
-            cq_qact* a = cq_qact_new(att, 1, nh * vd, m->out[l]->parts[0]->bits, 1);
+            for (size_t i = 0; i < t; ++i) {
+                const size_t pos = p0 + i;
+                const size_t lo = window ? (pos + 1 > (size_t)window ? pos + 1 - (size_t)window : 0) : 0;
+                for (int hh = 0; hh < nh; ++hh) {
+                    float* ah = att + (i * nh + hh) * vd;
+                    attend_head(m, s, l, qkv + i * W + hh * qk, hh / group, lo, pos, nested, ah);
+                    const float* gate = proj + i * nq + W + hh * vd;
+                    for (int k = 0; k < vd; ++k) ah[k] /= nf_nexp(-gate[k]) + 1.0f;
+                }
+            }
+            cq_qact* a = cq_qact_new(att, t, nh * vd, m->out[l]->parts[0]->bits, 1);
             cq_qlinear_matmul(m->out[l], a, o, nthreads);
             cq_qact_free(a);
         }
-        /* (k) post block and the Hadamard MLP */
+        /* (k) post block and the Hadamard MLP, the post and residual gates,
+         * the mHC write, per row */
         const float ga = 1.0f / (lexpf(-Lw->attn_gate) + 1.0f);
-        cq_zcn16(o, Lw->post_norm, d, on);
-        for (int i = 0; i < d; ++i) x2[i] = fmaf(on[i], ga, x1[i]);
-        cq_zcn16(x2, Lw->pre_hada, d, h2);
-        float wk[8];
-        nf_cond_weights(h2, d, Lw->cond_v, wk);
-        for (int i = 0; i < d; ++i) z[i] = h2[i] * cq_f16_to_f32(Lw->d1[i]);
-        for (int i = d; i < HN; ++i) z[i] = 0.0f;
-        nf_mix8(1, Lw->kron[0], 1, z, 0, mt, 16);
-        nf_mix8(0, mt, 0, Lw->kron[1], 1, bt, 16);
-        for (int j = 0; j < HN; ++j) cond[j] = 1.0f;
-        for (int k = 0; k < HADA_COND_RANK; ++k)
-            for (int j = 0; j < HN; ++j) cond[j] = fmaf(cq_f16_to_f32(Lw->cond_u[(size_t)k * HN + j]), wk[k], cond[j]);
-        for (int j = 0; j < HN; ++j)
-            zs[j] = fmaf(bt[m->perm1[j]], cond[j] * cq_f16_to_f32(Lw->d2[j]), cq_f16_to_f32(Lw->b2[j]));
-        for (int j = 0; j < HN; ++j) zs[j] /= nf_nexp(-zs[j]) + 1.0f;
-        nf_mix8(1, Lw->kron[2], 1, zs, 0, mt, 16);
-        nf_mix8(0, mt, 0, Lw->kron[3], 1, bt, 16);
-        for (int j = 0; j < HN; ++j) zs[j] = bt[m->perm2[j]] * cq_f16_to_f32(Lw->d3[j]);
-        nf_mix8(1, Lw->kron[4], 1, zs, 0, mt, 16);
-        nf_mix8(0, mt, 0, Lw->kron[5], 1, t3, d / NB / 8 * 4);
-        /* the post and residual gates, then the mHC write */
-        float hpost[4], zres[16], hres[16];
-        for (int j = 0; j < 4; ++j) {
-            const float off = j == lane ? 0.0f : -4.0f;
-            const float zz = ((p[n + j] * Lw->a_post) + off) + Lw->b_post[j];
-            hpost[j] = 2.0f / (lexpf(-zz) + 1.0f);
-        }
-        for (int k = 0; k < 16; ++k) zres[k] = fmaf(p[2 * n + k], Lw->a_res, Lw->b_res[k]);
-        nf_sinkhorn64(zres, hres);
-        for (int ch = 0; ch < d; ++ch) {
-            const float y = (x2[ch] + t3[ch] * cq_f16_to_f32(Lw->d4[ch])) - u[ch];
-            float old[4];
-            for (int b = 0; b < 4; ++b) old[b] = xs[b * d + ch];
-            for (int a2 = 0; a2 < n; ++a2) {
-                float v = y * hpost[a2];
-                for (int b = 0; b < 4; ++b) v = fmaf(old[b], hres[a2 * n + b], v);
-                xs[a2 * d + ch] = v;
+        for (size_t i = 0; i < t; ++i) {
+            const float* pr = p + i * ncols;
+            float* x = xs + i * nc;
+            cq_zcn16(o + i * d, Lw->post_norm, d, on);
+            for (int k = 0; k < d; ++k) x2[k] = fmaf(on[k], ga, x1[i * d + k]);
+            cq_zcn16(x2, Lw->pre_hada, d, h2);
+            float wk[8];
+            nf_cond_weights(h2, d, Lw->cond_v, wk);
+            for (int k = 0; k < d; ++k) z[k] = h2[k] * cq_f16_to_f32(Lw->d1[k]);
+            for (int k = d; k < HN; ++k) z[k] = 0.0f;
+            nf_mix8(1, Lw->kron[0], 1, z, 0, mt, 16);
+            nf_mix8(0, mt, 0, Lw->kron[1], 1, bt, 16);
+            for (int j = 0; j < HN; ++j) cond[j] = 1.0f;
+            for (int k = 0; k < HADA_COND_RANK; ++k)
+                for (int j = 0; j < HN; ++j) cond[j] = fmaf(cq_f16_to_f32(Lw->cond_u[(size_t)k * HN + j]), wk[k], cond[j]);
+            for (int j = 0; j < HN; ++j)
+                zs[j] = fmaf(bt[m->perm1[j]], cond[j] * cq_f16_to_f32(Lw->d2[j]), cq_f16_to_f32(Lw->b2[j]));
+            for (int j = 0; j < HN; ++j) zs[j] /= nf_nexp(-zs[j]) + 1.0f;
+            nf_mix8(1, Lw->kron[2], 1, zs, 0, mt, 16);
+            nf_mix8(0, mt, 0, Lw->kron[3], 1, bt, 16);
+            for (int j = 0; j < HN; ++j) zs[j] = bt[m->perm2[j]] * cq_f16_to_f32(Lw->d3[j]);
+            nf_mix8(1, Lw->kron[4], 1, zs, 0, mt, 16);
+            nf_mix8(0, mt, 0, Lw->kron[5], 1, t3, d / NB / 8 * 4);
+            float hpost[4], zres[16], hres[16];
+            for (int j = 0; j < 4; ++j) {
+                const float off = j == lane ? 0.0f : -4.0f;
+                const float zz = ((pr[n + j] * Lw->a_post) + off) + Lw->b_post[j];
+                hpost[j] = 2.0f / (lexpf(-zz) + 1.0f);
+            }
+            for (int k = 0; k < 16; ++k) zres[k] = fmaf(pr[2 * n + k], Lw->a_res, Lw->b_res[k]);
+            nf_sinkhorn64(zres, hres);
+            for (int ch = 0; ch < d; ++ch) {
+                const float y = (x2[ch] + t3[ch] * cq_f16_to_f32(Lw->d4[ch])) - u[i * d + ch];
+                float old[4];
+                for (int b = 0; b < 4; ++b) old[b] = x[b * d + ch];
+                for (int a2 = 0; a2 < n; ++a2) {
+                    float v = y * hpost[a2];
+                    for (int b = 0; b < 4; ++b) v = fmaf(old[b], hres[a2 * n + b], v);
+                    x[a2 * d + ch] = v;
+                }
             }
         }
     }
-    s->hrows += 1;
 
-    /* head: lane mean, final norm, tied embedding (step.rs:706-728) */
-    float* mean = (float*)malloc(sizeof(float) * d);
-    for (int ch = 0; ch < d; ++ch) mean[ch] = (((xs[ch] + xs[d + ch]) + xs[2 * d + ch]) + xs[3 * d + ch]) * 0.25f;
-    zcn(mean, m->final_norm, d, hloc);
+    /* head of the last row: lane mean, final norm, tied embedding
+     * (step.rs:706-728, chunk.rs:322-347) */
     if (logits) {
+        const float* x = xs + (t - 1) * nc;
+        float* mean = (float*)malloc(sizeof(float) * d);
+        for (int ch = 0; ch < d; ++ch) mean[ch] = (((x[ch] + x[d + ch]) + x[2 * d + ch]) + x[3 * d + ch]) * 0.25f;
+        zcn(mean, m->final_norm, d, hloc);
         cq_qact* a = cq_qact_new(hloc, 1, d, m->embedding->bits, 1);
         float* full = (float*)malloc(sizeof(float) * m->embedding->out);
         cq_matmul_into(m->embedding, a, full, m->embedding->out, 0, nthreads);
         memcpy(logits, full, sizeof(float) * c->out_rows);
-        free(full);
+        free(full), free(mean);
         cq_qact_free(a);
     }
-    free(mean), free(row), free(ekv), free(evals), free(nx), free(nx8), free(u), free(x1), free(hloc), free(proj);
-    free(qbuf), free(att), free(o), free(on), free(x2), free(h2), free(ea), free(eb), free(z), free(mt), free(bt);
-    free(cond), free(zs), free(t3), free(newh);
+    free(xs), free(row), free(ekv), free(evals), free(cs), free(sn), free(nx), free(nx8), free(u), free(x1), free(p);
+    free(hloc), free(proj), free(qkv), free(att), free(o), free(on), free(x2), free(h2), free(ea), free(eb), free(z);
+    free(mt), free(bt), free(cond), free(zs), free(t3);
     return 0;
+}
+
+int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int nthreads) {
+    return nf_rows(m, s, &tok, 1, logits, nthreads);
+}
+
+int nf_chunk(const nf_model* m, nf_session* s, const uint32_t* toks, size_t t, float* logits, int nthreads) {
+    return t == 1 ? nf_step(m, s, toks[0], logits, nthreads) : nf_rows(m, s, toks, t, logits, nthreads);
 }

@@ -46,8 +46,11 @@ void nf_set_globals(nf_model* m, const float* final_norm, const int32_t* perm1, 
 nf_session* nf_session_new(const nf_model* m, size_t cap);
 void nf_session_free(const nf_model* m, nf_session* s);
 size_t nf_session_len(const nf_session* s);
-/* One decode step; logits [out_rows] (NULL: none).  0 or -1. */
+/* One decode step (step_native); logits [out_rows] (NULL: none).  0 or -1. */
 int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int nthreads);
+/* One prompt chunk of t <= 32 tokens (chunk_job; a single token is a step);
+ * logits of its last row.  0 or -1. */
+int nf_chunk(const nf_model* m, nf_session* s, const uint32_t* toks, size_t t, float* logits, int nthreads);
 
 /* Helpers, exposed for their own checks. */
 float nf_nexp(float x);

@@ -51,6 +51,7 @@ def _lib():
             "nf_session_free": (None, [P, P]),
             "nf_session_len": (C.c_size_t, [P]),
             "nf_step": (C.c_int, [P, P, C.c_uint32, P, C.c_int]),
+            "nf_chunk": (C.c_int, [P, P, P, C.c_size_t, P, C.c_int]),
             "nf_nexp": (C.c_float, [C.c_float]),
             "nf_rope_rotate": (None, [P, C.c_size_t, P, P]),
             "nf_cond_weights": (None, [P, C.c_size_t, P, P]),
@@ -230,6 +231,25 @@ class Session:
         if rc != 0:
             raise ValueError("step outside the session's capacity or geometry")
         return out
+
+    def chunk(self, toks) -> np.ndarray:
+        """One chunk of <= 32 tokens (chunk_job, infer/chunk.rs:32-358; one
+        token is a step): the last row's logits."""
+        t = np.ascontiguousarray(np.asarray(toks, dtype=np.uint32).reshape(-1))
+        out = np.zeros(self.f.cfg.out_rows, dtype=np.float32)
+        rc = _lib().nf_chunk(self.f.m, self.s, _p(t), t.size, _p(out), self.f.threads)
+        if rc != 0:
+            raise ValueError("chunk outside the session's capacity or geometry")
+        return out
+
+    def feed(self, toks) -> np.ndarray:
+        """Model::forward with Outputs::LastLogits as forward_native feeds it
+        (infer.rs:1105-1132): chunks of 32, a single-token chunk as a step."""
+        toks = np.asarray(toks, dtype=np.uint32).reshape(-1)
+        last = None
+        for i in range(0, toks.size, 32):
+            last = self.chunk(toks[i:i + 32])
+        return last
 
     def __len__(self):
         return _lib().nf_session_len(self.s)

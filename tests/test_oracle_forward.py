@@ -170,3 +170,61 @@ def test_attention_window_bounds_the_receptive_field():
     g1, g2 = fg.session(32), fg.session(32)
     last = [(g1.step(a), g2.step(b)) for a, b in zip(toks, alt)][-1]
     assert not np.array_equal(last[0], last[1])
+
+
+# ------------------------------------------------------------ prompt chunks
+# chunk_job (infer/chunk.rs:32-358) is the step's arithmetic row for row
+# except the projections (the prefill combine over the chunk's rows), the
+# RoPE rows (sincosf per position) and attention (nested chunking).  What
+# pins it beyond the shared, step-checked code: a chunk's logits stay
+# within the combines' rounding of the step-by-step feed; the same window
+# bound; determinism; a chunk fed after steps and steps after a chunk.
+
+def _rel(a, b):
+    return float(np.abs(a - b).max() / np.abs(b).max())
+
+
+def test_chunk_close_to_steps():
+    f = _model((1,), (1,), 8)
+    toks = o.random_tokens(40, 300, seed=21)
+    a, b = f.session(48), f.session(48)
+    for t in toks:
+        la = a.step(t)
+    lb = b.feed(toks)   # 32 + 8
+    assert len(a) == len(b) == 40
+    assert not np.array_equal(la, lb)        # a different combine order
+    assert _rel(lb, la) < 2e-2 and int(np.argmax(lb)) == int(np.argmax(la))
+
+
+def test_chunk_deterministic_and_split_invariant_state():
+    f = _model((1,), (1,), 8)
+    toks = o.random_tokens(24, 300, seed=22)
+    a, b = f.session(40), f.session(40)
+    la, lb = a.feed(toks), b.feed(toks)
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+    # a step after the chunk continues from the chunk's RoPE row and caches
+    na, nb = a.step(7), b.step(7)
+    assert np.array_equal(na.view(np.uint32), nb.view(np.uint32)) and len(a) == 25
+
+
+def test_chunk_window_bounds_the_receptive_field():
+    f = _model((), (), 3)
+    toks = o.random_tokens(24, 300, seed=23)
+    alt = toks.copy()
+    alt[0] = (alt[0] + 1) % 300
+    s1, s2 = f.session(32), f.session(32)
+    # tokens 0..15 as one chunk, then 16..23 as one chunk: the last logits
+    # (position 23 >= 3 x (3 + 2)) cannot see token 0
+    s1.chunk(toks[:16]), s2.chunk(alt[:16])
+    l1, l2 = s1.chunk(toks[16:]), s2.chunk(alt[16:])
+    assert np.array_equal(l1.view(np.uint32), l2.view(np.uint32))
+    fg = _model((1,), (), 3)
+    g1, g2 = fg.session(32), fg.session(32)
+    assert not np.array_equal(g1.feed(toks), g2.feed(alt))
+
+
+def test_chunk_rejects_overflow():
+    f = _model((1,), (1,), 8)
+    s = f.session(8)
+    with pytest.raises(ValueError):
+        s.chunk(o.random_tokens(9, 300, seed=1))
