@@ -188,11 +188,12 @@ int nh_session_len(const nh_session* s);
 /* Back to an empty session (Model::session again, without reallocating). */
 int nh_session_reset(nh_session* s);
 /* Model::forward (model.rs:304-306) with Outputs::LastLogits for HOST token
- * ids, one step_native (crates/needle-engine/src/infer/step.rs:171-760) per
- * token; `logits` (DEVICE, out_rows floats, or NULL) receives the last
- * token's.  The reference feeds multi-token input in chunks of 32 through
- * its prefill path (infer.rs:1105-1132); one step per token is the same
- * arithmetic in decode order. */
+ * ids, fed as forward_native feeds them (crates/needle-engine/src/infer.rs:
+ * 1105-1132): chunks of 32 tokens through chunk_job
+ * (crates/needle-engine/src/infer/chunk.rs:32-358, the products over the
+ * chunk's rows with the prefill combine), a single-token chunk through
+ * step_native (crates/needle-engine/src/infer/step.rs:171-760).  `logits`
+ * (DEVICE, out_rows floats, or NULL) receives the last token's. */
 int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* stream);
 /* The greedy loop of generate (crates/needle-engine/src/generate.rs:87-139)
  * at temperature 0, on the device: `steps` times argmax of the current

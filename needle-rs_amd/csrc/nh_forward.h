@@ -26,12 +26,15 @@ constexpr int MAX_TABLES = 16;
 constexpr int ENGRAM_TAPS = 4;      // ENGRAM_CONV_TAPS (config.rs:10)
 constexpr int ATT_CHUNK_MAX = 256;  // key_chunks never makes a chunk longer
 constexpr int ATT_THREADS = 256;
+constexpr int FWD_ROWS = 32;        // token rows of one feed (a prompt chunk, infer.rs:1105-1132)
+constexpr int ACT_ROWS = 64;        // rows of an A8 buffer (the GEMM reads whole 64-token tiles)
 
 struct Dims {
     int d, nh, nkv, qk, vd, lanes, taps, layers;
     int W;      // (nh + nkv) * qk + nkv * vd: the pre-tap q | k | v width
     int nq;     // W + nh * vd: the fused q | k | v | gate rows
-    int keep;   // history rows kept: taps - 1 (at least 1)
+    int keep;   // history rows the conv reads: taps - 1 (at least 1)
+    int hist_slots;  // the history ring: keep + FWD_ROWS slots, position p at p % hist_slots
     int vocab, out_rows;
     int sites, ntab, eheads, seed_stride, slots, sub, dilation;
     int orders[4];
@@ -56,41 +59,45 @@ struct LayerDev {
 struct Globals {
     const float* final_norm;  // [d] f32
     const int32_t *perm1, *perm2;
+    const float *freq;        // RoPE: powf(theta, i * (-2 / qk))
     const float *sd, *cd;     // RoPE: sincosf(freq)
     const float* etaps;       // [sites][4][d] f32
 };
 
-// One session's state, all device memory.
+// One session's state, all device memory.  Row buffers hold the rows of
+// the current feed (FWD_ROWS at most); activations feed the products.
 struct SessDev {
-    float* xs;        // [4][d] residual lanes
-    float* u;         // [d] mHC read of the layer
-    float* x1;        // [d] after the engram gate
-    float* p;         // [64]: the 24 mHC gate projections, then hpost [4]
-                      // at 24 and the Sinkhorn mixing hres [16] at 28
-    float* proj;      // [nq] q | k | v | gate
-    float* qbuf;      // [nh][qk] rotated queries
-    float* o;         // [d] attention output projection
-    float* ekv;       // [sites][2d] engram key | value
-    float* evals;     // [sites][d] engram conv
+    float* xs;        // [rows][4][d] residual lanes
+    float* u;         // [rows][d] mHC read of the layer
+    float* x1;        // [rows][d] after the engram gate
+    float* p;         // [rows][64]: the 24 mHC gate projections, then hpost
+                      // [4] at 24 and the Sinkhorn mixing hres [16] at 28
+    float* proj;      // [rows][nq] q | k | v | gate
+    float* qbuf;      // [rows][nh][qk] rotated queries
+    float* o;         // [rows][d] attention output projection
+    float* ekv;       // [sites][rows][2d] engram key | value
+    float* evals;     // [sites][rows][d] engram conv
     float* logits;    // [out_rows]
-    float* rope_c;    // [qk/2]
+    float* rope_c;    // [rows][qk/2] the feed's RoPE rows
     float* rope_s;
+    float* rope_pc;   // [qk/2] the newest position's RoPE row
+    float* rope_ps;
     uint32_t* tokens; // [cap]
-    float* po;        // [nh][max_chunks][vd] attention chunk partials
-    float* pm;        // [nh][max_chunks]
-    float* psum;      // [nh][max_chunks]
-    float* hist;      // [layers][keep][W] ring: position p in slot p % keep
+    float* po;        // [rows][nh][max_chunks][vd] attention chunk partials
+    float* pm;        // [rows][nh][max_chunks]
+    float* psum;      // [rows][nh][max_chunks]
+    float* hist;      // [layers][hist_slots][W] ring of pre-tap rows
     int8_t* k8;       // [layers][cap][nkv][qk]
     float* ks;        // [layers][cap][nkv]
     int8_t* v8t;      // [layers][nkv][vd][cap]
     float* vs;        // [layers][cap][nkv]
     int8_t* ev8;      // [sites][cap][d]
     float* evs;       // [sites][cap][d / 32]
-    int8_t* xq_in;    // A8 activations: the layer input (K = d), rows 0
-    float* sx_in;
-    int8_t* xq_att;   // the gated heads (K = nh * vd)
+    int8_t* xq_in;    // [ACT_ROWS][G(d)][128] the layer inputs (K = d)
+    float* sx_in;     // [ACT_ROWS][G(d)]
+    int8_t* xq_att;   // [ACT_ROWS][G(nh vd)][128] the gated heads
     float* sx_att;
-    int8_t* xq_eng;   // the engram rows, one row per site (K = d)
+    int8_t* xq_eng;   // [sites][ACT_ROWS][G(d)][128] the engram rows
     float* sx_eng;
     int32_t* argmax;  // scratch of the greedy pick
 };
@@ -109,20 +116,21 @@ struct BeginArgs {
     int eng_bits[MAX_SITES];  // code width of each site's key | value matrix
 };
 
-// Launchers (nh_forward.hip).
-// The start of a step: the embedding row into the lanes, the RoPE rows of
-// the position, and per engram site the hashed table rows as A8 rows.
-hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const BeginArgs& B, int p0, hipStream_t s);
-hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, int p0, hipStream_t s);
-// The per-layer boundary: the Hadamard MLP and mHC write of layer `prev`
-// (null: none, the lanes hold the embedding row), then the mHC read, engram
-// gate, input norm and A8 of layer `next` (null: the head's lane mean,
-// final norm and A8 instead).
+// Launchers (nh_forward.hip).  A feed is rows p0 .. p0 + t - 1 (t <= 32).
+// The start of a feed: the embedding rows into the lanes, the RoPE rows, and
+// per engram site the hashed table rows as A8 rows.
+hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const BeginArgs& B, int p0, int t,
+                     hipStream_t s);
+hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, int p0, int t, hipStream_t s);
+// The per-layer boundary for rows row0 .. row0 + rows - 1: the Hadamard MLP
+// and mHC write of layer `prev` (null: none, the lanes hold the embedding
+// rows), then the mHC read, engram gate, input norm and A8 of layer `next`
+// (null: the head's lane mean, final norm and A8 into activation row 0).
 hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
-                     int in_bits, int head_bits, hipStream_t s);
-hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, hipStream_t s);
-hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, hipStream_t s);
-hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
+                     int row0, int rows, int in_bits, int head_bits, hipStream_t s);
+hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, hipStream_t s);
+hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, hipStream_t s);
+hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int p0, int t, int out_bits,
                         hipStream_t s);
 hipError_t fwd_argmax(const float* logits, int n, uint32_t* dst, hipStream_t s);
 hipError_t fwd_phi8(const float* rows, int nrows, int width, int8_t* q, float* scale, hipStream_t s);

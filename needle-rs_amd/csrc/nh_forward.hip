@@ -118,10 +118,12 @@ __device__ __forceinline__ float wave_quant_scale(float v) {
     return m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
 }
 
-// key_chunks (infer.rs:2093-2101): the chunk count and length of n keys.
-__device__ __forceinline__ void key_chunks(int n, int nkv, int& count, int& size) {
+// key_chunks (infer.rs:2093-2101): the chunk count and length of n keys,
+// at least k = 2 NATIVE_TEAM / nkv chunks past 64 k keys, or 1 for a
+// feed's rows (nested, infer.rs:1888).
+__device__ __forceinline__ void key_chunks(int n, int nkv, bool nested, int& count, int& size) {
     int k = 2 * NATIVE_TEAM / nkv;
-    if (k < 1) k = 1;
+    if (k < 1 || nested) k = 1;
     int c = (n + 255) / 256;
     if (k * 64 <= n && c < k) c = k;
     if (c < 1) c = 1;
@@ -138,107 +140,140 @@ __device__ __forceinline__ int window_lo(int window, int p0) {
 }  // namespace
 
 // ------------------------------------------------------------------ begin
-// Waves 0 .. Gd-1: embedding row groups (step.rs:228-235: row * sqrt(d)
-// into every lane).  Then per site e and group g: the hashed row of table
-// g (step.rs:245-269 with the hash of infer.rs engram rows) dequantized and
-// rotated (QMat::row), A8-prepared as group g of the site's row
-// (QAct::new over the concatenated rows); missing rows are zeros.  The last
-// wave: the RoPE rows of p0 (rope_rows, infer.rs:1716-1747), by the
-// angle-addition recurrence from the previous position, exact (cos 0, sin 0)
-// = (1, 0) at position 0.
-__global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, BeginArgs B, int p0) {
+// Per row i of the feed (position p0 + i): waves for the embedding row
+// groups (step.rs:228-235, chunk.rs:58-66: row * sqrt(d) into every lane),
+// then per engram site e and group g the hashed row of table g
+// (engram_native, infer.rs:1261-1275) dequantized and rotated (QMat::row),
+// A8-prepared as group g of the site's activation row i (QAct::new over the
+// concatenated rows); missing rows are zeros.  The last wave: the RoPE rows
+// (rope_rows, infer.rs:1716-1747): for one token after a known position the
+// angle-addition recurrence from it, else sincosf(freq * pos) per row.
+__global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, BeginArgs B, int p0, int t) {
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     const int Gd = (D.d + GROUP - 1) / GROUP;
-    const int eng_waves = D.sites * Gd;
-    if (wave < Gd) {
-        const uint32_t tok = S.tokens[p0];
-        float v0, v1;
-        if (B.emb.bits == 2)
-            row_group<2>(B.emb.codes, B.emb.norms, B.emb.fsel, B.emb.groups, tok, wave, lane, v0, v1);
-        else
-            row_group<4>(B.emb.codes, B.emb.norms, B.emb.fsel, B.emb.groups, tok, wave, lane, v0, v1);
-        const float scale = __builtin_sqrtf((float)D.d);
-        const int i0 = wave * GROUP + lane, i1 = i0 + 64;
-        for (int b = 0; b < MHC_LANES; ++b) {
-            if (i0 < D.d) S.xs[b * D.d + i0] = v0 * scale;
-            if (i1 < D.d) S.xs[b * D.d + i1] = v1 * scale;
-        }
-    } else if (wave < Gd + eng_waves) {
-        const int e = (wave - Gd) / Gd, g = (wave - Gd) % Gd;
-        float v0 = 0.0f, v1 = 0.0f;
-        if (g < D.ntab) {
-            const int oi = g / D.eheads, h = g % D.eheads, order = D.orders[oi];
-            if (p0 + 1 >= order) {
-                uint32_t acc = ENGRAM_SEED * (uint32_t)(oi * D.seed_stride + h + 1);
-                for (int j = 0; j < order; ++j) acc = (acc ^ S.tokens[p0 - j]) * ENGRAM_PRIME;
-                acc ^= acc >> 15;
-                const uint32_t row = (uint32_t)g * (uint32_t)D.slots + acc % (uint32_t)D.slots;
-                const RowSrc& t = B.tab[e];
-                if (t.bits == 2)
-                    row_group<2>(t.codes, t.norms, t.fsel, t.groups, row, 0, lane, v0, v1);
-                else
-                    row_group<4>(t.codes, t.norms, t.fsel, t.groups, row, 0, lane, v0, v1);
+    const int per_row = Gd * (1 + D.sites);
+    if (wave < t * per_row) {
+        const int i = wave / per_row, r = wave % per_row, pos = p0 + i;
+        if (r < Gd) {
+            const uint32_t tok = S.tokens[pos];
+            float v0, v1;
+            if (B.emb.bits == 2)
+                row_group<2>(B.emb.codes, B.emb.norms, B.emb.fsel, B.emb.groups, tok, r, lane, v0, v1);
+            else
+                row_group<4>(B.emb.codes, B.emb.norms, B.emb.fsel, B.emb.groups, tok, r, lane, v0, v1);
+            const float scale = __builtin_sqrtf((float)D.d);
+            const int i0 = r * GROUP + lane, i1 = i0 + 64;
+            float* xs = S.xs + (size_t)i * MHC_LANES * D.d;
+            for (int b = 0; b < MHC_LANES; ++b) {
+                if (i0 < D.d) xs[b * D.d + i0] = v0 * scale;
+                if (i1 < D.d) xs[b * D.d + i1] = v1 * scale;
             }
+        } else {
+            const int e = (r - Gd) / Gd, g = (r - Gd) % Gd;
+            float v0 = 0.0f, v1 = 0.0f;
+            if (g < D.ntab) {
+                const int oi = g / D.eheads, h = g % D.eheads, order = D.orders[oi];
+                if (pos + 1 >= order) {
+                    uint32_t acc = ENGRAM_SEED * (uint32_t)(oi * D.seed_stride + h + 1);
+                    for (int j = 0; j < order; ++j) acc = (acc ^ S.tokens[pos - j]) * ENGRAM_PRIME;
+                    acc ^= acc >> 15;
+                    const uint32_t row = (uint32_t)g * (uint32_t)D.slots + acc % (uint32_t)D.slots;
+                    const RowSrc& tb = B.tab[e];
+                    if (tb.bits == 2)
+                        row_group<2>(tb.codes, tb.norms, tb.fsel, tb.groups, row, 0, lane, v0, v1);
+                    else
+                        row_group<4>(tb.codes, tb.norms, tb.fsel, tb.groups, row, 0, lane, v0, v1);
+                }
+            }
+            const size_t unit = ((size_t)e * ACT_ROWS + i) * Gd + g;
+            a8_group(v0, v1, lane, B.eng_bits[e], S.xq_eng + unit * GROUP, S.sx_eng + unit);
         }
-        a8_group(v0, v1, lane, B.eng_bits[e], S.xq_eng + ((size_t)e * Gd + g) * GROUP, S.sx_eng + e * Gd + g);
-    } else if (wave == Gd + eng_waves) {
+    } else if (wave == t * per_row) {
         const int half = D.qk / 2;
         if (lane < half) {
-            float c = 1.0f, s = 0.0f;
-            if (p0 > 0) {
-                const float oc = S.rope_c[lane], os = S.rope_s[lane];
+            float c, sn;
+            if (t == 1 && p0 > 0) {
+                const float oc = S.rope_pc[lane], os = S.rope_ps[lane];
                 c = __builtin_fmaf(-G.sd[lane], os, G.cd[lane] * oc);
-                s = __builtin_fmaf(G.sd[lane], oc, G.cd[lane] * os);
+                sn = __builtin_fmaf(G.sd[lane], oc, G.cd[lane] * os);
+                S.rope_c[lane] = c;
+                S.rope_s[lane] = sn;
+            } else {
+                for (int i = 0; i < t; ++i) {
+                    double sv, cv;
+                    sincos((double)(G.freq[lane] * (float)(p0 + i)), &sv, &cv);
+                    c = (float)cv;
+                    sn = (float)sv;
+                    S.rope_c[i * half + lane] = c;
+                    S.rope_s[i * half + lane] = sn;
+                }
             }
-            S.rope_c[lane] = c;
-            S.rope_s[lane] = s;
+            S.rope_pc[lane] = c;
+            S.rope_ps[lane] = sn;
         }
     }
 }
 
-hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const BeginArgs& B, int p0, hipStream_t s) {
+hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const BeginArgs& B, int p0, int t,
+                     hipStream_t s) {
     const int Gd = (D.d + GROUP - 1) / GROUP;
-    const int waves = Gd + D.sites * Gd + 1;
-    hipLaunchKernelGGL(k_begin, dim3((waves + 3) / 4), dim3(256), 0, s, D, G, S, B, p0);
+    const int waves = t * Gd * (1 + D.sites) + 1;
+    hipLaunchKernelGGL(k_begin, dim3((waves + 3) / 4), dim3(256), 0, s, D, G, S, B, p0, t);
     return hipGetLastError();
 }
 
 // ---------------------------------------------------------- engram history
-// Per site: the value half of key | value as int8 groups of 32 appended to
-// the site's history, then the dilated causal conv over the last
-// ENGRAM_TAPS history rows (step.rs:346-391): dst = fma(tap, s * q, dst)
-// from the newest row back, stopping at position 0.
-__global__ __launch_bounds__(1024) void k_engram_hist(Dims D, Globals G, SessDev S, int p0) {
-    const int e = blockIdx.x, k = threadIdx.x, d = D.d;
-    const bool on = k < d;
-    const float v = on ? S.ekv[(size_t)e * 2 * d + d + k] : 0.0f;
+// Per site and row: the value half of key | value as int8 groups of 32
+// appended to the site's history, then the dilated causal conv over the
+// last ENGRAM_TAPS history rows (infer.rs:1283-1330): dst = fma(tap, s * q,
+// dst) from the newest row back, stopping at position 0.  A tap on a row of
+// the same feed re-quantizes that row here (the same values its own block
+// appends), so no block reads another's writes.
+__device__ __forceinline__ int8_t group_quant32(float v, float& s) {
     float m = fabsf(v);
 #pragma unroll
     for (int o = 1; o < 32; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    const float s = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
-    const int8_t q = quant_one(v, 1.0f / s);
-    if (!on) return;
+    s = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
+    return quant_one(v, 1.0f / s);
+}
+
+__global__ __launch_bounds__(1024) void k_engram_hist(Dims D, Globals G, SessDev S, int p0) {
+    const int e = blockIdx.x, i = blockIdx.y, k = threadIdx.x, d = D.d, pos = p0 + i;
+    const bool on = k < d;
+    const float* kv = S.ekv + (size_t)e * FWD_ROWS * 2 * d;
+    float s;
+    const int8_t q = group_quant32(on ? kv[(size_t)i * 2 * d + d + k] : 0.0f, s);
     const int gs = d / 32;
     int8_t* ev8 = S.ev8 + (size_t)e * D.cap * d;
     float* evs = S.evs + (size_t)e * D.cap * gs;
-    ev8[(size_t)p0 * d + k] = q;
-    if ((k & 31) == 0) evs[(size_t)p0 * gs + k / 32] = s;
+    if (on) {
+        ev8[(size_t)pos * d + k] = q;
+        if ((k & 31) == 0) evs[(size_t)pos * gs + k / 32] = s;
+    }
     float dst = 0.0f;
     for (int j = 0; j < ENGRAM_TAPS; ++j) {
-        if (p0 < j * D.dilation) break;
-        const int pj = p0 - j * D.dilation;
-        const float qs = j == 0 ? s : evs[(size_t)pj * gs + k / 32];
-        const int8_t q8 = j == 0 ? q : ev8[(size_t)pj * d + k];
-        const float tw = G.etaps[((size_t)e * ENGRAM_TAPS + j) * d + k];
+        if (pos < j * D.dilation) break;
+        const int pj = pos - j * D.dilation;
+        float qs;
+        int8_t q8;
+        if (j == 0) {
+            qs = s, q8 = q;
+        } else if (pj >= p0) {
+            q8 = group_quant32(on ? kv[(size_t)(pj - p0) * 2 * d + d + k] : 0.0f, qs);
+        } else {
+            qs = on ? evs[(size_t)pj * gs + k / 32] : 0.0f;
+            q8 = on ? ev8[(size_t)pj * d + k] : 0;
+        }
+        const float tw = on ? G.etaps[((size_t)e * ENGRAM_TAPS + j) * d + k] : 0.0f;
         dst = __builtin_fmaf(tw, qs * (float)q8, dst);
     }
-    S.evals[(size_t)e * d + k] = dst;
+    if (on) S.evals[((size_t)e * FWD_ROWS + i) * d + k] = dst;
 }
 
-hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, int p0, hipStream_t s) {
+hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, int p0, int t, hipStream_t s) {
     if (D.sites <= 0) return hipSuccess;
     const int threads = (D.d + 63) / 64 * 64;
-    hipLaunchKernelGGL(k_engram_hist, dim3(D.sites), dim3(threads), 0, s, D, G, S, p0);
+    hipLaunchKernelGGL(k_engram_hist, dim3(D.sites, t), dim3(threads), 0, s, D, G, S, p0);
     return hipGetLastError();
 }
 
@@ -483,8 +518,8 @@ __device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const
     if (t < d) {
         q.norm = h2f(N.norm_in[t]);
         if (N.site >= 0) {
-            q.kr = S.ekv[(size_t)N.site * 2 * d + t];
-            q.ev = S.evals[(size_t)N.site * d + t];
+            q.kr = S.ekv[(size_t)N.site * FWD_ROWS * 2 * d + t];
+            q.ev = S.evals[(size_t)N.site * FWD_ROWS * d + t];
         }
     }
     const int per = nc / 16;  // uint4 per row
@@ -660,38 +695,50 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
 }  // namespace
 
 __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int has_prev,
-                                              int has_next, int in_bits, int head_bits) {
+                                              int has_next, int row0, int in_bits, int head_bits) {
     __shared__ LayerShared sh;
-    const int t = threadIdx.x, d = D.d, nc = MHC_LANES * d;
+    const int t = threadIdx.x, d = D.d, nc = MHC_LANES * d, Gd = (d + GROUP - 1) / GROUP;
+    // this block's row of every row buffer
+    const int row = row0 + blockIdx.x;
+    SessDev R = S;
+    R.xs += (size_t)row * nc;
+    R.u += (size_t)row * d;
+    R.x1 += (size_t)row * d;
+    R.p += (size_t)row * 64;
+    R.o += (size_t)row * d;
+    R.ekv += (size_t)row * 2 * d;
+    R.evals += (size_t)row * d;
+    R.xq_in += (size_t)row * Gd * GROUP;
+    R.sx_in += (size_t)row * Gd;
     // every global read first
-    for (int i = t; i < nc; i += LT) sh.xs[i] = S.xs[i];
+    for (int i = t; i < nc; i += LT) sh.xs[i] = R.xs[i];
     OutRegs qo{};
     if (has_prev) {
-        qo = load_out(D, G, S, P, sh);
+        qo = load_out(D, G, R, P, sh);
         if (t < d) sh.o[t] = qo.o;
     }
     InRegs qi{};
     float fnorm = 0.0f;
     if (has_next)
-        qi = load_in(D, S, N);
+        qi = load_in(D, R, N);
     else if (t < d)
         fnorm = G.final_norm[t];
     __syncthreads();
     if (has_prev) {
         layer_out(D, P, qo, sh);
-        for (int i = t; i < nc; i += LT) S.xs[i] = sh.xs[i];
+        for (int i = t; i < nc; i += LT) R.xs[i] = sh.xs[i];
     }
     if (has_next)
-        layer_in(D, S, N, qi, in_bits, sh);
+        layer_in(D, R, N, qi, in_bits, sh);
     else
-        head_in(D, S, fnorm, head_bits, sh);
+        head_in(D, S, fnorm, head_bits, sh);  // A8 into activation row 0
 }
 
 hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
-                     int in_bits, int head_bits, hipStream_t s) {
+                     int row0, int rows, int in_bits, int head_bits, hipStream_t s) {
     const LayerDev none{};
-    hipLaunchKernelGGL(k_layer, dim3(1), dim3(LT), 0, s, D, G, S, prev ? *prev : none, next ? *next : none,
-                       prev ? 1 : 0, next ? 1 : 0, in_bits, head_bits);
+    hipLaunchKernelGGL(k_layer, dim3(rows), dim3(LT), 0, s, D, G, S, prev ? *prev : none, next ? *next : none,
+                       prev ? 1 : 0, next ? 1 : 0, row0, in_bits, head_bits);
     return hipGetLastError();
 }
 
@@ -723,27 +770,36 @@ __device__ __forceinline__ float sinkhorn_lane(float z, int lane) {
 }
 
 // The post and residual gates of the layer (step.rs:636-660), written
-// after the 24 mHC projections: hpost[j] = 2 sigmoid(p_post[j] a_post +
-// off_j + b_post[j]) at 24, hres = sinkhorn64(fma(p_res, a_res, b_res)) at
-// 28.  One wavefront, beside the units.
-__device__ __forceinline__ void post_gates(const SessDev& S, const LayerDev& L, int lane) {
+// after the 24 mHC projections of a row: hpost[j] = 2 sigmoid(p_post[j]
+// a_post + off_j + b_post[j]) at 24, hres = sinkhorn64(fma(p_res, a_res,
+// b_res)) at 28.  One wavefront, beside the units.
+__device__ __forceinline__ void post_gates(float* p, const LayerDev& L, int lane) {
     const int k = lane & 15;
-    const float z = __builtin_fmaf(S.p[2 * MHC_LANES + k], L.a_res, L.b_res[k]);
+    const float z = __builtin_fmaf(p[2 * MHC_LANES + k], L.a_res, L.b_res[k]);
     const float hr = sinkhorn_lane(z, lane);
-    if (lane < 16) S.p[MHC_COLS + MHC_LANES + lane] = hr;
+    if (lane < 16) p[MHC_COLS + MHC_LANES + lane] = hr;
     if (lane < MHC_LANES) {
         const float off = lane == L.lane ? 0.0f : -4.0f;
-        const float zz = ((S.p[MHC_LANES + lane] * L.a_post) + off) + L.b_post[lane];
-        S.p[MHC_COLS + lane] = 2.0f / (lexpf(-zz) + 1.0f);
+        const float zz = ((p[MHC_LANES + lane] * L.a_post) + off) + L.b_post[lane];
+        p[MHC_COLS + lane] = 2.0f / (lexpf(-zz) + 1.0f);
     }
 }
 
-__global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, LayerDev L, int layer, int p0) {
+// Blocks 0 .. t-1: row i's units, one wavefront per unit (q heads, k heads,
+// v heads; step.rs:481-556, chunk.rs:202-253), lane = element: the causal
+// conv over the row and the pre-tap rows before it (fma from the newest
+// back; a row before position 0 contributes fma(w, 0, v)), then for q and
+// k the head zcn16 and RoPE, and for k and v the int8 cache append.  Rows
+// of the same feed are read from the projection, earlier ones from the
+// history ring; the row's pre-tap values go to the ring at a slot no row of
+// the feed reads.  Blocks t .. 2t-1: the row's post gates.
+__global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, LayerDev L, int layer, int p0, int t) {
     const int unit = threadIdx.x >> 6, i = threadIdx.x & 63;
-    if (blockIdx.x == 1) {
-        if (unit == 0) post_gates(S, L, i);
+    if ((int)blockIdx.x >= t) {
+        if (unit == 0) post_gates(S.p + (size_t)(blockIdx.x - t) * 64, L, i);
         return;
     }
+    const int row = blockIdx.x, pos = p0 + row;
     const int nh = D.nh, nkv = D.nkv, qk = D.qk, vd = D.vd;
     const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd, W = D.W;
     int start, cw, cc, len;
@@ -757,17 +813,20 @@ __global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, Lay
         const int vh = unit - nh - nkv;
         start = qd + kd + vh * vd, cw = vdim, cc = vh * vd, w = L.v_taps, len = vd;
     }
-    float* hist = S.hist + (size_t)layer * D.keep * W;
+    float* hist = S.hist + (size_t)layer * D.hist_slots * W;
     float v = 0.0f;
     if (i < len) {
-        const float cur = S.proj[start + i];
+        const float cur = S.proj[(size_t)row * D.nq + start + i];
         v = h2f(w[cc + i]) * cur;
         for (int j = 1; j < D.taps; ++j) {
             const float wj = h2f(w[(size_t)j * cw + cc + i]);
-            const float rr = p0 >= j ? hist[(size_t)((p0 - j) % D.keep) * W + start + i] : 0.0f;
+            float rr = 0.0f;
+            if (pos >= j)
+                rr = j <= row ? S.proj[(size_t)(row - j) * D.nq + start + i]
+                              : hist[(size_t)((pos - j) % D.hist_slots) * W + start + i];
             v = __builtin_fmaf(wj, rr, v);
         }
-        hist[(size_t)(p0 % D.keep) * W + start + i] = cur;
+        hist[(size_t)(pos % D.hist_slots) * W + start + i] = cur;
     }
     if (unit < nh + nkv) {
         const float ss = dot16_lanes(v, qk, i);
@@ -779,31 +838,31 @@ __global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, Lay
         const int half = qk / 2, f = i < half ? i : i - half;
         const float a = __shfl(v, f, 64), b = __shfl(v, f + half, 64);
         if (i < qk) {
-            const float cs = S.rope_c[f], sn = S.rope_s[f];
+            const float cs = S.rope_c[row * half + f], sn = S.rope_s[row * half + f];
             v = i < half ? __builtin_fmaf(-sn, b, cs * a) : __builtin_fmaf(sn, a, cs * b);
         }
     }
     if (unit < nh) {
-        if (i < qk) S.qbuf[start + i] = v;
+        if (i < qk) S.qbuf[(size_t)row * qd + start + i] = v;
     } else {
         const float s = wave_quant_scale(i < len ? v : 0.0f);
         const int8_t q = quant_one(v, 1.0f / s);
         const size_t lc = (size_t)layer * D.cap;
         if (unit < nh + nkv) {
             const int kh = unit - nh;
-            if (i < qk) S.k8[((lc + p0) * nkv + kh) * qk + i] = q;
-            if (i == 0) S.ks[(lc + p0) * nkv + kh] = s;
+            if (i < qk) S.k8[((lc + pos) * nkv + kh) * qk + i] = q;
+            if (i == 0) S.ks[(lc + pos) * nkv + kh] = s;
         } else {
             const int vh = unit - nh - nkv;
-            if (i < vd) S.v8t[(((size_t)layer * nkv + vh) * vd + i) * D.cap + p0] = q;
-            if (i == 0) S.vs[(lc + p0) * nkv + vh] = s;
+            if (i < vd) S.v8t[(((size_t)layer * nkv + vh) * vd + i) * D.cap + pos] = q;
+            if (i == 0) S.vs[(lc + pos) * nkv + vh] = s;
         }
     }
 }
 
-hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, hipStream_t s) {
+hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, hipStream_t s) {
     const int units = D.nh + 2 * D.nkv;
-    hipLaunchKernelGGL(k_units, dim3(2), dim3(units * 64), 0, s, D, S, L, layer, p0);
+    hipLaunchKernelGGL(k_units, dim3(2 * t), dim3(units * 64), 0, s, D, S, L, layer, p0, t);
     return hipGetLastError();
 }
 
@@ -815,12 +874,14 @@ hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int lay
 // summed in 8 lane classes, lexpf over the tail, infer.rs:2222-2279), the
 // weights times v-scales as 21-bit digits (digits21, infer.rs:2171-2220)
 // and their exact integer P.V with the int8 values.
-__global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, LayerDev L, int layer, int p0) {
-    const int hh = blockIdx.x, ci = blockIdx.y, t = threadIdx.x, wave = t >> 6, lane = t & 63;
+__global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, LayerDev L, int layer, int p0,
+                                                       int rows) {
+    const int row = blockIdx.x / D.nh, hh = blockIdx.x % D.nh, ci = blockIdx.y, t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63, pos = p0 + row;
     const int nkv = D.nkv, qk = D.qk, vd = D.vd, kvh = hh / (D.nh / nkv);
-    const int lo = window_lo(L.window, p0), n = p0 + 1 - lo;
+    const int lo = window_lo(L.window, pos), n = pos + 1 - lo;
     int count, chunk;
-    key_chunks(n, nkv, count, chunk);
+    key_chunks(n, nkv, rows > 1, count, chunk);
     if (ci >= count) return;
     const int c0 = ci * chunk, len = min(chunk, n - c0), blocked = len / 4 * 4, slot0 = lo + c0;
     __shared__ alignas(16) int8_t q8[MAX_HEAD_DIM];
@@ -829,7 +890,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     __shared__ float red[ATT_THREADS / 64];
     __shared__ float s_qs, s_sum;
     if (wave == 0) {
-        const float v = lane < qk ? S.qbuf[hh * qk + lane] : 0.0f;
+        const float v = lane < qk ? S.qbuf[((size_t)row * D.nh + hh) * qk + lane] : 0.0f;
         const float s = wave_quant_scale(v);
         if (lane < qk) q8[lane] = quant_one(v, 1.0f / s);
         if (lane == 0) s_qs = s * bits_f32(0x3e13cd3au);
@@ -914,7 +975,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     b += __shfl_xor(b, 2, 64);
     c += __shfl_xor(c, 1, 64);
     c += __shfl_xor(c, 2, 64);
-    const size_t pi = (size_t)hh * D.max_chunks + ci;
+    const size_t pi = ((size_t)row * D.nh + hh) * D.max_chunks + ci;
     if (dm < vd && part == 0)
         S.po[pi * vd + dm] = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
     if (t == 0) {
@@ -923,22 +984,23 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     }
 }
 
-hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, hipStream_t s) {
-    hipLaunchKernelGGL(k_attend, dim3(D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer, p0);
+hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, hipStream_t s) {
+    hipLaunchKernelGGL(k_attend, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer, p0, t);
     return hipGetLastError();
 }
 
 // The chunk merge (infer.rs:1990-2006), the head gate
 // (att / (nexp(-gate) + 1), step.rs:558-572) and A8 of the heads.
-__global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, int p0, int out_bits) {
+__global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, int p0, int rows, int out_bits) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, vd = D.vd, K = D.nh * vd;
+    const int row = blockIdx.x, pos = p0 + row, Ga = (K + GROUP - 1) / GROUP;
     __shared__ float att[FWD_MAX_D];
-    const int lo = window_lo(L.window, p0), n = p0 + 1 - lo;
+    const int lo = window_lo(L.window, pos), n = pos + 1 - lo;
     int count, chunk;
-    key_chunks(n, D.nkv, count, chunk);
+    key_chunks(n, D.nkv, rows > 1, count, chunk);
     if (t < K) {
         const int hh = t / vd, i = t % vd;
-        const size_t base = (size_t)hh * D.max_chunks;
+        const size_t base = ((size_t)row * D.nh + hh) * D.max_chunks;
         float out;
         if (count == 1) {
             const float inv = 1.0f / S.psum[base];
@@ -955,21 +1017,20 @@ __global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, 
             const float inv = 1.0f / total;
             out = acc * inv;
         }
-        att[t] = out / (nexp(-S.proj[D.W + t]) + 1.0f);
+        att[t] = out / (nexp(-S.proj[(size_t)row * D.nq + D.W + t]) + 1.0f);
     }
     __syncthreads();
     const int groups = (K + GROUP - 1) / GROUP;
     for (int g = wave; g < groups; g += LT / 64) {
         const int q0 = g * GROUP + lane, q1 = q0 + 64;
-        a8_group(q0 < K ? att[q0] : 0.0f, q1 < K ? att[q1] : 0.0f, lane, out_bits, S.xq_att + (size_t)g * GROUP,
-                 S.sx_att + g);
+        a8_group(q0 < K ? att[q0] : 0.0f, q1 < K ? att[q1] : 0.0f, lane, out_bits,
+                 S.xq_att + ((size_t)row * Ga + g) * GROUP, S.sx_att + (size_t)row * Ga + g);
     }
 }
 
-hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
+hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int p0, int t, int out_bits,
                         hipStream_t s) {
-    (void)layer;
-    hipLaunchKernelGGL(k_attn_out, dim3(1), dim3(LT), 0, s, D, S, L, p0, out_bits);
+    hipLaunchKernelGGL(k_attn_out, dim3(t), dim3(LT), 0, s, D, S, L, p0, t, out_bits);
     return hipGetLastError();
 }
 

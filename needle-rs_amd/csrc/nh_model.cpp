@@ -176,6 +176,7 @@ int check_geometry(nh_model* m, const nh::ArchiveSmall& sm) {
     D.W = qd + kd + vdim;
     D.nq = D.W + D.nh * D.vd;
     D.keep = D.taps > 1 ? D.taps - 1 : 1;
+    D.hist_slots = D.keep + nh::FWD_ROWS;
     if (D.taps <= 0) return fail(NH_EINVAL, "the decode step needs qkv conv taps");
     // engram geometry (config.rs:273-288 with heads = tables / orders, cact.rs:191)
     if (D.sites > nh::MAX_SITES || norders > 4) return fail(NH_EINVAL, "corrupt engram geometry");
@@ -296,15 +297,17 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
     float theta;
     memcpy(&theta, &h[48], 4);
     const int half = D.qk / 2;
-    std::vector<float> sd(half), cd(half);
+    std::vector<float> freq(half), sd(half), cd(half);
     const float coef = -2.0f / (float)D.qk;
     for (int i = 0; i < half; ++i) {
         const float f = (float)pow((double)theta, (double)((float)i * coef));
         double sv, cv;
         sincos((double)f, &sv, &cv);
+        freq[i] = f;
         sd[i] = (float)sv;
         cd[i] = (float)cv;
     }
+    const size_t o_fr = A.put(freq.data(), half * 4);
     const size_t o_sd = A.put(sd.data(), half * 4), o_cd = A.put(cd.data(), half * 4);
     std::vector<float> etaps;
     for (int s = 0; s < D.sites; ++s)
@@ -340,6 +343,7 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
     m->glob.final_norm = (const float*)(base + o_final);
     m->glob.perm1 = (const int32_t*)(base + o_p1);
     m->glob.perm2 = (const int32_t*)(base + o_p2);
+    m->glob.freq = (const float*)(base + o_fr);
     m->glob.sd = (const float*)(base + o_sd);
     m->glob.cd = (const float*)(base + o_cd);
     m->glob.etaps = (const float*)(base + o_et);
@@ -389,29 +393,40 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
     return NH_OK;
 }
 
-// One decode step at position s->len; the head when `logits`.
-int step(nh_session* s, bool logits, hipStream_t st) {
+// One product over the feed's rows: the decode combine for one row, the
+// prefill combine (block = i < t / 4 * 4) for more (QMat::matmul_into,
+// qlinear.rs:468-487).
+hipError_t product(const nh_qmat* w, nh_qact* a, int rows, float* y, int ldy, hipStream_t st) {
+    a->rows = rows;
+    return rows == 1 ? nh::launch_gemv(w, a, y, 0, nullptr, st) : nh::launch_gemm(w, a, nullptr, y, ldy, 0, nullptr, st);
+}
+
+// One feed of t <= 32 tokens at positions s->len ..: step_native for one
+// token, chunk_job for more (forward_native, infer.rs:1105-1132); the head
+// of the last row when `logits`.
+int feed(nh_session* s, int t, bool logits, hipStream_t st) {
     const nh_model* m = s->m;
     const nh::Dims& D = s->dims;
     const nh::SessDev& S = s->S;
     const int p0 = s->len;
-    NH_TRY(nh::fwd_begin(D, m->glob, S, m->begin, p0, st), "step begin");
+    NH_TRY(nh::fwd_begin(D, m->glob, S, m->begin, p0, t, st), "feed begin");
     for (int e = 0; e < D.sites; ++e)
-        NH_TRY(nh::launch_gemv(m->ekv[e], &s->a_eng[e], S.ekv + (size_t)e * 2 * D.d, 0, nullptr, st), "engram kv");
-    NH_TRY(nh::fwd_engram_hist(D, m->glob, S, p0, st), "engram history");
+        NH_TRY(product(m->ekv[e], &s->a_eng[e], t, S.ekv + (size_t)e * nh::FWD_ROWS * 2 * D.d, 2 * D.d, st),
+               "engram kv");
+    NH_TRY(nh::fwd_engram_hist(D, m->glob, S, p0, t, st), "engram history");
     for (int l = 0; l < D.layers; ++l) {
         const nh::LayerDev* prev = l > 0 ? &m->layers[l - 1] : nullptr;
-        NH_TRY(nh::fwd_layer(D, m->glob, S, prev, &m->layers[l], m->qkvg[l]->m.bits, 0, st), "layer");
-        NH_TRY(nh::launch_gemv(m->qkvg[l], &s->a_in, S.proj, 0, nullptr, st), "q|k|v|gate");
-        NH_TRY(nh::fwd_units(D, S, m->layers[l], l, p0, st), "units");
-        NH_TRY(nh::fwd_attend(D, S, m->layers[l], l, p0, st), "attend");
-        NH_TRY(nh::fwd_attn_out(D, S, m->layers[l], l, p0, m->out[l]->m.bits, st), "attention out");
-        NH_TRY(nh::launch_gemv(m->out[l], &s->a_att, S.o, 0, nullptr, st), "out");
+        NH_TRY(nh::fwd_layer(D, m->glob, S, prev, &m->layers[l], 0, t, m->qkvg[l]->m.bits, 0, st), "layer");
+        NH_TRY(product(m->qkvg[l], &s->a_in, t, S.proj, D.nq, st), "q|k|v|gate");
+        NH_TRY(nh::fwd_units(D, S, m->layers[l], l, p0, t, st), "units");
+        NH_TRY(nh::fwd_attend(D, S, m->layers[l], l, p0, t, st), "attend");
+        NH_TRY(nh::fwd_attn_out(D, S, m->layers[l], p0, t, m->out[l]->m.bits, st), "attention out");
+        NH_TRY(product(m->out[l], &s->a_att, t, S.o, D.d, st), "out");
     }
     const nh::LayerDev* last = D.layers > 0 ? &m->layers[D.layers - 1] : nullptr;
-    NH_TRY(nh::fwd_layer(D, m->glob, S, last, nullptr, 0, m->head_bits, st), "head input");
-    if (logits) NH_TRY(nh::launch_gemv(m->head, &s->a_in, S.logits, 0, nullptr, st), "head");
-    s->len = p0 + 1;
+    NH_TRY(nh::fwd_layer(D, m->glob, S, last, nullptr, t - 1, 1, 0, m->head_bits, st), "head input");
+    if (logits) NH_TRY(product(m->head, &s->a_in, 1, S.logits, D.out_rows, st), "head");
+    s->len = p0 + t;
     s->have_logits = logits;
     return NH_OK;
 }
@@ -473,23 +488,24 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     int mc = 1;
     for (int n = 1; n <= cap; ++n) mc = std::max(mc, key_chunk_count(n, D.nkv));
     D.max_chunks = mc;
-    const size_t d = D.d, L = D.layers, c = cap, E = D.sites;
+    const size_t d = D.d, L = D.layers, c = cap, E = D.sites, R = nh::FWD_ROWS, AR = nh::ACT_ROWS;
     const int Gd = (D.d + nh::GROUP - 1) / nh::GROUP, Ga = (D.nh * D.vd + nh::GROUP - 1) / nh::GROUP;
     Layout Y;
-    const size_t o_xs = Y.take(4 * d * 4), o_u = Y.take(d * 4), o_x1 = Y.take(d * 4), o_p = Y.take(64 * 4);
-    const size_t o_proj = Y.take((size_t)D.nq * 4), o_q = Y.take((size_t)D.nh * D.qk * 4), o_o = Y.take(d * 4);
-    const size_t o_ekv = Y.take(E * 2 * d * 4), o_ev = Y.take(E * d * 4);
+    const size_t o_xs = Y.take(R * 4 * d * 4), o_u = Y.take(R * d * 4), o_x1 = Y.take(R * d * 4);
+    const size_t o_p = Y.take(R * 64 * 4), o_proj = Y.take(R * D.nq * 4), o_q = Y.take(R * D.nh * D.qk * 4);
+    const size_t o_o = Y.take(R * d * 4), o_ekv = Y.take(E * R * 2 * d * 4), o_ev = Y.take(E * R * d * 4);
     const size_t o_lg = Y.take(round_up(D.out_rows, nh::PANEL_ROWS) * 4);
-    const size_t o_rc = Y.take(D.qk / 2 * 4), o_rs = Y.take(D.qk / 2 * 4), o_tok = Y.take(c * 4);
-    const size_t o_po = Y.take((size_t)D.nh * mc * D.vd * 4), o_pm = Y.take((size_t)D.nh * mc * 4),
-                 o_ps = Y.take((size_t)D.nh * mc * 4);
-    const size_t o_hist = Y.take(L * D.keep * D.W * 4);
+    const size_t o_rc = Y.take(R * (D.qk / 2) * 4), o_rs = Y.take(R * (D.qk / 2) * 4);
+    const size_t o_rpc = Y.take(D.qk / 2 * 4), o_rps = Y.take(D.qk / 2 * 4), o_tok = Y.take(c * 4);
+    const size_t o_po = Y.take(R * D.nh * mc * D.vd * 4), o_pm = Y.take(R * D.nh * mc * 4),
+                 o_ps = Y.take(R * D.nh * mc * 4);
+    const size_t o_hist = Y.take(L * D.hist_slots * D.W * 4);
     const size_t o_k8 = Y.take(L * c * D.nkv * D.qk), o_ks = Y.take(L * c * D.nkv * 4);
     const size_t o_v8 = Y.take(L * D.nkv * D.vd * c), o_vs = Y.take(L * c * D.nkv * 4);
     const size_t o_e8 = Y.take(E * c * d), o_es = Y.take(E * c * (d / 32) * 4);
-    const size_t o_xi = Y.take((size_t)Gd * nh::GROUP), o_si = Y.take((size_t)Gd * 4);
-    const size_t o_xa = Y.take((size_t)Ga * nh::GROUP), o_sa = Y.take((size_t)Ga * 4);
-    const size_t o_xe = Y.take(E * Gd * nh::GROUP), o_se = Y.take(E * Gd * 4);
+    const size_t o_xi = Y.take(AR * Gd * nh::GROUP), o_si = Y.take(AR * Gd * 4);
+    const size_t o_xa = Y.take(AR * Ga * nh::GROUP), o_sa = Y.take(AR * Ga * 4);
+    const size_t o_xe = Y.take(E * AR * Gd * nh::GROUP), o_se = Y.take(E * AR * Gd * 4);
     const size_t o_am = Y.take(16);
     hipError_t e = hipMalloc(&s->d_buf, Y.size);
     if (e == hipSuccess) e = hipMemset(s->d_buf, 0, Y.size);
@@ -504,6 +520,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     S.proj = (float*)(b + o_proj), S.qbuf = (float*)(b + o_q), S.o = (float*)(b + o_o);
     S.ekv = (float*)(b + o_ekv), S.evals = (float*)(b + o_ev), S.logits = (float*)(b + o_lg);
     S.rope_c = (float*)(b + o_rc), S.rope_s = (float*)(b + o_rs), S.tokens = (uint32_t*)(b + o_tok);
+    S.rope_pc = (float*)(b + o_rpc), S.rope_ps = (float*)(b + o_rps);
     S.po = (float*)(b + o_po), S.pm = (float*)(b + o_pm), S.psum = (float*)(b + o_ps);
     S.hist = (float*)(b + o_hist), S.k8 = (int8_t*)(b + o_k8), S.ks = (float*)(b + o_ks);
     S.v8t = (int8_t*)(b + o_v8), S.vs = (float*)(b + o_vs), S.ev8 = (int8_t*)(b + o_e8), S.evs = (float*)(b + o_es);
@@ -513,7 +530,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     S.argmax = (int32_t*)(b + o_am);
     auto view = [](int8_t* xq, float* sx, int in_dim, int groups) {
         nh_qact a{};
-        a.cap_rows = 1;
+        a.cap_rows = nh::ACT_ROWS;
         a.rows = 1;
         a.in_dim = in_dim;
         a.groups = groups;
@@ -524,7 +541,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     s->a_in = view(S.xq_in, S.sx_in, D.d, Gd);
     s->a_att = view(S.xq_att, S.sx_att, D.nh * D.vd, Ga);
     for (int i = 0; i < D.sites; ++i)
-        s->a_eng.push_back(view(S.xq_eng + (size_t)i * Gd * nh::GROUP, S.sx_eng + (size_t)i * Gd, D.d, Gd));
+        s->a_eng.push_back(view(S.xq_eng + (size_t)i * AR * Gd * nh::GROUP, S.sx_eng + (size_t)i * AR * Gd, D.d, Gd));
     *out = s;
     return NH_OK;
 }
@@ -556,8 +573,10 @@ int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* 
     hipStream_t st = (hipStream_t)stream;
     NH_TRY(hipMemcpyAsync(s->S.tokens + s->len, toks, (size_t)n * 4, hipMemcpyHostToDevice, st), "tokens");
     NH_TRY(hipStreamSynchronize(st), "tokens");
-    for (int i = 0; i < n; ++i)
-        if (int rc = step(s, i + 1 == n, st)) return rc;
+    for (int i = 0; i < n; i += nh::FWD_ROWS) {
+        const int t = std::min(nh::FWD_ROWS, n - i);
+        if (int rc = feed(s, t, i + t == n, st)) return rc;
+    }
     if (logits)
         NH_TRY(hipMemcpyAsync(logits, s->S.logits, (size_t)s->dims.out_rows * 4, hipMemcpyDeviceToDevice, st),
                "logits");
@@ -573,7 +592,7 @@ int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, v
     const int len0 = s->len;
     for (int i = 0; i < steps; ++i) {
         NH_TRY(nh::fwd_argmax(s->S.logits, s->dims.out_rows, s->S.tokens + s->len, st), "argmax");
-        if (int rc = step(s, true, st)) return rc;
+        if (int rc = feed(s, 1, true, st)) return rc;
     }
     if (logits)
         NH_TRY(hipMemcpyAsync(logits, s->S.logits, (size_t)s->dims.out_rows * 4, hipMemcpyDeviceToDevice, st),

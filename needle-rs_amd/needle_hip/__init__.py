@@ -431,8 +431,10 @@ class Session:
         _check(_lib.nh_session_reset(self.h))
 
     def forward(self, tokens, stream=None) -> torch.Tensor:
-        """Model::forward with Outputs::LastLogits (model.rs:304-306), one
-        step_native per token: the last token's logits [out_rows] (device)."""
+        """Model::forward with Outputs::LastLogits (model.rs:304-306) as
+        forward_native feeds it (infer.rs:1105-1132): chunks of 32 tokens
+        (chunk_job), a single token as a step; the last token's logits
+        [out_rows] (device)."""
         toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(-1))
         logits = torch.empty(self.model.out_rows, dtype=torch.float32, device="cuda")
         _check(_lib.nh_forward(self.h, _hptr(toks), toks.size, _dptr(logits), _stream(stream)))

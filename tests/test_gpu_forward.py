@@ -131,13 +131,11 @@ def test_greedy_loop(nh):
     compare("greedy last logits", logits.cpu().numpy(), last, stats)
     say(f"greedy: picks {picks[:8].tolist()}..., last logits max rel {stats['max_rel']:.3g}")
     assert stats["exact"] == 1
-    # reset starts the sequence over
+    # reset starts the sequence over (the prompt now as one chunk)
     s.reset()
     assert len(s) == 0
     again = s.forward(prompt).cpu().numpy()
-    ref2 = forward.Forward(data).session(64)
-    for t in prompt:
-        l2 = ref2.step(int(t))
+    l2 = forward.Forward(data).session(64).feed(prompt)
     st2 = {}
     compare("after reset", again, l2, st2)
     assert st2["exact"] == 1
@@ -181,3 +179,64 @@ def test_product_archive_writer(nh):
     g = W.Needle3(vocab=300, num_layers=2, engram_slots=64, engram_sites=(1,), global_layers=(0,), sliding_window=16)
     data = W.random_needle3(nh, g, seed=3)
     run_pair(nh, data, o.random_tokens(12, g.vocab, seed=8), 16, "written")
+
+
+# ---------------------------------------------------------- prompt chunks
+def run_feed(nh, data, prompt, cap, label, then_steps=0):
+    f = forward.Forward(data)
+    m = nh.Model.from_archive(data)
+    s, os_ = m.session(cap), f.session(cap)
+    stats = {}
+    got = s.forward(prompt).cpu().numpy()
+    want = os_.feed(prompt)
+    compare(f"{label} prompt", got, want, stats)
+    toks = o.random_tokens(then_steps, 300, seed=31)
+    for i, t in enumerate(toks):
+        compare(f"{label} step {i}", s.forward([int(t)]).cpu().numpy(), os_.step(int(t)), stats)
+    say(f"{label}: prompt of {len(prompt)} + {then_steps} steps: {stats['exact']}/{stats['steps']} bit-identical")
+    assert stats["exact"] == stats["steps"], stats
+    return m, s
+
+
+def test_prefill_chunks_then_steps(nh):
+    say("prompt chunks (32 + 8) then steps, 3 layers with a window and an engram site")
+    g = cact.Geometry(**SMALL)
+    run_feed(nh, archive(g, seed=41), o.random_tokens(40, g.vocab, seed=9), 64, "chunks", then_steps=6)
+
+
+def test_prefill_single_token_tail(nh):
+    say("a 33-token prompt: one chunk of 32 and a single-token step")
+    g = cact.Geometry(**SMALL)
+    run_feed(nh, archive(g, seed=42), o.random_tokens(33, g.vocab, seed=10), 40, "tail", then_steps=2)
+
+
+def test_prefill_long_nested_chunks(nh):
+    say("a 300-token prompt in 10 chunks (rows past 256 keys attend in 2 nested chunks)")
+    g = cact.Geometry(vocab=300, num_layers=2, engram_slots=64, engram_sites=(1,), global_layers=(0,),
+                      sliding_window=64)
+    run_feed(nh, archive(g, seed=43), o.random_tokens(300, g.vocab, seed=11), 320, "long prompt", then_steps=3)
+
+
+def test_prefill_mixed_widths(nh):
+    say("prompt chunks over 2-bit / ternary / f16 records and two engram sites")
+    g = cact.Geometry(vocab=300, num_layers=4, engram_slots=64, engram_sites=(0, 3), global_layers=(2,),
+                      sliding_window=5)
+
+    def kind(name):
+        if name == "embedding":
+            return ("cq", 4)
+        if name.startswith("engram_table"):
+            return ("random", 2)
+        if name.startswith("phi"):
+            return ("random", 5)
+        layer = int(name.split(".")[1]) if "." in name and name.split(".")[1].isdigit() else 0
+        return ("random", 2 if layer == 1 else 4)
+
+    run_feed(nh, archive(g, seed=44, kind=kind), o.random_tokens(45, g.vocab, seed=12), 64, "mixed prompt",
+             then_steps=2)
+
+
+def test_prefill_full_needle3(nh):
+    say("the full Needle-3 geometry: a 37-token prompt (32 + 5) then 2 steps")
+    g = cact.Geometry()
+    run_feed(nh, archive(g, seed=45), o.random_tokens(37, g.vocab, seed=13), 48, "needle3 prompt", then_steps=2)
