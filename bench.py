@@ -251,10 +251,11 @@ def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
     """The full Needle-3 decode (crates/needle-core/src/config.rs:61-100:
     20 layers, d 768, vocab 16384, 5 engram sites) from random-init weights
     0.02*N(0,1) through CQ-W4 (needle_hip.archive.random_needle3, seed 0):
-    a prompt of 118 uniform random token ids fed one step_native per token,
-    then 64 greedy decode steps on the device (argmax, step, no host round
-    trip), the KV cache and every activation in HBM.  decode_tok_s counts
-    the 64 greedy steps over their HIP-event time on the launch stream.
+    a prompt of 118 uniform random token ids fed as forward_native feeds it
+    (chunks of 32 through chunk_job), then 64 greedy decode steps on the
+    device (argmax, step_native, no host round trip), the KV cache and every
+    activation in HBM.  decode_tok_s counts the 64 greedy steps over their
+    HIP-event time on the launch stream.
 
     The CPU leg runs the oracle's step_native (oracle/forward.c, OpenMP over
     the products' rows) on the same archive and tokens, for as many steps
@@ -290,7 +291,7 @@ def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
     prompt_ms = min(a for a, _ in runs)
     decode_ms = min(b for _, b in runs)
     sites, layers = 5, 20
-    out = {"workload": "Needle-3 random-init decode: 118 random prompt tokens (one step each), then 64 greedy "
+    out = {"workload": "Needle-3 random-init decode: 118 random prompt tokens (32-token chunks), then 64 greedy "
                        "steps on the device",
            "prompt_tokens": DECODE_PROMPT, "decode_steps": DECODE_STEPS,
            "decode_tok_s": round(DECODE_STEPS * 1e3 / decode_ms, 1),
@@ -306,8 +307,7 @@ def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
         f = forward.Forward(data)
         ses = f.session(DECODE_PROMPT + DECODE_STEPS)
         t1 = time.perf_counter()
-        for t in prompt:
-            last = ses.step(int(t))
+        last = ses.feed(prompt)
         t_prompt = time.perf_counter() - t1
         agree, steps, t2 = 0, 0, time.perf_counter()
         for t in picks:
@@ -323,6 +323,81 @@ def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
                                          f"{steps} of the 64 decode steps fed the device's picks ({t_dec:.1f} s)"}
         out["parity"] = {"greedy_picks_checked": steps, "oracle_argmax_agrees": agree}
         out["gpu_over_cpu"] = round(out["decode_tok_s"] / out["cpu_baseline"]["value"], 1)
+    return out
+
+
+PREFILL_SEQS, PREFILL_LEN = 16, 512
+
+
+def needle3_prefill(nh, torch, cpu_seconds: float, with_cpu: bool):
+    """The prefill-heavy run: 16 independent sequences of 512 uniform random
+    token ids, one sequence at a time, each fed as forward_native feeds a
+    prompt (16 chunks of 32 through chunk_job: every product over the
+    chunk's rows on the W4A8 GEMM, the prefill combine) into a fresh
+    session, Outputs::LastLogits.  Same random-init archive as the decode
+    run.  prefill_tok_s = 16 x 512 tokens over the HIP-event time of the
+    16 sequences on the launch stream.
+
+    The CPU leg feeds the oracle's chunk_job the same sequences for as many
+    chunks as fit the time bound, and checks its last logits' argmax at the
+    end of every whole sequence it reaches."""
+    import numpy as np
+
+    from needle_hip import archive
+
+    data = archive.random_needle3(nh, seed=0)
+    model = nh.Model.from_archive(data)
+    rng = np.random.default_rng(1)
+    seqs = [rng.integers(0, model.out_rows, PREFILL_LEN).astype(np.uint32) for _ in range(PREFILL_SEQS)]
+    sess = model.session(PREFILL_LEN)
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    runs, last = [], []
+    for r in range(3):  # the first run warms up
+        last = []
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for q in seqs:
+            sess.reset()
+            last.append(sess.forward(q))
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        if r > 0:
+            runs.append(ev0.elapsed_time(ev1))
+    ms = min(runs)
+    picks = [int(torch.argmax(x).item()) for x in last]
+    out = {"workload": "Needle-3 random-init prefill: 16 sequences x 512 random tokens, one at a time, 32-token "
+                       "chunks on the W4A8 GEMM",
+           "sequences": PREFILL_SEQS, "tokens_per_sequence": PREFILL_LEN,
+           "prefill_tok_s": round(PREFILL_SEQS * PREFILL_LEN * 1e3 / ms, 1),
+           "ms_per_sequence": round(ms / PREFILL_SEQS, 3), "runs": len(runs)}
+    progress(f"Needle-3 prefill: {out['ms_per_sequence']:.2f} ms per 512-token sequence")
+    if with_cpu:
+        import oracle as o
+        from oracle import forward
+
+        f = forward.Forward(data)
+        tokens, agree, whole, t0 = 0, 0, 0, time.perf_counter()
+        for q, pick in zip(seqs, picks):
+            ses = f.session(PREFILL_LEN)
+            lg = None
+            for i in range(0, PREFILL_LEN, 32):
+                lg = ses.chunk(q[i:i + 32])
+                tokens += 32
+                if time.perf_counter() - t0 >= cpu_seconds:
+                    break
+            if len(ses) == PREFILL_LEN:
+                whole += 1
+                agree += int(int(np.argmax(lg)) == pick)
+            if time.perf_counter() - t0 >= cpu_seconds:
+                break
+        el = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(tokens / el, 1), "unit": "tok/s", "cores": o.default_threads(),
+                               "kind": "port",
+                               "sample": f"the oracle's chunk_job over {tokens} tokens of the same sequences "
+                                         f"({el:.1f} s)"}
+        out["parity"] = {"sequences_checked": whole, "oracle_argmax_agrees": agree}
+        out["gpu_over_cpu"] = round(out["prefill_tok_s"] / out["cpu_baseline"]["value"], 1)
     return out
 
 
@@ -449,6 +524,8 @@ def main():
         progress("Needle-3 products done")
         line["needle3_decode"] = needle3_decode(nh, torch, args.cpu_seconds * 2, not args.no_cpu)
         progress("Needle-3 decode done")
+        line["needle3_prefill"] = needle3_prefill(nh, torch, args.cpu_seconds * 2, not args.no_cpu)
+        progress("Needle-3 prefill done")
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(gpu, args.cpu_seconds)
         line["cpu_baseline"]["gpu_over_cpu"] = round(gpu["gbs"] / line["cpu_baseline"]["value"], 1)
