@@ -132,6 +132,12 @@ hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int lay
 hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, hipStream_t s);
 hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int p0, int t, int out_bits,
                         hipStream_t s);
+// One decode token's units, attention, gate and A8 in one launch (the three
+// launches above for a single row), for positions whose keys form one chunk
+// and geometries with 2 or 4 heads per A8 group (dec_group_fits).
+bool dec_group_fits(const Dims& D, int p0, int window);
+hipError_t fwd_dec_attn(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
+                        hipStream_t s);
 hipError_t fwd_argmax(const float* logits, int n, uint32_t* dst, hipStream_t s);
 hipError_t fwd_phi8(const float* rows, int nrows, int width, int8_t* q, float* scale, hipStream_t s);
 

@@ -1034,6 +1034,241 @@ hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int 
     return hipGetLastError();
 }
 
+// ------------------------------------------------------- decode attention
+// One decode token's units, attention, gate and A8 in one launch while the
+// position's keys form a single chunk (key_chunks gives one chunk below
+// 64 k keys; the arithmetic of k_units, k_attend and k_attn_out for one
+// row).  Block g owns the heads of A8 group g (GROUP / vd heads sharing one
+// kv head), 256 threads per head; the keys' int8 rows, scales and values
+// are staged in LDS up front.  The waves of the heads' query units and of
+// the kv head's new key and value compute them first (the same values in
+// every block of the kv group; its first block appends them to the cache
+// and the history ring).  With no cross-block data the group's A8 runs in
+// the block.  One more block computes the row's post gates.
+constexpr int DG_HEAD_T = 256;
+
+// A unit's post-tap value for lane i (zcn16 and RoPE when `norm` is set):
+// the causal conv over the row and the kept history rows of the ring.
+__device__ __forceinline__ float unit_value(const Dims& D, const SessDev& S, int layer, int p0, int start, int cw,
+                                            int cc, int len, const uint16_t* w, const uint16_t* norm, int i,
+                                            bool write_hist) {
+    float* hist = S.hist + (size_t)layer * D.hist_slots * D.W;
+    float v = 0.0f;
+    if (i < len) {
+        const float cur = S.proj[start + i];
+        v = h2f(w[cc + i]) * cur;
+        for (int j = 1; j < D.taps; ++j) {
+            const float wj = h2f(w[(size_t)j * cw + cc + i]);
+            const float rr = p0 >= j ? hist[(size_t)((p0 - j) % D.hist_slots) * D.W + start + i] : 0.0f;
+            v = __builtin_fmaf(wj, rr, v);
+        }
+        if (write_hist) hist[(size_t)(p0 % D.hist_slots) * D.W + start + i] = cur;
+    }
+    if (norm) {
+        const int qk = D.qk;
+        const float ss = dot16_lanes(v, qk, i);
+        const float r = rinv(ss, qk);
+        if (i < qk) {
+            const float tt = v * r;
+            v = __builtin_fmaf(tt, h2f(norm[i]), tt);
+        }
+        const int half = qk / 2, f = i < half ? i : i - half;
+        const float a = __shfl(v, f, 64), b = __shfl(v, f + half, 64);
+        if (i < qk) {
+            const float cs = S.rope_c[f], sn = S.rope_s[f];
+            v = i < half ? __builtin_fmaf(-sn, b, cs * a) : __builtin_fmaf(sn, a, cs * b);
+        }
+    }
+    return v;
+}
+
+template <int HP>
+__global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S, LayerDev L, int layer, int p0,
+                                                              int out_bits) {
+    constexpr int NT = HP * DG_HEAD_T;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int nh = D.nh, nkv = D.nkv, qk = D.qk, vd = D.vd, group = nh / nkv;
+    const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd;
+    if ((int)blockIdx.x * HP >= nh) {
+        if (wave == 0) post_gates(S.p, L, lane);
+        return;
+    }
+    const int hh0 = blockIdx.x * HP, kvh = hh0 / group;
+    const bool owner = hh0 % group == 0;
+    const int lo = window_lo(L.window, p0), n = p0 + 1 - lo, blocked = n / 4 * 4;
+    const int h = t / DG_HEAD_T, u = t % DG_HEAD_T, hw = u >> 6;  // head, thread and wavefront in it
+    __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][MAX_HEAD_DIM];  // key rows by slot - lo
+    __shared__ int8_t vs8[MAX_HEAD_DIM][ATT_CHUNK_MAX + 4];          // value columns by slot - lo
+    __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
+    __shared__ alignas(16) int8_t q8[HP][MAX_HEAD_DIM];
+    __shared__ float sc[HP][ATT_CHUNK_MAX];
+    __shared__ int8_t dig[HP][3][ATT_CHUNK_MAX];
+    __shared__ float red[HP][DG_HEAD_T / 64];
+    __shared__ float s_qs[HP], s_sum[HP];
+    __shared__ float att[HP * MAX_HEAD_DIM];
+    const size_t lc = (size_t)layer * D.cap;
+    // The keys before the position: int8 rows, scales and value columns.
+    {
+        const int nold = n - 1, rq = qk / 16;
+        for (int e = t; e < nold * rq; e += NT) {
+            const int i = e / rq, c = e % rq;
+            reinterpret_cast<uint4*>(ks8[i])[c] =
+                reinterpret_cast<const uint4*>(S.k8 + ((lc + lo + i) * nkv + kvh) * qk)[c];
+        }
+        for (int i = t; i < nold; i += NT) {
+            kss[i] = S.ks[(lc + lo + i) * nkv + kvh];
+            vss[i] = S.vs[(lc + lo + i) * nkv + kvh];
+        }
+        const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.cap + lo;
+        for (int e = t; e < vd * nold; e += NT) {
+            const int dm = e / nold, i = e % nold;
+            vs8[dm][i] = vcol[(size_t)dm * D.cap + i];
+        }
+    }
+    // The units: queries on waves 0 .. HP-1, the new key and value on the next two.
+    if (wave < HP) {
+        const int hq = hh0 + wave;
+        const float v = unit_value(D, S, layer, p0, hq * qk, qd, hq * qk, qk, L.q_taps, L.q_norm, lane, true);
+        const float s = wave_quant_scale(lane < qk ? v : 0.0f);
+        if (lane < qk) q8[wave][lane] = quant_one(v, 1.0f / s);
+        if (lane == 0) s_qs[wave] = s * bits_f32(0x3e13cd3au);
+    } else if (wave == HP) {
+        const float v = unit_value(D, S, layer, p0, qd + kvh * qk, kd, kvh * qk, qk, L.k_taps, L.k_norm, lane, owner);
+        const float s = wave_quant_scale(lane < qk ? v : 0.0f);
+        const int8_t q = quant_one(v, 1.0f / s);
+        if (lane < qk) {
+            ks8[n - 1][lane] = q;
+            if (owner) S.k8[((lc + p0) * nkv + kvh) * qk + lane] = q;
+        }
+        if (lane == 0) {
+            kss[n - 1] = s;
+            if (owner) S.ks[(lc + p0) * nkv + kvh] = s;
+        }
+    } else if (wave == HP + 1) {
+        const float v = unit_value(D, S, layer, p0, qd + kd + kvh * vd, vdim, kvh * vd, vd, L.v_taps, nullptr, lane,
+                                   owner);
+        const float s = wave_quant_scale(lane < vd ? v : 0.0f);
+        const int8_t q = quant_one(v, 1.0f / s);
+        if (lane < vd) {
+            vs8[lane][n - 1] = q;
+            if (owner) S.v8t[(((size_t)layer * nkv + kvh) * vd + lane) * D.cap + p0] = q;
+        }
+        if (lane == 0) {
+            vss[n - 1] = s;
+            if (owner) S.vs[(lc + p0) * nkv + kvh] = s;
+        }
+    }
+    __syncthreads();
+    // attend_head_ref over the one chunk, one head per 256 threads
+    const float qs = s_qs[h];
+    float mx = -__builtin_inff();
+    for (int i = u; i < n; i += DG_HEAD_T) {
+        int dot = 0;
+        for (int j = 0; j < qk; j += 4)
+            dot = __builtin_amdgcn_sdot4(*(const int*)(&ks8[i][j]), *(const int*)(&q8[h][j]), dot, false);
+        const float ksc = kss[i];
+        const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
+        sc[h][i] = sv;
+        mx = fmaxf(mx, sv);
+    }
+    mx = wave_max(mx);
+    if (lane == 0) red[h][hw] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
+    for (int i = u; i < n; i += DG_HEAD_T) sc[h][i] = i < blocked ? nexp(sc[h][i] - mx) : lexpf(sc[h][i] - mx);
+    __syncthreads();
+    if (hw == 0) {
+        float acc = 0.0f;
+        const int nb8 = n / 8;
+        if (lane < 8) {
+            const int k = lane & 3, hi = lane >> 2;
+            for (int b = 0; b < nb8; ++b) acc += sc[h][b * 8 + hi * 4 + k];
+            if (hi == 0 && n - nb8 * 8 >= 4) acc += sc[h][nb8 * 8 + k];
+        }
+        const int k = lane & 3;
+        const float tk = __shfl(acc, k, 64) + __shfl(acc, 4 + k, 64);
+        float sum = (__shfl(tk, 0, 64) + __shfl(tk, 1, 64)) + (__shfl(tk, 2, 64) + __shfl(tk, 3, 64));
+        int i = blocked;
+        if (n - i >= 2) {
+            sum = (sc[h][i] + sum) + sc[h][i + 1];
+            i += 2;
+        }
+        if (n - i == 1) sum += sc[h][i];
+        if (lane == 0) s_sum[h] = sum;
+    }
+    __syncthreads();
+    float wmax = 0.0f;
+    for (int i = u; i < n; i += DG_HEAD_T) {
+        const float w = sc[h][i] * vss[i];
+        sc[h][i] = w;
+        wmax = fmaxf(wmax, w);
+    }
+    wmax = wave_max(wmax);
+    if (lane == 0) red[h][hw] = wmax;
+    __syncthreads();
+    wmax = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
+    const float qw = bits_f32(0x49fffff8u) / wmax;
+    for (int i = u; i < n; i += DG_HEAD_T) {
+        const int32_t wq = (int32_t)roundf(sc[h][i] * qw);
+        dig[h][0][i] = (int8_t)(wq >> 14);
+        dig[h][1][i] = (int8_t)((wq >> 7) & 127);
+        dig[h][2][i] = (int8_t)(wq & 127);
+    }
+    __syncthreads();
+    {
+        const float cw = wmax * bits_f32(0x35000004u);
+        const int dm = u >> 2, part = u & 3;
+        int a = 0, b = 0, c = 0;
+        if (dm < vd)
+            for (int i = part; i < n; i += 4) {
+                const int v = vs8[dm][i];
+                a += dig[h][0][i] * v;
+                b += dig[h][1][i] * v;
+                c += dig[h][2][i] * v;
+            }
+        a += __shfl_xor(a, 1, 64);
+        a += __shfl_xor(a, 2, 64);
+        b += __shfl_xor(b, 1, 64);
+        b += __shfl_xor(b, 2, 64);
+        c += __shfl_xor(c, 1, 64);
+        c += __shfl_xor(c, 2, 64);
+        if (dm < vd && part == 0) {
+            const float po = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
+            const float inv = 1.0f / s_sum[h];
+            const float out = po * inv;
+            att[h * vd + dm] = out / (nexp(-S.proj[D.W + (hh0 + h) * vd + dm]) + 1.0f);
+        }
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int K = HP * vd;
+        a8_group(lane < K ? att[lane] : 0.0f, lane + 64 < K ? att[lane + 64] : 0.0f, lane, out_bits,
+                 S.xq_att + (size_t)blockIdx.x * GROUP, S.sx_att + blockIdx.x);
+    }
+}
+
+bool dec_group_fits(const Dims& D, int p0, int window) {
+    const int lo = (window > 0 && p0 + 1 > window) ? p0 + 1 - window : 0, n = p0 + 1 - lo;
+    int k = 2 * NATIVE_TEAM / D.nkv;
+    if (k < 1) k = 1;
+    int c = (n + 255) / 256;
+    if (k * 64 <= n && c < k) c = k;
+    if (c > 1 || n > ATT_CHUNK_MAX) return false;
+    if (GROUP % D.vd != 0) return false;
+    const int hp = GROUP / D.vd;
+    return (hp == 2 || hp == 4) && D.nh % hp == 0 && (D.nh / D.nkv) % hp == 0 && D.qk % 16 == 0;
+}
+
+hipError_t fwd_dec_attn(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
+                        hipStream_t s) {
+    const int hp = GROUP / D.vd, blocks = D.nh / hp + 1;
+    if (hp == 2)
+        hipLaunchKernelGGL(k_dec_group<2>, dim3(blocks), dim3(2 * DG_HEAD_T), 0, s, D, S, L, layer, p0, out_bits);
+    else
+        hipLaunchKernelGGL(k_dec_group<4>, dim3(blocks), dim3(4 * DG_HEAD_T), 0, s, D, S, L, layer, p0, out_bits);
+    return hipGetLastError();
+}
+
 // ----------------------------------------------------------------- argmax
 // argmax (crates/needle-engine/src/generate.rs:42-50): the first maximum.
 __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, uint32_t* __restrict__ dst) {

@@ -418,9 +418,13 @@ int feed(nh_session* s, int t, bool logits, hipStream_t st) {
         const nh::LayerDev* prev = l > 0 ? &m->layers[l - 1] : nullptr;
         NH_TRY(nh::fwd_layer(D, m->glob, S, prev, &m->layers[l], 0, t, m->qkvg[l]->m.bits, 0, st), "layer");
         NH_TRY(product(m->qkvg[l], &s->a_in, t, S.proj, D.nq, st), "q|k|v|gate");
-        NH_TRY(nh::fwd_units(D, S, m->layers[l], l, p0, t, st), "units");
-        NH_TRY(nh::fwd_attend(D, S, m->layers[l], l, p0, t, st), "attend");
-        NH_TRY(nh::fwd_attn_out(D, S, m->layers[l], p0, t, m->out[l]->m.bits, st), "attention out");
+        if (t == 1 && nh::dec_group_fits(D, p0, m->layers[l].window)) {
+            NH_TRY(nh::fwd_dec_attn(D, S, m->layers[l], l, p0, m->out[l]->m.bits, st), "decode attention");
+        } else {
+            NH_TRY(nh::fwd_units(D, S, m->layers[l], l, p0, t, st), "units");
+            NH_TRY(nh::fwd_attend(D, S, m->layers[l], l, p0, t, st), "attend");
+            NH_TRY(nh::fwd_attn_out(D, S, m->layers[l], p0, t, m->out[l]->m.bits, st), "attention out");
+        }
         NH_TRY(product(m->out[l], &s->a_att, t, S.o, D.d, st), "out");
     }
     const nh::LayerDev* last = D.layers > 0 ? &m->layers[D.layers - 1] : nullptr;
