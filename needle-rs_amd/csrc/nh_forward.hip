@@ -278,16 +278,18 @@ hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, in
 }
 
 // -------------------------------------------------------------- the layer
-// One workgroup of 1024 threads; thread t owns element t of every d- and
-// hada_n-long vector (d <= 1024 = hada_n) and elements t + 1024 k of the
-// 4 d residual lanes.  Every global read is issued at the start: the
-// Kronecker factors and the cond_v / cond_u tables land in LDS, the
-// elementwise weights and this wavefront's Phi8 rows in registers, so the
-// serial chains (dot16, cond_weights, mix8) wait on LDS only.
+// One workgroup of 1024 threads per token row; thread t owns element t of
+// every d- and hada_n-long vector (d <= 1024 = hada_n) and elements
+// t + 1024 k of the 4 d residual lanes.  Every global read is issued at the
+// start: the Kronecker factors (widened to f32) and the cond_v / cond_u
+// tables land in LDS, the elementwise weights and this wavefront's Phi8
+// rows in registers.  The short serial chains (dot16 over d, the gates) run
+// in every wavefront that needs their result, so no barrier is spent on
+// handing it out.
 namespace {
 
-constexpr int MIX_T = 256;             // threads of one mix8 (4 outputs each)
 constexpr int BT_STRIDE = HADA_NB + 1;  // padded row of a transposed mix8 output
+constexpr int MIX_T = 256;              // threads of one mix8 (4 outputs each)
 
 struct LayerShared {
     float xs[MHC_LANES * FWD_MAX_D];
@@ -298,29 +300,27 @@ struct LayerShared {
     alignas(16) float A[HADA_N];
     alignas(16) float B[HADA_NB * BT_STRIDE];
     alignas(16) float C[HADA_N];
+    alignas(16) float kron[6][HADA_N];
     alignas(16) int8_t nx8[MHC_LANES * FWD_MAX_D];
-    alignas(16) uint16_t kron[6][HADA_N];
     alignas(16) uint16_t cond_v[FWD_MAX_D * COND_RANK];
     alignas(16) uint16_t cond_u[COND_RANK * HADA_N];
     float red[LT / 64];
     float p[64];
     float wk[COND_RANK];
-    float hp[MHC_LANES];
-    float r, r2;
+    float r_sx, r_a, r_b, r_c;
 };
 
 // mix8 (infer.rs:2343-2380), portable branch: out[r][c] =
 // sum_j ct[j][r] * rows[j][c], each output an fma chain from j = 0.  Thread
 // u < 256 computes r = u / 8 and c = 4 (u % 8) .. + 3, so each step reads
 // one ct value and four row values.
-// Transposed (ct = an f16 factor, rows = f32 [32][32]): stored at
-// out[c * 33 + r].
-__device__ __forceinline__ void mix8_t(int u, const uint16_t* ct, const float* rows, float* out) {
+// Transposed (ct = a factor, rows = [32][32]): stored at out[c * 33 + r].
+__device__ __forceinline__ void mix8_t(int u, const float* ct, const float* rows, float* out) {
     const int r = u >> 3, c0 = (u & 7) * 4;
     float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
 #pragma unroll
     for (int j = 0; j < HADA_NB; ++j) {
-        const float a = h2f(ct[j * HADA_NB + r]);
+        const float a = ct[j * HADA_NB + r];
         const float4 b = *reinterpret_cast<const float4*>(rows + j * HADA_NB + c0);
         o0 = __builtin_fmaf(a, b.x, o0);
         o1 = __builtin_fmaf(a, b.y, o1);
@@ -333,44 +333,61 @@ __device__ __forceinline__ void mix8_t(int u, const uint16_t* ct, const float* r
     out[(c0 + 3) * BT_STRIDE + r] = o3;
 }
 
-// Plain (ct = the f32 output of mix8_t, rows = an f16 factor): out[r][c],
-// rows r < rows_limit.
-__device__ __forceinline__ void mix8_n(int u, const float* ct, const uint16_t* rows, float* out, int rows_limit) {
+// Plain (ct = the output of mix8_t, rows = a factor): out[r][c], rows
+// r < rows_limit.
+__device__ __forceinline__ void mix8_n(int u, const float* ct, const float* rows, float* out, int rows_limit) {
     const int r = u >> 3, c0 = (u & 7) * 4;
     if (r >= rows_limit) return;
     float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
 #pragma unroll
     for (int j = 0; j < HADA_NB; ++j) {
         const float a = ct[j * BT_STRIDE + r];
-        const uint2 b = *reinterpret_cast<const uint2*>(rows + j * HADA_NB + c0);
-        o0 = __builtin_fmaf(a, h2f((uint16_t)(b.x & 0xffffu)), o0);
-        o1 = __builtin_fmaf(a, h2f((uint16_t)(b.x >> 16)), o1);
-        o2 = __builtin_fmaf(a, h2f((uint16_t)(b.y & 0xffffu)), o2);
-        o3 = __builtin_fmaf(a, h2f((uint16_t)(b.y >> 16)), o3);
+        const float4 b = *reinterpret_cast<const float4*>(rows + j * HADA_NB + c0);
+        o0 = __builtin_fmaf(a, b.x, o0);
+        o1 = __builtin_fmaf(a, b.y, o1);
+        o2 = __builtin_fmaf(a, b.z, o2);
+        o3 = __builtin_fmaf(a, b.w, o3);
     }
     *reinterpret_cast<float4*>(out + r * HADA_NB + c0) = make_float4(o0, o1, o2, o3);
 }
 
-// 16-byte copies of n bytes from global to LDS by the whole block (n a
-// multiple of 16, both ends 16-byte aligned).
-__device__ __forceinline__ void stage16(void* dst, const void* src, int n) {
-    for (int i = threadIdx.x; i < n / 16; i += LT)
-        reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+// rinv(dot16(x, y)) by wavefront 0, handed to the block through LDS.
+__device__ __forceinline__ float block_rinv(const float* x, const float* y, int n, float* slot) {
+    if ((threadIdx.x >> 6) == 0) {
+        const float r = rinv(dot16_wave(x, y, n, threadIdx.x & 63), n);
+        if (threadIdx.x == 0) *slot = r;
+    }
+    __syncthreads();
+    return *slot;
 }
 
 // The previous layer's inputs and weights a thread needs, read up front.
+// The LDS tables go out as one list of 16-byte chunks, up to STAGE_PER per
+// thread: [0, 768) the six Kronecker factors (128 each), then cond_v
+// (d chunks), then cond_u (1024).
+constexpr int STAGE_PER = 3;
+
 struct OutRegs {
     float o, x1, u, pn, ph, d1, d2, b2, d3, d4;
     int p1, p2;
+    uint4 st[STAGE_PER];
 };
 
 __device__ __forceinline__ OutRegs load_out(const Dims& D, const Globals& G, const SessDev& S, const LayerDev& P,
                                             LayerShared& sh) {
     const int t = threadIdx.x, d = D.d;
     OutRegs q{};
-    for (int k = 0; k < 6; ++k) stage16(sh.kron[k], P.kron[k], HADA_N * 2);
-    stage16(sh.cond_v, P.cond_v, d * COND_RANK * 2);
-    stage16(sh.cond_u, P.cond_u, COND_RANK * HADA_N * 2);
+    const int kron_n = 6 * HADA_N / 8, cv_n = d * COND_RANK / 8, cu_n = COND_RANK * HADA_N / 8;
+#pragma unroll
+    for (int r = 0; r < STAGE_PER; ++r) {
+        const int e = t + r * LT;
+        if (e < kron_n)
+            q.st[r] = reinterpret_cast<const uint4*>(P.kron[e / (HADA_N / 8)])[e % (HADA_N / 8)];
+        else if (e < kron_n + cv_n)
+            q.st[r] = reinterpret_cast<const uint4*>(P.cond_v)[e - kron_n];
+        else if (e < kron_n + cv_n + cu_n)
+            q.st[r] = reinterpret_cast<const uint4*>(P.cond_u)[e - kron_n - cv_n];
+    }
     if (t < d) {
         q.o = S.o[t];
         q.x1 = S.x1[t];
@@ -387,6 +404,34 @@ __device__ __forceinline__ OutRegs load_out(const Dims& D, const Globals& G, con
     q.p2 = G.perm2[t];
     if (t < 64) sh.p[t] = S.p[t];
     return q;
+}
+
+__device__ __forceinline__ void store_out(const Dims& D, const OutRegs& q, LayerShared& sh) {
+    const int t = threadIdx.x;
+    const int kron_n = 6 * HADA_N / 8, cv_n = D.d * COND_RANK / 8, cu_n = COND_RANK * HADA_N / 8;
+#pragma unroll
+    for (int r = 0; r < STAGE_PER; ++r) {
+        const int e = t + r * LT;
+        if (e < kron_n) {
+            // 8 f16 -> 8 f32 (exact)
+            const uint4 v = q.st[r];
+            float* dst = sh.kron[e / (HADA_N / 8)] + (e % (HADA_N / 8)) * 8;
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            float f[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                f[2 * k] = h2f((uint16_t)(w[k] & 0xffffu));
+                f[2 * k + 1] = h2f((uint16_t)(w[k] >> 16));
+            }
+            *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
+            *reinterpret_cast<float4*>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
+        } else if (e < kron_n + cv_n) {
+            reinterpret_cast<uint4*>(sh.cond_v)[e - kron_n] = q.st[r];
+        } else if (e < kron_n + cv_n + cu_n) {
+            reinterpret_cast<uint4*>(sh.cond_u)[e - kron_n - cv_n] = q.st[r];
+        }
+    }
+    if (t < D.d) sh.o[t] = q.o;
 }
 
 // cond_weights (infer.rs:1640-1656) by wavefront 0: lane 8 jm + k carries
@@ -425,39 +470,36 @@ __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int l
     if (lane < 8) wk[lane] = e * inv;
 }
 
-// The Hadamard MLP and mHC write of layer P (step.rs:600-705).
-__device__ void layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, LayerShared& sh) {
+// The Hadamard MLP and mHC write of layer P (step.rs:600-705); returns this
+// thread's max |new lane value| (for the next layer's mHC read).
+__device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, LayerShared& sh) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
     // mix8 runs on waves 4..7 (threads 256..511), beside cond_weights on wave 0
     const bool mixer = t >= MIX_T && t < 2 * MIX_T;
     const int mu = t - MIX_T;
     // on = zcn16(o, post_norm); x2 = fma(on, sigmoid(attn_gate), x1)
-    if (wave == 0) {
-        const float ss = dot16_wave(sh.o, sh.o, d, lane);
-        if (lane == 0) sh.r = rinv(ss, d);
-    }
-    __syncthreads();
     float x2 = 0.0f;
-    if (t < d) {
-        const float tt = q.o * sh.r;
-        const float on = __builtin_fmaf(tt, q.pn, tt);
-        x2 = __builtin_fmaf(on, P.ga, q.x1);
-        sh.x2[t] = x2;
+    {
+        const float r = block_rinv(sh.o, sh.o, d, &sh.r_a);
+        if (t < d) {
+            const float tt = q.o * r;
+            const float on = __builtin_fmaf(tt, q.pn, tt);
+            x2 = __builtin_fmaf(on, P.ga, q.x1);
+            sh.x2[t] = x2;
+        }
     }
     __syncthreads();
     // h2 = zcn16(x2, pre_hada); z = h2 * d1 zero-padded to hada_n
-    if (wave == 0) {
-        const float ss = dot16_wave(sh.x2, sh.x2, d, lane);
-        if (lane == 0) sh.r = rinv(ss, d);
-    }
-    __syncthreads();
     float h2 = 0.0f;
-    if (t < d) {
-        const float tt = x2 * sh.r;
-        h2 = __builtin_fmaf(tt, q.ph, tt);
-        sh.h[t] = h2;
+    {
+        const float r = block_rinv(sh.x2, sh.x2, d, &sh.r_b);
+        if (t < d) {
+            const float tt = x2 * r;
+            h2 = __builtin_fmaf(tt, q.ph, tt);
+            sh.h[t] = h2;
+        }
+        sh.A[t] = t < d ? h2 * q.d1 : 0.0f;
     }
-    sh.A[t] = t < d ? h2 * q.d1 : 0.0f;
     __syncthreads();
     if (wave == 0) cond_weights(sh, d, lane, sh.wk);
     if (mixer) mix8_t(mu, sh.kron[0], sh.A, sh.B);
@@ -485,6 +527,7 @@ __device__ void layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, La
     __syncthreads();
     // The mHC write: y = (x2 + t3 * d4) - u; lane a = y hpost[a] + sum_b
     // hres[a][b] old[b] as an fma chain over b.
+    float m = 0.0f;
     if (t < d) {
         const float* hpost = sh.p + MHC_COLS;
         const float* hres = sh.p + MHC_COLS + MHC_LANES;
@@ -498,9 +541,10 @@ __device__ void layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, La
 #pragma unroll
             for (int b = 0; b < MHC_LANES; ++b) v = __builtin_fmaf(old[b], hres[a * MHC_LANES + b], v);
             sh.xs[a * d + t] = v;
+            m = fmaxf(m, fabsf(v));
         }
     }
-    __syncthreads();
+    return m;
 }
 
 // The next layer's weights a thread needs, read up front: its norm scale,
@@ -558,36 +602,31 @@ __device__ __forceinline__ int dot_row(const uint4* r, const int8_t* x8, int per
 }
 
 // The mHC read, engram gate, input norm and A8 of layer N
-// (step.rs:400-479).  The post and residual gates of the layer (hpost,
-// the Sinkhorn hres) are computed beside its units (fwd_units), off this
-// kernel's path.
+// (step.rs:400-479).  `m` is this thread's max |xs| (its share of the
+// lanes); the lanes are in LDS behind a barrier.  The post and residual
+// gates of the layer (hpost, the Sinkhorn hres) are computed beside its
+// units, off this kernel's path.
 __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, const InRegs& q, int in_bits,
                          LayerShared& sh) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d, nc = MHC_LANES * d;
-    // max |xs| beside the dot16 chain: rounding is monotonic, so
-    // max_i |xs_i * r| = max_i |xs_i| * r for r > 0.
+    // every wavefront: r = rinv(dot16(xs)), the amax over the wavefronts'
+    // maxima of |xs| (rounding is monotonic, so max_i |xs_i r| =
+    // max_i |xs_i| r for r > 0), then the int8 lanes
     {
-        float m = 0.0f;
-        for (int i = t; i < nc; i += LT) m = fmaxf(m, fabsf(sh.xs[i]));
-        m = wave_max(m);
-        if (lane == 0) sh.red[wave] = m;
-    }
-    if (wave == 0) {
-        const float ss = dot16_wave(sh.xs, sh.xs, nc, lane);
-        if (lane == 0) sh.r = rinv(ss, nc);
-    }
-    __syncthreads();
-    const float r = sh.r;
-    float m = sh.red[0];
+        const float r = block_rinv(sh.xs, sh.xs, nc, &sh.r_a);
+        float m = sh.red[0];
 #pragma unroll
-    for (int i = 1; i < LT / 64; ++i) m = fmaxf(m, sh.red[i]);
-    m = m * r;
-    const float sx = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
-    const float inv = 1.0f / sx;
-    for (int i = t; i < nc; i += LT) sh.nx8[i] = quant_one(sh.xs[i] * r, inv);
+        for (int i = 1; i < LT / 64; ++i) m = fmaxf(m, sh.red[i]);
+        m = m * r;
+        const float sx = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
+        const float inv = 1.0f / sx;
+        for (int i = t; i < nc; i += LT) sh.nx8[i] = quant_one(sh.xs[i] * r, inv);
+        if (t == 0) sh.r_sx = sx;
+    }
     __syncthreads();
     // Phi8 rows: p[k] = (sx * s_k) * idot(phi_q[k], nx8)
     {
+        const float sx = sh.r_sx;
         const int per = nc / 16;
         if (wave < MHC_COLS) {
             const int acc = dot_row(q.r0, sh.nx8, per, lane);
@@ -599,18 +638,23 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, con
         }
     }
     __syncthreads();
-    // The pre gate hp (sigmoid).
-    if (wave == 0 && lane < MHC_LANES) {
-        const float off = lane == N.lane ? 4.0f : -4.0f;
-        const float zz = ((sh.p[lane] * N.a_pre) + off) + N.b_pre[lane];
-        sh.hp[lane] = 1.0f / (lexpf(-zz) + 1.0f);
+    // The pre gate hp (sigmoid) in every wavefront, then u and x1.
+    float hp[MHC_LANES];
+    {
+        float g = 0.0f;
+        if (lane < MHC_LANES) {
+            const float off = lane == N.lane ? 4.0f : -4.0f;
+            const float zz = ((sh.p[lane] * N.a_pre) + off) + N.b_pre[lane];
+            g = 1.0f / (lexpf(-zz) + 1.0f);
+        }
+#pragma unroll
+        for (int b = 0; b < MHC_LANES; ++b) hp[b] = __shfl(g, b, 64);
     }
-    __syncthreads();
     float u = 0.0f, x1 = 0.0f;
     if (t < d) {
-        u = sh.xs[t] * sh.hp[0];
+        u = sh.xs[t] * hp[0];
 #pragma unroll
-        for (int b = 1; b < MHC_LANES; ++b) u = __builtin_fmaf(sh.xs[b * d + t], sh.hp[b], u);
+        for (int b = 1; b < MHC_LANES; ++b) u = __builtin_fmaf(sh.xs[b * d + t], hp[b], u);
         x1 = u;
         sh.x1[t] = x1;
         if (N.site >= 0) sh.o[t] = q.kr;
@@ -618,41 +662,38 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, con
     __syncthreads();
     if (N.site >= 0) {
         // alpha = sigmoid(dot16(x1 / |x1|, k / |k|) / sqrt(d)); x1 += alpha * conv
-        if (wave == 0) {
-            const float ss = dot16_wave(sh.x1, sh.x1, d, lane);
-            if (lane == 0) sh.r = rinv(ss, d);
-        } else if (wave == 1) {
-            const float ss = dot16_wave(sh.o, sh.o, d, lane);
-            if (lane == 0) sh.r2 = rinv(ss, d);
+        if (wave == 1) {
+            const float rk = rinv(dot16_wave(sh.o, sh.o, d, lane), d);
+            if (lane == 0) sh.r_b = rk;
         }
-        __syncthreads();
+        const float rx = block_rinv(sh.x1, sh.x1, d, &sh.r_a);
+        const float rk = sh.r_b;
         if (t < d) {
-            sh.x2[t] = x1 * sh.r;
-            sh.h[t] = q.kr * sh.r2;
+            sh.x2[t] = x1 * rx;
+            sh.h[t] = q.kr * rk;
         }
         __syncthreads();
         if (wave == 0) {
             const float dd = dot16_wave(sh.x2, sh.h, d, lane);
-            if (lane == 0) sh.r = 1.0f / (lexpf((-dd) / __builtin_sqrtf((float)d)) + 1.0f);
+            if (lane == 0) sh.r_c = 1.0f / (lexpf((-dd) / __builtin_sqrtf((float)d)) + 1.0f);
         }
         __syncthreads();
+        const float alpha = sh.r_c;
         if (t < d) {
-            x1 = __builtin_fmaf(q.ev, sh.r, x1);
+            x1 = __builtin_fmaf(q.ev, alpha, x1);
             sh.x1[t] = x1;
         }
         __syncthreads();
     }
     // hloc = norm_apply16(x1, rinv(dot16(x1)), norm_in), then A8.
-    if (wave == 0) {
-        const float ss = dot16_wave(sh.x1, sh.x1, d, lane);
-        if (lane == 0) sh.r = rinv(ss, d);
-    }
-    __syncthreads();
-    if (t < d) {
-        const float tt = x1 * sh.r;
-        sh.h[t] = __builtin_fmaf(tt, q.norm, tt);
-        S.u[t] = u;
-        S.x1[t] = x1;
+    {
+        const float r = block_rinv(sh.x1, sh.x1, d, &sh.r_b);
+        if (t < d) {
+            const float tt = x1 * r;
+            sh.h[t] = __builtin_fmaf(tt, q.norm, tt);
+            S.u[t] = u;
+            S.x1[t] = x1;
+        }
     }
     if (t < MHC_COLS) S.p[t] = sh.p[t];
     __syncthreads();
@@ -674,14 +715,12 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
         sh.h[t] = mean;
     }
     __syncthreads();
-    if (wave == 0) {
-        const float ss = dot16_wave(sh.h, sh.h, d, lane);
-        if (lane == 0) sh.r = rinv(ss, d);
-    }
-    __syncthreads();
-    if (t < d) {
-        const float tt = mean * sh.r;
-        sh.x2[t] = __builtin_fmaf(tt, fnorm, tt);
+    {
+        const float r = block_rinv(sh.h, sh.h, d, &sh.r_a);
+        if (t < d) {
+            const float tt = mean * r;
+            sh.x2[t] = __builtin_fmaf(tt, fnorm, tt);
+        }
     }
     __syncthreads();
     const int groups = (d + GROUP - 1) / GROUP;
@@ -697,7 +736,8 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
 __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int has_prev,
                                               int has_next, int row0, int in_bits, int head_bits) {
     __shared__ LayerShared sh;
-    const int t = threadIdx.x, d = D.d, nc = MHC_LANES * d, Gd = (d + GROUP - 1) / GROUP;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, d = D.d, nc = MHC_LANES * d;
+    const int Gd = (d + GROUP - 1) / GROUP;
     // this block's row of every row buffer
     const int row = row0 + blockIdx.x;
     SessDev R = S;
@@ -710,24 +750,34 @@ __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, Laye
     R.evals += (size_t)row * d;
     R.xq_in += (size_t)row * Gd * GROUP;
     R.sx_in += (size_t)row * Gd;
-    // every global read first
-    for (int i = t; i < nc; i += LT) sh.xs[i] = R.xs[i];
+    // every global read first, then the LDS stores
+    float xv[MHC_LANES];
+#pragma unroll
+    for (int k = 0; k < MHC_LANES; ++k) xv[k] = t + k * LT < nc ? R.xs[t + k * LT] : 0.0f;
     OutRegs qo{};
-    if (has_prev) {
-        qo = load_out(D, G, R, P, sh);
-        if (t < d) sh.o[t] = qo.o;
-    }
+    if (has_prev) qo = load_out(D, G, R, P, sh);
     InRegs qi{};
     float fnorm = 0.0f;
     if (has_next)
         qi = load_in(D, R, N);
     else if (t < d)
         fnorm = G.final_norm[t];
+    float m = 0.0f;
+#pragma unroll
+    for (int k = 0; k < MHC_LANES; ++k)
+        if (t + k * LT < nc) {
+            sh.xs[t + k * LT] = xv[k];
+            m = fmaxf(m, fabsf(xv[k]));
+        }
+    if (has_prev) store_out(D, qo, sh);
     __syncthreads();
-    if (has_prev) {
-        layer_out(D, P, qo, sh);
+    if (has_prev) m = layer_out(D, P, qo, sh);
+    // the wavefronts' maxima of |xs| for the mHC read
+    m = wave_max(m);
+    if (lane == 0) sh.red[wave] = m;
+    __syncthreads();
+    if (has_prev)
         for (int i = t; i < nc; i += LT) R.xs[i] = sh.xs[i];
-    }
     if (has_next)
         layer_in(D, R, N, qi, in_bits, sh);
     else
@@ -1098,32 +1148,38 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
     const int lo = window_lo(L.window, p0), n = p0 + 1 - lo, blocked = n / 4 * 4;
     const int h = t / DG_HEAD_T, u = t % DG_HEAD_T, hw = u >> 6;  // head, thread and wavefront in it
     __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][MAX_HEAD_DIM];  // key rows by slot - lo
-    __shared__ int8_t vs8[MAX_HEAD_DIM][ATT_CHUNK_MAX + 4];          // value columns by slot - lo
+    __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][ATT_CHUNK_MAX + 4];  // value columns by slot - lo
     __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
     __shared__ alignas(16) int8_t q8[HP][MAX_HEAD_DIM];
     __shared__ float sc[HP][ATT_CHUNK_MAX];
-    __shared__ int8_t dig[HP][3][ATT_CHUNK_MAX];
+    __shared__ alignas(16) int8_t dig[HP][3][ATT_CHUNK_MAX];
     __shared__ float red[HP][DG_HEAD_T / 64];
     __shared__ float s_qs[HP], s_sum[HP];
     __shared__ float att[HP * MAX_HEAD_DIM];
     const size_t lc = (size_t)layer * D.cap;
-    // The keys before the position: int8 rows, scales and value columns.
-    {
-        const int nold = n - 1, rq = qk / 16;
-        for (int e = t; e < nold * rq; e += NT) {
-            const int i = e / rq, c = e % rq;
-            reinterpret_cast<uint4*>(ks8[i])[c] =
-                reinterpret_cast<const uint4*>(S.k8 + ((lc + lo + i) * nkv + kvh) * qk)[c];
-        }
-        for (int i = t; i < nold; i += NT) {
-            kss[i] = S.ks[(lc + lo + i) * nkv + kvh];
-            vss[i] = S.vs[(lc + lo + i) * nkv + kvh];
-        }
-        const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.cap + lo;
-        for (int e = t; e < vd * nold; e += NT) {
-            const int dm = e / nold, i = e % nold;
-            vs8[dm][i] = vcol[(size_t)dm * D.cap + i];
-        }
+    // The keys before the position: int8 rows, scales and value columns,
+    // loaded into registers first (every load in flight at once) and
+    // stored to LDS after the units.  Indices run over the padded
+    // [256][4] row chunks and [64][256] value bytes.
+    constexpr int KR = ATT_CHUNK_MAX * 4 / NT, VB = MAX_HEAD_DIM * ATT_CHUNK_MAX / NT;
+    const int nold = n - 1, rq = qk / 16;
+    uint4 kr[KR];
+    int vb[VB];
+    float ksr = 0.0f, vsr = 0.0f;
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+        const int e = t + r * NT, i = e >> 2, c = e & 3;
+        if (i < nold && c < rq) kr[r] = reinterpret_cast<const uint4*>(S.k8 + ((lc + lo + i) * nkv + kvh) * qk)[c];
+    }
+    if (t < nold) {
+        ksr = S.ks[(lc + lo + t) * nkv + kvh];
+        vsr = S.vs[(lc + lo + t) * nkv + kvh];
+    }
+    const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.cap + lo;
+#pragma unroll
+    for (int r = 0; r < VB; ++r) {
+        const int e = t + r * NT, dm = e >> 8, i = e & (ATT_CHUNK_MAX - 1);
+        if (dm < vd && i < nold) vb[r] = vcol[(size_t)dm * D.cap + i];
     }
     // The units: queries on waves 0 .. HP-1, the new key and value on the next two.
     if (wave < HP) {
@@ -1157,6 +1213,20 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
             vss[n - 1] = s;
             if (owner) S.vs[(lc + p0) * nkv + kvh] = s;
         }
+    }
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+        const int e = t + r * NT, i = e >> 2, c = e & 3;
+        if (i < nold && c < rq) reinterpret_cast<uint4*>(ks8[i])[c] = kr[r];
+    }
+    if (t < nold) {
+        kss[t] = ksr;
+        vss[t] = vsr;
+    }
+#pragma unroll
+    for (int r = 0; r < VB; ++r) {
+        const int e = t + r * NT, dm = e >> 8, i = e & (ATT_CHUNK_MAX - 1);
+        if (dm < vd && i < nold) vs8[dm][i] = (int8_t)vb[r];
     }
     __syncthreads();
     // attend_head_ref over the one chunk, one head per 256 threads
@@ -1214,17 +1284,19 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
         dig[h][1][i] = (int8_t)((wq >> 7) & 127);
         dig[h][2][i] = (int8_t)(wq & 127);
     }
+    if (u >= n && u < (n + 3) / 4 * 4) dig[h][0][u] = dig[h][1][u] = dig[h][2][u] = 0;  // the last dword's tail
     __syncthreads();
     {
+        // exact integer P.V: four slots per sdot4 (tail digits are zero)
         const float cw = wmax * bits_f32(0x35000004u);
         const int dm = u >> 2, part = u & 3;
         int a = 0, b = 0, c = 0;
         if (dm < vd)
-            for (int i = part; i < n; i += 4) {
-                const int v = vs8[dm][i];
-                a += dig[h][0][i] * v;
-                b += dig[h][1][i] * v;
-                c += dig[h][2][i] * v;
+            for (int i = part * 4; i < n; i += 16) {
+                const int v = *reinterpret_cast<const int*>(&vs8[dm][i]);
+                a = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(&dig[h][0][i]), v, a, false);
+                b = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(&dig[h][1][i]), v, b, false);
+                c = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(&dig[h][2][i]), v, c, false);
             }
         a += __shfl_xor(a, 1, 64);
         a += __shfl_xor(a, 2, 64);
