@@ -15,6 +15,8 @@
 // arithmetic, so a launch costs one memory round trip; each wavefront
 // turns its groups into (float(L), scale) pairs and wave 0 runs the
 // group-ordered fma chain from LDS.
+#include <string.h>
+
 #include <type_traits>
 
 #include "nh_device.h"
@@ -23,12 +25,11 @@
 namespace nh {
 
 template <int GPS, int S, int BITS, bool DBG>
-__global__ __launch_bounds__(S * 64) void k_gemv(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
-                                                 const uint4* __restrict__ xq, const float* __restrict__ sx,
-                                                 float* __restrict__ y, int32_t* __restrict__ dbg, int out, int G,
-                                                 float cbs, Lut lut) {
+__device__ __forceinline__ void gemv_tile(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
+                                          const uint4* __restrict__ xq, const float* __restrict__ sx,
+                                          float* __restrict__ y, int32_t* __restrict__ dbg, int out, int G, float cbs,
+                                          Lut lut, int tile) {
     static_assert(S * 64 >= GPS * S * 8, "one thread per activation uint4");
-    const int tile = blockIdx.x;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int r = lane >> 2, l = lane & 3;
@@ -96,6 +97,23 @@ __global__ __launch_bounds__(S * 64) void k_gemv(const void* __restrict__ codes,
     if (y && l == 0 && n < out) y[n] = u;
 }
 
+template <int GPS, int S, int BITS, bool DBG>
+__global__ __launch_bounds__(S * 64) void k_gemv(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
+                                                 const uint4* __restrict__ xq, const float* __restrict__ sx,
+                                                 float* __restrict__ y, int32_t* __restrict__ dbg, int out, int G,
+                                                 float cbs, Lut lut) {
+    gemv_tile<GPS, S, BITS, DBG>(codes, norms, xq, sx, y, dbg, out, G, cbs, lut, blockIdx.x);
+}
+
+// Several same-shaped products in one launch (blockIdx.y picks the member),
+// e.g. the engram key | value products of every site.
+template <int GPS, int S, int BITS>
+__global__ __launch_bounds__(S * 64) void k_gemv_batch(GemvBatch b, int out, int G, float cbs, Lut lut) {
+    const int e = blockIdx.y;
+    gemv_tile<GPS, S, BITS, false>(b.codes[e], b.norms[e], b.xq[e], b.sx[e], b.y[e], nullptr, out, G, cbs, lut,
+                                   blockIdx.x);
+}
+
 template <int GPS, int S, int BITS>
 static hipError_t run(const nh_qmat* w, const nh_qact* a, float* y, int32_t* dbg, hipStream_t s) {
     const QMatMeta& m = w->m;
@@ -129,6 +147,52 @@ static hipError_t dispatch(const nh_qmat* w, const nh_qact* a, float* y, int32_t
     if (G <= 24) return run<4, 6, BITS>(w, a, y, dbg, s);
     if (G <= 32) return run<4, 8, BITS>(w, a, y, dbg, s);
     return hipErrorInvalidValue;
+}
+
+template <int GPS, int S, int BITS>
+static hipError_t run_batch(const nh_qmat* w, const GemvBatch& b, int n, hipStream_t s) {
+    const QMatMeta& m = w->m;
+    const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
+    hipLaunchKernelGGL((k_gemv_batch<GPS, S, BITS>), dim3(m.out_pad / TILE_ROWS, n), dim3(S * 64), 0, s, b, m.out,
+                       m.groups, m.cbs, lut);
+    return hipGetLastError();
+}
+
+template <int BITS>
+static hipError_t dispatch_batch(const nh_qmat* w, const GemvBatch& b, int n, hipStream_t s) {
+    const int G = w->m.groups;
+    if (G <= 1) return run_batch<1, 1, BITS>(w, b, n, s);
+    if (G <= 2) return run_batch<2, 1, BITS>(w, b, n, s);
+    if (G <= 3) return run_batch<3, 1, BITS>(w, b, n, s);
+    if (G <= 4) return run_batch<2, 2, BITS>(w, b, n, s);
+    if (G <= 6) return run_batch<3, 2, BITS>(w, b, n, s);
+    if (G <= 8) return run_batch<2, 4, BITS>(w, b, n, s);
+    if (G <= 12) return run_batch<3, 4, BITS>(w, b, n, s);
+    if (G <= 16) return run_batch<4, 4, BITS>(w, b, n, s);
+    if (G <= 24) return run_batch<4, 6, BITS>(w, b, n, s);
+    if (G <= 32) return run_batch<4, 8, BITS>(w, b, n, s);
+    return hipErrorInvalidValue;
+}
+
+bool gemv_batchable(const nh_qmat* const* w, int n) {
+    if (n < 1 || n > GEMV_BATCH_MAX) return false;
+    for (int i = 1; i < n; ++i)
+        if (w[i]->m.out != w[0]->m.out || w[i]->m.groups != w[0]->m.groups || w[i]->m.bits != w[0]->m.bits ||
+            w[i]->m.cbs != w[0]->m.cbs || memcmp(&w[i]->m.lut, &w[0]->m.lut, sizeof(LutTables)) != 0)
+            return false;
+    return true;
+}
+
+hipError_t launch_gemv_batch(const nh_qmat* const* w, const nh_qact* const* a, float* const* y, int n, hipStream_t s) {
+    GemvBatch b{};
+    for (int i = 0; i < n; ++i) {
+        b.codes[i] = w[i]->d_codes;
+        b.norms[i] = w[i]->d_norms;
+        b.xq[i] = (const uint4*)a[i]->d_xq;
+        b.sx[i] = a[i]->d_sx;
+        b.y[i] = y[i];
+    }
+    return w[0]->m.bits == 2 ? dispatch_batch<2>(w[0], b, n, s) : dispatch_batch<4>(w[0], b, n, s);
 }
 
 hipError_t launch_gemv(const nh_qmat* w, const nh_qact* a, float* y, int col0, int32_t* dbg, hipStream_t s) {

@@ -124,6 +124,19 @@ struct ArchiveSmall {
 // one of them is a CQ record).
 int load_archive(const uint8_t* bytes, uint64_t n, nh_weights** w, ArchiveSmall* small);
 
+// Same-shaped decode products launched together (k_gemv_batch).
+constexpr int GEMV_BATCH_MAX = 16;
+struct GemvBatch {
+    const void* codes[GEMV_BATCH_MAX];
+    const uint16_t* norms[GEMV_BATCH_MAX];
+    const uint4* xq[GEMV_BATCH_MAX];
+    const float* sx[GEMV_BATCH_MAX];
+    float* y[GEMV_BATCH_MAX];
+};
+// Whether n matrices share out, groups, code width and tables.
+bool gemv_batchable(const nh_qmat* const* w, int n);
+hipError_t launch_gemv_batch(const nh_qmat* const* w, const nh_qact* const* a, float* const* y, int n, hipStream_t s);
+
 // Launchers (one per kernel translation unit).
 hipError_t launch_act_prep(const float* x, int rows, int in_dim, int groups, int bits, const uint16_t* norm_scale,
                            int8_t* xq, float* sx, hipStream_t s);

@@ -410,9 +410,21 @@ int feed(nh_session* s, int t, bool logits, hipStream_t st) {
     const nh::SessDev& S = s->S;
     const int p0 = s->len;
     NH_TRY(nh::fwd_begin(D, m->glob, S, m->begin, p0, t, st), "feed begin");
-    for (int e = 0; e < D.sites; ++e)
-        NH_TRY(product(m->ekv[e], &s->a_eng[e], t, S.ekv + (size_t)e * nh::FWD_ROWS * 2 * D.d, 2 * D.d, st),
-               "engram kv");
+    if (t == 1 && D.sites > 1 && nh::gemv_batchable(m->ekv.data(), D.sites)) {
+        // every site's key | value product in one launch
+        const nh_qact* acts[nh::GEMV_BATCH_MAX];
+        float* ys[nh::GEMV_BATCH_MAX];
+        for (int e = 0; e < D.sites; ++e) {
+            s->a_eng[e].rows = 1;
+            acts[e] = &s->a_eng[e];
+            ys[e] = S.ekv + (size_t)e * nh::FWD_ROWS * 2 * D.d;
+        }
+        NH_TRY(nh::launch_gemv_batch(m->ekv.data(), acts, ys, D.sites, st), "engram kv");
+    } else {
+        for (int e = 0; e < D.sites; ++e)
+            NH_TRY(product(m->ekv[e], &s->a_eng[e], t, S.ekv + (size_t)e * nh::FWD_ROWS * 2 * D.d, 2 * D.d, st),
+                   "engram kv");
+    }
     NH_TRY(nh::fwd_engram_hist(D, m->glob, S, p0, t, st), "engram history");
     for (int l = 0; l < D.layers; ++l) {
         const nh::LayerDev* prev = l > 0 ? &m->layers[l - 1] : nullptr;
