@@ -465,6 +465,8 @@ def main():
     ap.add_argument("--gemm-shape", default="", metavar="M,K,N",
                     help="only run one prefill product shape, eagerly (for GEMM profiles)")
     ap.add_argument("--launches", type=int, default=200, help="launches for --gemm-shape")
+    ap.add_argument("--needle3-only", action="store_true",
+                    help="only run the Needle-3 decode and prefill lines (for model profiles)")
     args = ap.parse_args()
     if args.copy_calibration:
         import torch
@@ -491,6 +493,10 @@ def main():
     torch.cuda.synchronize()
     if args.gemm_shape:
         print(json.dumps(gemm_shape(args.gemm_shape, args.launches, nh, torch)))
+        return
+    if args.needle3_only:
+        print(json.dumps({"needle3_decode": needle3_decode(nh, torch, args.cpu_seconds * 2, not args.no_cpu),
+                          "needle3_prefill": needle3_prefill(nh, torch, args.cpu_seconds * 2, not args.no_cpu)}))
         return
     gpu = gpu_gemv(args, nh, torch)
     progress(f"decode GEMV: {gpu['ms_launch'] * 1e3:.3f} us per launch")

@@ -39,12 +39,13 @@ struct Dims {
     int sites, ntab, eheads, seed_stride, slots, sub, dilation;
     int orders[4];
     int cap;    // session positions
+    int vcap;   // row stride of the transposed int8 values: cap + 4 rounded up to 16
     int max_chunks;  // attention chunks a position can need
 };
 
 struct LayerDev {
-    const uint16_t* kron[6];
-    const uint16_t *cond_v, *cond_u, *d1, *d2, *b2, *d3, *d4;
+    const uint16_t* stage;  // the six Kronecker factors [32][32], cond_v [d][8], cond_u [8][1024]
+    const uint16_t *d1, *d2, *b2, *d3, *d4;
     const uint16_t *norm_in, *post_norm, *pre_hada, *q_taps, *k_taps, *v_taps, *q_norm, *k_norm;
     const int8_t* phi_q;  // [24][lanes * d]
     const float* phi_s;   // [24]
@@ -89,7 +90,7 @@ struct SessDev {
     float* hist;      // [layers][hist_slots][W] ring of pre-tap rows
     int8_t* k8;       // [layers][cap][nkv][qk]
     float* ks;        // [layers][cap][nkv]
-    int8_t* v8t;      // [layers][nkv][vd][cap]
+    int8_t* v8t;      // [layers][nkv][vd][vcap]
     float* vs;        // [layers][cap][nkv]
     int8_t* ev8;      // [sites][cap][d]
     float* evs;       // [sites][cap][d / 32]

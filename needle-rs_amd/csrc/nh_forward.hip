@@ -65,37 +65,10 @@ __device__ __forceinline__ float rinv(float ss, int n) {
     return 1.0f / __builtin_sqrtf(v);
 }
 
-// dot16 (infer.rs:369-419, portable branch), by one wavefront: lane
-// i16 = 4 j + l carries accumulator a[j][l] over 16-element chunks in
-// order; t[l] = ((a[2][l] + a[3][l]) + a[1][l]) + a[0][l]; the result
-// (t0 + t1) + (t2 + t3) reaches every lane.
-__device__ __forceinline__ float dot16_wave(const float* x, const float* y, int n, int lane) {
-    float a = 0.0f;
-    if (lane < 16) {
-        const int chunks = n / 16;
-        int c = 0;
-        // batches of 16 chunks: the loads issue together, then the chain
-        for (; c + 16 <= chunks; c += 16) {
-            float xv[16], yv[16];
-#pragma unroll
-            for (int u = 0; u < 16; ++u) {
-                xv[u] = x[(c + u) * 16 + lane];
-                yv[u] = y[(c + u) * 16 + lane];
-            }
-#pragma unroll
-            for (int u = 0; u < 16; ++u) a = __builtin_fmaf(xv[u], yv[u], a);
-        }
-        for (; c < chunks; ++c) a = __builtin_fmaf(x[c * 16 + lane], y[c * 16 + lane], a);
-    }
-    const int l = lane & 3;
-    const float a0 = __shfl(a, l, 64), a1 = __shfl(a, 4 + l, 64), a2 = __shfl(a, 8 + l, 64),
-                a3 = __shfl(a, 12 + l, 64);
-    const float t = ((a2 + a3) + a1) + a0;
-    const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
-    return (t0 + t1) + (t2 + t3);
-}
-
-// The same over a vector held one element per lane (n <= 64).
+// dot16 (infer.rs:369-419, portable branch) over a vector held one element
+// per lane (n <= 64): lane i16 = 4 j + l carries accumulator a[j][l] over
+// 16-element chunks in order; t[l] = ((a[2][l] + a[3][l]) + a[1][l]) +
+// a[0][l]; the result (t0 + t1) + (t2 + t3) reaches every lane.
 __device__ __forceinline__ float dot16_lanes(float v, int n, int lane) {
     float a = 0.0f;
     const int chunks = n / 16;
@@ -290,11 +263,18 @@ namespace {
 
 constexpr int BT_STRIDE = HADA_NB + 1;  // padded row of a transposed mix8 output
 constexpr int MIX_T = 256;              // threads of one mix8 (4 outputs each)
+// Transposed copies for the serial chains, so a chain lane reads its
+// operands as contiguous 16-byte vectors: a dot16 operand x[16 c + l] at
+// l * pitch + c (pitch TP_D for d-long vectors, TP_X for the 4 lanes);
+// h2[4 u + jm] at jm * TP_H + u and cond_v[4 u + jm][k] at
+// (8 jm + k) * TP_C + u for cond_weights.
+constexpr int TP_D = FWD_MAX_D / 16 + 4;
+constexpr int TP_X = MHC_LANES * FWD_MAX_D / 16 + 4;
+constexpr int TP_H = FWD_MAX_D / 4 + 4;
+constexpr int TP_C = FWD_MAX_D / 4 + 8;
 
 struct LayerShared {
     float xs[MHC_LANES * FWD_MAX_D];
-    float o[FWD_MAX_D];   // attention output, later the engram key row
-    float x1[FWD_MAX_D];
     float x2[FWD_MAX_D];
     float h[FWD_MAX_D];
     alignas(16) float A[HADA_N];
@@ -302,8 +282,12 @@ struct LayerShared {
     alignas(16) float C[HADA_N];
     alignas(16) float kron[6][HADA_N];
     alignas(16) int8_t nx8[MHC_LANES * FWD_MAX_D];
-    alignas(16) uint16_t cond_v[FWD_MAX_D * COND_RANK];
+    alignas(16) uint16_t cvT[4 * COND_RANK * TP_C];
     alignas(16) uint16_t cond_u[COND_RANK * HADA_N];
+    alignas(16) float tA[16 * TP_D];
+    alignas(16) float tB[16 * TP_D];
+    alignas(16) float tX[16 * TP_X];
+    alignas(16) float hT[4 * TP_H];
     float red[LT / 64];
     float p[64];
     float wk[COND_RANK];
@@ -351,15 +335,72 @@ __device__ __forceinline__ void mix8_n(int u, const float* ct, const float* rows
     *reinterpret_cast<float4*>(out + r * HADA_NB + c0) = make_float4(o0, o1, o2, o3);
 }
 
-// rinv(dot16(x, y)) by wavefront 0, handed to the block through LDS.
-__device__ __forceinline__ float block_rinv(const float* x, const float* y, int n, float* slot) {
+// Element i of a dot16 operand into its transposed copy.
+__device__ __forceinline__ void put_t(float* T, int pitch, int i, float v) { T[(i & 15) * pitch + (i >> 4)] = v; }
+
+// dot16 over operands held transposed (x[16 c + l] at xT[l * pitch + c]),
+// the same chains and combine as dot16_wave: lane l < 16 carries
+// accumulator l over c in order.  Batches of 16 chunks, the next batch's
+// loads issued before this batch's fmas.
+template <bool SELF>
+__device__ __forceinline__ float dot16_t(const float* xT, const float* yT, int pitch, int n, int lane) {
+    float a = 0.0f;
+    if (lane < 16) {
+        const int chunks = n / 16, nb = chunks / 16;
+        const float4* xr = reinterpret_cast<const float4*>(xT + lane * pitch);
+        const float4* yr = reinterpret_cast<const float4*>(yT + lane * pitch);
+        float4 xc[4], yc[4];
+        if (nb > 0) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                xc[u] = xr[u];
+                yc[u] = SELF ? xc[u] : yr[u];
+            }
+        }
+        for (int b = 0; b < nb; ++b) {
+            float4 xn[4], yn[4];
+            const int nx = b + 1 < nb ? (b + 1) * 4 : b * 4;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                xn[u] = xr[nx + u];
+                yn[u] = SELF ? xn[u] : yr[nx + u];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                a = __builtin_fmaf(xc[u].x, yc[u].x, a);
+                a = __builtin_fmaf(xc[u].y, yc[u].y, a);
+                a = __builtin_fmaf(xc[u].z, yc[u].z, a);
+                a = __builtin_fmaf(xc[u].w, yc[u].w, a);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                xc[u] = xn[u];
+                yc[u] = yn[u];
+            }
+        }
+        const float* xs = xT + lane * pitch;
+        const float* ys = yT + lane * pitch;
+        for (int c = nb * 16; c < chunks; ++c) a = __builtin_fmaf(xs[c], ys[c], a);
+    }
+    const int l = lane & 3;
+    const float a0 = __shfl(a, l, 64), a1 = __shfl(a, 4 + l, 64), a2 = __shfl(a, 8 + l, 64),
+                a3 = __shfl(a, 12 + l, 64);
+    const float t = ((a2 + a3) + a1) + a0;
+    const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
+    return (t0 + t1) + (t2 + t3);
+}
+
+// rinv(dot16(x, x)) over a transposed operand by wavefront 0, handed to
+// the block through LDS.
+__device__ __forceinline__ float block_rinv_t(const float* xT, int pitch, int n, float* slot) {
     if ((threadIdx.x >> 6) == 0) {
-        const float r = rinv(dot16_wave(x, y, n, threadIdx.x & 63), n);
+        const float r = rinv(dot16_t<true>(xT, xT, pitch, n, threadIdx.x & 63), n);
         if (threadIdx.x == 0) *slot = r;
     }
     __syncthreads();
     return *slot;
 }
+
 
 // The previous layer's inputs and weights a thread needs, read up front.
 // The LDS tables go out as one list of 16-byte chunks, up to STAGE_PER per
@@ -367,8 +408,12 @@ __device__ __forceinline__ float block_rinv(const float* x, const float* y, int 
 // (d chunks), then cond_u (1024).
 constexpr int STAGE_PER = 3;
 
+// f16 weights stay raw bits (one per register) until their use:
+// converting or packing them on arrival would make the wave wait for each
+// load before issuing the next.
 struct OutRegs {
-    float o, x1, u, pn, ph, d1, d2, b2, d3, d4;
+    float o, x1, u, pv;
+    uint32_t pn, ph, d1, d2, b2, d3, d4;
     int p1, p2;
     uint4 st[STAGE_PER];
 };
@@ -380,30 +425,32 @@ __device__ __forceinline__ OutRegs load_out(const Dims& D, const Globals& G, con
     const int kron_n = 6 * HADA_N / 8, cv_n = d * COND_RANK / 8, cu_n = COND_RANK * HADA_N / 8;
 #pragma unroll
     for (int r = 0; r < STAGE_PER; ++r) {
-        const int e = t + r * LT;
-        if (e < kron_n)
-            q.st[r] = reinterpret_cast<const uint4*>(P.kron[e / (HADA_N / 8)])[e % (HADA_N / 8)];
-        else if (e < kron_n + cv_n)
-            q.st[r] = reinterpret_cast<const uint4*>(P.cond_v)[e - kron_n];
-        else if (e < kron_n + cv_n + cu_n)
-            q.st[r] = reinterpret_cast<const uint4*>(P.cond_u)[e - kron_n - cv_n];
+        const int e = min(t + r * LT, kron_n + cv_n + cu_n - 1);
+        q.st[r] = reinterpret_cast<const uint4*>(P.stage)[e];
     }
-    if (t < d) {
-        q.o = S.o[t];
-        q.x1 = S.x1[t];
-        q.u = S.u[t];
-        q.pn = h2f(P.post_norm[t]);
-        q.ph = h2f(P.pre_hada[t]);
-        q.d1 = h2f(P.d1[t]);
-        q.d4 = h2f(P.d4[t]);
-    }
-    q.d2 = h2f(P.d2[t]);
-    q.b2 = h2f(P.b2[t]);
-    q.d3 = h2f(P.d3[t]);
+    // (unconditional loads: threads past d read element d - 1 and ignore it)
+    const int td = min(t, d - 1);
+    q.o = S.o[td];
+    q.x1 = S.x1[td];
+    q.u = S.u[td];
+    q.pn = P.post_norm[td];
+    q.ph = P.pre_hada[td];
+    q.d1 = P.d1[td];
+    q.d4 = P.d4[td];
+    q.d2 = P.d2[t];
+    q.b2 = P.b2[t];
+    q.d3 = P.d3[t];
     q.p1 = G.perm1[t];
     q.p2 = G.perm2[t];
-    if (t < 64) sh.p[t] = S.p[t];
+    q.pv = S.p[t & 63];
     return q;
+}
+
+// A raw f16 weight as f32 at its use: the empty asm keeps the conversion
+// (and so the wait for the load) from being hoisted up to the load.
+__device__ __forceinline__ float h2f_late(uint32_t b) {
+    asm volatile("" : "+v"(b));
+    return h2f((uint16_t)b);
 }
 
 __device__ __forceinline__ void store_out(const Dims& D, const OutRegs& q, LayerShared& sh) {
@@ -426,33 +473,55 @@ __device__ __forceinline__ void store_out(const Dims& D, const OutRegs& q, Layer
             *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
             *reinterpret_cast<float4*>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
         } else if (e < kron_n + cv_n) {
-            reinterpret_cast<uint4*>(sh.cond_v)[e - kron_n] = q.st[r];
+            // row j of cond_v (8 f16) into column j / 4 of rows 8 (j % 4) + k
+            const int j = e - kron_n;
+            const uint4 v = q.st[r];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            uint16_t* dst = sh.cvT + (j & 3) * COND_RANK * TP_C + (j >> 2);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                dst[(2 * k) * TP_C] = (uint16_t)(w[k] & 0xffffu);
+                dst[(2 * k + 1) * TP_C] = (uint16_t)(w[k] >> 16);
+            }
         } else if (e < kron_n + cv_n + cu_n) {
             reinterpret_cast<uint4*>(sh.cond_u)[e - kron_n - cv_n] = q.st[r];
         }
     }
-    if (t < D.d) sh.o[t] = q.o;
+    if (t < D.d) put_t(sh.tA, TP_D, t, q.o);
+    if (t < 64) sh.p[t] = q.pv;
 }
 
 // cond_weights (infer.rs:1640-1656) by wavefront 0: lane 8 jm + k carries
-// acc[jm][k] = fma(h2[j], cond_v[j][k], .) over j = jm, jm + 4, ... in
-// batches of 32 steps; then the softmax of the combined logits.
+// acc[jm][k] = fma(h2[j], cond_v[j][k], .) over j = jm, jm + 4, ...
+// (u = j / 4 in order), reading h2 and cond_v from their transposed copies
+// 8 steps per load, the next batch's loads issued before this batch's fmas;
+// then the softmax of the combined logits.
 __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int lane, float* wk) {
     const int k = lane & 7, jm = lane >> 3;
     float a = 0.0f;
     if (lane < 32) {
-        int j = jm;
-        for (; j + 4 * 31 < d; j += 4 * 32) {
-            float hv[32], cv[32];
+        const int steps = d / 4, nb = steps / 8;
+        const float4* hr = reinterpret_cast<const float4*>(sh.hT + jm * TP_H);
+        const uint4* cr = reinterpret_cast<const uint4*>(sh.cvT + (jm * COND_RANK + k) * TP_C);
+        float4 h0 = hr[0], h1 = hr[1];
+        uint4 c0 = cr[0];
+        for (int b = 0; b < nb; ++b) {
+            const int nx = b + 1 < nb ? b + 1 : b;
+            const float4 n0 = hr[2 * nx], n1 = hr[2 * nx + 1];
+            const uint4 nc = cr[nx];
+            const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+            const uint32_t cw[4] = {c0.x, c0.y, c0.z, c0.w};
 #pragma unroll
-            for (int u = 0; u < 32; ++u) {
-                hv[u] = sh.h[j + 4 * u];
-                cv[u] = h2f(sh.cond_v[(j + 4 * u) * 8 + k]);
+            for (int u = 0; u < 4; ++u) {
+                a = __builtin_fmaf(hv[2 * u], h2f((uint16_t)(cw[u] & 0xffffu)), a);
+                a = __builtin_fmaf(hv[2 * u + 1], h2f((uint16_t)(cw[u] >> 16)), a);
             }
-#pragma unroll
-            for (int u = 0; u < 32; ++u) a = __builtin_fmaf(hv[u], cv[u], a);
+            h0 = n0;
+            h1 = n1;
+            c0 = nc;
         }
-        for (; j < d; j += 4) a = __builtin_fmaf(sh.h[j], h2f(sh.cond_v[j * 8 + k]), a);
+        for (int u = nb * 8; u < steps; ++u)
+            a = __builtin_fmaf(sh.hT[jm * TP_H + u], h2f(sh.cvT[(jm * COND_RANK + k) * TP_C + u]), a);
     }
     const float a0 = __shfl(a, k, 64), a1 = __shfl(a, 8 + k, 64), a2 = __shfl(a, 16 + k, 64),
                 a3 = __shfl(a, 24 + k, 64);
@@ -480,25 +549,25 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
     // on = zcn16(o, post_norm); x2 = fma(on, sigmoid(attn_gate), x1)
     float x2 = 0.0f;
     {
-        const float r = block_rinv(sh.o, sh.o, d, &sh.r_a);
+        const float r = block_rinv_t(sh.tA, TP_D, d, &sh.r_a);
         if (t < d) {
             const float tt = q.o * r;
-            const float on = __builtin_fmaf(tt, q.pn, tt);
+            const float on = __builtin_fmaf(tt, h2f_late(q.pn), tt);
             x2 = __builtin_fmaf(on, P.ga, q.x1);
-            sh.x2[t] = x2;
+            put_t(sh.tB, TP_D, t, x2);
         }
     }
     __syncthreads();
     // h2 = zcn16(x2, pre_hada); z = h2 * d1 zero-padded to hada_n
     float h2 = 0.0f;
     {
-        const float r = block_rinv(sh.x2, sh.x2, d, &sh.r_b);
+        const float r = block_rinv_t(sh.tB, TP_D, d, &sh.r_b);
         if (t < d) {
             const float tt = x2 * r;
-            h2 = __builtin_fmaf(tt, q.ph, tt);
-            sh.h[t] = h2;
+            h2 = __builtin_fmaf(tt, h2f_late(q.ph), tt);
+            sh.hT[(t & 3) * TP_H + (t >> 2)] = h2;
         }
-        sh.A[t] = t < d ? h2 * q.d1 : 0.0f;
+        sh.A[t] = t < d ? h2 * h2f_late(q.d1) : 0.0f;
     }
     __syncthreads();
     if (wave == 0) cond_weights(sh, d, lane, sh.wk);
@@ -510,7 +579,7 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
         float cond = 1.0f;
 #pragma unroll
         for (int k = 0; k < COND_RANK; ++k) cond = __builtin_fmaf(h2f(sh.cond_u[k * HADA_N + t]), sh.wk[k], cond);
-        float zs = __builtin_fmaf(sh.C[q.p1], cond * q.d2, q.b2);
+        float zs = __builtin_fmaf(sh.C[q.p1], cond * h2f_late(q.d2), h2f_late(q.b2));
         zs = zs / (nexp(-zs) + 1.0f);
         sh.A[t] = zs;
     }
@@ -519,7 +588,7 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
     __syncthreads();
     if (mixer) mix8_n(mu, sh.B, sh.kron[3], sh.C, HADA_NB);
     __syncthreads();
-    sh.A[t] = sh.C[q.p2] * q.d3;
+    sh.A[t] = sh.C[q.p2] * h2f_late(q.d3);
     __syncthreads();
     if (mixer) mix8_t(mu, sh.kron[4], sh.A, sh.B);
     __syncthreads();
@@ -531,7 +600,7 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
     if (t < d) {
         const float* hpost = sh.p + MHC_COLS;
         const float* hres = sh.p + MHC_COLS + MHC_LANES;
-        const float y = (x2 + sh.C[t] * q.d4) - q.u;
+        const float y = (x2 + sh.C[t] * h2f_late(q.d4)) - q.u;
         float old[MHC_LANES];
 #pragma unroll
         for (int b = 0; b < MHC_LANES; ++b) old[b] = sh.xs[b * d + t];
@@ -541,6 +610,7 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
 #pragma unroll
             for (int b = 0; b < MHC_LANES; ++b) v = __builtin_fmaf(old[b], hres[a * MHC_LANES + b], v);
             sh.xs[a * d + t] = v;
+            put_t(sh.tX, TP_X, a * d + t, v);
             m = fmaxf(m, fabsf(v));
         }
     }
@@ -552,35 +622,37 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
 // wave + 16, 16 bytes at lane + 64 j of each, j < 4: rows of up to 4096).
 constexpr int PHI_CHUNKS = MHC_LANES * FWD_MAX_D / 16 / 64;
 struct InRegs {
-    float norm, kr, ev, ps0, ps1;
+    uint32_t norm;
+    float kr, ev, ps0, ps1;
     uint4 r0[PHI_CHUNKS], r1[PHI_CHUNKS];
 };
 
 __device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const LayerDev& N) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d, nc = MHC_LANES * d;
-    InRegs q{};
-    if (t < d) {
-        q.norm = h2f(N.norm_in[t]);
-        if (N.site >= 0) {
-            q.kr = S.ekv[(size_t)N.site * FWD_ROWS * 2 * d + t];
-            q.ev = S.evals[(size_t)N.site * FWD_ROWS * d + t];
-        }
-    }
+    // Unconditional loads at clamped addresses (threads, rows and chunks
+    // past the ranges read an in-range element and ignore it; a layer
+    // without an engram site reads the projection row instead, which
+    // nothing else here reads).
+    InRegs q;
+    const int td = min(t, d - 1);
+    q.norm = N.norm_in[td];
+    const bool site = N.site >= 0;
+    const float* kp = site ? S.ekv + (size_t)N.site * FWD_ROWS * 2 * d : S.proj;
+    const float* ep = site ? S.evals + (size_t)N.site * FWD_ROWS * d : S.proj + d;
+    q.kr = kp[td];
+    q.ev = ep[td];
     const int per = nc / 16;  // uint4 per row
-    if (wave < MHC_COLS) {
-        const uint4* row = reinterpret_cast<const uint4*>(N.phi_q + (size_t)wave * nc);
+    const int w0 = min(wave, MHC_COLS - 1), w1 = min(wave + LT / 64, MHC_COLS - 1);
+    const uint4* row0 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)w0 * nc);
+    const uint4* row1 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)w1 * nc);
 #pragma unroll
-        for (int j = 0; j < PHI_CHUNKS; ++j)
-            if (lane + 64 * j < per) q.r0[j] = row[lane + 64 * j];
-        q.ps0 = N.phi_s[wave];
+    for (int j = 0; j < PHI_CHUNKS; ++j) {
+        const int c = min(lane + 64 * j, per - 1);
+        q.r0[j] = row0[c];
+        q.r1[j] = row1[c];
     }
-    if (wave + LT / 64 < MHC_COLS) {
-        const uint4* row = reinterpret_cast<const uint4*>(N.phi_q + (size_t)(wave + LT / 64) * nc);
-#pragma unroll
-        for (int j = 0; j < PHI_CHUNKS; ++j)
-            if (lane + 64 * j < per) q.r1[j] = row[lane + 64 * j];
-        q.ps1 = N.phi_s[wave + LT / 64];
-    }
+    q.ps0 = N.phi_s[w0];
+    q.ps1 = N.phi_s[w1];
     return q;
 }
 
@@ -613,7 +685,7 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, con
     // maxima of |xs| (rounding is monotonic, so max_i |xs_i r| =
     // max_i |xs_i| r for r > 0), then the int8 lanes
     {
-        const float r = block_rinv(sh.xs, sh.xs, nc, &sh.r_a);
+        const float r = block_rinv_t(sh.tX, TP_X, nc, &sh.r_a);
         float m = sh.red[0];
 #pragma unroll
         for (int i = 1; i < LT / 64; ++i) m = fmaxf(m, sh.red[i]);
@@ -656,41 +728,41 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, con
 #pragma unroll
         for (int b = 1; b < MHC_LANES; ++b) u = __builtin_fmaf(sh.xs[b * d + t], hp[b], u);
         x1 = u;
-        sh.x1[t] = x1;
-        if (N.site >= 0) sh.o[t] = q.kr;
+        put_t(sh.tA, TP_D, t, x1);
+        if (N.site >= 0) put_t(sh.tB, TP_D, t, q.kr);
     }
     __syncthreads();
     if (N.site >= 0) {
         // alpha = sigmoid(dot16(x1 / |x1|, k / |k|) / sqrt(d)); x1 += alpha * conv
         if (wave == 1) {
-            const float rk = rinv(dot16_wave(sh.o, sh.o, d, lane), d);
+            const float rk = rinv(dot16_t<true>(sh.tB, sh.tB, TP_D, d, lane), d);
             if (lane == 0) sh.r_b = rk;
         }
-        const float rx = block_rinv(sh.x1, sh.x1, d, &sh.r_a);
+        const float rx = block_rinv_t(sh.tA, TP_D, d, &sh.r_a);
         const float rk = sh.r_b;
         if (t < d) {
-            sh.x2[t] = x1 * rx;
-            sh.h[t] = q.kr * rk;
+            put_t(sh.tA, TP_D, t, x1 * rx);
+            put_t(sh.tB, TP_D, t, q.kr * rk);
         }
         __syncthreads();
         if (wave == 0) {
-            const float dd = dot16_wave(sh.x2, sh.h, d, lane);
+            const float dd = dot16_t<false>(sh.tA, sh.tB, TP_D, d, lane);
             if (lane == 0) sh.r_c = 1.0f / (lexpf((-dd) / __builtin_sqrtf((float)d)) + 1.0f);
         }
         __syncthreads();
         const float alpha = sh.r_c;
         if (t < d) {
             x1 = __builtin_fmaf(q.ev, alpha, x1);
-            sh.x1[t] = x1;
+            put_t(sh.tA, TP_D, t, x1);
         }
         __syncthreads();
     }
     // hloc = norm_apply16(x1, rinv(dot16(x1)), norm_in), then A8.
     {
-        const float r = block_rinv(sh.x1, sh.x1, d, &sh.r_b);
+        const float r = block_rinv_t(sh.tA, TP_D, d, &sh.r_b);
         if (t < d) {
             const float tt = x1 * r;
-            sh.h[t] = __builtin_fmaf(tt, q.norm, tt);
+            sh.h[t] = __builtin_fmaf(tt, h2f_late(q.norm), tt);
             S.u[t] = u;
             S.x1[t] = x1;
         }
@@ -712,11 +784,11 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
     float mean = 0.0f;
     if (t < d) {
         mean = (((sh.xs[t] + sh.xs[d + t]) + sh.xs[2 * d + t]) + sh.xs[3 * d + t]) * 0.25f;
-        sh.h[t] = mean;
+        put_t(sh.tA, TP_D, t, mean);
     }
     __syncthreads();
     {
-        const float r = block_rinv(sh.h, sh.h, d, &sh.r_a);
+        const float r = block_rinv_t(sh.tA, TP_D, d, &sh.r_a);
         if (t < d) {
             const float tt = mean * r;
             sh.x2[t] = __builtin_fmaf(tt, fnorm, tt);
@@ -733,8 +805,10 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
 
 }  // namespace
 
-__global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int has_prev,
-                                              int has_next, int row0, int in_bits, int head_bits) {
+template <bool PREV, bool NEXT>
+__global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int row0,
+                                              int in_bits, int head_bits) {
+    constexpr bool has_prev = PREV, has_next = NEXT;
     __shared__ LayerShared sh;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, d = D.d, nc = MHC_LANES * d;
     const int Gd = (d + GROUP - 1) / GROUP;
@@ -753,32 +827,33 @@ __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, Laye
     // every global read first, then the LDS stores
     float xv[MHC_LANES];
 #pragma unroll
-    for (int k = 0; k < MHC_LANES; ++k) xv[k] = t + k * LT < nc ? R.xs[t + k * LT] : 0.0f;
-    OutRegs qo{};
-    if (has_prev) qo = load_out(D, G, R, P, sh);
-    InRegs qi{};
+    for (int k = 0; k < MHC_LANES; ++k) xv[k] = R.xs[min(t + k * LT, nc - 1)];
+    OutRegs qo;
+    if constexpr (has_prev) qo = load_out(D, G, R, P, sh);
+    InRegs qi;
     float fnorm = 0.0f;
-    if (has_next)
+    if constexpr (has_next)
         qi = load_in(D, R, N);
-    else if (t < d)
-        fnorm = G.final_norm[t];
+    else
+        fnorm = G.final_norm[min(t, d - 1)];
     float m = 0.0f;
 #pragma unroll
     for (int k = 0; k < MHC_LANES; ++k)
         if (t + k * LT < nc) {
             sh.xs[t + k * LT] = xv[k];
+            put_t(sh.tX, TP_X, t + k * LT, xv[k]);
             m = fmaxf(m, fabsf(xv[k]));
         }
-    if (has_prev) store_out(D, qo, sh);
+    if constexpr (has_prev) store_out(D, qo, sh);
     __syncthreads();
-    if (has_prev) m = layer_out(D, P, qo, sh);
+    if constexpr (has_prev) m = layer_out(D, P, qo, sh);
     // the wavefronts' maxima of |xs| for the mHC read
     m = wave_max(m);
     if (lane == 0) sh.red[wave] = m;
     __syncthreads();
-    if (has_prev)
+    if constexpr (has_prev)
         for (int i = t; i < nc; i += LT) R.xs[i] = sh.xs[i];
-    if (has_next)
+    if constexpr (has_next)
         layer_in(D, R, N, qi, in_bits, sh);
     else
         head_in(D, S, fnorm, head_bits, sh);  // A8 into activation row 0
@@ -787,8 +862,18 @@ __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, Laye
 hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
                      int row0, int rows, int in_bits, int head_bits, hipStream_t s) {
     const LayerDev none{};
-    hipLaunchKernelGGL(k_layer, dim3(rows), dim3(LT), 0, s, D, G, S, prev ? *prev : none, next ? *next : none,
-                       prev ? 1 : 0, next ? 1 : 0, row0, in_bits, head_bits);
+    if (prev && next)
+        hipLaunchKernelGGL((k_layer<true, true>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, *next, row0, in_bits,
+                           head_bits);
+    else if (next)
+        hipLaunchKernelGGL((k_layer<false, true>), dim3(rows), dim3(LT), 0, s, D, G, S, none, *next, row0, in_bits,
+                           head_bits);
+    else if (prev)
+        hipLaunchKernelGGL((k_layer<true, false>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, none, row0, in_bits,
+                           head_bits);
+    else
+        hipLaunchKernelGGL((k_layer<false, false>), dim3(rows), dim3(LT), 0, s, D, G, S, none, none, row0, in_bits,
+                           head_bits);
     return hipGetLastError();
 }
 
@@ -904,7 +989,7 @@ __global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, Lay
             if (i == 0) S.ks[(lc + pos) * nkv + kh] = s;
         } else {
             const int vh = unit - nh - nkv;
-            if (i < vd) S.v8t[(((size_t)layer * nkv + vh) * vd + i) * D.cap + pos] = q;
+            if (i < vd) S.v8t[(((size_t)layer * nkv + vh) * vd + i) * D.vcap + pos] = q;
             if (i == 0) S.vs[(lc + pos) * nkv + vh] = s;
         }
     }
@@ -1011,7 +1096,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     const int dm = t >> 2, part = t & 3;
     int a = 0, b = 0, c = 0;
     if (dm < vd) {
-        const int8_t* row = S.v8t + (((size_t)layer * nkv + kvh) * vd + dm) * D.cap + slot0;
+        const int8_t* row = S.v8t + (((size_t)layer * nkv + kvh) * vd + dm) * D.vcap + slot0;
         for (int i = part; i < len; i += 4) {
             const int v = row[i];
             a += dig[0][i] * v;
@@ -1097,37 +1182,74 @@ hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int 
 // the block.  One more block computes the row's post gates.
 constexpr int DG_HEAD_T = 256;
 
-// A unit's post-tap value for lane i (zcn16 and RoPE when `norm` is set):
-// the causal conv over the row and the kept history rows of the ring.
-__device__ __forceinline__ float unit_value(const Dims& D, const SessDev& S, int layer, int p0, int start, int cw,
-                                            int cc, int len, const uint16_t* w, const uint16_t* norm, int i,
-                                            bool write_hist) {
-    float* hist = S.hist + (size_t)layer * D.hist_slots * D.W;
+constexpr int DG_MAX_TAPS = 8;                   // conv taps the decode-attention launch takes
+constexpr int DG_PITCH = ATT_CHUNK_MAX + 8;      // value / digit row: 3 alignment bytes + 256 slots + dword tail
+constexpr int DG_KPITCH = MAX_HEAD_DIM + 16;     // key row (80 bytes: 8 rows cover the 32 banks)
+constexpr int DG_VDW = (ATT_CHUNK_MAX + 3 + 3) / 4;  // value dwords per column (alignment offset + slots)
+
+// A unit's inputs for lane i: the pre-tap row value, the taps, the kept
+// history rows of the ring, and (normed units) the norm scale and RoPE row.
+// Loaded before the key / value stream, so waiting for them does not wait
+// for it.
+struct UnitIn {
+    float cur, rc, rs;
+    uint16_t nrm;
+    uint16_t w[DG_MAX_TAPS];
+    float h[DG_MAX_TAPS];
+};
+
+// Every load is unconditional (lanes, taps and history rows past the
+// ranges read a clamped in-range address; `norm` is read for every unit,
+// used by the normed ones) and raw, so all of them issue before the first
+// wait.
+__device__ __forceinline__ UnitIn unit_load(const Dims& D, const SessDev& S, int layer, int p0, int start, int cw,
+                                            int cc, int len, const uint16_t* w, const uint16_t* norm, int i) {
+    const float* hist = S.hist + (size_t)layer * D.hist_slots * D.W;
+    const int ii = i < len ? i : 0;
+    UnitIn u{};
+    u.cur = S.proj[start + ii];
+#pragma unroll
+    for (int j = 0; j < DG_MAX_TAPS; ++j) {
+        const int jj = j < D.taps ? j : D.taps - 1;
+        u.w[j] = w[(size_t)jj * cw + cc + ii];
+        if (j > 0) {
+            const int pj = p0 >= jj ? p0 - jj : 0;
+            u.h[j] = hist[(size_t)(pj % D.hist_slots) * D.W + start + ii];
+        }
+    }
+    {
+        const int qi = i < D.qk ? i : 0, half = D.qk / 2, f = qi < half ? qi : qi - half;
+        u.nrm = norm[qi];
+        u.rc = S.rope_c[f];
+        u.rs = S.rope_s[f];
+    }
+    return u;
+}
+
+// The unit's post-tap value (zcn16 and RoPE when `normed`): the causal conv
+// over the row and the kept history rows, v = w0 cur, then
+// fma(w_j, row_{p0 - j}, v) (a row before position 0 is zero).
+__device__ __forceinline__ float unit_finish(const Dims& D, const SessDev& S, int layer, int p0, int start, int len,
+                                             const UnitIn& u, bool normed, int i, bool write_hist) {
     float v = 0.0f;
     if (i < len) {
-        const float cur = S.proj[start + i];
-        v = h2f(w[cc + i]) * cur;
-        for (int j = 1; j < D.taps; ++j) {
-            const float wj = h2f(w[(size_t)j * cw + cc + i]);
-            const float rr = p0 >= j ? hist[(size_t)((p0 - j) % D.hist_slots) * D.W + start + i] : 0.0f;
-            v = __builtin_fmaf(wj, rr, v);
-        }
-        if (write_hist) hist[(size_t)(p0 % D.hist_slots) * D.W + start + i] = cur;
+        v = h2f(u.w[0]) * u.cur;
+#pragma unroll
+        for (int j = 1; j < DG_MAX_TAPS; ++j)
+            if (j < D.taps) v = __builtin_fmaf(h2f(u.w[j]), p0 >= j ? u.h[j] : 0.0f, v);
+        if (write_hist) S.hist[((size_t)layer * D.hist_slots + p0 % D.hist_slots) * D.W + start + i] = u.cur;
     }
-    if (norm) {
+    if (normed) {
         const int qk = D.qk;
         const float ss = dot16_lanes(v, qk, i);
         const float r = rinv(ss, qk);
         if (i < qk) {
             const float tt = v * r;
-            v = __builtin_fmaf(tt, h2f(norm[i]), tt);
+            v = __builtin_fmaf(tt, h2f(u.nrm), tt);
         }
         const int half = qk / 2, f = i < half ? i : i - half;
         const float a = __shfl(v, f, 64), b = __shfl(v, f + half, 64);
-        if (i < qk) {
-            const float cs = S.rope_c[f], sn = S.rope_s[f];
-            v = i < half ? __builtin_fmaf(-sn, b, cs * a) : __builtin_fmaf(sn, a, cs * b);
-        }
+        if (i < qk) v = i < half ? __builtin_fmaf(-u.rs, b, u.rc * a) : __builtin_fmaf(u.rs, a, u.rc * b);
     }
     return v;
 }
@@ -1146,50 +1268,69 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
     const int hh0 = blockIdx.x * HP, kvh = hh0 / group;
     const bool owner = hh0 % group == 0;
     const int lo = window_lo(L.window, p0), n = p0 + 1 - lo, blocked = n / 4 * 4;
+    // value columns and digits are kept from slot lo - sh (a dword
+    // boundary of the cache row): column index j = i + sh for key i
+    const int sh = lo & 3, base = lo - sh;
     const int h = t / DG_HEAD_T, u = t % DG_HEAD_T, hw = u >> 6;  // head, thread and wavefront in it
-    __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][MAX_HEAD_DIM];  // key rows by slot - lo
-    __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][ATT_CHUNK_MAX + 4];  // value columns by slot - lo
+    __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][DG_KPITCH];  // key rows by slot - lo
+    __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][DG_PITCH];    // value columns by slot - base
     __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
     __shared__ alignas(16) int8_t q8[HP][MAX_HEAD_DIM];
     __shared__ float sc[HP][ATT_CHUNK_MAX];
-    __shared__ alignas(16) int8_t dig[HP][3][ATT_CHUNK_MAX];
+    __shared__ alignas(16) int8_t dig[HP][3][DG_PITCH];
     __shared__ float red[HP][DG_HEAD_T / 64];
     __shared__ float s_qs[HP], s_sum[HP];
     __shared__ float att[HP * MAX_HEAD_DIM];
     const size_t lc = (size_t)layer * D.cap;
-    // The keys before the position: int8 rows, scales and value columns,
-    // loaded into registers first (every load in flight at once) and
-    // stored to LDS after the units.  Indices run over the padded
-    // [256][4] row chunks and [64][256] value bytes.
-    constexpr int KR = ATT_CHUNK_MAX * 4 / NT, VB = MAX_HEAD_DIM * ATT_CHUNK_MAX / NT;
-    const int nold = n - 1, rq = qk / 16;
+    // The unit inputs first: queries on waves 0 .. HP-1, the new key and
+    // value on the next two.
+    // (The role is made wave-uniform for the compiler, so the loads sit
+    // under a scalar branch and nothing waits for them before the stream.)
+    // Waves past the units load the value unit's inputs too and ignore
+    // them.  The role is wave-uniform (scalar branches, each with constant
+    // argument fields: selecting the fields by role would copy the
+    // argument struct to scratch).
+    const int role = __builtin_amdgcn_readfirstlane(wave < HP ? 0 : wave - HP + 1);  // 0 q, 1 k, 2 v, 3+ none
+    UnitIn ui;
+    if (role == 0)
+        ui = unit_load(D, S, layer, p0, (hh0 + wave) * qk, qd, (hh0 + wave) * qk, qk, L.q_taps, L.q_norm, lane);
+    else if (role == 1)
+        ui = unit_load(D, S, layer, p0, qd + kvh * qk, kd, kvh * qk, qk, L.k_taps, L.k_norm, lane);
+    else
+        ui = unit_load(D, S, layer, p0, qd + kd + kvh * vd, vdim, kvh * vd, vd, L.v_taps, L.k_norm, lane);
+    // The keys before the position: int8 rows (16-byte chunks), scales and
+    // value dwords, all in flight at once, stored to LDS after the units.
+    constexpr int KR = ATT_CHUNK_MAX * 4 / NT, VR = (MAX_HEAD_DIM * DG_VDW + NT - 1) / NT;
+    const int nold = n - 1, rq = qk / 16, vdw = (sh + nold + 3) / 4;
     uint4 kr[KR];
-    int vb[VB];
+    uint32_t vw[VR];
     float ksr = 0.0f, vsr = 0.0f;
+    // (unconditional loads at clamped in-range addresses; what lies past
+    // the keys is never stored)
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
-        const int e = t + r * NT, i = e >> 2, c = e & 3;
-        if (i < nold && c < rq) kr[r] = reinterpret_cast<const uint4*>(S.k8 + ((lc + lo + i) * nkv + kvh) * qk)[c];
+        const int e = t + r * NT, i = min(e >> 2, n - 1), c = min(e & 3, rq - 1);
+        kr[r] = reinterpret_cast<const uint4*>(S.k8 + ((lc + lo + i) * nkv + kvh) * qk)[c];
     }
-    if (t < nold) {
-        ksr = S.ks[(lc + lo + t) * nkv + kvh];
-        vsr = S.vs[(lc + lo + t) * nkv + kvh];
+    {
+        const int i = min(t, n - 1);
+        ksr = S.ks[(lc + lo + i) * nkv + kvh];
+        vsr = S.vs[(lc + lo + i) * nkv + kvh];
     }
-    const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.cap + lo;
+    const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
 #pragma unroll
-    for (int r = 0; r < VB; ++r) {
-        const int e = t + r * NT, dm = e >> 8, i = e & (ATT_CHUNK_MAX - 1);
-        if (dm < vd && i < nold) vb[r] = vcol[(size_t)dm * D.cap + i];
+    for (int r = 0; r < VR; ++r) {
+        const int e = t + r * NT, dm = min(e / DG_VDW, vd - 1), k = min(e % DG_VDW, vdw - 1);
+        vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
     }
-    // The units: queries on waves 0 .. HP-1, the new key and value on the next two.
+    // the units
     if (wave < HP) {
-        const int hq = hh0 + wave;
-        const float v = unit_value(D, S, layer, p0, hq * qk, qd, hq * qk, qk, L.q_taps, L.q_norm, lane, true);
+        const float v = unit_finish(D, S, layer, p0, (hh0 + wave) * qk, qk, ui, true, lane, true);
         const float s = wave_quant_scale(lane < qk ? v : 0.0f);
         if (lane < qk) q8[wave][lane] = quant_one(v, 1.0f / s);
         if (lane == 0) s_qs[wave] = s * bits_f32(0x3e13cd3au);
     } else if (wave == HP) {
-        const float v = unit_value(D, S, layer, p0, qd + kvh * qk, kd, kvh * qk, qk, L.k_taps, L.k_norm, lane, owner);
+        const float v = unit_finish(D, S, layer, p0, qd + kvh * qk, qk, ui, true, lane, owner);
         const float s = wave_quant_scale(lane < qk ? v : 0.0f);
         const int8_t q = quant_one(v, 1.0f / s);
         if (lane < qk) {
@@ -1201,13 +1342,12 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
             if (owner) S.ks[(lc + p0) * nkv + kvh] = s;
         }
     } else if (wave == HP + 1) {
-        const float v = unit_value(D, S, layer, p0, qd + kd + kvh * vd, vdim, kvh * vd, vd, L.v_taps, nullptr, lane,
-                                   owner);
+        const float v = unit_finish(D, S, layer, p0, qd + kd + kvh * vd, vd, ui, false, lane, owner);
         const float s = wave_quant_scale(lane < vd ? v : 0.0f);
         const int8_t q = quant_one(v, 1.0f / s);
         if (lane < vd) {
-            vs8[lane][n - 1] = q;
-            if (owner) S.v8t[(((size_t)layer * nkv + kvh) * vd + lane) * D.cap + p0] = q;
+            vs8[lane][sh + n - 1] = q;
+            if (owner) S.v8t[(((size_t)layer * nkv + kvh) * vd + lane) * D.vcap + p0] = q;
         }
         if (lane == 0) {
             vss[n - 1] = s;
@@ -1223,23 +1363,45 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
         kss[t] = ksr;
         vss[t] = vsr;
     }
+    // value bytes of keys 0 .. nold - 1 (columns sh .. sh + nold - 1); the
+    // bytes before sh and past the keys meet zero digits
 #pragma unroll
-    for (int r = 0; r < VB; ++r) {
-        const int e = t + r * NT, dm = e >> 8, i = e & (ATT_CHUNK_MAX - 1);
-        if (dm < vd && i < nold) vs8[dm][i] = (int8_t)vb[r];
+    for (int r = 0; r < VR; ++r) {
+        const int e = t + r * NT, dm = e / DG_VDW, k = e % DG_VDW;
+        if (dm < vd && k < vdw) {
+            if (4 * k + 3 < sh + nold) {
+                reinterpret_cast<uint32_t*>(vs8[dm])[k] = vw[r];
+            } else {
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    if (4 * k + b < sh + nold) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
+            }
+        }
     }
     __syncthreads();
     // attend_head_ref over the one chunk, one head per 256 threads
     const float qs = s_qs[h];
     float mx = -__builtin_inff();
-    for (int i = u; i < n; i += DG_HEAD_T) {
-        int dot = 0;
-        for (int j = 0; j < qk; j += 4)
-            dot = __builtin_amdgcn_sdot4(*(const int*)(&ks8[i][j]), *(const int*)(&q8[h][j]), dot, false);
-        const float ksc = kss[i];
-        const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
-        sc[h][i] = sv;
-        mx = fmaxf(mx, sv);
+    {
+        uint4 qv[MAX_HEAD_DIM / 16];
+#pragma unroll
+        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) qv[c] = reinterpret_cast<const uint4*>(q8[h])[c];
+        for (int i = u; i < n; i += DG_HEAD_T) {
+            int dot = 0;
+#pragma unroll
+            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
+                if (c < rq) {
+                    const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
+                    dot = __builtin_amdgcn_sdot4((int)kv.x, (int)qv[c].x, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)kv.y, (int)qv[c].y, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)kv.z, (int)qv[c].z, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)kv.w, (int)qv[c].w, dot, false);
+                }
+            const float ksc = kss[i];
+            const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
+            sc[h][i] = sv;
+            mx = fmaxf(mx, sv);
+        }
     }
     mx = wave_max(mx);
     if (lane == 0) red[h][hw] = mx;
@@ -1248,11 +1410,22 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
     for (int i = u; i < n; i += DG_HEAD_T) sc[h][i] = i < blocked ? nexp(sc[h][i] - mx) : lexpf(sc[h][i] - mx);
     __syncthreads();
     if (hw == 0) {
+        // lane 4 hi + k sums sc[8 b + 4 hi + k] over b in order, the loads
+        // of a batch of 8 issued ahead of its adds
         float acc = 0.0f;
         const int nb8 = n / 8;
         if (lane < 8) {
             const int k = lane & 3, hi = lane >> 2;
-            for (int b = 0; b < nb8; ++b) acc += sc[h][b * 8 + hi * 4 + k];
+            const float* col = &sc[h][hi * 4 + k];
+            int b = 0;
+            for (; b + 8 <= nb8; b += 8) {
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = col[(b + j) * 8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc += v[j];
+            }
+            for (; b < nb8; ++b) acc += col[b * 8];
             if (hi == 0 && n - nb8 * 8 >= 4) acc += sc[h][nb8 * 8 + k];
         }
         const int k = lane & 3;
@@ -1280,24 +1453,51 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
     const float qw = bits_f32(0x49fffff8u) / wmax;
     for (int i = u; i < n; i += DG_HEAD_T) {
         const int32_t wq = (int32_t)roundf(sc[h][i] * qw);
-        dig[h][0][i] = (int8_t)(wq >> 14);
-        dig[h][1][i] = (int8_t)((wq >> 7) & 127);
-        dig[h][2][i] = (int8_t)(wq & 127);
+        dig[h][0][sh + i] = (int8_t)(wq >> 14);
+        dig[h][1][sh + i] = (int8_t)((wq >> 7) & 127);
+        dig[h][2][sh + i] = (int8_t)(wq & 127);
     }
-    if (u >= n && u < (n + 3) / 4 * 4) dig[h][0][u] = dig[h][1][u] = dig[h][2][u] = 0;  // the last dword's tail
+    // zero digits in the first dword before the keys and the last one past them
+    if (u < 4) {
+        const int j0 = u, j1 = sh + n + u;
+        if (j0 < sh) dig[h][0][j0] = dig[h][1][j0] = dig[h][2][j0] = 0;
+        if (j1 < (sh + n + 3) / 4 * 4) dig[h][0][j1] = dig[h][1][j1] = dig[h][2][j1] = 0;
+    }
     __syncthreads();
     {
-        // exact integer P.V: four slots per sdot4 (tail digits are zero)
+        // exact integer P.V: four columns per sdot4, 16 per thread step
         const float cw = wmax * bits_f32(0x35000004u);
-        const int dm = u >> 2, part = u & 3;
+        const int dm = u >> 2, part = u & 3, cols = sh + n;
         int a = 0, b = 0, c = 0;
-        if (dm < vd)
-            for (int i = part * 4; i < n; i += 16) {
-                const int v = *reinterpret_cast<const int*>(&vs8[dm][i]);
-                a = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(&dig[h][0][i]), v, a, false);
-                b = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(&dig[h][1][i]), v, b, false);
-                c = __builtin_amdgcn_sdot4(*reinterpret_cast<const int*>(&dig[h][2][i]), v, c, false);
+        if (dm < vd) {
+            const int* vrow = reinterpret_cast<const int*>(vs8[dm]);
+            const int* d0 = reinterpret_cast<const int*>(dig[h][0]);
+            const int* d1 = reinterpret_cast<const int*>(dig[h][1]);
+            const int* d2 = reinterpret_cast<const int*>(dig[h][2]);
+            int i = part;
+            for (; 4 * (i + 12) < cols; i += 16) {
+                int v[4], x0[4], x1[4], x2[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    v[q] = vrow[i + 4 * q];
+                    x0[q] = d0[i + 4 * q];
+                    x1[q] = d1[i + 4 * q];
+                    x2[q] = d2[i + 4 * q];
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    a = __builtin_amdgcn_sdot4(x0[q], v[q], a, false);
+                    b = __builtin_amdgcn_sdot4(x1[q], v[q], b, false);
+                    c = __builtin_amdgcn_sdot4(x2[q], v[q], c, false);
+                }
             }
+            for (; 4 * i < cols; i += 4) {
+                const int v = vrow[i];
+                a = __builtin_amdgcn_sdot4(d0[i], v, a, false);
+                b = __builtin_amdgcn_sdot4(d1[i], v, b, false);
+                c = __builtin_amdgcn_sdot4(d2[i], v, c, false);
+            }
+        }
         a += __shfl_xor(a, 1, 64);
         a += __shfl_xor(a, 2, 64);
         b += __shfl_xor(b, 1, 64);
@@ -1326,7 +1526,7 @@ bool dec_group_fits(const Dims& D, int p0, int window) {
     int c = (n + 255) / 256;
     if (k * 64 <= n && c < k) c = k;
     if (c > 1 || n > ATT_CHUNK_MAX) return false;
-    if (GROUP % D.vd != 0) return false;
+    if (GROUP % D.vd != 0 || D.taps > DG_MAX_TAPS) return false;
     const int hp = GROUP / D.vd;
     return (hp == 2 || hp == 4) && D.nh % hp == 0 && (D.nh / D.nkv) % hp == 0 && D.qk % 16 == 0;
 }

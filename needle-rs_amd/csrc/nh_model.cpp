@@ -247,6 +247,8 @@ int check_geometry(nh_model* m, const nh::ArchiveSmall& sm) {
         if (!rc) rc = need(L[nh::S_D3], nh::HADA_N, "d3");
         if (!rc) rc = need(L[nh::S_D4], d, "d4");
         if (!rc) rc = need(L[nh::S_COND_V], d * nh::COND_RANK, "cond_v");
+        if (!rc) rc = need(L[nh::S_COND_U], (size_t)nh::COND_RANK * nh::HADA_N, "cond_u");
+        for (int k = 0; k < 6 && !rc; ++k) rc = need(L[nh::S_KRON0 + k], nh::HADA_N, "Kronecker factor");
         if (rc) return rc;
     }
     const size_t L = D.layers;
@@ -282,8 +284,21 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
         for (size_t i = 0; i < v.size(); ++i) b[i] = f32_to_f16(v[i]);
         return A.put(b.data(), b.size() * 2);
     };
+    // The tables the layer kernel stages into LDS, as one block per layer:
+    // the six Kronecker factors, cond_v [d][8], cond_u [8][hada_n] (f16).
+    std::vector<size_t> stage(D.layers);
     for (int l = 0; l < D.layers; ++l) {
         for (int k = 0; k < nh::SMALL_KINDS; ++k) off[l].t[k] = put16(sm.layer[l][k]);
+        std::vector<float> blk;
+        for (int k = 0; k < 6; ++k) {
+            const auto& f = sm.layer[l][nh::S_KRON0 + k];
+            blk.insert(blk.end(), f.begin(), f.begin() + nh::HADA_N);
+        }
+        const auto& cv = sm.layer[l][nh::S_COND_V];
+        blk.insert(blk.end(), cv.begin(), cv.begin() + (size_t)D.d * nh::COND_RANK);
+        const auto& cu = sm.layer[l][nh::S_COND_U];
+        blk.insert(blk.end(), cu.begin(), cu.begin() + (size_t)nh::COND_RANK * nh::HADA_N);
+        stage[l] = put16(blk);
         off[l].phi_q = A.reserve((size_t)nh::MHC_COLS * nc);
         off[l].phi_s = A.reserve(nh::MHC_COLS * 4);
     }
@@ -353,8 +368,7 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
     for (int l = 0; l < D.layers; ++l) {
         nh::LayerDev L{};
         auto p16 = [&](int k) { return (const uint16_t*)(base + off[l].t[k]); };
-        for (int k = 0; k < 6; ++k) L.kron[k] = p16(nh::S_KRON0 + k);
-        L.cond_v = p16(nh::S_COND_V), L.cond_u = p16(nh::S_COND_U);
+        L.stage = (const uint16_t*)(base + stage[l]);
         L.d1 = p16(nh::S_D1), L.d2 = p16(nh::S_D2), L.b2 = p16(nh::S_B2), L.d3 = p16(nh::S_D3), L.d4 = p16(nh::S_D4);
         L.norm_in = p16(nh::S_NORM_IN), L.post_norm = p16(nh::S_POST_NORM), L.pre_hada = p16(nh::S_PRE_HADA);
         L.q_taps = p16(nh::S_Q_TAPS), L.k_taps = p16(nh::S_K_TAPS), L.v_taps = p16(nh::S_V_TAPS);
@@ -501,6 +515,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     nh::Dims& D = s->dims;
     D = m->dims;
     D.cap = cap;
+    D.vcap = (int)round_up((size_t)cap + 4, 16);
     int mc = 1;
     for (int n = 1; n <= cap; ++n) mc = std::max(mc, key_chunk_count(n, D.nkv));
     D.max_chunks = mc;
@@ -517,7 +532,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
                  o_ps = Y.take(R * D.nh * mc * 4);
     const size_t o_hist = Y.take(L * D.hist_slots * D.W * 4);
     const size_t o_k8 = Y.take(L * c * D.nkv * D.qk), o_ks = Y.take(L * c * D.nkv * 4);
-    const size_t o_v8 = Y.take(L * D.nkv * D.vd * c), o_vs = Y.take(L * c * D.nkv * 4);
+    const size_t o_v8 = Y.take(L * D.nkv * D.vd * D.vcap), o_vs = Y.take(L * c * D.nkv * 4);
     const size_t o_e8 = Y.take(E * c * d), o_es = Y.take(E * c * (d / 32) * 4);
     const size_t o_xi = Y.take(AR * Gd * nh::GROUP), o_si = Y.take(AR * Gd * 4);
     const size_t o_xa = Y.take(AR * Ga * nh::GROUP), o_sa = Y.take(AR * Ga * 4);
