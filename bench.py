@@ -290,14 +290,17 @@ def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
             runs.append((ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])))
     prompt_ms = min(a for a, _ in runs)
     decode_ms = min(b for _, b in runs)
-    sites, layers = 5, 20
+    layers = 20
     out = {"workload": "Needle-3 random-init decode: 118 random prompt tokens (32-token chunks), then 64 greedy "
                        "steps on the device",
            "prompt_tokens": DECODE_PROMPT, "decode_steps": DECODE_STEPS,
            "decode_tok_s": round(DECODE_STEPS * 1e3 / decode_ms, 1),
            "decode_ms_per_token": round(decode_ms / DECODE_STEPS, 4),
            "prompt_tok_s": round(DECODE_PROMPT * 1e3 / prompt_ms, 1),
-           "runs": len(runs), "launches_per_token": 2 + sites + 6 * layers + 3,
+           # begin, batched engram key | value, engram history; per layer
+           # the layer boundary, q|k|v|gate, decode attention, out; head
+           # input, head, argmax (positions below 256 keys)
+           "runs": len(runs), "launches_per_token": 3 + 4 * layers + 3,
            "first_picks": [int(t) for t in picks[:8]]}
     progress(f"Needle-3 decode: {out['decode_ms_per_token'] * 1e3:.1f} us per token")
     if with_cpu:
