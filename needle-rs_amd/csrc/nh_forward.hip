@@ -292,6 +292,7 @@ struct LayerShared {
     float p[64];
     float wk[COND_RANK];
     float r_sx, r_a, r_b, r_c;
+    int mix_count;  // the mixer wavefronts' arrivals (mixer_sync)
 };
 
 // mix8 (infer.rs:2343-2380), portable branch: out[r][c] =
@@ -339,48 +340,67 @@ __device__ __forceinline__ void mix8_n(int u, const float* ct, const float* rows
 __device__ __forceinline__ void put_t(float* T, int pitch, int i, float v) { T[(i & 15) * pitch + (i >> 4)] = v; }
 
 // dot16 over operands held transposed (x[16 c + l] at xT[l * pitch + c]),
-// the same chains and combine as dot16_wave: lane l < 16 carries
-// accumulator l over c in order.  Batches of 16 chunks, the next batch's
-// loads issued before this batch's fmas.
+// the same chains and combine as the reference's dot16: lane l < 16
+// carries accumulator l over c in order.  The chain is a 3-stage pipeline of
+// 8-step batches (two 16-byte reads per operand): batch b + 2's reads issue
+// before batch b's fmas, and scheduling barriers keep the compiler from
+// sinking them back to their use (which would leave every batch waiting a
+// full LDS round trip).
 template <bool SELF>
 __device__ __forceinline__ float dot16_t(const float* xT, const float* yT, int pitch, int n, int lane) {
     float a = 0.0f;
     if (lane < 16) {
-        const int chunks = n / 16, nb = chunks / 16;
+        const int chunks = n / 16, nb = chunks / 8;
         const float4* xr = reinterpret_cast<const float4*>(xT + lane * pitch);
         const float4* yr = reinterpret_cast<const float4*>(yT + lane * pitch);
-        float4 xc[4], yc[4];
+        float4 x0[2], x1[2], x2[2], y0[2], y1[2], y2[2];
+        auto load = [&](float4* xd, float4* yd, int b) {
+            const int c = min(b, nb - 1) * 2;
+            xd[0] = xr[c];
+            xd[1] = xr[c + 1];
+            if (!SELF) {
+                yd[0] = yr[c];
+                yd[1] = yr[c + 1];
+            }
+        };
+        auto chain = [&](const float4* xd, const float4* yd) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const float4 x = xd[u], y = SELF ? xd[u] : yd[u];
+                a = __builtin_fmaf(x.x, y.x, a);
+                a = __builtin_fmaf(x.y, y.y, a);
+                a = __builtin_fmaf(x.z, y.z, a);
+                a = __builtin_fmaf(x.w, y.w, a);
+            }
+        };
         if (nb > 0) {
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                xc[u] = xr[u];
-                yc[u] = SELF ? xc[u] : yr[u];
-            }
+            load(x0, y0, 0);
+            load(x1, y1, 1);
         }
-        for (int b = 0; b < nb; ++b) {
-            float4 xn[4], yn[4];
-            const int nx = b + 1 < nb ? (b + 1) * 4 : b * 4;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                xn[u] = xr[nx + u];
-                yn[u] = SELF ? xn[u] : yr[nx + u];
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                a = __builtin_fmaf(xc[u].x, yc[u].x, a);
-                a = __builtin_fmaf(xc[u].y, yc[u].y, a);
-                a = __builtin_fmaf(xc[u].z, yc[u].z, a);
-                a = __builtin_fmaf(xc[u].w, yc[u].w, a);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                xc[u] = xn[u];
-                yc[u] = yn[u];
-            }
+        int b = 0;
+        for (; b + 3 <= nb; b += 3) {
+            load(x2, y2, b + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(x0, y0);
+            __builtin_amdgcn_sched_barrier(0);
+            load(x0, y0, b + 3);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(x1, y1);
+            __builtin_amdgcn_sched_barrier(0);
+            load(x1, y1, b + 4);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(x2, y2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (b < nb) chain(x0, y0);
+        if (b + 1 < nb) chain(x1, y1);
+        if (b + 2 < nb) {
+            load(x2, y2, b + 2);
+            chain(x2, y2);
         }
         const float* xs = xT + lane * pitch;
         const float* ys = yT + lane * pitch;
-        for (int c = nb * 16; c < chunks; ++c) a = __builtin_fmaf(xs[c], ys[c], a);
+        for (int c = nb * 8; c < chunks; ++c) a = __builtin_fmaf(xs[c], ys[c], a);
     }
     const int l = lane & 3;
     const float a0 = __shfl(a, l, 64), a1 = __shfl(a, 4 + l, 64), a2 = __shfl(a, 8 + l, 64),
@@ -388,6 +408,19 @@ __device__ __forceinline__ float dot16_t(const float* xT, const float* yT, int p
     const float t = ((a2 + a3) + a1) + a0;
     const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
     return (t0 + t1) + (t2 + t3);
+}
+
+// A barrier among the mix8 wavefronts only (the other wavefronts go on):
+// lane 0 of each adds its arrival to an LDS counter and waits for `target`
+// arrivals.  LDS operations of a wavefront complete in order, so the
+// wavefront's earlier LDS writes are visible once its arrival is.
+__device__ __forceinline__ void mixer_sync(int* count, int target) {
+    if ((threadIdx.x & 63) == 0) {
+        __hip_atomic_fetch_add(count, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        while (__hip_atomic_load(count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+            __builtin_amdgcn_s_sleep(1);
+    }
+    __builtin_amdgcn_wave_barrier();
 }
 
 // rinv(dot16(x, x)) over a transposed operand by wavefront 0, handed to
@@ -494,8 +527,8 @@ __device__ __forceinline__ void store_out(const Dims& D, const OutRegs& q, Layer
 // cond_weights (infer.rs:1640-1656) by wavefront 0: lane 8 jm + k carries
 // acc[jm][k] = fma(h2[j], cond_v[j][k], .) over j = jm, jm + 4, ...
 // (u = j / 4 in order), reading h2 and cond_v from their transposed copies
-// 8 steps per load, the next batch's loads issued before this batch's fmas;
-// then the softmax of the combined logits.
+// in 8-step batches, pipelined as dot16_t's chains; then the softmax of the
+// combined logits.
 __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int lane, float* wk) {
     const int k = lane & 7, jm = lane >> 3;
     float a = 0.0f;
@@ -503,22 +536,47 @@ __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int l
         const int steps = d / 4, nb = steps / 8;
         const float4* hr = reinterpret_cast<const float4*>(sh.hT + jm * TP_H);
         const uint4* cr = reinterpret_cast<const uint4*>(sh.cvT + (jm * COND_RANK + k) * TP_C);
-        float4 h0 = hr[0], h1 = hr[1];
-        uint4 c0 = cr[0];
-        for (int b = 0; b < nb; ++b) {
-            const int nx = b + 1 < nb ? b + 1 : b;
-            const float4 n0 = hr[2 * nx], n1 = hr[2 * nx + 1];
-            const uint4 nc = cr[nx];
-            const float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
-            const uint32_t cw[4] = {c0.x, c0.y, c0.z, c0.w};
+        float4 h0[2], h1[2], h2[2];
+        uint4 c0, c1, c2;
+        auto load = [&](float4* hd, uint4& cd, int bb) {
+            const int b = min(bb, nb - 1);
+            hd[0] = hr[2 * b];
+            hd[1] = hr[2 * b + 1];
+            cd = cr[b];
+        };
+        auto chain = [&](const float4* hd, const uint4& cd) {
+            const float hv[8] = {hd[0].x, hd[0].y, hd[0].z, hd[0].w, hd[1].x, hd[1].y, hd[1].z, hd[1].w};
+            const uint32_t cw[4] = {cd.x, cd.y, cd.z, cd.w};
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 a = __builtin_fmaf(hv[2 * u], h2f((uint16_t)(cw[u] & 0xffffu)), a);
                 a = __builtin_fmaf(hv[2 * u + 1], h2f((uint16_t)(cw[u] >> 16)), a);
             }
-            h0 = n0;
-            h1 = n1;
-            c0 = nc;
+        };
+        if (nb > 0) {
+            load(h0, c0, 0);
+            load(h1, c1, 1);
+        }
+        int b = 0;
+        for (; b + 3 <= nb; b += 3) {
+            load(h2, c2, b + 2);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(h0, c0);
+            __builtin_amdgcn_sched_barrier(0);
+            load(h0, c0, b + 3);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(h1, c1);
+            __builtin_amdgcn_sched_barrier(0);
+            load(h1, c1, b + 4);
+            __builtin_amdgcn_sched_barrier(0);
+            chain(h2, c2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (b < nb) chain(h0, c0);
+        if (b + 1 < nb) chain(h1, c1);
+        if (b + 2 < nb) {
+            load(h2, c2, b + 2);
+            chain(h2, c2);
         }
         for (int u = nb * 8; u < steps; ++u)
             a = __builtin_fmaf(sh.hT[jm * TP_H + u], h2f(sh.cvT[(jm * COND_RANK + k) * TP_C + u]), a);
@@ -570,10 +628,14 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
         sh.A[t] = t < d ? h2 * h2f_late(q.d1) : 0.0f;
     }
     __syncthreads();
+    // cond_weights (wavefront 0) spans both passes of the first mix8; the
+    // mixers meet between their passes on their own
     if (wave == 0) cond_weights(sh, d, lane, sh.wk);
-    if (mixer) mix8_t(mu, sh.kron[0], sh.A, sh.B);
-    __syncthreads();
-    if (mixer) mix8_n(mu, sh.B, sh.kron[1], sh.C, HADA_NB);
+    if (mixer) {
+        mix8_t(mu, sh.kron[0], sh.A, sh.B);
+        mixer_sync(&sh.mix_count, MIX_T / 64);
+        mix8_n(mu, sh.B, sh.kron[1], sh.C, HADA_NB);
+    }
     __syncthreads();
     {
         float cond = 1.0f;
@@ -832,11 +894,14 @@ __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, Laye
     if constexpr (has_prev) qo = load_out(D, G, R, P, sh);
     InRegs qi;
     float fnorm = 0.0f;
-    if constexpr (has_next)
-        qi = load_in(D, R, N);
-    else
-        fnorm = G.final_norm[min(t, d - 1)];
+    // Without a previous layer nothing else loads: the next layer's reads
+    // go now.  With one they go after the first barrier: the Phi8 rows are
+    // half the kernel's bytes and are not needed before the mHC read, so
+    // they stay out of the way of the tables the MLP waits for.
+    if constexpr (has_next && !has_prev) qi = load_in(D, R, N);
+    if constexpr (!has_next) fnorm = G.final_norm[min(t, d - 1)];
     float m = 0.0f;
+    if (t == 0) sh.mix_count = 0;
 #pragma unroll
     for (int k = 0; k < MHC_LANES; ++k)
         if (t + k * LT < nc) {
@@ -846,17 +911,24 @@ __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, Laye
         }
     if constexpr (has_prev) store_out(D, qo, sh);
     __syncthreads();
+    if constexpr (has_next && has_prev) qi = load_in(D, R, N);
     if constexpr (has_prev) m = layer_out(D, P, qo, sh);
     // the wavefronts' maxima of |xs| for the mHC read
     m = wave_max(m);
     if (lane == 0) sh.red[wave] = m;
     __syncthreads();
-    if constexpr (has_prev)
-        for (int i = t; i < nc; i += LT) R.xs[i] = sh.xs[i];
+    // (the new lanes go back to HBM last: nothing here reads them there, and
+    // stores issued earlier would sit in the memory counter ahead of loads
+    // that are waited for)
     if constexpr (has_next)
         layer_in(D, R, N, qi, in_bits, sh);
     else
         head_in(D, S, fnorm, head_bits, sh);  // A8 into activation row 0
+    if constexpr (has_prev) {
+#pragma unroll
+        for (int k = 0; k < MHC_LANES; ++k)
+            if (t + k * LT < nc) R.xs[t + k * LT] = sh.xs[t + k * LT];
+    }
 }
 
 hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
