@@ -24,6 +24,33 @@ __device__ __forceinline__ float quad_xor2(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
 }
 
+// The value of lane (lane ^ H), H = 4 or 8, within each row of 16 lanes:
+// two DPP row shifts (lane i reads i + H, resp. i - H) and a select.
+template <int H>
+__device__ __forceinline__ float row_xor(float v, int lane) {
+    const int up = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + H, 0xF, 0xF, false);
+    const int dn = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x110 + H, 0xF, 0xF, false);
+    return __builtin_bit_cast(float, (lane & H) ? dn : up);
+}
+
+// The value of lane (lane ^ 16), by a swizzle in xor mode (no address
+// computation, unlike a shuffle).
+__device__ __forceinline__ float lane_xor16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x1F | (16 << 10)));
+}
+
+// The value of lane (lane ^ h) for h = 1, 2, 4, 8, 16, 32.
+__device__ __forceinline__ float lane_xor(float v, int h, int lane) {
+    switch (h) {
+        case 1: return quad_xor1(v);
+        case 2: return quad_xor2(v);
+        case 4: return row_xor<4>(v, lane);
+        case 8: return row_xor<8>(v, lane);
+        case 16: return lane_xor16(v);
+        default: return __shfl_xor(v, h, 64);
+    }
+}
+
 // A streamed 16-byte load (read once, non-temporal hint).
 __device__ __forceinline__ uint4 load_stream(const uint4* p) {
     u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
@@ -106,8 +133,8 @@ __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
 __device__ __forceinline__ void fwht128(float& v0, float& v1, int lane) {
 #pragma unroll
     for (int h = 1; h < 64; h <<= 1) {
-        float p0 = __shfl_xor(v0, h, 64);
-        float p1 = __shfl_xor(v1, h, 64);
+        float p0 = lane_xor(v0, h, lane);
+        float p1 = lane_xor(v1, h, lane);
         bool upper = (lane & h) != 0;
         v0 = upper ? (p0 - v0) : (v0 + p0);
         v1 = upper ? (p1 - v1) : (v1 + p1);

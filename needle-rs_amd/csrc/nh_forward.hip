@@ -65,6 +65,26 @@ __device__ __forceinline__ float rinv(float ss, int n) {
     return 1.0f / __builtin_sqrtf(v);
 }
 
+// dot16's combine of its 16 accumulators held by lanes 0..15 (lane
+// i16 = 4 j + l holds a[j][l]): t[l] = ((a[2][l] + a[3][l]) + a[1][l]) +
+// a[0][l], then (t0 + t1) + (t2 + t3), the result in every lane.  DPP row
+// shifts bring lanes l + 4, l + 8, l + 12 to lane l and quad broadcasts
+// t0..t3 (no LDS round trips); lanes 0..3 hold the exact value.
+__device__ __forceinline__ float dot16_combine(float a) {
+    const int ai = __builtin_bit_cast(int, a);
+    const float a1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ai, 0x104, 0xF, 0xF, false));
+    const float a2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ai, 0x108, 0xF, 0xF, false));
+    const float a3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ai, 0x10C, 0xF, 0xF, false));
+    const float t = ((a2 + a3) + a1) + a;
+    const int ti = __builtin_bit_cast(int, t);
+    const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x00, 0xF, 0xF, false));
+    const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x55, 0xF, 0xF, false));
+    const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xAA, 0xF, 0xF, false));
+    const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xFF, 0xF, 0xF, false));
+    const float r = (t0 + t1) + (t2 + t3);
+    return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, r)));
+}
+
 // dot16 (infer.rs:369-419, portable branch) over a vector held one element
 // per lane (n <= 64): lane i16 = 4 j + l carries accumulator a[j][l] over
 // 16-element chunks in order; t[l] = ((a[2][l] + a[3][l]) + a[1][l]) +
@@ -76,12 +96,7 @@ __device__ __forceinline__ float dot16_lanes(float v, int n, int lane) {
         const float x = __shfl(v, c * 16 + (lane & 15), 64);
         a = __builtin_fmaf(x, x, a);
     }
-    const int l = lane & 3;
-    const float a0 = __shfl(a, l, 64), a1 = __shfl(a, 4 + l, 64), a2 = __shfl(a, 8 + l, 64),
-                a3 = __shfl(a, 12 + l, 64);
-    const float t = ((a2 + a3) + a1) + a0;
-    const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
-    return (t0 + t1) + (t2 + t3);
+    return dot16_combine(a);
 }
 
 // quant_i8's scale (qlinear.rs:92-108) of a value per lane, max over the
@@ -402,12 +417,7 @@ __device__ __forceinline__ float dot16_t(const float* xT, const float* yT, int p
         const float* ys = yT + lane * pitch;
         for (int c = nb * 8; c < chunks; ++c) a = __builtin_fmaf(xs[c], ys[c], a);
     }
-    const int l = lane & 3;
-    const float a0 = __shfl(a, l, 64), a1 = __shfl(a, 4 + l, 64), a2 = __shfl(a, 8 + l, 64),
-                a3 = __shfl(a, 12 + l, 64);
-    const float t = ((a2 + a3) + a1) + a0;
-    const float t0 = __shfl(t, 0, 64), t1 = __shfl(t, 1, 64), t2 = __shfl(t, 2, 64), t3 = __shfl(t, 3, 64);
-    return (t0 + t1) + (t2 + t3);
+    return dot16_combine(a);
 }
 
 // A barrier among the mix8 wavefronts only (the other wavefronts go on):
