@@ -1083,6 +1083,14 @@ hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int lay
     return hipGetLastError();
 }
 
+// The sum of an integer over each group of four lanes (DPP quad permutes;
+// integer adds are exact in any order).
+__device__ __forceinline__ int quad_sum_i32(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+    return v;
+}
+
 // -------------------------------------------------------------- attention
 // attend_head_ref (infer.rs:1871-2007), one workgroup per (query head,
 // key chunk): q as int8 (scale x INV_SQRT_QK), int8 scores
@@ -1143,9 +1151,17 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
             for (int b = 0; b < nb8; ++b) acc += sc[b * 8 + hi * 4 + k];
             if (hi == 0 && len - nb8 * 8 >= 4) acc += sc[nb8 * 8 + k];
         }
-        const int k = lane & 3;
-        const float tk = __shfl(acc, k, 64) + __shfl(acc, 4 + k, 64);
-        float sum = (__shfl(tk, 0, 64) + __shfl(tk, 1, 64)) + (__shfl(tk, 2, 64) + __shfl(tk, 3, 64));
+        // t[k] = a[k] + b[k] (lane 4 + k brought to lane k by a DPP row
+        // shift), then (t0 + t1) + (t2 + t3) by quad broadcasts: exact in
+        // lane 0, which alone uses it
+        const float tk = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
+                                                                                       0x104, 0xF, 0xF, false));
+        const int ti = __builtin_bit_cast(int, tk);
+        const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x00, 0xF, 0xF, false));
+        const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x55, 0xF, 0xF, false));
+        const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xAA, 0xF, 0xF, false));
+        const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xFF, 0xF, 0xF, false));
+        float sum = (t0 + t1) + (t2 + t3);
         int i = blocked;
         if (len - i >= 2) {
             sum = (sc[i] + sum) + sc[i + 1];
@@ -1186,12 +1202,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
             c += dig[2][i] * v;
         }
     }
-    a += __shfl_xor(a, 1, 64);
-    a += __shfl_xor(a, 2, 64);
-    b += __shfl_xor(b, 1, 64);
-    b += __shfl_xor(b, 2, 64);
-    c += __shfl_xor(c, 1, 64);
-    c += __shfl_xor(c, 2, 64);
+    a = quad_sum_i32(a);
+    b = quad_sum_i32(b);
+    c = quad_sum_i32(c);
     const size_t pi = ((size_t)row * D.nh + hh) * D.max_chunks + ci;
     if (dm < vd && part == 0)
         S.po[pi * vd + dm] = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
@@ -1284,6 +1297,7 @@ struct UnitIn {
 // ranges read a clamped in-range address; `norm` is read for every unit,
 // used by the normed ones) and raw, so all of them issue before the first
 // wait.
+template <int TAPS, bool EXACT>
 __device__ __forceinline__ UnitIn unit_load(const Dims& D, const SessDev& S, int layer, int p0, int start, int cw,
                                             int cc, int len, const uint16_t* w, const uint16_t* norm, int i) {
     const float* hist = S.hist + (size_t)layer * D.hist_slots * D.W;
@@ -1291,8 +1305,8 @@ __device__ __forceinline__ UnitIn unit_load(const Dims& D, const SessDev& S, int
     UnitIn u{};
     u.cur = S.proj[start + ii];
 #pragma unroll
-    for (int j = 0; j < DG_MAX_TAPS; ++j) {
-        const int jj = j < D.taps ? j : D.taps - 1;
+    for (int j = 0; j < TAPS; ++j) {
+        const int jj = EXACT || j < D.taps ? j : D.taps - 1;
         u.w[j] = w[(size_t)jj * cw + cc + ii];
         if (j > 0) {
             const int pj = p0 >= jj ? p0 - jj : 0;
@@ -1311,14 +1325,15 @@ __device__ __forceinline__ UnitIn unit_load(const Dims& D, const SessDev& S, int
 // The unit's post-tap value (zcn16 and RoPE when `normed`): the causal conv
 // over the row and the kept history rows, v = w0 cur, then
 // fma(w_j, row_{p0 - j}, v) (a row before position 0 is zero).
+template <int TAPS, bool EXACT>
 __device__ __forceinline__ float unit_finish(const Dims& D, const SessDev& S, int layer, int p0, int start, int len,
                                              const UnitIn& u, bool normed, int i, bool write_hist) {
     float v = 0.0f;
     if (i < len) {
         v = h2f(u.w[0]) * u.cur;
 #pragma unroll
-        for (int j = 1; j < DG_MAX_TAPS; ++j)
-            if (j < D.taps) v = __builtin_fmaf(h2f(u.w[j]), p0 >= j ? u.h[j] : 0.0f, v);
+        for (int j = 1; j < TAPS; ++j)
+            if (EXACT || j < D.taps) v = __builtin_fmaf(h2f(u.w[j]), p0 >= j ? u.h[j] : 0.0f, v);
         if (write_hist) S.hist[((size_t)layer * D.hist_slots + p0 % D.hist_slots) * D.W + start + i] = u.cur;
     }
     if (normed) {
@@ -1336,7 +1351,7 @@ __device__ __forceinline__ float unit_finish(const Dims& D, const SessDev& S, in
     return v;
 }
 
-template <int HP>
+template <int HP, int TAPS, bool EXACT>
 __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S, LayerDev L, int layer, int p0,
                                                               int out_bits) {
     constexpr int NT = HP * DG_HEAD_T;
@@ -1375,11 +1390,13 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
     const int role = __builtin_amdgcn_readfirstlane(wave < HP ? 0 : wave - HP + 1);  // 0 q, 1 k, 2 v, 3+ none
     UnitIn ui;
     if (role == 0)
-        ui = unit_load(D, S, layer, p0, (hh0 + wave) * qk, qd, (hh0 + wave) * qk, qk, L.q_taps, L.q_norm, lane);
+        ui = unit_load<TAPS, EXACT>(D, S, layer, p0, (hh0 + wave) * qk, qd, (hh0 + wave) * qk, qk, L.q_taps, L.q_norm,
+                                    lane);
     else if (role == 1)
-        ui = unit_load(D, S, layer, p0, qd + kvh * qk, kd, kvh * qk, qk, L.k_taps, L.k_norm, lane);
+        ui = unit_load<TAPS, EXACT>(D, S, layer, p0, qd + kvh * qk, kd, kvh * qk, qk, L.k_taps, L.k_norm, lane);
     else
-        ui = unit_load(D, S, layer, p0, qd + kd + kvh * vd, vdim, kvh * vd, vd, L.v_taps, L.k_norm, lane);
+        ui = unit_load<TAPS, EXACT>(D, S, layer, p0, qd + kd + kvh * vd, vdim, kvh * vd, vd, L.v_taps, L.k_norm,
+                                    lane);
     // The keys before the position: int8 rows (16-byte chunks), scales and
     // value dwords, all in flight at once, stored to LDS after the units.
     constexpr int KR = ATT_CHUNK_MAX * 4 / NT, VR = (MAX_HEAD_DIM * DG_VDW + NT - 1) / NT;
@@ -1407,12 +1424,12 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
     }
     // the units
     if (wave < HP) {
-        const float v = unit_finish(D, S, layer, p0, (hh0 + wave) * qk, qk, ui, true, lane, true);
+        const float v = unit_finish<TAPS, EXACT>(D, S, layer, p0, (hh0 + wave) * qk, qk, ui, true, lane, true);
         const float s = wave_quant_scale(lane < qk ? v : 0.0f);
         if (lane < qk) q8[wave][lane] = quant_one(v, 1.0f / s);
         if (lane == 0) s_qs[wave] = s * bits_f32(0x3e13cd3au);
     } else if (wave == HP) {
-        const float v = unit_finish(D, S, layer, p0, qd + kvh * qk, qk, ui, true, lane, owner);
+        const float v = unit_finish<TAPS, EXACT>(D, S, layer, p0, qd + kvh * qk, qk, ui, true, lane, owner);
         const float s = wave_quant_scale(lane < qk ? v : 0.0f);
         const int8_t q = quant_one(v, 1.0f / s);
         if (lane < qk) {
@@ -1424,7 +1441,7 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
             if (owner) S.ks[(lc + p0) * nkv + kvh] = s;
         }
     } else if (wave == HP + 1) {
-        const float v = unit_finish(D, S, layer, p0, qd + kd + kvh * vd, vd, ui, false, lane, owner);
+        const float v = unit_finish<TAPS, EXACT>(D, S, layer, p0, qd + kd + kvh * vd, vd, ui, false, lane, owner);
         const float s = wave_quant_scale(lane < vd ? v : 0.0f);
         const int8_t q = quant_one(v, 1.0f / s);
         if (lane < vd) {
@@ -1510,9 +1527,17 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
             for (; b < nb8; ++b) acc += col[b * 8];
             if (hi == 0 && n - nb8 * 8 >= 4) acc += sc[h][nb8 * 8 + k];
         }
-        const int k = lane & 3;
-        const float tk = __shfl(acc, k, 64) + __shfl(acc, 4 + k, 64);
-        float sum = (__shfl(tk, 0, 64) + __shfl(tk, 1, 64)) + (__shfl(tk, 2, 64) + __shfl(tk, 3, 64));
+        // t[k] = a[k] + b[k] (lane 4 + k brought to lane k by a DPP row
+        // shift), then (t0 + t1) + (t2 + t3) by quad broadcasts: exact in
+        // lane 0, which alone uses it
+        const float tk = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
+                                                                                       0x104, 0xF, 0xF, false));
+        const int ti = __builtin_bit_cast(int, tk);
+        const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x00, 0xF, 0xF, false));
+        const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x55, 0xF, 0xF, false));
+        const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xAA, 0xF, 0xF, false));
+        const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xFF, 0xF, 0xF, false));
+        float sum = (t0 + t1) + (t2 + t3);
         int i = blocked;
         if (n - i >= 2) {
             sum = (sc[h][i] + sum) + sc[h][i + 1];
@@ -1580,12 +1605,9 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
                 c = __builtin_amdgcn_sdot4(d2[i], v, c, false);
             }
         }
-        a += __shfl_xor(a, 1, 64);
-        a += __shfl_xor(a, 2, 64);
-        b += __shfl_xor(b, 1, 64);
-        b += __shfl_xor(b, 2, 64);
-        c += __shfl_xor(c, 1, 64);
-        c += __shfl_xor(c, 2, 64);
+        a = quad_sum_i32(a);
+        b = quad_sum_i32(b);
+        c = quad_sum_i32(c);
         if (dm < vd && part == 0) {
             const float po = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
             const float inv = 1.0f / s_sum[h];
@@ -1616,10 +1638,25 @@ bool dec_group_fits(const Dims& D, int p0, int window) {
 hipError_t fwd_dec_attn(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
                         hipStream_t s) {
     const int hp = GROUP / D.vd, blocks = D.nh / hp + 1;
-    if (hp == 2)
-        hipLaunchKernelGGL(k_dec_group<2>, dim3(blocks), dim3(2 * DG_HEAD_T), 0, s, D, S, L, layer, p0, out_bits);
-    else
-        hipLaunchKernelGGL(k_dec_group<4>, dim3(blocks), dim3(4 * DG_HEAD_T), 0, s, D, S, L, layer, p0, out_bits);
+    // exact tap counts 1..4, clamped loads up to DG_MAX_TAPS otherwise
+#define NH_DG(HP, TP, EX)                                                                                        \
+    hipLaunchKernelGGL((k_dec_group<HP, TP, EX>), dim3(blocks), dim3(HP * DG_HEAD_T), 0, s, D, S, L, layer, p0, \
+                       out_bits)
+#define NH_DG_TAPS(HP)                          \
+    switch (D.taps) {                           \
+        case 1: NH_DG(HP, 1, true); break;      \
+        case 2: NH_DG(HP, 2, true); break;      \
+        case 3: NH_DG(HP, 3, true); break;      \
+        case 4: NH_DG(HP, 4, true); break;      \
+        default: NH_DG(HP, DG_MAX_TAPS, false); \
+    }
+    if (hp == 2) {
+        NH_DG_TAPS(2)
+    } else {
+        NH_DG_TAPS(4)
+    }
+#undef NH_DG_TAPS
+#undef NH_DG
     return hipGetLastError();
 }
 
