@@ -276,8 +276,8 @@ hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, in
 // handing it out.
 namespace {
 
-constexpr int BT_STRIDE = HADA_NB + 1;  // padded row of a transposed mix8 output
-constexpr int MIX_T = 256;              // threads of one mix8 (4 outputs each)
+constexpr int BT_STRIDE = HADA_NB + 2;  // padded (even: 8-byte reads) row of a transposed mix8 output
+constexpr int MIX_T = 256;              // threads of one mix8 (a 2 x 2 output block each)
 // Transposed copies for the serial chains, so a chain lane reads its
 // operands as contiguous 16-byte vectors: a dot16 operand x[16 c + l] at
 // l * pitch + c (pitch TP_D for d-long vectors, TP_X for the 4 lanes);
@@ -312,43 +312,43 @@ struct LayerShared {
 
 // mix8 (infer.rs:2343-2380), portable branch: out[r][c] =
 // sum_j ct[j][r] * rows[j][c], each output an fma chain from j = 0.  Thread
-// u < 256 computes r = u / 8 and c = 4 (u % 8) .. + 3, so each step reads
-// one ct value and four row values.
-// Transposed (ct = a factor, rows = [32][32]): stored at out[c * 33 + r].
+// u < 256 computes the 2 x 2 block r = 2 (u / 16) + {0, 1}, c = 2 (u % 16) +
+// {0, 1}, so each step reads two ct values and two row values (8-byte
+// reads) for four fmas.
+// Transposed (ct = a factor, rows = [32][32]): stored at out[c * BT_STRIDE + r].
 __device__ __forceinline__ void mix8_t(int u, const float* ct, const float* rows, float* out) {
-    const int r = u >> 3, c0 = (u & 7) * 4;
-    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+    const int r = (u >> 4) * 2, c = (u & 15) * 2;
+    float o00 = 0.0f, o01 = 0.0f, o10 = 0.0f, o11 = 0.0f;
 #pragma unroll
     for (int j = 0; j < HADA_NB; ++j) {
-        const float a = ct[j * HADA_NB + r];
-        const float4 b = *reinterpret_cast<const float4*>(rows + j * HADA_NB + c0);
-        o0 = __builtin_fmaf(a, b.x, o0);
-        o1 = __builtin_fmaf(a, b.y, o1);
-        o2 = __builtin_fmaf(a, b.z, o2);
-        o3 = __builtin_fmaf(a, b.w, o3);
+        const float2 a = *reinterpret_cast<const float2*>(ct + j * HADA_NB + r);
+        const float2 b = *reinterpret_cast<const float2*>(rows + j * HADA_NB + c);
+        o00 = __builtin_fmaf(a.x, b.x, o00);
+        o01 = __builtin_fmaf(a.x, b.y, o01);
+        o10 = __builtin_fmaf(a.y, b.x, o10);
+        o11 = __builtin_fmaf(a.y, b.y, o11);
     }
-    out[(c0 + 0) * BT_STRIDE + r] = o0;
-    out[(c0 + 1) * BT_STRIDE + r] = o1;
-    out[(c0 + 2) * BT_STRIDE + r] = o2;
-    out[(c0 + 3) * BT_STRIDE + r] = o3;
+    *reinterpret_cast<float2*>(out + c * BT_STRIDE + r) = make_float2(o00, o10);
+    *reinterpret_cast<float2*>(out + (c + 1) * BT_STRIDE + r) = make_float2(o01, o11);
 }
 
 // Plain (ct = the output of mix8_t, rows = a factor): out[r][c], rows
-// r < rows_limit.
+// r < rows_limit (a multiple of 2).
 __device__ __forceinline__ void mix8_n(int u, const float* ct, const float* rows, float* out, int rows_limit) {
-    const int r = u >> 3, c0 = (u & 7) * 4;
+    const int r = (u >> 4) * 2, c = (u & 15) * 2;
     if (r >= rows_limit) return;
-    float o0 = 0.0f, o1 = 0.0f, o2 = 0.0f, o3 = 0.0f;
+    float o00 = 0.0f, o01 = 0.0f, o10 = 0.0f, o11 = 0.0f;
 #pragma unroll
     for (int j = 0; j < HADA_NB; ++j) {
-        const float a = ct[j * BT_STRIDE + r];
-        const float4 b = *reinterpret_cast<const float4*>(rows + j * HADA_NB + c0);
-        o0 = __builtin_fmaf(a, b.x, o0);
-        o1 = __builtin_fmaf(a, b.y, o1);
-        o2 = __builtin_fmaf(a, b.z, o2);
-        o3 = __builtin_fmaf(a, b.w, o3);
+        const float2 a = *reinterpret_cast<const float2*>(ct + j * BT_STRIDE + r);
+        const float2 b = *reinterpret_cast<const float2*>(rows + j * HADA_NB + c);
+        o00 = __builtin_fmaf(a.x, b.x, o00);
+        o01 = __builtin_fmaf(a.x, b.y, o01);
+        o10 = __builtin_fmaf(a.y, b.x, o10);
+        o11 = __builtin_fmaf(a.y, b.y, o11);
     }
-    *reinterpret_cast<float4*>(out + r * HADA_NB + c0) = make_float4(o0, o1, o2, o3);
+    *reinterpret_cast<float2*>(out + r * HADA_NB + c) = make_float2(o00, o01);
+    *reinterpret_cast<float2*>(out + (r + 1) * HADA_NB + c) = make_float2(o10, o11);
 }
 
 // Element i of a dot16 operand into its transposed copy.
