@@ -1416,6 +1416,8 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
         ksr = S.ks[(lc + lo + i) * nkv + kvh];
         vsr = S.vs[(lc + lo + i) * nkv + kvh];
     }
+    // the head gate of this thread's P.V output (head h, dimension u / 4)
+    const float gate = S.proj[D.W + (hh0 + h) * vd + min(u >> 2, vd - 1)];
     const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
 #pragma unroll
     for (int r = 0; r < VR; ++r) {
@@ -1612,7 +1614,7 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
             const float po = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
             const float inv = 1.0f / s_sum[h];
             const float out = po * inv;
-            att[h * vd + dm] = out / (nexp(-S.proj[D.W + (hh0 + h) * vd + dm]) + 1.0f);
+            att[h * vd + dm] = out / (nexp(-gate) + 1.0f);
         }
     }
     __syncthreads();
