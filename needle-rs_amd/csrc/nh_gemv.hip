@@ -131,7 +131,8 @@ static hipError_t run(const nh_qmat* w, const nh_qact* a, float* y, int32_t* dbg
 // Groups per wavefront (GPS) and wavefronts per tile (S) by group count:
 // two to four groups per lane keeps 2-4 KiB of loads in flight per
 // wavefront while giving the big shapes several wavefronts per CU (at
-// K = 2048, 8 wavefronts x 2 groups measured 2.4 % faster than 4 x 4).  Any G
+// K = 2048, 8 wavefronts x 2 groups measured 2.4 % faster than 4 x 4; at
+// K = 768, 6 x 1 5 % faster than 2 x 3).  Any G
 // up to 32 maps to the smallest listed G' >= G (wavefronts skip the
 // groups past G).
 template <int BITS>
@@ -141,7 +142,7 @@ static hipError_t dispatch(const nh_qmat* w, const nh_qact* a, float* y, int32_t
     if (G <= 2) return run<2, 1, BITS>(w, a, y, dbg, s);
     if (G <= 3) return run<3, 1, BITS>(w, a, y, dbg, s);
     if (G <= 4) return run<2, 2, BITS>(w, a, y, dbg, s);
-    if (G <= 6) return run<3, 2, BITS>(w, a, y, dbg, s);
+    if (G <= 6) return run<1, 6, BITS>(w, a, y, dbg, s);
     if (G <= 8) return run<2, 4, BITS>(w, a, y, dbg, s);
     if (G <= 12) return run<3, 4, BITS>(w, a, y, dbg, s);
     if (G <= 16) return run<2, 8, BITS>(w, a, y, dbg, s);
