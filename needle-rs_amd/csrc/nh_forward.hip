@@ -1098,7 +1098,16 @@ __device__ __forceinline__ int quad_sum_i32(int v) {
 // for the rest, the chunk max, chunk_exp (nexp over the 4-blocked prefix
 // summed in 8 lane classes, lexpf over the tail, infer.rs:2222-2279), the
 // weights times v-scales as 21-bit digits (digits21, infer.rs:2171-2220)
-// and their exact integer P.V with the int8 values.
+// and their exact integer P.V with the int8 values.  The chunk's key rows,
+// scales and value columns are staged in LDS with every load in flight at
+// once (value dwords of the transposed cache from the dword boundary at or
+// before the chunk's first slot; the digits are shifted by the same
+// offset, so bytes before the first key meet zero digits), and P.V runs
+// four keys per sdot4.
+constexpr int ATT_KPITCH = MAX_HEAD_DIM + 16;        // key row (80 bytes: 8 rows cover the 32 banks)
+constexpr int ATT_PITCH = ATT_CHUNK_MAX + 8;         // value / digit row: 3 alignment bytes + 256 keys + tail
+constexpr int ATT_VDW = (ATT_CHUNK_MAX + 3 + 3) / 4; // value dwords per column
+
 __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, LayerDev L, int layer, int p0,
                                                        int rows) {
     const int row = blockIdx.x / D.nh, hh = blockIdx.x % D.nh, ci = blockIdx.y, t = threadIdx.x;
@@ -1109,31 +1118,89 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     key_chunks(n, nkv, rows > 1, count, chunk);
     if (ci >= count) return;
     const int c0 = ci * chunk, len = min(chunk, n - c0), blocked = len / 4 * 4, slot0 = lo + c0;
+    const int sh = slot0 & 3, base = slot0 - sh, cols = sh + len;
+    __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][ATT_KPITCH];
+    __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][ATT_PITCH];
+    __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
     __shared__ alignas(16) int8_t q8[MAX_HEAD_DIM];
     __shared__ float sc[ATT_CHUNK_MAX];
-    __shared__ int8_t dig[3][ATT_CHUNK_MAX];
+    __shared__ alignas(16) int8_t dig[3][ATT_PITCH];
     __shared__ float red[ATT_THREADS / 64];
     __shared__ float s_qs, s_sum;
+    const size_t lc = (size_t)layer * D.cap;
+    // every load first (unconditional, at clamped in-range addresses)
+    const float qv = S.qbuf[((size_t)row * D.nh + hh) * qk + min(lane, qk - 1)];
+    constexpr int KR = ATT_CHUNK_MAX * 4 / ATT_THREADS, VR = (MAX_HEAD_DIM * ATT_VDW + ATT_THREADS - 1) / ATT_THREADS;
+    const int rq = qk / 16, vdw = (cols + 3) / 4;
+    uint4 kr[KR];
+    uint32_t vw[VR];
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+        const int e = t + r * ATT_THREADS, i = min(e >> 2, len - 1), c = min(e & 3, rq - 1);
+        kr[r] = reinterpret_cast<const uint4*>(S.k8 + ((lc + slot0 + i) * nkv + kvh) * qk)[c];
+    }
+    float ksr, vsr;
+    {
+        const int i = min(t, len - 1);
+        ksr = S.ks[(lc + slot0 + i) * nkv + kvh];
+        vsr = S.vs[(lc + slot0 + i) * nkv + kvh];
+    }
+    const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
+#pragma unroll
+    for (int r = 0; r < VR; ++r) {
+        const int e = t + r * ATT_THREADS, dm = min(e / ATT_VDW, vd - 1), k = min(e % ATT_VDW, vdw - 1);
+        vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
+    }
     if (wave == 0) {
-        const float v = lane < qk ? S.qbuf[((size_t)row * D.nh + hh) * qk + lane] : 0.0f;
-        const float s = wave_quant_scale(v);
-        if (lane < qk) q8[lane] = quant_one(v, 1.0f / s);
+        const float s = wave_quant_scale(lane < qk ? qv : 0.0f);
+        if (lane < qk) q8[lane] = quant_one(qv, 1.0f / s);
         if (lane == 0) s_qs = s * bits_f32(0x3e13cd3au);
     }
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+        const int e = t + r * ATT_THREADS, i = e >> 2, c = e & 3;
+        if (i < len && c < rq) reinterpret_cast<uint4*>(ks8[i])[c] = kr[r];
+    }
+    if (t < len) {
+        kss[t] = ksr;
+        vss[t] = vsr;
+    }
+#pragma unroll
+    for (int r = 0; r < VR; ++r) {
+        const int e = t + r * ATT_THREADS, dm = e / ATT_VDW, k = e % ATT_VDW;
+        if (dm < vd && k < vdw) {
+            if (4 * k + 3 < cols) {
+                reinterpret_cast<uint32_t*>(vs8[dm])[k] = vw[r];
+            } else {
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    if (4 * k + b < cols) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
+            }
+        }
+    }
     __syncthreads();
-    const size_t lc = (size_t)layer * D.cap;
     const float qs = s_qs;
     float mx = -__builtin_inff();
-    for (int i = t; i < len; i += ATT_THREADS) {
-        const size_t slot = lc + slot0 + i;
-        const int8_t* kr = S.k8 + (slot * nkv + kvh) * qk;
-        int dot = 0;
-        for (int j = 0; j < qk; j += 4)
-            dot = __builtin_amdgcn_sdot4(*(const int*)(kr + j), *(const int*)(q8 + j), dot, false);
-        const float ksc = S.ks[slot * nkv + kvh];
-        const float s = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
-        sc[i] = s;
-        mx = fmaxf(mx, s);
+    {
+        uint4 qw[MAX_HEAD_DIM / 16];
+#pragma unroll
+        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) qw[c] = reinterpret_cast<const uint4*>(q8)[c];
+        for (int i = t; i < len; i += ATT_THREADS) {
+            int dot = 0;
+#pragma unroll
+            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
+                if (c < rq) {
+                    const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
+                    dot = __builtin_amdgcn_sdot4((int)kv.x, (int)qw[c].x, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)kv.y, (int)qw[c].y, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)kv.z, (int)qw[c].z, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)kv.w, (int)qw[c].w, dot, false);
+                }
+            const float ksc = kss[i];
+            const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
+            sc[i] = sv;
+            mx = fmaxf(mx, sv);
+        }
     }
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
@@ -1143,17 +1210,25 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     __syncthreads();
     if (wave == 0) {
         // a[k] over the 8-blocks' first halves plus a trailing 4-block,
-        // b[k] over their second halves; t = a + b; (t0 + t1) + (t2 + t3).
+        // b[k] over their second halves (lane 4 hi + k sums sc[8 b + 4 hi + k]
+        // over b in order, batches of 8 loads ahead of their adds)
         float acc = 0.0f;
         const int nb8 = len / 8;
         if (lane < 8) {
             const int k = lane & 3, hi = lane >> 2;
-            for (int b = 0; b < nb8; ++b) acc += sc[b * 8 + hi * 4 + k];
+            const float* col = &sc[hi * 4 + k];
+            int b = 0;
+            for (; b + 8 <= nb8; b += 8) {
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = col[(b + j) * 8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc += v[j];
+            }
+            for (; b < nb8; ++b) acc += col[b * 8];
             if (hi == 0 && len - nb8 * 8 >= 4) acc += sc[nb8 * 8 + k];
         }
-        // t[k] = a[k] + b[k] (lane 4 + k brought to lane k by a DPP row
-        // shift), then (t0 + t1) + (t2 + t3) by quad broadcasts: exact in
-        // lane 0, which alone uses it
+        // t = a + b; (t0 + t1) + (t2 + t3) (DPP; exact in lane 0)
         const float tk = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
                                                                                        0x104, 0xF, 0xF, false));
         const int ti = __builtin_bit_cast(int, tk);
@@ -1173,33 +1248,59 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     __syncthreads();
     float wmax = 0.0f;
     for (int i = t; i < len; i += ATT_THREADS) {
-        const float w = sc[i] * S.vs[(lc + slot0 + i) * nkv + kvh];
+        const float w = sc[i] * vss[i];
         sc[i] = w;
         wmax = fmaxf(wmax, w);
     }
     wmax = wave_max(wmax);
-    __syncthreads();
     if (lane == 0) red[wave] = wmax;
     __syncthreads();
     wmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     const float qw = bits_f32(0x49fffff8u) / wmax;
     for (int i = t; i < len; i += ATT_THREADS) {
         const int32_t wq = (int32_t)roundf(sc[i] * qw);
-        dig[0][i] = (int8_t)(wq >> 14);
-        dig[1][i] = (int8_t)((wq >> 7) & 127);
-        dig[2][i] = (int8_t)(wq & 127);
+        dig[0][sh + i] = (int8_t)(wq >> 14);
+        dig[1][sh + i] = (int8_t)((wq >> 7) & 127);
+        dig[2][sh + i] = (int8_t)(wq & 127);
+    }
+    // zero digits in the first dword before the keys and the last one past them
+    if (t < 4) {
+        const int j0 = t, j1 = cols + t;
+        if (j0 < sh) dig[0][j0] = dig[1][j0] = dig[2][j0] = 0;
+        if (j1 < (cols + 3) / 4 * 4) dig[0][j1] = dig[1][j1] = dig[2][j1] = 0;
     }
     __syncthreads();
     const float cw = wmax * bits_f32(0x35000004u);
     const int dm = t >> 2, part = t & 3;
     int a = 0, b = 0, c = 0;
     if (dm < vd) {
-        const int8_t* row = S.v8t + (((size_t)layer * nkv + kvh) * vd + dm) * D.vcap + slot0;
-        for (int i = part; i < len; i += 4) {
-            const int v = row[i];
-            a += dig[0][i] * v;
-            b += dig[1][i] * v;
-            c += dig[2][i] * v;
+        // exact integer P.V: four keys per sdot4, 16 per thread step
+        const int* vrow = reinterpret_cast<const int*>(vs8[dm]);
+        const int* d0 = reinterpret_cast<const int*>(dig[0]);
+        const int* d1 = reinterpret_cast<const int*>(dig[1]);
+        const int* d2 = reinterpret_cast<const int*>(dig[2]);
+        int i = part;
+        for (; 4 * (i + 12) < cols; i += 16) {
+            int v[4], x0[4], x1[4], x2[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v[q] = vrow[i + 4 * q];
+                x0[q] = d0[i + 4 * q];
+                x1[q] = d1[i + 4 * q];
+                x2[q] = d2[i + 4 * q];
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                a = __builtin_amdgcn_sdot4(x0[q], v[q], a, false);
+                b = __builtin_amdgcn_sdot4(x1[q], v[q], b, false);
+                c = __builtin_amdgcn_sdot4(x2[q], v[q], c, false);
+            }
+        }
+        for (; 4 * i < cols; i += 4) {
+            const int v = vrow[i];
+            a = __builtin_amdgcn_sdot4(d0[i], v, a, false);
+            b = __builtin_amdgcn_sdot4(d1[i], v, b, false);
+            c = __builtin_amdgcn_sdot4(d2[i], v, c, false);
         }
     }
     a = quad_sum_i32(a);
