@@ -690,9 +690,11 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
 }
 
 // The next layer's weights a thread needs, read up front: its norm scale,
-// engram key / conv element, and its wavefront's Phi8 rows (rows wave and
-// wave + 16, 16 bytes at lane + 64 j of each, j < 4: rows of up to 4096).
+// engram key / conv element, and its wavefront's Phi8 rows (16 bytes at
+// lane + 64 j of each, j < 4: rows of up to 4096).
 constexpr int PHI_CHUNKS = MHC_LANES * FWD_MAX_D / 16 / 64;
+constexpr int PHI_B = LT / 64 - 1;  // wavefronts holding Phi8 rows
+static_assert(2 * PHI_B >= MHC_COLS, "two Phi8 rows per wavefront cover the 24 rows");
 struct InRegs {
     uint32_t norm;
     float kr, ev, ps0, ps1;
@@ -713,18 +715,24 @@ __device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const
     const float* ep = site ? S.evals + (size_t)N.site * FWD_ROWS * d : S.proj + d;
     q.kr = kp[td];
     q.ev = ep[td];
-    const int per = nc / 16;  // uint4 per row
-    const int w0 = min(wave, MHC_COLS - 1), w1 = min(wave + LT / 64, MHC_COLS - 1);
-    const uint4* row0 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)w0 * nc);
-    const uint4* row1 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)w1 * nc);
+    // Phi8 rows: wavefront w >= 1 holds rows w - 1 and w + PHI_B - 1 (the
+    // second past the 24 rows is a clamped duplicate); wavefront 0, which
+    // runs the first chain of the MLP right after these loads are issued,
+    // holds none, so it never waits behind them in the CU's load queue.
+    if (__builtin_amdgcn_readfirstlane(wave) != 0) {
+        const int per = nc / 16;  // uint4 per row
+        const int w0 = wave - 1, w1 = min(wave - 1 + PHI_B, MHC_COLS - 1);
+        const uint4* row0 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)w0 * nc);
+        const uint4* row1 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)w1 * nc);
 #pragma unroll
-    for (int j = 0; j < PHI_CHUNKS; ++j) {
-        const int c = min(lane + 64 * j, per - 1);
-        q.r0[j] = row0[c];
-        q.r1[j] = row1[c];
+        for (int j = 0; j < PHI_CHUNKS; ++j) {
+            const int c = min(lane + 64 * j, per - 1);
+            q.r0[j] = row0[c];
+            q.r1[j] = row1[c];
+        }
+        q.ps0 = N.phi_s[w0];
+        q.ps1 = N.phi_s[w1];
     }
-    q.ps0 = N.phi_s[w0];
-    q.ps1 = N.phi_s[w1];
     return q;
 }
 
@@ -772,13 +780,13 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, con
     {
         const float sx = sh.r_sx;
         const int per = nc / 16;
-        if (wave < MHC_COLS) {
+        if (wave >= 1) {
             const int acc = dot_row(q.r0, sh.nx8, per, lane);
-            if (lane == 0) sh.p[wave] = (sx * q.ps0) * (float)acc;
-        }
-        if (wave + LT / 64 < MHC_COLS) {
-            const int acc = dot_row(q.r1, sh.nx8, per, lane);
-            if (lane == 0) sh.p[wave + LT / 64] = (sx * q.ps1) * (float)acc;
+            if (lane == 0) sh.p[wave - 1] = (sx * q.ps0) * (float)acc;
+            if (wave - 1 + PHI_B < MHC_COLS) {
+                const int acc1 = dot_row(q.r1, sh.nx8, per, lane);
+                if (lane == 0) sh.p[wave - 1 + PHI_B] = (sx * q.ps1) * (float)acc1;
+            }
         }
     }
     __syncthreads();
