@@ -1010,6 +1010,79 @@ __device__ __forceinline__ void post_gates(float* p, const LayerDev& L, int lane
     }
 }
 
+constexpr int DG_MAX_TAPS = 8;  // conv taps the unit kernels specialise up to
+
+// A unit's inputs for lane i of feed row `row` (position pos): the pre-tap
+// value, the taps, the earlier pre-tap rows (rows of the same feed from the
+// projection, older ones from the history ring), and (normed units) the
+// norm scale and the row's RoPE entry.  Every load is unconditional (lanes,
+// taps and rows past the ranges read a clamped in-range address; `norm` is
+// read for every unit, used by the normed ones) and raw, so all of them
+// issue before the first wait.
+struct UnitIn {
+    float cur, rc, rs;
+    uint16_t nrm;
+    uint16_t w[DG_MAX_TAPS];
+    float h[DG_MAX_TAPS];
+};
+
+template <int TAPS, bool EXACT>
+__device__ __forceinline__ UnitIn unit_load(const Dims& D, const SessDev& S, int layer, int pos, int row, int start,
+                                            int cw, int cc, int len, const uint16_t* w, const uint16_t* norm, int i) {
+    const float* hist = S.hist + (size_t)layer * D.hist_slots * D.W;
+    const int ii = i < len ? i : 0;
+    UnitIn u{};
+    u.cur = S.proj[(size_t)row * D.nq + start + ii];
+#pragma unroll
+    for (int j = 0; j < TAPS; ++j) {
+        const int jj = EXACT || j < D.taps ? j : D.taps - 1;
+        u.w[j] = w[(size_t)jj * cw + cc + ii];
+        if (j > 0) {
+            const int pj = pos >= jj ? pos - jj : 0;
+            const float* src = jj <= row ? S.proj + (size_t)(row - jj) * D.nq
+                                         : hist + (size_t)(pj % D.hist_slots) * D.W;
+            u.h[j] = src[start + ii];
+        }
+    }
+    {
+        const int qi = i < D.qk ? i : 0, half = D.qk / 2, f = qi < half ? qi : qi - half;
+        u.nrm = norm[qi];
+        u.rc = S.rope_c[row * half + f];
+        u.rs = S.rope_s[row * half + f];
+    }
+    return u;
+}
+
+// The unit's post-tap value (zcn16 and RoPE when `normed`): the causal conv
+// over the row and the earlier pre-tap rows, v = w0 cur, then
+// fma(w_j, row_{pos - j}, v) (a row before position 0 is zero); the row's
+// pre-tap value goes to the ring at pos.
+template <int TAPS, bool EXACT>
+__device__ __forceinline__ float unit_finish(const Dims& D, const SessDev& S, int layer, int pos, int start, int len,
+                                             const UnitIn& u, bool normed, int i, bool write_hist) {
+    float v = 0.0f;
+    if (i < len) {
+        v = h2f(u.w[0]) * u.cur;
+#pragma unroll
+        for (int j = 1; j < TAPS; ++j)
+            if (EXACT || j < D.taps) v = __builtin_fmaf(h2f(u.w[j]), pos >= j ? u.h[j] : 0.0f, v);
+        if (write_hist) S.hist[((size_t)layer * D.hist_slots + pos % D.hist_slots) * D.W + start + i] = u.cur;
+    }
+    if (normed) {
+        const int qk = D.qk;
+        const float ss = dot16_lanes(v, qk, i);
+        const float r = rinv(ss, qk);
+        if (i < qk) {
+            const float tt = v * r;
+            v = __builtin_fmaf(tt, h2f(u.nrm), tt);
+        }
+        const int half = qk / 2, f = i < half ? i : i - half;
+        const float a = __shfl(v, f, 64), b = __shfl(v, f + half, 64);
+        if (i < qk) v = i < half ? __builtin_fmaf(-u.rs, b, u.rc * a) : __builtin_fmaf(u.rs, a, u.rc * b);
+    }
+    return v;
+}
+
 // Blocks 0 .. t-1: row i's units, one wavefront per unit (q heads, k heads,
 // v heads; step.rs:481-556, chunk.rs:202-253), lane = element: the causal
 // conv over the row and the pre-tap rows before it (fma from the newest
@@ -1018,55 +1091,35 @@ __device__ __forceinline__ void post_gates(float* p, const LayerDev& L, int lane
 // of the same feed are read from the projection, earlier ones from the
 // history ring; the row's pre-tap values go to the ring at a slot no row of
 // the feed reads.  Blocks t .. 2t-1: the row's post gates.
+template <int TAPS, bool EXACT>
 __global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, LayerDev L, int layer, int p0, int t) {
-    const int unit = threadIdx.x >> 6, i = threadIdx.x & 63;
+    const int unit = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), i = threadIdx.x & 63;
     if ((int)blockIdx.x >= t) {
         if (unit == 0) post_gates(S.p + (size_t)(blockIdx.x - t) * 64, L, i);
         return;
     }
     const int row = blockIdx.x, pos = p0 + row;
     const int nh = D.nh, nkv = D.nkv, qk = D.qk, vd = D.vd;
-    const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd, W = D.W;
-    int start, cw, cc, len;
-    const uint16_t* w;
-    if (unit < nh) {
-        start = unit * qk, cw = qd, cc = unit * qk, w = L.q_taps, len = qk;
-    } else if (unit < nh + nkv) {
-        const int kh = unit - nh;
-        start = qd + kh * qk, cw = kd, cc = kh * qk, w = L.k_taps, len = qk;
+    const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd;
+    // the unit's inputs (wave-uniform branches, each with constant argument
+    // fields); waves past the units load the last v unit's and ignore them
+    const int uu = min(unit, nh + 2 * nkv - 1);
+    int start, len;
+    UnitIn u;
+    if (uu < nh) {
+        start = uu * qk, len = qk;
+        u = unit_load<TAPS, EXACT>(D, S, layer, pos, row, start, qd, uu * qk, qk, L.q_taps, L.q_norm, i);
+    } else if (uu < nh + nkv) {
+        const int kh = uu - nh;
+        start = qd + kh * qk, len = qk;
+        u = unit_load<TAPS, EXACT>(D, S, layer, pos, row, start, kd, kh * qk, qk, L.k_taps, L.k_norm, i);
     } else {
-        const int vh = unit - nh - nkv;
-        start = qd + kd + vh * vd, cw = vdim, cc = vh * vd, w = L.v_taps, len = vd;
+        const int vh = uu - nh - nkv;
+        start = qd + kd + vh * vd, len = vd;
+        u = unit_load<TAPS, EXACT>(D, S, layer, pos, row, start, vdim, vh * vd, vd, L.v_taps, L.k_norm, i);
     }
-    float* hist = S.hist + (size_t)layer * D.hist_slots * W;
-    float v = 0.0f;
-    if (i < len) {
-        const float cur = S.proj[(size_t)row * D.nq + start + i];
-        v = h2f(w[cc + i]) * cur;
-        for (int j = 1; j < D.taps; ++j) {
-            const float wj = h2f(w[(size_t)j * cw + cc + i]);
-            float rr = 0.0f;
-            if (pos >= j)
-                rr = j <= row ? S.proj[(size_t)(row - j) * D.nq + start + i]
-                              : hist[(size_t)((pos - j) % D.hist_slots) * W + start + i];
-            v = __builtin_fmaf(wj, rr, v);
-        }
-        hist[(size_t)(pos % D.hist_slots) * W + start + i] = cur;
-    }
-    if (unit < nh + nkv) {
-        const float ss = dot16_lanes(v, qk, i);
-        const float r = rinv(ss, qk);
-        if (i < qk) {
-            const float tt = v * r;
-            v = __builtin_fmaf(tt, h2f((unit < nh ? L.q_norm : L.k_norm)[i]), tt);
-        }
-        const int half = qk / 2, f = i < half ? i : i - half;
-        const float a = __shfl(v, f, 64), b = __shfl(v, f + half, 64);
-        if (i < qk) {
-            const float cs = S.rope_c[row * half + f], sn = S.rope_s[row * half + f];
-            v = i < half ? __builtin_fmaf(-sn, b, cs * a) : __builtin_fmaf(sn, a, cs * b);
-        }
-    }
+    if (unit >= nh + 2 * nkv) return;
+    const float v = unit_finish<TAPS, EXACT>(D, S, layer, pos, start, len, u, unit < nh + nkv, i, true);
     if (unit < nh) {
         if (i < qk) S.qbuf[(size_t)row * qd + start + i] = v;
     } else {
@@ -1087,7 +1140,16 @@ __global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, Lay
 
 hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, hipStream_t s) {
     const int units = D.nh + 2 * D.nkv;
-    hipLaunchKernelGGL(k_units, dim3(2 * t), dim3(units * 64), 0, s, D, S, L, layer, p0, t);
+    switch (D.taps) {
+#define NH_UNITS(TP, EX) \
+    hipLaunchKernelGGL((k_units<TP, EX>), dim3(2 * t), dim3(units * 64), 0, s, D, S, L, layer, p0, t)
+        case 1: NH_UNITS(1, true); break;
+        case 2: NH_UNITS(2, true); break;
+        case 3: NH_UNITS(3, true); break;
+        case 4: NH_UNITS(4, true); break;
+        default: NH_UNITS(DG_MAX_TAPS, false);
+#undef NH_UNITS
+    }
     return hipGetLastError();
 }
 
@@ -1386,79 +1448,9 @@ hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int 
 // the block.  One more block computes the row's post gates.
 constexpr int DG_HEAD_T = 256;
 
-constexpr int DG_MAX_TAPS = 8;                   // conv taps the decode-attention launch takes
 constexpr int DG_PITCH = ATT_CHUNK_MAX + 8;      // value / digit row: 3 alignment bytes + 256 slots + dword tail
 constexpr int DG_KPITCH = MAX_HEAD_DIM + 16;     // key row (80 bytes: 8 rows cover the 32 banks)
 constexpr int DG_VDW = (ATT_CHUNK_MAX + 3 + 3) / 4;  // value dwords per column (alignment offset + slots)
-
-// A unit's inputs for lane i: the pre-tap row value, the taps, the kept
-// history rows of the ring, and (normed units) the norm scale and RoPE row.
-// Loaded before the key / value stream, so waiting for them does not wait
-// for it.
-struct UnitIn {
-    float cur, rc, rs;
-    uint16_t nrm;
-    uint16_t w[DG_MAX_TAPS];
-    float h[DG_MAX_TAPS];
-};
-
-// Every load is unconditional (lanes, taps and history rows past the
-// ranges read a clamped in-range address; `norm` is read for every unit,
-// used by the normed ones) and raw, so all of them issue before the first
-// wait.
-template <int TAPS, bool EXACT>
-__device__ __forceinline__ UnitIn unit_load(const Dims& D, const SessDev& S, int layer, int p0, int start, int cw,
-                                            int cc, int len, const uint16_t* w, const uint16_t* norm, int i) {
-    const float* hist = S.hist + (size_t)layer * D.hist_slots * D.W;
-    const int ii = i < len ? i : 0;
-    UnitIn u{};
-    u.cur = S.proj[start + ii];
-#pragma unroll
-    for (int j = 0; j < TAPS; ++j) {
-        const int jj = EXACT || j < D.taps ? j : D.taps - 1;
-        u.w[j] = w[(size_t)jj * cw + cc + ii];
-        if (j > 0) {
-            const int pj = p0 >= jj ? p0 - jj : 0;
-            u.h[j] = hist[(size_t)(pj % D.hist_slots) * D.W + start + ii];
-        }
-    }
-    {
-        const int qi = i < D.qk ? i : 0, half = D.qk / 2, f = qi < half ? qi : qi - half;
-        u.nrm = norm[qi];
-        u.rc = S.rope_c[f];
-        u.rs = S.rope_s[f];
-    }
-    return u;
-}
-
-// The unit's post-tap value (zcn16 and RoPE when `normed`): the causal conv
-// over the row and the kept history rows, v = w0 cur, then
-// fma(w_j, row_{p0 - j}, v) (a row before position 0 is zero).
-template <int TAPS, bool EXACT>
-__device__ __forceinline__ float unit_finish(const Dims& D, const SessDev& S, int layer, int p0, int start, int len,
-                                             const UnitIn& u, bool normed, int i, bool write_hist) {
-    float v = 0.0f;
-    if (i < len) {
-        v = h2f(u.w[0]) * u.cur;
-#pragma unroll
-        for (int j = 1; j < TAPS; ++j)
-            if (EXACT || j < D.taps) v = __builtin_fmaf(h2f(u.w[j]), p0 >= j ? u.h[j] : 0.0f, v);
-        if (write_hist) S.hist[((size_t)layer * D.hist_slots + p0 % D.hist_slots) * D.W + start + i] = u.cur;
-    }
-    if (normed) {
-        const int qk = D.qk;
-        const float ss = dot16_lanes(v, qk, i);
-        const float r = rinv(ss, qk);
-        if (i < qk) {
-            const float tt = v * r;
-            v = __builtin_fmaf(tt, h2f(u.nrm), tt);
-        }
-        const int half = qk / 2, f = i < half ? i : i - half;
-        const float a = __shfl(v, f, 64), b = __shfl(v, f + half, 64);
-        if (i < qk) v = i < half ? __builtin_fmaf(-u.rs, b, u.rc * a) : __builtin_fmaf(u.rs, a, u.rc * b);
-    }
-    return v;
-}
 
 template <int HP, int TAPS, bool EXACT>
 __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S, LayerDev L, int layer, int p0,
@@ -1499,12 +1491,12 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
     const int role = __builtin_amdgcn_readfirstlane(wave < HP ? 0 : wave - HP + 1);  // 0 q, 1 k, 2 v, 3+ none
     UnitIn ui;
     if (role == 0)
-        ui = unit_load<TAPS, EXACT>(D, S, layer, p0, (hh0 + wave) * qk, qd, (hh0 + wave) * qk, qk, L.q_taps, L.q_norm,
-                                    lane);
+        ui = unit_load<TAPS, EXACT>(D, S, layer, p0, 0, (hh0 + wave) * qk, qd, (hh0 + wave) * qk, qk, L.q_taps,
+                                    L.q_norm, lane);
     else if (role == 1)
-        ui = unit_load<TAPS, EXACT>(D, S, layer, p0, qd + kvh * qk, kd, kvh * qk, qk, L.k_taps, L.k_norm, lane);
+        ui = unit_load<TAPS, EXACT>(D, S, layer, p0, 0, qd + kvh * qk, kd, kvh * qk, qk, L.k_taps, L.k_norm, lane);
     else
-        ui = unit_load<TAPS, EXACT>(D, S, layer, p0, qd + kd + kvh * vd, vdim, kvh * vd, vd, L.v_taps, L.k_norm,
+        ui = unit_load<TAPS, EXACT>(D, S, layer, p0, 0, qd + kd + kvh * vd, vdim, kvh * vd, vd, L.v_taps, L.k_norm,
                                     lane);
     // The keys before the position: int8 rows (16-byte chunks), scales and
     // value dwords, all in flight at once, stored to LDS after the units.
