@@ -9,6 +9,7 @@
 // Wavefront reductions of the device library (DPP sequences).
 extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
 extern "C" __device__ __attribute__((const)) int __ockl_wfred_add_i32(int);
+extern "C" __device__ __attribute__((const)) int __ockl_wfred_min_i32(int);
 
 namespace nh {
 

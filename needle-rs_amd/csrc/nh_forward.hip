@@ -1765,40 +1765,43 @@ hipError_t fwd_dec_attn(const Dims& D, const SessDev& S, const LayerDev& L, int 
 
 // ----------------------------------------------------------------- argmax
 // argmax (crates/needle-engine/src/generate.rs:42-50): the first maximum.
+// Each thread keeps the first maximum of its strided share (all its loads
+// issued first); a wavefront's first maximum is the smallest index among
+// the lanes holding the wavefront's maximum (two DPP reductions), and the
+// same again over the wavefronts' results.
 __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, uint32_t* __restrict__ dst) {
+    constexpr int PER = 16;  // elements per thread read in one batch
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     float best = -__builtin_inff();
     int bi = n;
-    for (int i = t; i < n; i += 1024) {
-        const float v = x[i];
-        if (bi == n || v > best) {
-            best = v;
-            bi = i;
-        }
-    }
+    for (int base = 0; base < n; base += 1024 * PER) {
+        float v[PER];
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const float ov = __shfl_xor(best, o, 64);
-        const int oi = __shfl_xor(bi, o, 64);
-        if (oi < n && (bi == n || ov > best || (ov == best && oi < bi))) {
-            best = ov;
-            bi = oi;
+        for (int k = 0; k < PER; ++k) v[k] = x[min(base + k * 1024 + t, n - 1)];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = base + k * 1024 + t;
+            if (i < n && (bi == n || v[k] > best)) {
+                best = v[k];
+                bi = i;
+            }
         }
     }
+    const float wm = wave_max(best);
+    const int wi = __ockl_wfred_min_i32(best == wm && bi < n ? bi : 0x7fffffff);
     __shared__ float sv[16];
     __shared__ int si[16];
     if (lane == 0) {
-        sv[wave] = best;
-        si[wave] = bi;
+        sv[wave] = wm;
+        si[wave] = wi;
     }
     __syncthreads();
-    if (t == 0) {
-        for (int w = 1; w < 16; ++w)
-            if (si[w] < n && (bi == n || sv[w] > best || (sv[w] == best && si[w] < bi))) {
-                best = sv[w];
-                bi = si[w];
-            }
-        dst[0] = (uint32_t)(bi < n ? bi : 0);
+    if (wave == 0) {
+        const float v = lane < 16 && si[min(lane, 15)] != 0x7fffffff ? sv[min(lane, 15)] : -__builtin_inff();
+        const int ix = lane < 16 ? si[min(lane, 15)] : 0x7fffffff;
+        const float m = wave_max(v);
+        const int first = __ockl_wfred_min_i32(v == m && ix != 0x7fffffff ? ix : 0x7fffffff);
+        if (lane == 0) dst[0] = (uint32_t)(first < n ? first : 0);
     }
 }
 
