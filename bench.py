@@ -109,9 +109,10 @@ def gpu_gemv(args, nh, torch):
 
 
 def gpu_gemv_steady(gpu, copies, nh, torch):
-    """The same GEMV kernel over the copies fused by row (one launch reads
+    """The decode GEMV over the copies fused by row (one launch reads
     copies * 8.7 MB), so the fixed per-dispatch cost is amortised: the
-    kernel's streaming rate."""
+    streaming rate (at this height the product runs as its persistent
+    streaming grid)."""
     import numpy as np
 
     nbig = N * copies
@@ -126,8 +127,9 @@ def gpu_gemv_steady(gpu, copies, nh, torch):
     ms = time_graph(sweep, 20, 2, torch) / 8
     nbytes = algorithmic_bytes(1, K, nbig)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"workload": f"one launch of the same decode GEMV over N={nbig} rows (the {copies} copies fused by row), "
-                        f"K={K}", "us_per_launch": round(ms * 1e3, 3), "bytes_per_launch": nbytes,
+    return {"workload": f"one launch of the decode GEMV (its persistent streaming grid) over N={nbig} rows (the "
+                        f"{copies} copies fused by row), K={K}", "us_per_launch": round(ms * 1e3, 3),
+            "bytes_per_launch": nbytes,
             "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 

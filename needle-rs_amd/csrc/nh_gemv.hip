@@ -24,6 +24,10 @@
 
 namespace nh {
 
+// Workgroups per CU of the streaming variant, and the tile count from which
+// it replaces one workgroup per tile (8 tiles per workgroup).
+constexpr int STREAM_WG_PER_CU = 4;
+
 template <int GPS, int S, int BITS, bool DBG>
 __device__ __forceinline__ void gemv_tile(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
                                           const uint4* __restrict__ xq, const float* __restrict__ sx,
@@ -114,11 +118,85 @@ __global__ __launch_bounds__(S * 64) void k_gemv_batch(GemvBatch b, int out, int
                                    blockIdx.x);
 }
 
+// The same product for very tall matrices (4-bit): a persistent grid of a
+// few workgroups per CU, each staging the token's activations once and
+// walking tiles blockIdx.x, + gridDim.x, ...; a tile's codes and norms are
+// loaded while the previous tile combines (two tiles per loop turn, so the
+// register buffers alternate statically; the combine slots alternate too,
+// so one barrier per tile suffices).
+template <int GPS, int S>
+__global__ __launch_bounds__(S * 64) void k_gemv_stream(const uint4* __restrict__ codes,
+                                                        const uint16_t* __restrict__ norms,
+                                                        const uint4* __restrict__ xq, const float* __restrict__ sx,
+                                                        float* __restrict__ y, int out, int G, float cbs, Lut lut,
+                                                        int tiles) {
+    static_assert(S * 64 >= GPS * S * 8, "one thread per activation uint4");
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane >> 2, l = lane & 3;
+    const int g0 = wave * GPS;
+    __shared__ uint4 xs[GPS * S * 8];
+    __shared__ float2 part[2][GPS * S][64];
+    if ((int)threadIdx.x < G * 8) xs[threadIdx.x] = xq[threadIdx.x];
+    float sxc[GPS];
+#pragma unroll
+    for (int j = 0; j < GPS; ++j) sxc[j] = sx[g0 + j < G ? g0 + j : 0] * cbs;
+    struct Tile {
+        uint4 c[GPS];
+        uint16_t nb[GPS];
+    };
+    auto load = [&](Tile& b, int tile) __attribute__((always_inline)) {
+        const int tl = tile < tiles ? tile : tiles - 1;  // past the end: reload the last tile, never stored
+#pragma unroll
+        for (int j = 0; j < GPS; ++j) {
+            const int g = g0 + j < G ? g0 + j : 0;
+            b.c[j] = load_stream(codes + ((size_t)(tl * G + g) * 64 + lane));
+            b.nb[j] = norms[(size_t)(tl * TILE_ROWS + r) * G + g];
+        }
+    };
+    auto combine = [&](const Tile& b, int tile, int slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < GPS; ++j) {
+            const int g = g0 + j < G ? g0 + j : 0;
+            const uint4* xp = xs + (g * 4 + l) * 2;
+            const float lf = (float)dot_chunk(b.c[j], xp[0], xp[1], lut);
+            part[slot][g0 + j][lane] = make_float2(lf, sxc[j] * f16_bits_to_f32(b.nb[j]));
+        }
+        __syncthreads();
+        if (wave == 0 && tile < tiles) {
+            float acc = 0.0f;
+            for (int g = 0; g < G; ++g) {
+                const float2 p = part[slot][g][lane];
+                acc = __builtin_fmaf(p.x, p.y, acc);
+            }
+            // (l0 + l1) + (l2 + l3) across the row's four lanes.
+            const float t = acc + quad_xor1(acc);
+            const float u = t + quad_xor2(t);
+            const int n = tile * TILE_ROWS + r;
+            if (l == 0 && n < out) y[n] = u;
+        }
+    };
+    Tile ta, tb;
+    load(ta, blockIdx.x);
+    __syncthreads();  // the activations
+    const int step = gridDim.x;
+    for (int tile = blockIdx.x; tile < tiles; tile += 2 * step) {
+        load(tb, tile + step);
+        combine(ta, tile, 0);
+        load(ta, tile + 2 * step);
+        combine(tb, tile + step, 1);
+    }
+}
+
 template <int GPS, int S, int BITS>
 static hipError_t run(const nh_qmat* w, const nh_qact* a, float* y, int32_t* dbg, hipStream_t s) {
     const QMatMeta& m = w->m;
     const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
     dim3 grid(m.out_pad / TILE_ROWS), block(S * 64);
+    const int tiles = m.out_pad / TILE_ROWS, slots = device_cus() * STREAM_WG_PER_CU;
+    if (BITS == 4 && !dbg && tiles >= 8 * slots) {
+        hipLaunchKernelGGL((k_gemv_stream<GPS, S>), dim3(slots), block, 0, s, (const uint4*)w->d_codes, w->d_norms,
+                           (const uint4*)a->d_xq, a->d_sx, y, m.out, m.groups, m.cbs, lut, tiles);
+        return hipGetLastError();
+    }
     if (dbg)
         hipLaunchKernelGGL((k_gemv<GPS, S, BITS, true>), grid, block, 0, s, w->d_codes, w->d_norms,
                            (const uint4*)a->d_xq, a->d_sx, y, dbg, m.out, m.groups, m.cbs, lut);

@@ -133,6 +133,21 @@ def test_gemv_c1_full_size(nh):
     assert np.all(np.abs(y[i] - approx) < 0.02 * (1 + np.abs(approx)))
 
 
+@pytest.mark.parametrize("K", [256, 768])
+def test_gemv_tall_streaming(nh, K):
+    # Past 8 tiles per resident workgroup (8192 16-row tiles on 256 CUs) the
+    # decode GEMV runs as a persistent streaming grid; rows not a multiple
+    # of 16.
+    N = 131112
+    say(f"gemv streaming K={K} N={N}")
+    w, x = seeded(N, K, 1, seed=3)
+    q, oq = pair(nh, w, N, K)
+    a = nh.QAct.new(dev(x), 1, K)
+    y = q.matmul(a).cpu().numpy()[0]
+    want = oq.matmul(o.OQAct.new(x, 1, K))[0]
+    assert bits_equal(y, want), report(y, want)
+
+
 C2 = [(M, K, N) for M in (64, 256, 1024) for (K, N) in ((768, 2304), (768, 3072), (3072, 768))]
 
 
