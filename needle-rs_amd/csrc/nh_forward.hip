@@ -278,6 +278,8 @@ namespace {
 
 constexpr int BT_STRIDE = HADA_NB + 2;  // padded (even: 8-byte reads) row of a transposed mix8 output
 constexpr int MIX_T = 256;              // threads of one mix8 (a 2 x 2 output block each)
+constexpr int MIX_STEPS = 4;            // j steps per pipelined batch of a mix8 pass (one 16-byte factor read)
+constexpr int KP_PITCH = HADA_NB + 4;   // dwords per pair row of a staged factor (16-byte reads, 2-way banks)
 // Transposed copies for the serial chains, so a chain lane reads its
 // operands as contiguous 16-byte vectors: a dot16 operand x[16 c + l] at
 // l * pitch + c (pitch TP_D for d-long vectors, TP_X for the 4 lanes);
@@ -295,7 +297,7 @@ struct LayerShared {
     alignas(16) float A[HADA_N];
     alignas(16) float B[HADA_NB * BT_STRIDE];
     alignas(16) float C[HADA_N];
-    alignas(16) float kron[6][HADA_N];
+    alignas(16) uint32_t kp[6][HADA_NB / 2 * KP_PITCH];  // Kronecker factors as f16 pairs, pair-major
     alignas(16) int8_t nx8[MHC_LANES * FWD_MAX_D];
     alignas(16) uint16_t cvT[4 * COND_RANK * TP_C];
     alignas(16) uint16_t cond_u[COND_RANK * HADA_N];
@@ -310,43 +312,91 @@ struct LayerShared {
     int mix_count;  // the mixer wavefronts' arrivals (mixer_sync)
 };
 
+// chain_pipe for a fixed batch count, fully unrolled (batch indices are
+// constants, so register arrays indexed by them stay in registers).
+template <int NB, int DEPTH, typename Buf, typename Load, typename Chain>
+__device__ __forceinline__ void chain_pipe_n(Load load, Chain chain) {
+    Buf buf[DEPTH];
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1 && i < NB; ++i) load(buf[i], i);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        if (b + DEPTH - 1 < NB) load(buf[(b + DEPTH - 1) % DEPTH], b + DEPTH - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        chain(buf[b % DEPTH], b);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
 // mix8 (infer.rs:2343-2380), portable branch: out[r][c] =
 // sum_j ct[j][r] * rows[j][c], each output an fma chain from j = 0.  Thread
 // u < 256 computes the 2 x 2 block r = 2 (u / 16) + {0, 1}, c = 2 (u % 16) +
-// {0, 1}, so each step reads two ct values and two row values (8-byte
-// reads) for four fmas.
+// {0, 1}.  The factor operand is read from its pair-major f16 copy (kp[p]
+// [j] = the factor's elements [j][2p], [j][2p + 1], p = the thread's pair):
+// one 16-byte read per MIX_STEPS steps, beside one 8-byte read of the
+// vector operand per step, for four fmas a step.
 // Transposed (ct = a factor, rows = [32][32]): stored at out[c * BT_STRIDE + r].
-__device__ __forceinline__ void mix8_t(int u, const float* ct, const float* rows, float* out) {
+__device__ __forceinline__ void mix8_t(int u, const uint32_t* kp, const float* rows, float* out) {
     const int r = (u >> 4) * 2, c = (u & 15) * 2;
+    const uint4* fr = reinterpret_cast<const uint4*>(kp + (u >> 4) * KP_PITCH);
     float o00 = 0.0f, o01 = 0.0f, o10 = 0.0f, o11 = 0.0f;
+    struct Buf {
+        uint4 f;
+        float2 v[MIX_STEPS];
+    };
+    auto load = [&](Buf& d, int b) {
+        d.f = fr[b];
 #pragma unroll
-    for (int j = 0; j < HADA_NB; ++j) {
-        const float2 a = *reinterpret_cast<const float2*>(ct + j * HADA_NB + r);
-        const float2 b = *reinterpret_cast<const float2*>(rows + j * HADA_NB + c);
-        o00 = __builtin_fmaf(a.x, b.x, o00);
-        o01 = __builtin_fmaf(a.x, b.y, o01);
-        o10 = __builtin_fmaf(a.y, b.x, o10);
-        o11 = __builtin_fmaf(a.y, b.y, o11);
-    }
+        for (int i = 0; i < MIX_STEPS; ++i)
+            d.v[i] = *reinterpret_cast<const float2*>(rows + (b * MIX_STEPS + i) * HADA_NB + c);
+    };
+    auto chain = [&](const Buf& d, int) {
+        const uint32_t fw[4] = {d.f.x, d.f.y, d.f.z, d.f.w};
+#pragma unroll
+        for (int i = 0; i < MIX_STEPS; ++i) {
+            const float ax = h2f((uint16_t)(fw[i] & 0xffffu)), ay = h2f((uint16_t)(fw[i] >> 16));
+            const float2 b = d.v[i];
+            o00 = __builtin_fmaf(ax, b.x, o00);
+            o01 = __builtin_fmaf(ax, b.y, o01);
+            o10 = __builtin_fmaf(ay, b.x, o10);
+            o11 = __builtin_fmaf(ay, b.y, o11);
+        }
+    };
+    chain_pipe_n<HADA_NB / MIX_STEPS, 3, Buf>(load, chain);
     *reinterpret_cast<float2*>(out + c * BT_STRIDE + r) = make_float2(o00, o10);
     *reinterpret_cast<float2*>(out + (c + 1) * BT_STRIDE + r) = make_float2(o01, o11);
 }
 
 // Plain (ct = the output of mix8_t, rows = a factor): out[r][c], rows
 // r < rows_limit (a multiple of 2).
-__device__ __forceinline__ void mix8_n(int u, const float* ct, const float* rows, float* out, int rows_limit) {
+__device__ __forceinline__ void mix8_n(int u, const float* ct, const uint32_t* kp, float* out, int rows_limit) {
     const int r = (u >> 4) * 2, c = (u & 15) * 2;
     if (r >= rows_limit) return;
+    const uint4* fr = reinterpret_cast<const uint4*>(kp + (u & 15) * KP_PITCH);
     float o00 = 0.0f, o01 = 0.0f, o10 = 0.0f, o11 = 0.0f;
+    struct Buf {
+        uint4 f;
+        float2 v[MIX_STEPS];
+    };
+    auto load = [&](Buf& d, int b) {
+        d.f = fr[b];
 #pragma unroll
-    for (int j = 0; j < HADA_NB; ++j) {
-        const float2 a = *reinterpret_cast<const float2*>(ct + j * BT_STRIDE + r);
-        const float2 b = *reinterpret_cast<const float2*>(rows + j * HADA_NB + c);
-        o00 = __builtin_fmaf(a.x, b.x, o00);
-        o01 = __builtin_fmaf(a.x, b.y, o01);
-        o10 = __builtin_fmaf(a.y, b.x, o10);
-        o11 = __builtin_fmaf(a.y, b.y, o11);
-    }
+        for (int i = 0; i < MIX_STEPS; ++i)
+            d.v[i] = *reinterpret_cast<const float2*>(ct + (b * MIX_STEPS + i) * BT_STRIDE + r);
+    };
+    auto chain = [&](const Buf& d, int) {
+        const uint32_t fw[4] = {d.f.x, d.f.y, d.f.z, d.f.w};
+#pragma unroll
+        for (int i = 0; i < MIX_STEPS; ++i) {
+            const float2 a = d.v[i];
+            const float bx = h2f((uint16_t)(fw[i] & 0xffffu)), by = h2f((uint16_t)(fw[i] >> 16));
+            o00 = __builtin_fmaf(a.x, bx, o00);
+            o01 = __builtin_fmaf(a.x, by, o01);
+            o10 = __builtin_fmaf(a.y, bx, o10);
+            o11 = __builtin_fmaf(a.y, by, o11);
+        }
+    };
+    chain_pipe_n<HADA_NB / MIX_STEPS, 3, Buf>(load, chain);
     *reinterpret_cast<float2*>(out + r * HADA_NB + c) = make_float2(o00, o01);
     *reinterpret_cast<float2*>(out + (r + 1) * HADA_NB + c) = make_float2(o10, o11);
 }
@@ -354,13 +404,41 @@ __device__ __forceinline__ void mix8_n(int u, const float* ct, const float* rows
 // Element i of a dot16 operand into its transposed copy.
 __device__ __forceinline__ void put_t(float* T, int pitch, int i, float v) { T[(i & 15) * pitch + (i >> 4)] = v; }
 
+// A dependent fma chain over nb batches read from LDS: a ring of DEPTH
+// batch buffers, batch b + DEPTH - 1's reads issued before batch b's fmas;
+// scheduling barriers keep the compiler from sinking the reads back to
+// their use (which would leave every batch waiting a full LDS round trip).
+// Reads past the last batch are clamped to it (read and ignored).  A chain
+// step costs ~13 cycles (the dependent fma's latency) at any depth from 3
+// up, so 3 is used.  Requires nb >= 1.
+template <int DEPTH, typename Buf, typename Load, typename Chain>
+__device__ __forceinline__ void chain_pipe(int nb, Load load, Chain chain) {
+    Buf buf[DEPTH];
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i) load(buf[i], min(i, nb - 1));
+    int b = 0;
+    for (; b + DEPTH <= nb; b += DEPTH) {
+#pragma unroll
+        for (int i = 0; i < DEPTH; ++i) {
+            load(buf[(i + DEPTH - 1) % DEPTH], min(b + i + DEPTH - 1, nb - 1));
+            __builtin_amdgcn_sched_barrier(0);
+            chain(buf[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < DEPTH - 1; ++i)
+        if (b + i < nb) chain(buf[i]);
+    if (b + DEPTH - 1 < nb) {
+        load(buf[DEPTH - 1], b + DEPTH - 1);
+        chain(buf[DEPTH - 1]);
+    }
+}
+
 // dot16 over operands held transposed (x[16 c + l] at xT[l * pitch + c]),
 // the same chains and combine as the reference's dot16: lane l < 16
-// carries accumulator l over c in order.  The chain is a 3-stage pipeline of
-// 8-step batches (two 16-byte reads per operand): batch b + 2's reads issue
-// before batch b's fmas, and scheduling barriers keep the compiler from
-// sinking them back to their use (which would leave every batch waiting a
-// full LDS round trip).
+// carries accumulator l over c in order, in 8-step batches (two 16-byte
+// reads per operand) on chain_pipe.
 template <bool SELF>
 __device__ __forceinline__ float dot16_t(const float* xT, const float* yT, int pitch, int n, int lane) {
     float a = 0.0f;
@@ -368,51 +446,33 @@ __device__ __forceinline__ float dot16_t(const float* xT, const float* yT, int p
         const int chunks = n / 16, nb = chunks / 8;
         const float4* xr = reinterpret_cast<const float4*>(xT + lane * pitch);
         const float4* yr = reinterpret_cast<const float4*>(yT + lane * pitch);
-        float4 x0[2], x1[2], x2[2], y0[2], y1[2], y2[2];
-        auto load = [&](float4* xd, float4* yd, int b) {
-            const int c = min(b, nb - 1) * 2;
-            xd[0] = xr[c];
-            xd[1] = xr[c + 1];
-            if (!SELF) {
-                yd[0] = yr[c];
-                yd[1] = yr[c + 1];
+        struct Buf {
+            float4 x[2], y[SELF ? 1 : 2];
+        };
+        auto load = [&](Buf& d, int b) {
+            d.x[0] = xr[2 * b];
+            d.x[1] = xr[2 * b + 1];
+            if constexpr (!SELF) {
+                d.y[0] = yr[2 * b];
+                d.y[1] = yr[2 * b + 1];
             }
         };
-        auto chain = [&](const float4* xd, const float4* yd) {
+        auto chain = [&](const Buf& d) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const float4 x = xd[u], y = SELF ? xd[u] : yd[u];
+                const float4 x = d.x[u];
+                float4 y;
+                if constexpr (SELF)
+                    y = x;
+                else
+                    y = d.y[u];
                 a = __builtin_fmaf(x.x, y.x, a);
                 a = __builtin_fmaf(x.y, y.y, a);
                 a = __builtin_fmaf(x.z, y.z, a);
                 a = __builtin_fmaf(x.w, y.w, a);
             }
         };
-        if (nb > 0) {
-            load(x0, y0, 0);
-            load(x1, y1, 1);
-        }
-        int b = 0;
-        for (; b + 3 <= nb; b += 3) {
-            load(x2, y2, b + 2);
-            __builtin_amdgcn_sched_barrier(0);
-            chain(x0, y0);
-            __builtin_amdgcn_sched_barrier(0);
-            load(x0, y0, b + 3);
-            __builtin_amdgcn_sched_barrier(0);
-            chain(x1, y1);
-            __builtin_amdgcn_sched_barrier(0);
-            load(x1, y1, b + 4);
-            __builtin_amdgcn_sched_barrier(0);
-            chain(x2, y2);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (b < nb) chain(x0, y0);
-        if (b + 1 < nb) chain(x1, y1);
-        if (b + 2 < nb) {
-            load(x2, y2, b + 2);
-            chain(x2, y2);
-        }
+        if (nb > 0) chain_pipe<3, Buf>(nb, load, chain);
         const float* xs = xT + lane * pitch;
         const float* ys = yT + lane * pitch;
         for (int c = nb * 8; c < chunks; ++c) a = __builtin_fmaf(xs[c], ys[c], a);
@@ -503,18 +563,12 @@ __device__ __forceinline__ void store_out(const Dims& D, const OutRegs& q, Layer
     for (int r = 0; r < STAGE_PER; ++r) {
         const int e = t + r * LT;
         if (e < kron_n) {
-            // 8 f16 -> 8 f32 (exact)
+            // 8 f16 of factor row j: pairs 4 (e % 4) + k, stored pair-major
+            const int i = e / (HADA_N / 8), ee = e % (HADA_N / 8), j = ee >> 2, p0 = (ee & 3) * 4;
             const uint4 v = q.st[r];
-            float* dst = sh.kron[e / (HADA_N / 8)] + (e % (HADA_N / 8)) * 8;
             const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-            float f[8];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                f[2 * k] = h2f((uint16_t)(w[k] & 0xffffu));
-                f[2 * k + 1] = h2f((uint16_t)(w[k] >> 16));
-            }
-            *reinterpret_cast<float4*>(dst) = make_float4(f[0], f[1], f[2], f[3]);
-            *reinterpret_cast<float4*>(dst + 4) = make_float4(f[4], f[5], f[6], f[7]);
+            for (int k = 0; k < 4; ++k) sh.kp[i][(p0 + k) * KP_PITCH + j] = w[k];
         } else if (e < kron_n + cv_n) {
             // row j of cond_v (8 f16) into column j / 4 of rows 8 (j % 4) + k
             const int j = e - kron_n;
@@ -537,7 +591,7 @@ __device__ __forceinline__ void store_out(const Dims& D, const OutRegs& q, Layer
 // cond_weights (infer.rs:1640-1656) by wavefront 0: lane 8 jm + k carries
 // acc[jm][k] = fma(h2[j], cond_v[j][k], .) over j = jm, jm + 4, ...
 // (u = j / 4 in order), reading h2 and cond_v from their transposed copies
-// in 8-step batches, pipelined as dot16_t's chains; then the softmax of the
+// in 8-step batches on chain_pipe; then the softmax of the
 // combined logits.
 __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int lane, float* wk) {
     const int k = lane & 7, jm = lane >> 3;
@@ -546,48 +600,25 @@ __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int l
         const int steps = d / 4, nb = steps / 8;
         const float4* hr = reinterpret_cast<const float4*>(sh.hT + jm * TP_H);
         const uint4* cr = reinterpret_cast<const uint4*>(sh.cvT + (jm * COND_RANK + k) * TP_C);
-        float4 h0[2], h1[2], h2[2];
-        uint4 c0, c1, c2;
-        auto load = [&](float4* hd, uint4& cd, int bb) {
-            const int b = min(bb, nb - 1);
-            hd[0] = hr[2 * b];
-            hd[1] = hr[2 * b + 1];
-            cd = cr[b];
+        struct Buf {
+            float4 h[2];
+            uint4 c;
         };
-        auto chain = [&](const float4* hd, const uint4& cd) {
-            const float hv[8] = {hd[0].x, hd[0].y, hd[0].z, hd[0].w, hd[1].x, hd[1].y, hd[1].z, hd[1].w};
-            const uint32_t cw[4] = {cd.x, cd.y, cd.z, cd.w};
+        auto load = [&](Buf& d, int b) {
+            d.h[0] = hr[2 * b];
+            d.h[1] = hr[2 * b + 1];
+            d.c = cr[b];
+        };
+        auto chain = [&](const Buf& d) {
+            const float hv[8] = {d.h[0].x, d.h[0].y, d.h[0].z, d.h[0].w, d.h[1].x, d.h[1].y, d.h[1].z, d.h[1].w};
+            const uint32_t cw[4] = {d.c.x, d.c.y, d.c.z, d.c.w};
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 a = __builtin_fmaf(hv[2 * u], h2f((uint16_t)(cw[u] & 0xffffu)), a);
                 a = __builtin_fmaf(hv[2 * u + 1], h2f((uint16_t)(cw[u] >> 16)), a);
             }
         };
-        if (nb > 0) {
-            load(h0, c0, 0);
-            load(h1, c1, 1);
-        }
-        int b = 0;
-        for (; b + 3 <= nb; b += 3) {
-            load(h2, c2, b + 2);
-            __builtin_amdgcn_sched_barrier(0);
-            chain(h0, c0);
-            __builtin_amdgcn_sched_barrier(0);
-            load(h0, c0, b + 3);
-            __builtin_amdgcn_sched_barrier(0);
-            chain(h1, c1);
-            __builtin_amdgcn_sched_barrier(0);
-            load(h1, c1, b + 4);
-            __builtin_amdgcn_sched_barrier(0);
-            chain(h2, c2);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if (b < nb) chain(h0, c0);
-        if (b + 1 < nb) chain(h1, c1);
-        if (b + 2 < nb) {
-            load(h2, c2, b + 2);
-            chain(h2, c2);
-        }
+        if (nb > 0) chain_pipe<3, Buf>(nb, load, chain);
         for (int u = nb * 8; u < steps; ++u)
             a = __builtin_fmaf(sh.hT[jm * TP_H + u], h2f(sh.cvT[(jm * COND_RANK + k) * TP_C + u]), a);
     }
@@ -642,9 +673,9 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
     // mixers meet between their passes on their own
     if (wave == 0) cond_weights(sh, d, lane, sh.wk);
     if (mixer) {
-        mix8_t(mu, sh.kron[0], sh.A, sh.B);
+        mix8_t(mu, sh.kp[0], sh.A, sh.B);
         mixer_sync(&sh.mix_count, MIX_T / 64);
-        mix8_n(mu, sh.B, sh.kron[1], sh.C, HADA_NB);
+        mix8_n(mu, sh.B, sh.kp[1], sh.C, HADA_NB);
     }
     __syncthreads();
     {
@@ -656,15 +687,15 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
         sh.A[t] = zs;
     }
     __syncthreads();
-    if (mixer) mix8_t(mu, sh.kron[2], sh.A, sh.B);
+    if (mixer) mix8_t(mu, sh.kp[2], sh.A, sh.B);
     __syncthreads();
-    if (mixer) mix8_n(mu, sh.B, sh.kron[3], sh.C, HADA_NB);
+    if (mixer) mix8_n(mu, sh.B, sh.kp[3], sh.C, HADA_NB);
     __syncthreads();
     sh.A[t] = sh.C[q.p2] * h2f_late(q.d3);
     __syncthreads();
-    if (mixer) mix8_t(mu, sh.kron[4], sh.A, sh.B);
+    if (mixer) mix8_t(mu, sh.kp[4], sh.A, sh.B);
     __syncthreads();
-    if (mixer) mix8_n(mu, sh.B, sh.kron[5], sh.C, d / HADA_NB / 8 * 8);
+    if (mixer) mix8_n(mu, sh.B, sh.kp[5], sh.C, d / HADA_NB / 8 * 8);
     __syncthreads();
     // The mHC write: y = (x2 + t3 * d4) - u; lane a = y hpost[a] + sum_b
     // hres[a][b] old[b] as an fma chain over b.
