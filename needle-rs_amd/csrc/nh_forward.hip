@@ -746,20 +746,27 @@ __device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const
     const float* ep = site ? S.evals + (size_t)N.site * FWD_ROWS * d : S.proj + d;
     q.kr = kp[td];
     q.ev = ep[td];
-    // Phi8 rows: wavefront w >= 1 holds rows w - 1 and w + PHI_B - 1 (the
-    // second past the 24 rows is a clamped duplicate); wavefront 0, which
-    // runs the first chain of the MLP right after these loads are issued,
-    // holds none, so it never waits behind them in the CU's load queue.
-    if (__builtin_amdgcn_readfirstlane(wave) != 0) {
+    // Phi8 rows: wavefront w >= 1 holds row w - 1, and row w + PHI_B - 1
+    // while that is below 24; wavefront 0, which runs the first chain of the
+    // MLP right after these loads are issued, holds none, so it never waits
+    // behind them in the CU's load queue.  Issuing them takes the CU's
+    // address unit ~16 cycles per 1 KB load, so none is issued that is not
+    // used: chunk j only while the row has one (a wavefront-uniform test;
+    // registers of skipped chunks stay unset and unread).
+    const int wu = __builtin_amdgcn_readfirstlane(wave);
+    if (wu != 0) {
         const int per = nc / 16;  // uint4 per row
-        const int w0 = wave - 1, w1 = min(wave - 1 + PHI_B, MHC_COLS - 1);
+        const int w0 = wu - 1, w1 = min(wu - 1 + PHI_B, MHC_COLS - 1);
+        const bool two = wu - 1 + PHI_B < MHC_COLS;
         const uint4* row0 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)w0 * nc);
         const uint4* row1 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)w1 * nc);
 #pragma unroll
         for (int j = 0; j < PHI_CHUNKS; ++j) {
-            const int c = min(lane + 64 * j, per - 1);
-            q.r0[j] = row0[c];
-            q.r1[j] = row1[c];
+            if (64 * j < per) {
+                const int c = min(lane + 64 * j, per - 1);
+                q.r0[j] = row0[c];
+                if (two) q.r1[j] = row1[c];
+            }
         }
         q.ps0 = N.phi_s[w0];
         q.ps1 = N.phi_s[w1];
