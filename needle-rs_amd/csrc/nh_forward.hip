@@ -504,6 +504,18 @@ __device__ __forceinline__ float block_rinv_t(const float* xT, int pitch, int n,
     return *slot;
 }
 
+// The same value computed by every wavefront (each runs the 16-lane chain;
+// the result is wavefront-uniform and identical in all of them), so no
+// barrier hands it over.  The chain is latency-bound (~13 cycles a step),
+// so four wavefronts on a SIMD run their copies side by side at about the
+// cost of one for d-long operands (measured: 0.5 k cycles saved); for the
+// 4d-long mHC operand the sixteen copies' LDS reads cost more than the
+// barrier (0.7 k cycles lost), so that one stays on wavefront 0.  The phase
+// that follows must not write the operand.
+__device__ __forceinline__ float block_rinv_all(const float* xT, int pitch, int n) {
+    return rinv(dot16_t<true>(xT, xT, pitch, n, threadIdx.x & 63), n);
+}
+
 
 // The previous layer's inputs and weights a thread needs, read up front.
 // The LDS tables go out as one list of 16-byte chunks, up to STAGE_PER per
@@ -660,7 +672,7 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
     // h2 = zcn16(x2, pre_hada); z = h2 * d1 zero-padded to hada_n
     float h2 = 0.0f;
     {
-        const float r = block_rinv_t(sh.tB, TP_D, d, &sh.r_b);
+        const float r = block_rinv_all(sh.tB, TP_D, d);
         if (t < d) {
             const float tt = x2 * r;
             h2 = __builtin_fmaf(tt, h2f_late(q.ph), tt);
