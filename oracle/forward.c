@@ -6,9 +6,13 @@
  * TEST INFRASTRUCTURE: the parity checker (and CPU baseline) for a GPU
  * forward; nothing in the product links it.
  *
- * Scope: Model::step_native for one token with attend = None (no attention
- * span: every position keeps its own KV slot, slot_of(p) = p), Outputs =
- * logits, no cells, no rollback.
+ * Scope: Model::forward_native (infer.rs:1105-1132) over step_native and
+ * chunk_job with every Outputs mode (model.rs:150-160, chunk.rs:331-353),
+ * Model::prefill_native's stale-slot re-feed (infer.rs:1078-1101), the
+ * session attention span (sink, ring) with its KV slot ring and slot map
+ * (model.rs:62-66, infer.rs:1749-1826), Session::rollback / rewind_zeroed /
+ * clone (model.rs:81-121, infer.rs:1039-1071) and the head functions
+ * (infer.rs:1135-1166).  No cells.
  *
  * libm: off Apple targets the reference computes its f32 functions in f64
  * with the Rust `libm` crate (0.2.16, Cargo.lock:647-650) and rounds once
@@ -246,6 +250,8 @@ void nf_key_chunks(size_t n, size_t nkv, size_t* count, size_t* size) {
 }
 
 /* ------------------------------------------------------------------ model */
+/* (nf_engram_rows, nf_mhc_read, nf_post_gates and nf_mhc_write are defined
+ * after the model; nf_rows calls each of them once per row.) */
 
 struct nf_layer16 {
     uint16_t *kron[6], *cond_v, *cond_u, *d1, *d2, *b2, *d3, *d4, *norm_in, *post_norm, *pre_hada, *q_taps, *k_taps,
@@ -270,24 +276,41 @@ struct nf_model {
     int site_of_layer[64];
 };
 
+/* ROLLBACK (model.rs:181-183): the conv history and the RoPE list keep
+ * this many extra rows. */
+#define NF_ROLLBACK 32
+#define NF_KEY_RUNS 16 /* KEY_RUNS (infer.rs:1760) */
+
 struct nf_session {
     size_t cap;     /* positions */
     size_t len;     /* tokens fed */
     uint32_t* tokens;
-    /* per layer: k8 [pos][nkv][qk], ks [pos][nkv], v8t [nkv][vd][cap], vs [pos][nkv], hist [pos][width] (the
-     * pre-tap q|k|v row of every position) */
+    /* per layer, by KV slot: k8 [slot][nkv][qk], ks [slot][nkv], v8t [nkv][vd][cap], vs [slot][nkv] */
     int8_t** k8;
     float** ks;
     int8_t** v8t;
     float** vs;
+    /* per layer: the pre-tap q|k|v row of every position [pos][width]; of
+     * them LayerState::hist holds the last `hrows` (infer.rs:968-980): the
+     * conv reads a row only from there (newest last, trimmed as
+     * step.rs:706-712 and chunk.rs:319-329 trim it) */
     float** hist;
+    size_t hrows;
     /* engram value history per site: [pos][d] int8 + [pos][d/32] */
     int8_t** ev8;
     float** evs;
-    /* RoPE state of the newest position */
-    int rope_ok;
-    size_t rope_pos;
+    /* RoPE rows of every position fed [pos][32]; NatState::rope holds the
+     * last `rope_n` of them, ending at position len - 1 (infer.rs:1716-1747) */
     float *rope_c, *rope_s;
+    size_t rope_n;
+    /* Session::attend (model.rs:62-66): sink, ring (ring 0: None), and the
+     * slot map NatState::slot_pos (infer.rs:1000-1006) with its length */
+    size_t sink, ring;
+    int64_t* slot_pos;
+    size_t nslot;
+    /* NatState::last_hidden (infer.rs:996-998) */
+    float* last_hidden;
+    int have_hidden;
 };
 
 static uint16_t* dup16(const uint16_t* p, size_t n) {
@@ -432,8 +455,11 @@ nf_session* nf_session_new(const nf_model* m, size_t cap) {
         s->ev8[e] = (int8_t*)calloc(cap * c->d, 1);
         s->evs[e] = (float*)calloc(cap * (c->d / 32), sizeof(float));
     }
-    s->rope_c = (float*)calloc((size_t)c->qk / 2, sizeof(float));
-    s->rope_s = (float*)calloc((size_t)c->qk / 2, sizeof(float));
+    s->rope_c = (float*)calloc(cap * 32, sizeof(float));
+    s->rope_s = (float*)calloc(cap * 32, sizeof(float));
+    s->slot_pos = (int64_t*)malloc(cap * sizeof(int64_t));
+    for (size_t i = 0; i < cap; ++i) s->slot_pos[i] = -1;
+    s->last_hidden = (float*)calloc((size_t)c->d, sizeof(float));
     return s;
 }
 
@@ -442,22 +468,171 @@ void nf_session_free(const nf_model* m, nf_session* s) {
     for (int l = 0; l < m->c.layers; ++l) free(s->k8[l]), free(s->ks[l]), free(s->v8t[l]), free(s->vs[l]), free(s->hist[l]);
     for (int e = 0; e < m->c.sites; ++e) free(s->ev8[e]), free(s->evs[e]);
     free(s->k8), free(s->ks), free(s->v8t), free(s->vs), free(s->hist), free(s->ev8), free(s->evs);
-    free(s->tokens), free(s->rope_c), free(s->rope_s);
+    free(s->tokens), free(s->rope_c), free(s->rope_s), free(s->slot_pos), free(s->last_hidden);
     free(s);
+}
+
+static void* dupb(const void* p, size_t n) {
+    void* q = malloc(n ? n : 1);
+    if (n) memcpy(q, p, n);
+    return q;
+}
+
+/* Session::clone (#[derive(Clone)], model.rs:53-55): every cache copied. */
+nf_session* nf_session_clone(const nf_model* m, const nf_session* s) {
+    const nf_config* c = &m->c;
+    const size_t cap = s->cap, W = (size_t)width_of(c);
+    nf_session* o = (nf_session*)malloc(sizeof *o);
+    *o = *s;
+    o->tokens = (uint32_t*)dupb(s->tokens, cap * 4);
+    o->k8 = (int8_t**)calloc((size_t)c->layers, sizeof(void*));
+    o->ks = (float**)calloc((size_t)c->layers, sizeof(void*));
+    o->v8t = (int8_t**)calloc((size_t)c->layers, sizeof(void*));
+    o->vs = (float**)calloc((size_t)c->layers, sizeof(void*));
+    o->hist = (float**)calloc((size_t)c->layers, sizeof(void*));
+    for (int l = 0; l < c->layers; ++l) {
+        o->k8[l] = (int8_t*)dupb(s->k8[l], cap * c->nkv * c->qk);
+        o->ks[l] = (float*)dupb(s->ks[l], cap * c->nkv * 4);
+        o->v8t[l] = (int8_t*)dupb(s->v8t[l], (size_t)c->nkv * c->vd * cap);
+        o->vs[l] = (float*)dupb(s->vs[l], cap * c->nkv * 4);
+        o->hist[l] = (float*)dupb(s->hist[l], cap * W * 4);
+    }
+    o->ev8 = (int8_t**)calloc((size_t)c->sites + 1, sizeof(void*));
+    o->evs = (float**)calloc((size_t)c->sites + 1, sizeof(void*));
+    for (int e = 0; e < c->sites; ++e) {
+        o->ev8[e] = (int8_t*)dupb(s->ev8[e], cap * c->d);
+        o->evs[e] = (float*)dupb(s->evs[e], cap * (c->d / 32) * 4);
+    }
+    o->rope_c = (float*)dupb(s->rope_c, cap * 32 * 4);
+    o->rope_s = (float*)dupb(s->rope_s, cap * 32 * 4);
+    o->slot_pos = (int64_t*)dupb(s->slot_pos, cap * 8);
+    o->last_hidden = (float*)dupb(s->last_hidden, (size_t)c->d * 4);
+    return o;
 }
 
 size_t nf_session_len(const nf_session* s) { return s->len; }
 
-/* attend_head_ref (infer.rs:1871-2007) with attend = None: keys are
- * positions lo..pos (inclusive), slot = position.  `nested` (a chunk's rows,
- * infer/chunk.rs:263) drops the minimum chunk count (infer.rs:1888). */
-static void attend_head(const nf_model* m, const nf_session* s, int l, const float* qh, int kvh, size_t lo, size_t pos,
-                        int nested, float* out) {
+/* Session::attend (model.rs:62-66): ring 0 is None. */
+int nf_session_set_attend(nf_session* s, size_t sink, size_t ring) {
+    if (ring > 0 && sink + ring > s->cap) return -1;
+    s->sink = sink;
+    s->ring = ring;
+    return 0;
+}
+
+/* Session::rollback (model.rs:81-113) with NatState::rollback
+ * (infer.rs:1053-1071): drop the last n <= ROLLBACK positions; the KV slots
+ * and the slot map keep what they hold. */
+int nf_session_rollback(const nf_model* m, nf_session* s, size_t n) {
+    (void)m;
+    if (n > NF_ROLLBACK || n > s->len) return -1;
+    if (n == 0) return 0;
+    s->len -= n;
+    s->hrows = s->hrows > n ? s->hrows - n : 0;
+    s->rope_n = s->rope_n > n ? s->rope_n - n : 0; /* rope.retain(p < len) */
+    return 0;
+}
+
+/* Session::rewind_zeroed (model.rs:115-121), NatState::rewind_zeroed
+ * (infer.rs:1039-1051): positions len.. forgotten, the conv history emptied
+ * and the RoPE list dropped; the KV slots and slot map stay. */
+int nf_session_rewind_zeroed(const nf_model* m, nf_session* s, size_t len) {
+    (void)m;
+    if (len < s->len) s->len = len;
+    s->hrows = 0;
+    s->rope_n = 0;
+    return 0;
+}
+
+/* NatState::last_hidden into out[d]; 0, or -1 when no feed has set it. */
+int nf_session_last_hidden(const nf_model* m, const nf_session* s, float* out) {
+    if (!s->have_hidden) return -1;
+    memcpy(out, s->last_hidden, sizeof(float) * m->c.d);
+    return 0;
+}
+
+/* slot_of (infer.rs:1749-1756). */
+static size_t slot_of(size_t p, const nf_session* s) {
+    return (s->ring > 0 && p >= s->sink) ? (p - s->sink) % s->ring + s->sink : p;
+}
+
+/* mark_slots (infer.rs:1770-1779). */
+static void mark_slots(nf_session* s, size_t p0, size_t end) {
+    for (size_t p = p0; p < end; ++p) {
+        const size_t sl = slot_of(p, s);
+        if (s->nslot <= sl) {
+            for (size_t i = s->nslot; i <= sl; ++i) s->slot_pos[i] = -1;
+            s->nslot = sl + 1;
+        }
+        s->slot_pos[sl] = (int64_t)p;
+    }
+}
+
+/* key_ranges (infer.rs:1781-1826) over the slot map snapshot `sp` (nsp
+ * entries): up to 16 ascending position ranges [lo, hi); returns how many,
+ * or -1 past KEY_RUNS (the reference asserts). */
+static int key_ranges(size_t pos, size_t chunk_end, size_t window, const nf_session* s, const int64_t* sp, size_t nsp,
+                      size_t* lo_out, size_t* hi_out) {
+    const size_t lo = window ? (pos + 1 > window ? pos + 1 - window : 0) : 0;
+    size_t clo[2], chi[2];
+    if (s->ring == 0) {
+        clo[0] = lo, chi[0] = pos + 1, clo[1] = chi[1] = 0;
+    } else {
+        const size_t sink = s->sink, ring = s->ring;
+        size_t ae = sink < pos + 1 ? sink : pos + 1;
+        if (ae < lo) ae = lo;
+        clo[0] = lo, chi[0] = ae;
+        size_t b0 = chunk_end > ring ? chunk_end - ring : 0;
+        if (b0 < sink) b0 = sink;
+        if (b0 > pos + 1) b0 = pos + 1;
+        clo[1] = b0, chi[1] = pos + 1;
+    }
+    int k = 0;
+    for (int r = 0; r < 2; ++r) {
+        if (s->ring == 0) {
+            if (chi[r] > clo[r]) {
+                if (k >= NF_KEY_RUNS) return -1;
+                lo_out[k] = clo[r], hi_out[k] = chi[r], ++k;
+            }
+            continue;
+        }
+        int open = 0;
+        size_t a = 0;
+        for (size_t p = clo[r]; p < chi[r]; ++p) {
+            const size_t sl = slot_of(p, s);
+            const int ok = sl < nsp && sp[sl] == (int64_t)p;
+            if (ok && !open) {
+                open = 1, a = p;
+            } else if (!ok && open) {
+                if (k >= NF_KEY_RUNS) return -1;
+                lo_out[k] = a, hi_out[k] = p, ++k, open = 0;
+            }
+        }
+        if (open) {
+            if (k >= NF_KEY_RUNS) return -1;
+            lo_out[k] = a, hi_out[k] = chi[r], ++k;
+        }
+    }
+    return k;
+}
+
+/* attend_head_ref (infer.rs:1871-2007) over the keys in `nr` ascending
+ * position ranges [klo, khi), each key read from its KV slot (slot_of).
+ * `nested` (a chunk's rows, infer/chunk.rs:263) drops the minimum chunk
+ * count (infer.rs:1888).  The P.V sums are integers, so summing per key
+ * gives the reference's per-run sums (infer.rs:1966-1985). */
+static void attend_head(const nf_model* m, const nf_session* s, int l, const float* qh, int kvh, const size_t* klo,
+                        const size_t* khi, int nr, int nested, float* out) {
     const nf_config* c = &m->c;
     const size_t qk = c->qk, vd = c->vd, nkv = c->nkv, cap = s->cap;
     int8_t q8[64];
     const float qs = cq_quant_i8(qh, qk, q8) * INV_SQRT_QK;
-    const size_t n = pos + 1 - lo;
+    size_t n = 0;
+    for (int r = 0; r < nr; ++r) n += khi[r] - klo[r];
+    size_t* slots = (size_t*)malloc((n ? n : 1) * sizeof(size_t));
+    n = 0;
+    for (int r = 0; r < nr; ++r)
+        for (size_t p = klo[r]; p < khi[r]; ++p) slots[n++] = slot_of(p, s);
     size_t count, chunk;
     size_t kmin = 2 * NATIVE_TEAM / nkv;
     if (kmin < 1 || nested) kmin = 1;
@@ -471,16 +646,15 @@ static void attend_head(const nf_model* m, const nf_session* s, int l, const flo
     for (size_t c0 = 0; c0 < n; c0 += chunk) {
         const size_t len = chunk < n - c0 ? chunk : n - c0;
         const size_t blocked = len / 4 * 4;
-        const size_t slot0 = lo + c0;
-        for (size_t i = 0; i < len; ++i)
-            dots[i] = idot(q8, s->k8[l] + ((slot0 + i) * nkv + kvh) * qk, qk);
-        for (size_t i = 0; i < len; ++i) scale[i] = s->ks[l][(slot0 + i) * nkv + kvh];
+        const size_t* sl = slots + c0;
+        for (size_t i = 0; i < len; ++i) dots[i] = idot(q8, s->k8[l] + (sl[i] * nkv + kvh) * qk, qk);
+        for (size_t i = 0; i < len; ++i) scale[i] = s->ks[l][sl[i] * nkv + kvh];
         for (size_t i = 0; i < blocked; ++i) sc[i] = (scale[i] * (float)dots[i]) * qs;
         for (size_t i = blocked; i < len; ++i) sc[i] = (scale[i] * qs) * (float)dots[i];
         float mx = -INFINITY;
         for (size_t i = 0; i < len; ++i) mx = fmaxf(mx, sc[i]);
         const float sum = nf_chunk_exp(sc, len, mx);
-        for (size_t i = 0; i < len; ++i) scale[i] = s->vs[l][(slot0 + i) * nkv + kvh];
+        for (size_t i = 0; i < len; ++i) scale[i] = s->vs[l][sl[i] * nkv + kvh];
         float wmax = 0.0f;
         for (size_t i = 0; i < len; ++i) {
             sc[i] *= scale[i];
@@ -490,10 +664,13 @@ static void attend_head(const nf_model* m, const nf_session* s, int l, const flo
         int8_t *hi = dig, *mid = dig + chunk, *lo8 = dig + 2 * chunk;
         nf_digits21(sc, len, qw, hi, mid, lo8);
         const float cw = wmax * C21;
-        /* one run of consecutive slots: slot0 .. slot0 + len */
         for (size_t dm = 0; dm < vd; ++dm) {
-            const int8_t* row = s->v8t[l] + ((size_t)kvh * vd + dm) * cap + slot0;
-            const int32_t a = idot(hi, row, len), b = idot(mid, row, len), cc = idot(lo8, row, len);
+            const int8_t* row = s->v8t[l] + ((size_t)kvh * vd + dm) * cap;
+            int32_t a = 0, b = 0, cc = 0;
+            for (size_t i = 0; i < len; ++i) {
+                const int32_t v = row[sl[i]];
+                a += (int32_t)hi[i] * v, b += (int32_t)mid[i] * v, cc += (int32_t)lo8[i] * v;
+            }
             po[np][dm] = fmaf(16384.0f, (float)a, fmaf(128.0f, (float)b, (float)cc)) * cw;
         }
         pm[np] = mx;
@@ -515,7 +692,143 @@ static void attend_head(const nf_model* m, const nf_session* s, int l, const flo
         const float inv = 1.0f / total;
         for (size_t i = 0; i < vd; ++i) out[i] = acc[i] * inv;
     }
-    free(sc), free(scale), free(dots), free(dig);
+    free(sc), free(scale), free(dots), free(dig), free(slots);
+}
+
+/* The test hook for attend_head: one head against keys written straight
+ * into layer 0's cache slots.  k8 [n][qk] / ks [n] / v8 [n][vd] / vs [n]
+ * fill slots 0 .. n-1 of kv head 0; the query attends to positions
+ * 0 .. n-1 (no attention span) in one chunk list as a step would. */
+int nf_attend_test(const nf_model* m, nf_session* s, const int8_t* k8, const float* ks, const int8_t* v8,
+                   const float* vs, size_t n, const float* q, int nested, float* out) {
+    const nf_config* c = &m->c;
+    if (n == 0 || n > s->cap) return -1;
+    const size_t qk = c->qk, vd = c->vd, nkv = c->nkv;
+    for (size_t i = 0; i < n; ++i) {
+        memcpy(s->k8[0] + i * nkv * qk, k8 + i * qk, qk);
+        s->ks[0][i * nkv] = ks[i];
+        s->vs[0][i * nkv] = vs[i];
+        for (size_t dm = 0; dm < vd; ++dm) s->v8t[0][dm * s->cap + i] = v8[i * vd + dm];
+    }
+    const size_t lo = 0, hi = n;
+    attend_head(m, s, 0, q, 0, &lo, &hi, 1, nested, out);
+    return 0;
+}
+
+/* The hashed engram rows of position `pos` (engram_native,
+ * infer.rs:1256-1275): for order oi and head h, table tbl = oi * heads + h
+ * takes row tbl * slots + (hash % slots), the hash seeded with
+ * ENGRAM_SEED * (oi * stride + h + 1) and folded over the last `order`
+ * tokens (token 0 before the start) with xor then * ENGRAM_PRIME, then
+ * acc ^= acc >> 15; -1 where pos + 1 < order.  rows[16]. */
+void nf_engram_rows(const nf_model* m, const uint32_t* tokens, size_t pos, long* rows) {
+    const nf_config* c = &m->c;
+    const int stride = c->seed_heads > 0 ? c->seed_heads : c->eheads;
+    for (int k = 0; k < 16; ++k) rows[k] = -1;
+    for (int oi = 0; oi < c->norders; ++oi)
+        for (int h = 0; h < c->eheads; ++h) {
+            const int order = c->orders[oi], tbl = oi * c->eheads + h;
+            if (pos + 1 < (size_t)order) continue;
+            uint32_t acc = ENGRAM_SEED * (uint32_t)(oi * stride + h + 1);
+            for (int j = 0; j < order; ++j) {
+                const uint32_t tk = pos >= (size_t)j ? tokens[pos - j] : 0;
+                acc = (acc ^ tk) * ENGRAM_PRIME;
+            }
+            acc ^= acc >> 15;
+            rows[tbl] = (long)tbl * c->engram_slots + (long)(acc % (uint32_t)c->engram_slots);
+        }
+}
+
+/* The engram input row of position `pos` at one site: each hashed table
+ * row (QMat::row) at its table's sub-width slot, zeros where no row
+ * (infer.rs:1261-1275).  out[d]. */
+void nf_engram_input(const nf_model* m, int site, const uint32_t* tokens, size_t pos, float* out) {
+    const nf_config* c = &m->c;
+    long rows[16];
+    nf_engram_rows(m, tokens, pos, rows);
+    memset(out, 0, sizeof(float) * c->d);
+    for (int tbl = 0; tbl < c->norders * c->eheads; ++tbl)
+        if (rows[tbl] >= 0) cq_qmat_row(m->etables[site], (size_t)rows[tbl], out + (size_t)tbl * c->engram_sub);
+}
+
+/* The mHC read of one row (infer.rs:1359-1393): the 4 lanes x[4d]
+ * normalized by rinv over all of them, int8 with one scale, projected on
+ * the Phi8 rows (p[k] = (sx * phi_s[k]) * idot), the pre gates
+ * hp[j] = 1 / (lexpf(-z) + 1) with z = ((p[j] * a_pre) + (+4 own lane,
+ * -4 others)) + b_pre[j], then u = x0 hp0 and fma(x_b, hp_b, u) for
+ * b = 1..3.  Scratch nx[4d], nx8[4d]. */
+void nf_mhc_read(const int8_t* phi_q, const float* phi_s, int ncols, int d, float a_pre, const float* b_pre, int lane,
+                 const float* x, float* p, float* u, float* nx, int8_t* nx8) {
+    const int nc = 4 * d;
+    const float r = cq_rinv(cq_dot16(x, x, nc), nc);
+    for (int k = 0; k < nc; ++k) nx[k] = x[k] * r;
+    const float sx = cq_quant_scale(nx, nc);
+    cq_quant_with(nx, nc, 1.0f / sx, nx8);
+    for (int k = 0; k < ncols; ++k) p[k] = (sx * phi_s[k]) * (float)idot(phi_q + (size_t)k * nc, nx8, nc);
+    float hp[4];
+    for (int j = 0; j < 4; ++j) {
+        const float off = j == lane ? 4.0f : -4.0f;
+        const float zz = ((p[j] * a_pre) + off) + b_pre[j];
+        hp[j] = 1.0f / (lexpf(-zz) + 1.0f);
+    }
+    for (int k = 0; k < d; ++k) u[k] = x[k] * hp[0];
+    for (int b = 1; b < 4; ++b)
+        for (int k = 0; k < d; ++k) u[k] = fmaf(x[b * d + k], hp[b], u[k]);
+}
+
+/* The post and residual gates of one row (infer.rs:1577-1583): hpost[j] =
+ * 2 / (lexpf(-z) + 1) with z = ((p[4 + j] * a_post) + (0 own lane, -4
+ * others)) + b_post[j]; zres[k] = fma(p[8 + k], a_res, b_res[k]) and
+ * hres = sinkhorn64(zres). */
+void nf_post_gates(const float* p, float a_post, const float* b_post, float a_res, const float* b_res, int lane,
+                   float hpost[4], float hres[16]) {
+    float zres[16];
+    for (int j = 0; j < 4; ++j) {
+        const float off = j == lane ? 0.0f : -4.0f;
+        const float zz = ((p[4 + j] * a_post) + off) + b_post[j];
+        hpost[j] = 2.0f / (lexpf(-zz) + 1.0f);
+    }
+    for (int k = 0; k < 16; ++k) zres[k] = fmaf(p[8 + k], a_res, b_res[k]);
+    nf_sinkhorn64(zres, hres);
+}
+
+/* The mHC write of one row (infer.rs:1584-1605): lane a becomes
+ * y hpost[a], then fma(old_b, hres[a * 4 + b], .) for b = 0..3, with the
+ * lanes as they were before the write.  x[4d] in place. */
+void nf_mhc_write(int d, const float* y, const float hpost[4], const float hres[16], float* x) {
+    for (int ch = 0; ch < d; ++ch) {
+        float old[4];
+        for (int b = 0; b < 4; ++b) old[b] = x[b * d + ch];
+        for (int a = 0; a < 4; ++a) {
+            float v = y[ch] * hpost[a];
+            for (int b = 0; b < 4; ++b) v = fmaf(old[b], hres[a * 4 + b], v);
+            x[a * d + ch] = v;
+        }
+    }
+}
+
+/* Model::head_logits (infer.rs:1135-1141): the tied head over the final
+ * normed hidden state h[d] with the decode combine, out_rows logits. */
+void nf_head_logits(const nf_model* m, const float* h, float* logits, int nthreads) {
+    cq_qact* a = cq_qact_new(h, 1, m->c.d, m->embedding->bits, 1);
+    float* full = (float*)malloc(sizeof(float) * m->embedding->out);
+    cq_matmul_into(m->embedding, a, full, m->embedding->out, 0, nthreads);
+    memcpy(logits, full, sizeof(float) * m->c.out_rows);
+    free(full);
+    cq_qact_free(a);
+}
+
+/* Model::head_logits_sparse (infer.rs:1145-1166): NEG (infer.rs:36)
+ * everywhere but the ids, scored with QMat::single_row.  0, or -1 for an id
+ * past out_rows. */
+int nf_head_logits_sparse(const nf_model* m, const float* h, const uint32_t* ids, size_t n, float* logits) {
+    for (size_t i = 0; i < n; ++i)
+        if (ids[i] >= (uint32_t)m->c.out_rows) return -1;
+    cq_qact* a = cq_qact_new(h, 1, m->c.d, m->embedding->bits, 1);
+    for (int i = 0; i < m->c.out_rows; ++i) logits[i] = bits_f(0xf149f2cau);
+    for (size_t i = 0; i < n; ++i) logits[ids[i]] = cq_single_row(m->embedding, ids[i], a);
+    cq_qact_free(a);
+    return 0;
 }
 
 /* The rows p0 .. p0 + t - 1 of one feed: Model::step_native
@@ -523,19 +836,29 @@ static void attend_head(const nf_model* m, const nf_session* s, int l, const flo
  * for a chunk of t > 1 tokens.  The two share the per-row arithmetic; a chunk
  * differs in its projections (the prefill combine over its t rows), its RoPE
  * rows (sincosf per position, rope_rows, infer.rs:1716-1747) and its
- * attention chunking (nested, infer.rs:1888).  Logits of the last row
- * [out_rows] when `logits` is set. */
-static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_t t, float* logits, int nthreads) {
+ * attention chunking (nested, infer.rs:1888).  `outputs` (NF_OUT_*) picks
+ * what goes to `out` (chunk.rs:331-353, step.rs:715-729): logits [rows]
+ * [out_rows] or hidden states [rows][d]; returns the rows written, or -1. */
+static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_t t, int outputs, float* outbuf,
+                   int nthreads) {
     const nf_config* c = &m->c;
     const int n = c->lanes, d = c->d, nc = n * d, L = c->layers;
     const int qk = c->qk, vd = c->vd, nh = c->nh, nkv = c->nkv;
     const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd, W = qd + kd + vdim, taps = c->taps;
     const int half = qk / 2, group = nh / nkv, sites = c->sites;
     const size_t p0 = s->len;
+    int rc = 0;
     if (t == 0 || p0 + t > s->cap || n != 4 || qk > 64 || vd > 64 || c->norders * c->eheads > 16 || L > 64) return -1;
     const int nested = t > 1;
     for (size_t i = 0; i < t; ++i) s->tokens[p0 + i] = toks[i];
     s->len = p0 + t;
+    /* the slot map with this feed's positions, and its snapshot
+     * (step.rs:193,229-231, chunk.rs:54,81) */
+    mark_slots(s, p0, p0 + t);
+    int64_t* sp = (int64_t*)dupb(s->slot_pos, s->nslot * 8);
+    const size_t nsp = s->nslot;
+    /* the first position LayerState::hist still holds */
+    const size_t hist_lo = p0 - s->hrows;
 
     /* embedding row * sqrt(d) into every lane (step.rs:228-235, chunk.rs:58-66) */
     float* xs = (float*)malloc(sizeof(float) * t * nc);
@@ -554,23 +877,7 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
     float* evals = (float*)calloc((size_t)sites * t * d + 1, sizeof(float));
     if (sites > 0) {
         long* erow = (long*)malloc(sizeof(long) * t * 16);
-        const int stride = c->seed_heads > 0 ? c->seed_heads : eheads;
-        for (size_t i = 0; i < t; ++i) {
-            const size_t pos = p0 + i;
-            for (int oi = 0; oi < norders; ++oi)
-                for (int h = 0; h < eheads; ++h) {
-                    const int order = c->orders[oi], tbl = oi * eheads + h;
-                    erow[i * 16 + tbl] = -1;
-                    if (pos + 1 < (size_t)order) continue;
-                    uint32_t acc = ENGRAM_SEED * (uint32_t)(oi * stride + h + 1);
-                    for (int j = 0; j < order; ++j) {
-                        const uint32_t tk = pos >= (size_t)j ? s->tokens[pos - j] : 0;
-                        acc = (acc ^ tk) * ENGRAM_PRIME;
-                    }
-                    acc ^= acc >> 15;
-                    erow[i * 16 + tbl] = (long)tbl * c->engram_slots + (long)(acc % (uint32_t)c->engram_slots);
-                }
-        }
+        for (size_t i = 0; i < t; ++i) nf_engram_rows(m, s->tokens, p0 + i, erow + i * 16);
         float* er = (float*)malloc(sizeof(float) * t * d);
         float* trow = (float*)malloc(sizeof(float) * sub);
         for (int e = 0; e < sites; ++e) {
@@ -610,21 +917,22 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
 
     /* RoPE rows (rope_rows, infer.rs:1716-1747): the recurrence for a single
      * token right after the newest known position, sincosf otherwise. */
-    float* cs = (float*)malloc(sizeof(float) * t * 32);
-    float* sn = (float*)malloc(sizeof(float) * t * 32);
-    if (t == 1 && s->rope_ok && s->rope_pos + 1 == p0) {
+    float* cs = s->rope_c + p0 * 32;
+    float* sn = s->rope_s + p0 * 32;
+    if (t == 1 && s->rope_n > 0) {
+        /* the list ends at position p0 - 1 */
+        const float *c0 = s->rope_c + (p0 - 1) * 32, *s0 = s->rope_s + (p0 - 1) * 32;
         for (int f = 0; f < half; ++f) {
-            cs[f] = fmaf(-m->sd[f], s->rope_s[f], m->cd[f] * s->rope_c[f]);
-            sn[f] = fmaf(m->sd[f], s->rope_c[f], m->cd[f] * s->rope_s[f]);
+            cs[f] = fmaf(-m->sd[f], s0[f], m->cd[f] * c0[f]);
+            sn[f] = fmaf(m->sd[f], c0[f], m->cd[f] * s0[f]);
         }
     } else {
         for (size_t i = 0; i < t; ++i)
             for (int f = 0; f < half; ++f) lsincosf(m->freq[f] * (float)(p0 + i), &sn[i * 32 + f], &cs[i * 32 + f]);
     }
-    memcpy(s->rope_c, cs + (t - 1) * 32, sizeof(float) * half);
-    memcpy(s->rope_s, sn + (t - 1) * 32, sizeof(float) * half);
-    s->rope_ok = 1;
-    s->rope_pos = p0 + t - 1;
+    /* push the rows, then trim to ROLLBACK + 1 past twice that */
+    s->rope_n += t;
+    if (s->rope_n > 2 * (NF_ROLLBACK + 1)) s->rope_n = NF_ROLLBACK + 1;
 
     const int nq = W + nh * vd;  /* the fused projection: q | k | v | gate */
     const int ncols = 2 * n + n * n;
@@ -651,20 +959,7 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
             float* pr = p + i * ncols;
             float* ur = u + i * d;
             float* xr = x1 + i * d;
-            const float r = cq_rinv(cq_dot16(x, x, nc), nc);
-            for (int k = 0; k < nc; ++k) nx[k] = x[k] * r;
-            const float sx = cq_quant_scale(nx, nc);
-            cq_quant_with(nx, nc, 1.0f / sx, nx8);
-            for (int k = 0; k < ncols; ++k) pr[k] = (sx * Lw->phi_s[k]) * (float)idot(Lw->phi_q + (size_t)k * nc, nx8, nc);
-            float hp[4];
-            for (int j = 0; j < 4; ++j) {
-                const float off = j == lane ? 4.0f : -4.0f;
-                const float zz = ((pr[j] * Lw->a_pre) + off) + Lw->b_pre[j];
-                hp[j] = 1.0f / (lexpf(-zz) + 1.0f);
-            }
-            for (int k = 0; k < d; ++k) ur[k] = x[k] * hp[0];
-            for (int b = 1; b < 4; ++b)
-                for (int k = 0; k < d; ++k) ur[k] = fmaf(x[b * d + k], hp[b], ur[k]);
+            nf_mhc_read(Lw->phi_q, Lw->phi_s, ncols, d, Lw->a_pre, Lw->b_pre, lane, x, pr, ur, nx, nx8);
             memcpy(xr, ur, sizeof(float) * d);
             if (site >= 0) {
                 const float* kr = ekv + ((size_t)site * t + i) * 2 * d;
@@ -698,7 +993,7 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
                 for (int k = 0; k < cw; ++k) out[start + k] = cq_f16_to_f32(w[k]) * cur[k];
                 for (int j = 1; j < taps; ++j) {
                     const uint16_t* wj = w + (size_t)j * cw;
-                    if (pos >= (size_t)j) {
+                    if (pos >= hist_lo + (size_t)j) {
                         const float* rr = hist + (pos - j) * (size_t)W + start;
                         for (int k = 0; k < cw; ++k) out[start + k] = fmaf(cq_f16_to_f32(wj[k]), rr[k], out[start + k]);
                     } else {
@@ -711,11 +1006,12 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
                 zcn16_inplace(v, hh < nh ? Lw->q_norm : Lw->k_norm, qk);
                 nf_rope_rotate(v, qk, cs + i * 32, sn + i * 32);
             }
+            const size_t slot = slot_of(pos, s);
             for (int kvh = 0; kvh < nkv; ++kvh) {
-                s->ks[l][pos * nkv + kvh] = cq_quant_i8(out + qd + kvh * qk, qk, s->k8[l] + (pos * nkv + kvh) * qk);
+                s->ks[l][slot * nkv + kvh] = cq_quant_i8(out + qd + kvh * qk, qk, s->k8[l] + (slot * nkv + kvh) * qk);
                 int8_t vq[64];
-                s->vs[l][pos * nkv + kvh] = cq_quant_i8(out + qd + kd + kvh * vd, vd, vq);
-                for (int dm = 0; dm < vd; ++dm) s->v8t[l][((size_t)kvh * vd + dm) * s->cap + pos] = vq[dm];
+                s->vs[l][slot * nkv + kvh] = cq_quant_i8(out + qd + kd + kvh * vd, vd, vq);
+                for (int dm = 0; dm < vd; ++dm) s->v8t[l][((size_t)kvh * vd + dm) * s->cap + slot] = vq[dm];
             }
         }
         /* (h) attention per (row, head), (i) its gate, (j) A8 and out */
@@ -723,10 +1019,15 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
             const int window = (c->sliding_window > 0 && !((c->global_mask >> l) & 1)) ? c->sliding_window : 0;
             for (size_t i = 0; i < t; ++i) {
                 const size_t pos = p0 + i;
-                const size_t lo = window ? (pos + 1 > (size_t)window ? pos + 1 - (size_t)window : 0) : 0;
+                size_t klo[NF_KEY_RUNS], khi[NF_KEY_RUNS];
+                const int nr = key_ranges(pos, p0 + t, (size_t)window, s, sp, nsp, klo, khi);
+                if (nr < 0) {
+                    rc = -1;
+                    goto done;
+                }
                 for (int hh = 0; hh < nh; ++hh) {
                     float* ah = att + (i * nh + hh) * vd;
-                    attend_head(m, s, l, qkv + i * W + hh * qk, hh / group, lo, pos, nested, ah);
+                    attend_head(m, s, l, qkv + i * W + hh * qk, hh / group, klo, khi, nr, nested, ah);
                     const float* gate = proj + i * nq + W + hh * vd;
                     for (int k = 0; k < vd; ++k) ah[k] /= nf_nexp(-gate[k]) + 1.0f;
                 }
@@ -761,51 +1062,102 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
             for (int j = 0; j < HN; ++j) zs[j] = bt[m->perm2[j]] * cq_f16_to_f32(Lw->d3[j]);
             nf_mix8(1, Lw->kron[4], 1, zs, 0, mt, 16);
             nf_mix8(0, mt, 0, Lw->kron[5], 1, t3, d / NB / 8 * 4);
-            float hpost[4], zres[16], hres[16];
-            for (int j = 0; j < 4; ++j) {
-                const float off = j == lane ? 0.0f : -4.0f;
-                const float zz = ((pr[n + j] * Lw->a_post) + off) + Lw->b_post[j];
-                hpost[j] = 2.0f / (lexpf(-zz) + 1.0f);
-            }
-            for (int k = 0; k < 16; ++k) zres[k] = fmaf(pr[2 * n + k], Lw->a_res, Lw->b_res[k]);
-            nf_sinkhorn64(zres, hres);
-            for (int ch = 0; ch < d; ++ch) {
-                const float y = (x2[ch] + t3[ch] * cq_f16_to_f32(Lw->d4[ch])) - u[i * d + ch];
-                float old[4];
-                for (int b = 0; b < 4; ++b) old[b] = x[b * d + ch];
-                for (int a2 = 0; a2 < n; ++a2) {
-                    float v = y * hpost[a2];
-                    for (int b = 0; b < 4; ++b) v = fmaf(old[b], hres[a2 * n + b], v);
-                    x[a2 * d + ch] = v;
-                }
-            }
+            float hpost[4], hres[16];
+            nf_post_gates(pr, Lw->a_post, Lw->b_post, Lw->a_res, Lw->b_res, lane, hpost, hres);
+            /* y = (x2 + mlp) - u, mlp = t3 * d4 (mlp_native, infer.rs:1610-1637) */
+            for (int ch = 0; ch < d; ++ch) z[ch] = (x2[ch] + t3[ch] * cq_f16_to_f32(Lw->d4[ch])) - u[i * d + ch];
+            nf_mhc_write(d, z, hpost, hres, x);
         }
     }
 
-    /* head of the last row: lane mean, final norm, tied embedding
-     * (step.rs:706-728, chunk.rs:322-347) */
-    if (logits) {
-        const float* x = xs + (t - 1) * nc;
-        float* mean = (float*)malloc(sizeof(float) * d);
-        for (int ch = 0; ch < d; ++ch) mean[ch] = (((x[ch] + x[d + ch]) + x[2 * d + ch]) + x[3 * d + ch]) * 0.25f;
-        zcn(mean, m->final_norm, d, hloc);
-        cq_qact* a = cq_qact_new(hloc, 1, d, m->embedding->bits, 1);
-        float* full = (float*)malloc(sizeof(float) * m->embedding->out);
-        cq_matmul_into(m->embedding, a, full, m->embedding->out, 0, nthreads);
-        memcpy(logits, full, sizeof(float) * c->out_rows);
-        free(full), free(mean);
-        cq_qact_free(a);
+    /* the history rows this feed wrote, then the trim (chunk.rs:319-329,
+     * step.rs:706-712) */
+    {
+        const size_t keep = (size_t)taps - 1 + NF_ROLLBACK;
+        s->hrows += t;
+        if (s->hrows > 2 * keep) s->hrows = keep;
     }
-    free(xs), free(row), free(ekv), free(evals), free(cs), free(sn), free(nx), free(nx8), free(u), free(x1), free(p);
+    /* outputs: lane mean, final norm, tied head per chosen row
+     * (chunk.rs:331-353, step.rs:715-729); last_hidden is the last chosen
+     * row's normed state */
+    {
+        const size_t first = (outputs == NF_OUT_ALL_LOGITS || outputs == NF_OUT_HIDDEN) ? 0 : t - 1;
+        const size_t nrows = outputs == NF_OUT_NONE ? 0 : t - first;
+        float* mean = (float*)malloc(sizeof(float) * d);
+        for (size_t r = 0; r < nrows; ++r) {
+            const float* x = xs + (first + r) * nc;
+            for (int ch = 0; ch < d; ++ch) mean[ch] = (((x[ch] + x[d + ch]) + x[2 * d + ch]) + x[3 * d + ch]) * 0.25f;
+            zcn(mean, m->final_norm, d, s->last_hidden);
+            s->have_hidden = 1;
+            if (!outbuf) continue;
+            if (outputs == NF_OUT_HIDDEN || outputs == NF_OUT_LAST_HIDDEN)
+                memcpy(outbuf + r * d, s->last_hidden, sizeof(float) * d);
+            else
+                nf_head_logits(m, s->last_hidden, outbuf + r * c->out_rows, nthreads);
+        }
+        free(mean);
+        rc = (int)nrows;
+    }
+done:
+    free(sp);
+    free(xs), free(row), free(ekv), free(evals), free(nx), free(nx8), free(u), free(x1), free(p);
     free(hloc), free(proj), free(qkv), free(att), free(o), free(on), free(x2), free(h2), free(ea), free(eb), free(z);
     free(mt), free(bt), free(cond), free(zs), free(t3);
-    return 0;
+    return rc;
 }
 
 int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int nthreads) {
-    return nf_rows(m, s, &tok, 1, logits, nthreads);
+    const int r = nf_rows(m, s, &tok, 1, logits ? NF_OUT_LAST_LOGITS : NF_OUT_NONE, logits, nthreads);
+    return r < 0 ? -1 : 0;
 }
 
 int nf_chunk(const nf_model* m, nf_session* s, const uint32_t* toks, size_t t, float* logits, int nthreads) {
-    return t == 1 ? nf_step(m, s, toks[0], logits, nthreads) : nf_rows(m, s, toks, t, logits, nthreads);
+    const int r = nf_rows(m, s, toks, t, logits ? NF_OUT_LAST_LOGITS : NF_OUT_NONE, logits, nthreads);
+    return r < 0 ? -1 : 0;
+}
+
+/* Model::forward_native (infer.rs:1105-1132): chunks of 32, a one-token
+ * chunk as a step; LastLogits / LastHidden only from the last chunk.
+ * Returns the rows written to `out`, or -1. */
+int nf_forward(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out, int nthreads) {
+    if (outputs < NF_OUT_NONE || outputs > NF_OUT_LAST_HIDDEN || s->len + n > s->cap) return -1;
+    const size_t width = (outputs == NF_OUT_HIDDEN || outputs == NF_OUT_LAST_HIDDEN) ? (size_t)m->c.d
+                                                                                    : (size_t)m->c.out_rows;
+    int rows = 0;
+    for (size_t i = 0; i < n; i += 32) {
+        const size_t t = n - i < 32 ? n - i : 32;
+        const int last = i + t == n;
+        const int want = (!last && (outputs == NF_OUT_LAST_LOGITS || outputs == NF_OUT_LAST_HIDDEN)) ? NF_OUT_NONE
+                                                                                                       : outputs;
+        const int r = nf_rows(m, s, toks + i, t, want, out ? out + (size_t)rows * width : NULL, nthreads);
+        if (r < 0) return -1;
+        rows += r;
+    }
+    return rows;
+}
+
+/* Model::prefill_native (infer.rs:1078-1101): with an attention span and
+ * a slot map, the first position in max(end - ring, sink) .. len whose
+ * slot another position holds now starts a re-feed with the conv history
+ * zeroed (rewind_zeroed); else forward_native. */
+int nf_prefill(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out, int nthreads) {
+    const size_t pos = s->len, end = pos + n;
+    if (s->ring > 0 && s->nslot > 0) {
+        size_t lo = end > s->ring ? end - s->ring : 0;
+        if (lo < s->sink) lo = s->sink;
+        for (size_t p = lo; p < pos; ++p) {
+            const size_t sl = slot_of(p, s);
+            if (sl < s->nslot && s->slot_pos[sl] == (int64_t)p) continue;
+            const size_t k = pos - p;
+            if (end > s->cap) return -1;
+            uint32_t* refeed = (uint32_t*)malloc((k + n + 1) * 4);
+            memcpy(refeed, s->tokens + p, k * 4);
+            if (n) memcpy(refeed + k, toks, n * 4);
+            nf_session_rewind_zeroed(m, s, p);
+            const int r = nf_forward(m, s, refeed, k + n, outputs, out, nthreads);
+            free(refeed);
+            return r;
+        }
+    }
+    return nf_forward(m, s, toks, n, outputs, out, nthreads);
 }

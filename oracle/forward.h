@@ -46,6 +46,25 @@ void nf_set_globals(nf_model* m, const float* final_norm, const int32_t* perm1, 
 nf_session* nf_session_new(const nf_model* m, size_t cap);
 void nf_session_free(const nf_model* m, nf_session* s);
 size_t nf_session_len(const nf_session* s);
+/* Outputs (crates/needle-engine/src/model.rs:150-160). */
+#define NF_OUT_NONE 0
+#define NF_OUT_LAST_LOGITS 1
+#define NF_OUT_ALL_LOGITS 2
+#define NF_OUT_HIDDEN 3
+#define NF_OUT_LAST_HIDDEN 4
+
+nf_session* nf_session_clone(const nf_model* m, const nf_session* s);
+int nf_session_set_attend(nf_session* s, size_t sink, size_t ring);
+int nf_session_rollback(const nf_model* m, nf_session* s, size_t n);
+int nf_session_rewind_zeroed(const nf_model* m, nf_session* s, size_t len);
+int nf_session_last_hidden(const nf_model* m, const nf_session* s, float* out);
+/* Model::forward / Model::prefill on the native path: rows written or -1. */
+int nf_forward(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out, int nthreads);
+int nf_prefill(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out, int nthreads);
+void nf_head_logits(const nf_model* m, const float* h, float* logits, int nthreads);
+int nf_head_logits_sparse(const nf_model* m, const float* h, const uint32_t* ids, size_t n, float* logits);
+int nf_attend_test(const nf_model* m, nf_session* s, const int8_t* k8, const float* ks, const int8_t* v8,
+                   const float* vs, size_t n, const float* q, int nested, float* out);
 /* One decode step (step_native); logits [out_rows] (NULL: none).  0 or -1. */
 int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int nthreads);
 /* One prompt chunk of t <= 32 tokens (chunk_job; a single token is a step);
@@ -53,6 +72,13 @@ int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int n
 int nf_chunk(const nf_model* m, nf_session* s, const uint32_t* toks, size_t t, float* logits, int nthreads);
 
 /* Helpers, exposed for their own checks. */
+void nf_engram_rows(const nf_model* m, const uint32_t* tokens, size_t pos, long* rows);
+void nf_engram_input(const nf_model* m, int site, const uint32_t* tokens, size_t pos, float* out);
+void nf_mhc_read(const int8_t* phi_q, const float* phi_s, int ncols, int d, float a_pre, const float* b_pre, int lane,
+                 const float* x, float* p, float* u, float* nx, int8_t* nx8);
+void nf_post_gates(const float* p, float a_post, const float* b_post, float a_res, const float* b_res, int lane,
+                   float hpost[4], float hres[16]);
+void nf_mhc_write(int d, const float* y, const float hpost[4], const float hres[16], float* x);
 float nf_nexp(float x);
 void nf_rope_rotate(float* x, size_t n, const float* cs, const float* sn);
 void nf_cond_weights(const float* h2, size_t d, const uint16_t* cond_v, float out[8]);

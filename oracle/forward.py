@@ -17,6 +17,9 @@ from .cact import CQ, F16, F32, Archive, hada_blocks
 
 P = C.c_void_p
 
+# Outputs (crates/needle-engine/src/model.rs:150-160)
+OUT_NONE, OUT_LAST_LOGITS, OUT_ALL_LOGITS, OUT_HIDDEN, OUT_LAST_HIDDEN = range(5)
+
 (KRON0, KRON1, KRON2, KRON3, KRON4, KRON5, COND_V, COND_U, D1, D2, B2, D3, D4, NORM_IN, POST_NORM, PRE_HADA, Q_TAPS,
  K_TAPS, V_TAPS, Q_NORM, K_NORM) = range(21)
 
@@ -60,6 +63,21 @@ def _lib():
             "nf_chunk_exp": (C.c_float, [P, C.c_size_t, C.c_float]),
             "nf_digits21": (None, [P, C.c_size_t, C.c_float, P, P, P]),
             "nf_key_chunks": (None, [C.c_size_t, C.c_size_t, P, P]),
+            "nf_session_clone": (P, [P, P]),
+            "nf_session_set_attend": (C.c_int, [P, C.c_size_t, C.c_size_t]),
+            "nf_session_rollback": (C.c_int, [P, P, C.c_size_t]),
+            "nf_session_rewind_zeroed": (C.c_int, [P, P, C.c_size_t]),
+            "nf_session_last_hidden": (C.c_int, [P, P, P]),
+            "nf_forward": (C.c_int, [P, P, P, C.c_size_t, C.c_int, P, C.c_int]),
+            "nf_prefill": (C.c_int, [P, P, P, C.c_size_t, C.c_int, P, C.c_int]),
+            "nf_head_logits": (None, [P, P, P, C.c_int]),
+            "nf_head_logits_sparse": (C.c_int, [P, P, P, C.c_size_t, P]),
+            "nf_attend_test": (C.c_int, [P, P, P, P, P, P, C.c_size_t, P, C.c_int, P]),
+            "nf_engram_rows": (None, [P, P, C.c_size_t, P]),
+            "nf_engram_input": (None, [P, C.c_int, P, C.c_size_t, P]),
+            "nf_mhc_read": (None, [P, P, C.c_int, C.c_int, C.c_float, P, C.c_int, P, P, P, P, P]),
+            "nf_post_gates": (None, [P, C.c_float, P, C.c_float, P, C.c_int, P, P]),
+            "nf_mhc_write": (None, [C.c_int, P, P, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(l, name)
@@ -210,6 +228,22 @@ class Forward:
     def session(self, cap: int = 256) -> "Session":
         return Session(self, cap)
 
+    def head_logits(self, h) -> np.ndarray:
+        """Model::head_logits (infer.rs:1135-1141)."""
+        h = np.ascontiguousarray(h, dtype=np.float32)
+        out = np.zeros(self.cfg.out_rows, dtype=np.float32)
+        _lib().nf_head_logits(self.m, _p(h), _p(out), self.threads)
+        return out
+
+    def head_logits_sparse(self, h, ids) -> np.ndarray:
+        """Model::head_logits_sparse (infer.rs:1145-1166)."""
+        h = np.ascontiguousarray(h, dtype=np.float32)
+        ids = np.ascontiguousarray(np.asarray(ids, dtype=np.uint32).reshape(-1))
+        out = np.zeros(self.cfg.out_rows, dtype=np.float32)
+        if _lib().nf_head_logits_sparse(self.m, _p(h), _p(ids), ids.size, _p(out)) != 0:
+            raise ValueError("id past out_rows")
+        return out
+
     def __del__(self):
         if getattr(self, "m", None) and lib is not None:
             _lib().nf_model_free(self.m)
@@ -217,11 +251,12 @@ class Forward:
 
 
 class Session:
-    """The decoding state of one sequence (NatState, infer.rs:1008-1071)."""
+    """The decoding state of one sequence (Session with NatState,
+    crates/needle-engine/src/model.rs:53-121, infer.rs:966-1071)."""
 
-    def __init__(self, f: Forward, cap: int):
+    def __init__(self, f: Forward, cap: int, handle=None):
         self.f = f
-        self.s = _lib().nf_session_new(f.m, cap)
+        self.s = handle if handle is not None else _lib().nf_session_new(f.m, cap)
         self.cap = cap
 
     def step(self, tok: int) -> np.ndarray:
@@ -242,14 +277,64 @@ class Session:
             raise ValueError("chunk outside the session's capacity or geometry")
         return out
 
+    def _width(self, outputs):
+        return self.f.cfg.d if outputs in (OUT_HIDDEN, OUT_LAST_HIDDEN) else self.f.cfg.out_rows
+
+    def _run(self, fn, toks, outputs):
+        t = np.ascontiguousarray(np.asarray(toks, dtype=np.uint32).reshape(-1))
+        rows_max = t.size if outputs in (OUT_ALL_LOGITS, OUT_HIDDEN) else 1
+        out = np.zeros((max(rows_max, 1), self._width(outputs)), dtype=np.float32)
+        r = fn(self.f.m, self.s, _p(t), t.size, int(outputs), _p(out), self.f.threads)
+        if r < 0:
+            raise ValueError("feed outside the session's capacity, geometry or key runs")
+        return out[:r]
+
+    def forward(self, toks, outputs: int = OUT_LAST_LOGITS) -> np.ndarray:
+        """Model::forward on the native path (forward_native,
+        infer.rs:1105-1132): the rows `outputs` selects, [rows][width]."""
+        return self._run(_lib().nf_forward, toks, outputs)
+
+    def prefill(self, toks, outputs: int = OUT_LAST_LOGITS) -> np.ndarray:
+        """Model::prefill on the native path (prefill_native, infer.rs:1078-1101)."""
+        return self._run(_lib().nf_prefill, toks, outputs)
+
     def feed(self, toks) -> np.ndarray:
-        """Model::forward with Outputs::LastLogits as forward_native feeds it
-        (infer.rs:1105-1132): chunks of 32, a single-token chunk as a step."""
-        toks = np.asarray(toks, dtype=np.uint32).reshape(-1)
-        last = None
-        for i in range(0, toks.size, 32):
-            last = self.chunk(toks[i:i + 32])
-        return last
+        """Model::forward with Outputs::LastLogits: the last row's logits."""
+        return self.forward(toks, OUT_LAST_LOGITS)[0]
+
+    def set_attend(self, sink: int, ring: int):
+        """Session::attend = Some((sink, ring)) (ring 0: None)."""
+        if _lib().nf_session_set_attend(self.s, int(sink), int(ring)) != 0:
+            raise ValueError("attention span past the capacity")
+
+    def rollback(self, n: int):
+        if _lib().nf_session_rollback(self.f.m, self.s, int(n)) != 0:
+            raise ValueError("rollback past ROLLBACK or the length")
+
+    def rewind_zeroed(self, length: int):
+        _lib().nf_session_rewind_zeroed(self.f.m, self.s, int(length))
+
+    def clone(self) -> "Session":
+        return Session(self.f, self.cap, handle=_lib().nf_session_clone(self.f.m, self.s))
+
+    def last_hidden(self) -> np.ndarray:
+        out = np.zeros(self.f.cfg.d, dtype=np.float32)
+        if _lib().nf_session_last_hidden(self.f.m, self.s, _p(out)) != 0:
+            raise ValueError("no hidden state yet")
+        return out
+
+    def attend_test(self, k8, ks, v8, vs, q, nested=False) -> np.ndarray:
+        """attend_head over keys written into layer 0's slots 0..n-1 (kv head 0)."""
+        k8 = np.ascontiguousarray(k8, dtype=np.int8)
+        v8 = np.ascontiguousarray(v8, dtype=np.int8)
+        ks = np.ascontiguousarray(ks, dtype=np.float32)
+        vs = np.ascontiguousarray(vs, dtype=np.float32)
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        out = np.zeros(self.f.cfg.vd, dtype=np.float32)
+        if _lib().nf_attend_test(self.f.m, self.s, _p(k8), _p(ks), _p(v8), _p(vs), ks.size, _p(q), int(nested),
+                                 _p(out)) != 0:
+            raise ValueError("bad key count")
+        return out
 
     def __len__(self):
         return _lib().nf_session_len(self.s)
