@@ -187,13 +187,63 @@ int nh_session_free(nh_session* s);
 int nh_session_len(const nh_session* s);
 /* Back to an empty session (Model::session again, without reallocating). */
 int nh_session_reset(nh_session* s);
+/* Outputs (crates/needle-engine/src/model.rs:150-160): what a feed returns. */
+#define NH_OUT_NONE 0        /* nothing: the head is not run */
+#define NH_OUT_LAST_LOGITS 1 /* logits of the last position [1][out_rows] */
+#define NH_OUT_ALL_LOGITS 2  /* logits of every new position [n][out_rows] (head_logits per row) */
+#define NH_OUT_HIDDEN 3      /* final normed hidden state of every new position [n][d_model] */
+#define NH_OUT_LAST_HIDDEN 4 /* final normed hidden state of the last position [1][d_model] */
+/* Model::forward (model.rs:304-306) on the native path (forward_native,
+ * crates/needle-engine/src/infer.rs:1105-1132) with any Outputs: chunks of 32
+ * tokens, LastLogits / LastHidden from the last chunk only (infer.rs:
+ * 1111-1116), the rows a chunk returns as chunk_job picks them
+ * (infer/chunk.rs:331-353).  `out` is DEVICE memory for out_cap floats (or
+ * NULL); returns the rows written (ForwardOut::rows), NH_ESMALL when they do
+ * not fit.  The session keeps the last returned row's hidden state
+ * (NatState::last_hidden) and, for the logits modes, its logits.  On a
+ * failure after the first chunk the session is reset. */
+int nh_forward_outputs(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, int64_t out_cap,
+                       void* stream);
+/* Model::prefill on the native path (prefill_native, infer.rs:1078-1101):
+ * with an attention span, a position in max(end - ring, sink) .. len whose KV
+ * slot another position holds now starts a re-feed from there with the
+ * conv history zeroed; else as nh_forward_outputs. */
+int nh_prefill(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, int64_t out_cap, void* stream);
+/* Session::clone (model.rs:53-55): a new session with a copy of every cache
+ * (one device-to-device copy on `stream`, then a synchronization). */
+int nh_session_clone(const nh_session* s, void* stream, nh_session** out);
+/* Session::attend = Some((sink, ring)) (model.rs:62-66; ring 0: None): every
+ * query sees the first `sink` positions and the last `ring`; positions past
+ * the sink share `ring` KV slots (slot_of, infer.rs:1749-1756) and a slot map
+ * (mark_slots / key_ranges, infer.rs:1770-1826) skips a position whose slot
+ * another has taken since.  A ring must be 0 or at least 32 (a shorter one
+ * would give two rows of a 32-token chunk one slot). */
+int nh_session_set_attend(nh_session* s, int sink, int ring);
+/* Session::rollback (model.rs:81-113, NatState::rollback infer.rs:1053-1071):
+ * drop the last n <= 32 positions without recomputing; the KV slots and the
+ * slot map keep what they hold. */
+int nh_session_rollback(nh_session* s, int n);
+/* Session::rewind_zeroed (model.rs:115-121, infer.rs:1039-1051): forget
+ * positions len.. as the engine's context-overflow re-feed does: the KV cache
+ * keeps what it holds, the conv history and the RoPE state start over. */
+int nh_session_rewind_zeroed(nh_session* s, int len);
+/* NatState::last_hidden (infer.rs:996-998) into DEVICE h[d_model]. */
+int nh_session_last_hidden(const nh_session* s, float* h, void* stream);
+/* Model::head_logits (infer.rs:1135-1141) of the session's last hidden state
+ * into DEVICE logits[out_rows]. */
+int nh_session_head_logits(nh_session* s, float* logits, void* stream);
+/* Model::head_logits_sparse (infer.rs:1145-1166) of the session's last hidden
+ * state: DEVICE ids[n], DEVICE logits[out_rows] (NEG off the ids), as the
+ * agent's sparse decode scores its candidates (agent.rs:398-409). */
+int nh_session_head_logits_sparse(nh_session* s, const uint32_t* ids, int n, float* logits, void* stream);
 /* Model::forward (model.rs:304-306) with Outputs::LastLogits for HOST token
  * ids, fed as forward_native feeds them (crates/needle-engine/src/infer.rs:
  * 1105-1132): chunks of 32 tokens through chunk_job
  * (crates/needle-engine/src/infer/chunk.rs:32-358, the products over the
  * chunk's rows with the prefill combine), a single-token chunk through
  * step_native (crates/needle-engine/src/infer/step.rs:171-760).  `logits`
- * (DEVICE, out_rows floats, or NULL) receives the last token's. */
+ * (DEVICE, out_rows floats, or NULL) receives the last token's; with n = 0
+ * they are the logits the session already holds (NH_EINVAL without any). */
 int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* stream);
 /* The greedy loop of generate (crates/needle-engine/src/generate.rs:87-139)
  * at temperature 0, on the device: `steps` times argmax of the current

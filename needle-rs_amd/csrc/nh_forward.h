@@ -28,19 +28,39 @@ constexpr int ATT_CHUNK_MAX = 256;  // key_chunks never makes a chunk longer
 constexpr int ATT_THREADS = 256;
 constexpr int FWD_ROWS = 32;        // token rows of one feed (a prompt chunk, infer.rs:1105-1132)
 constexpr int ACT_ROWS = 64;        // rows of an A8 buffer (the GEMM reads whole 64-token tiles)
+constexpr int ROLLBACK = 32;        // ROLLBACK (crates/needle-engine/src/model.rs:181-183)
+constexpr int ROPE_RING = 128;      // RoPE rows kept by position (the reference's list holds at most 66)
+constexpr int DG_MAX_TAPS = 8;      // conv taps the unit kernels are written for
+constexpr int SPAN_RUNS = 24;       // runs of live positions an attention span passes to a feed
 
 struct Dims {
     int d, nh, nkv, qk, vd, lanes, taps, layers;
     int W;      // (nh + nkv) * qk + nkv * vd: the pre-tap q | k | v width
     int nq;     // W + nh * vd: the fused q | k | v | gate rows
-    int keep;   // history rows the conv reads: taps - 1 (at least 1)
-    int hist_slots;  // the history ring: keep + FWD_ROWS slots, position p at p % hist_slots
+    int hist_slots;  // the history ring, position p at p % hist_slots: room for every row the
+                     // reference's history can hold, 2 (taps - 1 + ROLLBACK) + FWD_ROWS
     int vocab, out_rows;
     int sites, ntab, eheads, seed_stride, slots, sub, dilation;
     int orders[4];
     int cap;    // session positions
     int vcap;   // row stride of the transposed int8 values: cap + 4 rounded up to 16
     int max_chunks;  // attention chunks a position can need
+    // per-feed state, set by the host before each feed
+    int hist_lo;     // the first position the conv history still holds (LayerState::hist,
+                     // crates/needle-engine/src/infer.rs:968-980): older rows read as zero
+    int rope_prev;   // 1: a single token right after the newest RoPE row (the recurrence)
+    int sink, ring;  // Session::attend (model.rs:62-66); ring 0: no span
+};
+
+// The keys an attention span leaves a feed (key_ranges,
+// crates/needle-engine/src/infer.rs:1781-1826): the runs of positions in
+// [0, sink) and [max(end - ring, sink), end) whose KV slot still holds them
+// (the slot map), ascending.  A query at pos sees these runs cut to
+// [lo, min(sink, pos + 1)) and [min(max(end - ring, sink), pos + 1), pos + 1).
+struct KeySpan {
+    int end;
+    int nrun;
+    int lo[SPAN_RUNS], hi[SPAN_RUNS];
 };
 
 struct LayerDev {
@@ -81,8 +101,10 @@ struct SessDev {
     float* logits;    // [out_rows]
     float* rope_c;    // [rows][qk/2] the feed's RoPE rows
     float* rope_s;
-    float* rope_pc;   // [qk/2] the newest position's RoPE row
-    float* rope_ps;
+    float* rope_rc;   // [ROPE_RING][qk/2] the RoPE rows of recent positions, position p at p % ROPE_RING
+    float* rope_rs;
+    float* hid;       // [rows][d] final normed hidden states of the rows a feed outputs
+    float* last_hid;  // [d] NatState::last_hidden
     uint32_t* tokens; // [cap]
     float* po;        // [rows][nh][max_chunks][vd] attention chunk partials
     float* pm;        // [rows][nh][max_chunks]
@@ -126,13 +148,16 @@ hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, in
 // The per-layer boundary for rows row0 .. row0 + rows - 1: the Hadamard MLP
 // and mHC write of layer `prev` (null: none, the lanes hold the embedding
 // rows), then the mHC read, engram gate, input norm and A8 of layer `next`
-// (null: the head's lane mean, final norm and A8 into activation row 0).
+// (null: the head's lane mean and final norm into hid row i - row0 and its
+// A8 into activation row i - row0).
 hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
                      int row0, int rows, int in_bits, int head_bits, hipStream_t s);
 hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, hipStream_t s);
-hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, hipStream_t s);
+// `span`: the keys of a session with an attention span (null: none).
+hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t,
+                      const KeySpan* span, hipStream_t s);
 hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int p0, int t, int out_bits,
-                        hipStream_t s);
+                        const KeySpan* span, hipStream_t s);
 // One decode token's units, attention, gate and A8 in one launch (the three
 // launches above for a single row), for positions whose keys form one chunk
 // and geometries with 2 or 4 heads per A8 group (dec_group_fits).

@@ -121,6 +121,12 @@ __device__ __forceinline__ void key_chunks(int n, int nkv, bool nested, int& cou
 }
 
 // The attended range of position p0: keys lo..p0.
+// slot_of (infer.rs:1749-1756): the KV slot of position p; the sink keeps
+// its positions, the rest share the ring.
+__device__ __forceinline__ int slot_of(const Dims& D, int p) {
+    return (D.ring > 0 && p >= D.sink) ? (p - D.sink) % D.ring + D.sink : p;
+}
+
 __device__ __forceinline__ int window_lo(int window, int p0) {
     return (window > 0 && p0 + 1 > window) ? p0 + 1 - window : 0;
 }
@@ -134,8 +140,10 @@ __device__ __forceinline__ int window_lo(int window, int p0) {
 // (engram_native, infer.rs:1261-1275) dequantized and rotated (QMat::row),
 // A8-prepared as group g of the site's activation row i (QAct::new over the
 // concatenated rows); missing rows are zeros.  The last wave: the RoPE rows
-// (rope_rows, infer.rs:1716-1747): for one token after a known position the
-// angle-addition recurrence from it, else sincosf(freq * pos) per row.
+// (rope_rows, infer.rs:1716-1747): for one token right after the newest
+// row the reference still keeps (D.rope_prev, the host's mirror of its
+// list) the angle-addition recurrence from that row, else sincosf(freq *
+// pos) per row; every row also goes to the ring of recent rows.
 __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, BeginArgs B, int p0, int t) {
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     const int Gd = (D.d + GROUP - 1) / GROUP;
@@ -179,25 +187,26 @@ __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, Beg
     } else if (wave == t * per_row) {
         const int half = D.qk / 2;
         if (lane < half) {
-            float c, sn;
-            if (t == 1 && p0 > 0) {
-                const float oc = S.rope_pc[lane], os = S.rope_ps[lane];
-                c = __builtin_fmaf(-G.sd[lane], os, G.cd[lane] * oc);
-                sn = __builtin_fmaf(G.sd[lane], oc, G.cd[lane] * os);
+            if (t == 1 && D.rope_prev) {
+                const size_t prev = (size_t)((p0 + ROPE_RING - 1) % ROPE_RING) * half + lane;
+                const float oc = S.rope_rc[prev], os = S.rope_rs[prev];
+                const float c = __builtin_fmaf(-G.sd[lane], os, G.cd[lane] * oc);
+                const float sn = __builtin_fmaf(G.sd[lane], oc, G.cd[lane] * os);
                 S.rope_c[lane] = c;
                 S.rope_s[lane] = sn;
+                S.rope_rc[(size_t)(p0 % ROPE_RING) * half + lane] = c;
+                S.rope_rs[(size_t)(p0 % ROPE_RING) * half + lane] = sn;
             } else {
                 for (int i = 0; i < t; ++i) {
                     double sv, cv;
                     sincos((double)(G.freq[lane] * (float)(p0 + i)), &sv, &cv);
-                    c = (float)cv;
-                    sn = (float)sv;
+                    const float c = (float)cv, sn = (float)sv;
                     S.rope_c[i * half + lane] = c;
                     S.rope_s[i * half + lane] = sn;
+                    S.rope_rc[(size_t)((p0 + i) % ROPE_RING) * half + lane] = c;
+                    S.rope_rs[(size_t)((p0 + i) % ROPE_RING) * half + lane] = sn;
                 }
             }
-            S.rope_pc[lane] = c;
-            S.rope_ps[lane] = sn;
         }
     }
 }
@@ -907,9 +916,9 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, con
     }
 }
 
-// The head's input (step.rs:706-728): lane mean, zcn with the f32 final
-// norm, A8.
-__device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_bits, LayerShared& sh) {
+// The head's input (step.rs:706-728, chunk.rs:331-347): lane mean, zcn with
+// the f32 final norm into `hid`, A8 into activation row `arow`.
+__device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_bits, int arow, LayerShared& sh) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
     float mean = 0.0f;
     if (t < d) {
@@ -921,15 +930,17 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
         const float r = block_rinv_t(sh.tA, TP_D, d, &sh.r_a);
         if (t < d) {
             const float tt = mean * r;
-            sh.x2[t] = __builtin_fmaf(tt, fnorm, tt);
+            const float h = __builtin_fmaf(tt, fnorm, tt);
+            sh.x2[t] = h;
+            S.hid[(size_t)arow * d + t] = h;
         }
     }
     __syncthreads();
     const int groups = (d + GROUP - 1) / GROUP;
     for (int g = wave; g < groups; g += LT / 64) {
         const int p0 = g * GROUP + lane, p1 = p0 + 64;
-        a8_group(p0 < d ? sh.x2[p0] : 0.0f, p1 < d ? sh.x2[p1] : 0.0f, lane, head_bits, S.xq_in + (size_t)g * GROUP,
-                 S.sx_in + g);
+        a8_group(p0 < d ? sh.x2[p0] : 0.0f, p1 < d ? sh.x2[p1] : 0.0f, lane, head_bits,
+                 S.xq_in + ((size_t)arow * groups + g) * GROUP, S.sx_in + (size_t)arow * groups + g);
     }
 }
 
@@ -991,7 +1002,7 @@ __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, Laye
     if constexpr (has_next)
         layer_in(D, R, N, qi, in_bits, sh);
     else
-        head_in(D, S, fnorm, head_bits, sh);  // A8 into activation row 0
+        head_in(D, S, fnorm, head_bits, blockIdx.x, sh);  // row i - row0
     if constexpr (has_prev) {
 #pragma unroll
         for (int k = 0; k < MHC_LANES; ++k)
@@ -1060,7 +1071,6 @@ __device__ __forceinline__ void post_gates(float* p, const LayerDev& L, int lane
     }
 }
 
-constexpr int DG_MAX_TAPS = 8;  // conv taps the unit kernels specialise up to
 
 // A unit's inputs for lane i of feed row `row` (position pos): the pre-tap
 // value, the taps, the earlier pre-tap rows (rows of the same feed from the
@@ -1105,8 +1115,9 @@ __device__ __forceinline__ UnitIn unit_load(const Dims& D, const SessDev& S, int
 
 // The unit's post-tap value (zcn16 and RoPE when `normed`): the causal conv
 // over the row and the earlier pre-tap rows, v = w0 cur, then
-// fma(w_j, row_{pos - j}, v) (a row before position 0 is zero); the row's
-// pre-tap value goes to the ring at pos.
+// fma(w_j, row_{pos - j}, v) (a row the history no longer holds, before
+// D.hist_lo, is zero; hist_lo <= the feed's first position, so rows of the
+// feed always count); the row's pre-tap value goes to the ring at pos.
 template <int TAPS, bool EXACT>
 __device__ __forceinline__ float unit_finish(const Dims& D, const SessDev& S, int layer, int pos, int start, int len,
                                              const UnitIn& u, bool normed, int i, bool write_hist) {
@@ -1115,7 +1126,7 @@ __device__ __forceinline__ float unit_finish(const Dims& D, const SessDev& S, in
         v = h2f(u.w[0]) * u.cur;
 #pragma unroll
         for (int j = 1; j < TAPS; ++j)
-            if (EXACT || j < D.taps) v = __builtin_fmaf(h2f(u.w[j]), pos >= j ? u.h[j] : 0.0f, v);
+            if (EXACT || j < D.taps) v = __builtin_fmaf(h2f(u.w[j]), pos - j >= D.hist_lo ? u.h[j] : 0.0f, v);
         if (write_hist) S.hist[((size_t)layer * D.hist_slots + pos % D.hist_slots) * D.W + start + i] = u.cur;
     }
     if (normed) {
@@ -1176,14 +1187,20 @@ __global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, Lay
         const float s = wave_quant_scale(i < len ? v : 0.0f);
         const int8_t q = quant_one(v, 1.0f / s);
         const size_t lc = (size_t)layer * D.cap;
+        const int slot = slot_of(D, pos);
+        // A ring shorter than the feed gives two of its rows one slot: the
+        // later position keeps it (the slot map says so; the reference's
+        // members would race there).
+        const bool taken = D.ring > 0 && pos >= D.sink && pos + D.ring < p0 + t;
+        if (taken) return;
         if (unit < nh + nkv) {
             const int kh = unit - nh;
-            if (i < qk) S.k8[((lc + pos) * nkv + kh) * qk + i] = q;
-            if (i == 0) S.ks[(lc + pos) * nkv + kh] = s;
+            if (i < qk) S.k8[((lc + slot) * nkv + kh) * qk + i] = q;
+            if (i == 0) S.ks[(lc + slot) * nkv + kh] = s;
         } else {
             const int vh = unit - nh - nkv;
-            if (i < vd) S.v8t[(((size_t)layer * nkv + vh) * vd + i) * D.vcap + pos] = q;
-            if (i == 0) S.vs[(lc + pos) * nkv + vh] = s;
+            if (i < vd) S.v8t[(((size_t)layer * nkv + vh) * vd + i) * D.vcap + slot] = q;
+            if (i == 0) S.vs[(lc + slot) * nkv + vh] = s;
         }
     }
 }
@@ -1224,21 +1241,80 @@ __device__ __forceinline__ int quad_sum_i32(int v) {
 // before the chunk's first slot; the digits are shifted by the same
 // offset, so bytes before the first key meet zero digits), and P.V runs
 // four keys per sdot4.
+// The two coarse key ranges of a query at pos under an attention span
+// (key_ranges, infer.rs:1781-1791): [lo, max(lo, min(sink, pos + 1))) and
+// [min(max(end - ring, sink), pos + 1), pos + 1); the ring part is not cut
+// by the layer's window.
+__device__ __forceinline__ void span_ranges(const Dims& D, const KeySpan& K, int lo, int pos, int& alo, int& ahi,
+                                            int& blo, int& bhi) {
+    alo = lo;
+    ahi = max(lo, min(D.sink, pos + 1));
+    blo = min(max(K.end - D.ring, D.sink), pos + 1);
+    bhi = pos + 1;
+}
+
+__device__ __forceinline__ int span_overlap(int lo, int hi, int a, int b) { return max(0, min(hi, b) - max(lo, a)); }
+
+// The number of keys: the span's live runs cut to the two ranges.
+__device__ __forceinline__ int span_count(const KeySpan& K, int alo, int ahi, int blo, int bhi) {
+    int n = 0;
+    for (int r = 0; r < K.nrun; ++r)
+        n += span_overlap(K.lo[r], K.hi[r], alo, ahi) + span_overlap(K.lo[r], K.hi[r], blo, bhi);
+    return n;
+}
+
+// The position of key k (ascending: every position of the first range lies
+// below the sink, every one of the second at or past it).
+__device__ __forceinline__ int span_key(const KeySpan& K, int alo, int ahi, int blo, int bhi, int k) {
+    for (int r = 0; r < K.nrun; ++r) {
+        const int ca = span_overlap(K.lo[r], K.hi[r], alo, ahi);
+        if (k < ca) return max(K.lo[r], alo) + k;
+        k -= ca;
+        const int cb = span_overlap(K.lo[r], K.hi[r], blo, bhi);
+        if (k < cb) return max(K.lo[r], blo) + k;
+        k -= cb;
+    }
+    return 0;
+}
+
+// The key count of a query at pos: every position from the window's start
+// without a span.
+__device__ __forceinline__ int key_count(const Dims& D, const KeySpan& K, bool span, int window, int pos) {
+    const int lo = window_lo(window, pos);
+    if (!span) return pos + 1 - lo;
+    int alo, ahi, blo, bhi;
+    span_ranges(D, K, lo, pos, alo, ahi, blo, bhi);
+    return span_count(K, alo, ahi, blo, bhi);
+}
+
 constexpr int ATT_KPITCH = MAX_HEAD_DIM + 16;        // key row (80 bytes: 8 rows cover the 32 banks)
 constexpr int ATT_PITCH = ATT_CHUNK_MAX + 8;         // value / digit row: 3 alignment bytes + 256 keys + tail
 constexpr int ATT_VDW = (ATT_CHUNK_MAX + 3 + 3) / 4; // value dwords per column
 
-__global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, LayerDev L, int layer, int p0,
-                                                       int rows) {
+//
+// With an attention span (SPAN) the keys are the span's live positions (the
+// reference's key runs) in their KV slots (slot_of): each key's slot is
+// found first, then the key rows, scales and value bytes are gathered from
+// those slots (value column j = key j, no alignment offset).
+template <bool SPAN>
+__global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, LayerDev L, int layer, int p0, int rows,
+                                                        KeySpan K) {
     const int row = blockIdx.x / D.nh, hh = blockIdx.x % D.nh, ci = blockIdx.y, t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63, pos = p0 + row;
     const int nkv = D.nkv, qk = D.qk, vd = D.vd, kvh = hh / (D.nh / nkv);
-    const int lo = window_lo(L.window, pos), n = pos + 1 - lo;
+    const int lo = window_lo(L.window, pos);
+    int alo = 0, ahi = 0, blo = 0, bhi = 0, n;
+    if constexpr (SPAN) {
+        span_ranges(D, K, lo, pos, alo, ahi, blo, bhi);
+        n = span_count(K, alo, ahi, blo, bhi);
+    } else {
+        n = pos + 1 - lo;
+    }
     int count, chunk;
     key_chunks(n, nkv, rows > 1, count, chunk);
     if (ci >= count) return;
     const int c0 = ci * chunk, len = min(chunk, n - c0), blocked = len / 4 * 4, slot0 = lo + c0;
-    const int sh = slot0 & 3, base = slot0 - sh, cols = sh + len;
+    const int sh = SPAN ? 0 : slot0 & 3, base = slot0 - sh, cols = sh + len;
     __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][ATT_KPITCH];
     __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][ATT_PITCH];
     __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
@@ -1247,54 +1323,81 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     __shared__ alignas(16) int8_t dig[3][ATT_PITCH];
     __shared__ float red[ATT_THREADS / 64];
     __shared__ float s_qs, s_sum;
+    __shared__ int kslot[SPAN ? ATT_CHUNK_MAX : 1];
     const size_t lc = (size_t)layer * D.cap;
     // every load first (unconditional, at clamped in-range addresses)
     const float qv = S.qbuf[((size_t)row * D.nh + hh) * qk + min(lane, qk - 1)];
     constexpr int KR = ATT_CHUNK_MAX * 4 / ATT_THREADS, VR = (MAX_HEAD_DIM * ATT_VDW + ATT_THREADS - 1) / ATT_THREADS;
     const int rq = qk / 16, vdw = (cols + 3) / 4;
-    uint4 kr[KR];
-    uint32_t vw[VR];
+    if constexpr (SPAN) {
+        if (t < len) kslot[t] = slot_of(D, span_key(K, alo, ahi, blo, bhi, c0 + t));
+        __syncthreads();
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
-        const int e = t + r * ATT_THREADS, i = min(e >> 2, len - 1), c = min(e & 3, rq - 1);
-        kr[r] = reinterpret_cast<const uint4*>(S.k8 + ((lc + slot0 + i) * nkv + kvh) * qk)[c];
-    }
-    float ksr, vsr;
-    {
-        const int i = min(t, len - 1);
-        ksr = S.ks[(lc + slot0 + i) * nkv + kvh];
-        vsr = S.vs[(lc + slot0 + i) * nkv + kvh];
-    }
-    const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
+        for (int r = 0; r < KR; ++r) {
+            const int e = t + r * ATT_THREADS, i = e >> 2, c = e & 3;
+            if (i < len && c < rq)
+                reinterpret_cast<uint4*>(ks8[i])[c] =
+                    reinterpret_cast<const uint4*>(S.k8 + ((lc + kslot[i]) * nkv + kvh) * qk)[c];
+        }
+        if (t < len) {
+            kss[t] = S.ks[(lc + kslot[t]) * nkv + kvh];
+            vss[t] = S.vs[(lc + kslot[t]) * nkv + kvh];
+        }
+        const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap;
+        for (int e = t; e < vd * len; e += ATT_THREADS) {
+            const int dm = e / len, i = e % len;
+            vs8[dm][i] = vcol[(size_t)dm * D.vcap + kslot[i]];
+        }
+        if (wave == 0) {
+            const float s = wave_quant_scale(lane < qk ? qv : 0.0f);
+            if (lane < qk) q8[lane] = quant_one(qv, 1.0f / s);
+            if (lane == 0) s_qs = s * bits_f32(0x3e13cd3au);
+        }
+    } else {
+        uint4 kr[KR];
+        uint32_t vw[VR];
 #pragma unroll
-    for (int r = 0; r < VR; ++r) {
-        const int e = t + r * ATT_THREADS, dm = min(e / ATT_VDW, vd - 1), k = min(e % ATT_VDW, vdw - 1);
-        vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
-    }
-    if (wave == 0) {
-        const float s = wave_quant_scale(lane < qk ? qv : 0.0f);
-        if (lane < qk) q8[lane] = quant_one(qv, 1.0f / s);
-        if (lane == 0) s_qs = s * bits_f32(0x3e13cd3au);
-    }
+        for (int r = 0; r < KR; ++r) {
+            const int e = t + r * ATT_THREADS, i = min(e >> 2, len - 1), c = min(e & 3, rq - 1);
+            kr[r] = reinterpret_cast<const uint4*>(S.k8 + ((lc + slot0 + i) * nkv + kvh) * qk)[c];
+        }
+        float ksr, vsr;
+        {
+            const int i = min(t, len - 1);
+            ksr = S.ks[(lc + slot0 + i) * nkv + kvh];
+            vsr = S.vs[(lc + slot0 + i) * nkv + kvh];
+        }
+        const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
-        const int e = t + r * ATT_THREADS, i = e >> 2, c = e & 3;
-        if (i < len && c < rq) reinterpret_cast<uint4*>(ks8[i])[c] = kr[r];
-    }
-    if (t < len) {
-        kss[t] = ksr;
-        vss[t] = vsr;
-    }
+        for (int r = 0; r < VR; ++r) {
+            const int e = t + r * ATT_THREADS, dm = min(e / ATT_VDW, vd - 1), k = min(e % ATT_VDW, vdw - 1);
+            vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
+        }
+        if (wave == 0) {
+            const float s = wave_quant_scale(lane < qk ? qv : 0.0f);
+            if (lane < qk) q8[lane] = quant_one(qv, 1.0f / s);
+            if (lane == 0) s_qs = s * bits_f32(0x3e13cd3au);
+        }
 #pragma unroll
-    for (int r = 0; r < VR; ++r) {
-        const int e = t + r * ATT_THREADS, dm = e / ATT_VDW, k = e % ATT_VDW;
-        if (dm < vd && k < vdw) {
-            if (4 * k + 3 < cols) {
-                reinterpret_cast<uint32_t*>(vs8[dm])[k] = vw[r];
-            } else {
+        for (int r = 0; r < KR; ++r) {
+            const int e = t + r * ATT_THREADS, i = e >> 2, c = e & 3;
+            if (i < len && c < rq) reinterpret_cast<uint4*>(ks8[i])[c] = kr[r];
+        }
+        if (t < len) {
+            kss[t] = ksr;
+            vss[t] = vsr;
+        }
 #pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    if (4 * k + b < cols) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
+        for (int r = 0; r < VR; ++r) {
+            const int e = t + r * ATT_THREADS, dm = e / ATT_VDW, k = e % ATT_VDW;
+            if (dm < vd && k < vdw) {
+                if (4 * k + 3 < cols) {
+                    reinterpret_cast<uint32_t*>(vs8[dm])[k] = vw[r];
+                } else {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        if (4 * k + b < cols) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
+                }
             }
         }
     }
@@ -1435,18 +1538,25 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     }
 }
 
-hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, hipStream_t s) {
-    hipLaunchKernelGGL(k_attend, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer, p0, t);
+hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t,
+                      const KeySpan* span, hipStream_t s) {
+    if (span)
+        hipLaunchKernelGGL(k_attend<true>, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer, p0,
+                           t, *span);
+    else
+        hipLaunchKernelGGL(k_attend<false>, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer,
+                           p0, t, KeySpan{});
     return hipGetLastError();
 }
 
 // The chunk merge (infer.rs:1990-2006), the head gate
 // (att / (nexp(-gate) + 1), step.rs:558-572) and A8 of the heads.
-__global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, int p0, int rows, int out_bits) {
+__global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, int p0, int rows, int out_bits,
+                                                 KeySpan KS, int span) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, vd = D.vd, K = D.nh * vd;
     const int row = blockIdx.x, pos = p0 + row, Ga = (K + GROUP - 1) / GROUP;
     __shared__ float att[FWD_MAX_D];
-    const int lo = window_lo(L.window, pos), n = pos + 1 - lo;
+    const int n = key_count(D, KS, span != 0, L.window, pos);
     int count, chunk;
     key_chunks(n, D.nkv, rows > 1, count, chunk);
     if (t < K) {
@@ -1480,8 +1590,9 @@ __global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, 
 }
 
 hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int p0, int t, int out_bits,
-                        hipStream_t s) {
-    hipLaunchKernelGGL(k_attn_out, dim3(t), dim3(LT), 0, s, D, S, L, p0, t, out_bits);
+                        const KeySpan* span, hipStream_t s) {
+    hipLaunchKernelGGL(k_attn_out, dim3(t), dim3(LT), 0, s, D, S, L, p0, t, out_bits, span ? *span : KeySpan{},
+                       span ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -1572,7 +1683,7 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
     const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
 #pragma unroll
     for (int r = 0; r < VR; ++r) {
-        const int e = t + r * NT, dm = min(e / DG_VDW, vd - 1), k = min(e % DG_VDW, vdw - 1);
+        const int e = t + r * NT, dm = min(e / DG_VDW, vd - 1), k = min(e % DG_VDW, max(vdw - 1, 0));
         vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
     }
     // the units
@@ -1782,7 +1893,7 @@ bool dec_group_fits(const Dims& D, int p0, int window) {
     if (k < 1) k = 1;
     int c = (n + 255) / 256;
     if (k * 64 <= n && c < k) c = k;
-    if (c > 1 || n > ATT_CHUNK_MAX) return false;
+    if (c > 1 || n > ATT_CHUNK_MAX || D.ring > 0) return false;
     if (GROUP % D.vd != 0 || D.taps > DG_MAX_TAPS) return false;
     const int hp = GROUP / D.vd;
     return (hp == 2 || hp == 4) && D.nh % hp == 0 && (D.nh / D.nkv) % hp == 0 && D.qk % 16 == 0;

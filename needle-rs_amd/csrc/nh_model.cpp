@@ -129,8 +129,19 @@ struct nh_session {
     nh::Dims dims{};
     nh::SessDev S{};
     void* d_buf = nullptr;
+    size_t bytes = 0;
     int len = 0;
-    bool have_logits = false;
+    bool have_logits = false;  // S.logits holds the logits of position len - 1
+    bool have_hidden = false;  // S.last_hid holds NatState::last_hidden
+    // Host mirrors of the reference's session state: the rows LayerState::
+    // hist holds (the same in every layer, infer.rs:968-980), the length of
+    // NatState::rope (infer.rs:1716-1747), Session::attend and the slot map
+    // (model.rs:62-66, infer.rs:1000-1006), and the token ids.
+    int hrows = 0;
+    int rope_n = 0;
+    int sink = 0, ring = 0;
+    std::vector<int64_t> slot_pos;
+    std::vector<uint32_t> toks;
     nh_qact a_in{}, a_att{};
     std::vector<nh_qact> a_eng;
 
@@ -175,9 +186,12 @@ int check_geometry(nh_model* m, const nh::ArchiveSmall& sm) {
     const int qd = D.nh * D.qk, kd = D.nkv * D.qk, vdim = D.nkv * D.vd;
     D.W = qd + kd + vdim;
     D.nq = D.W + D.nh * D.vd;
-    D.keep = D.taps > 1 ? D.taps - 1 : 1;
-    D.hist_slots = D.keep + nh::FWD_ROWS;
     if (D.taps <= 0) return fail(NH_EINVAL, "the decode step needs qkv conv taps");
+    if (D.taps > nh::DG_MAX_TAPS)
+        return fail(NH_EINVAL, "the decode step takes at most " + std::to_string(nh::DG_MAX_TAPS) + " qkv conv taps");
+    // every row the reference's history can hold (rows <= 2 keep at rest,
+    // keep = taps - 1 + ROLLBACK, step.rs:706-712), plus a feed's rows
+    D.hist_slots = 2 * (D.taps - 1 + nh::ROLLBACK) + nh::FWD_ROWS;
     // engram geometry (config.rs:273-288 with heads = tables / orders, cact.rs:191)
     if (D.sites > nh::MAX_SITES || norders > 4) return fail(NH_EINVAL, "corrupt engram geometry");
     if (D.sites > 0) {
@@ -415,14 +429,99 @@ hipError_t product(const nh_qmat* w, nh_qact* a, int rows, float* y, int ldy, hi
     return rows == 1 ? nh::launch_gemv(w, a, y, 0, nullptr, st) : nh::launch_gemm(w, a, nullptr, y, ldy, 0, nullptr, st);
 }
 
+// slot_of (crates/needle-engine/src/infer.rs:1749-1756).
+int slot_of(const nh_session* s, int p) { return (s->ring > 0 && p >= s->sink) ? (p - s->sink) % s->ring + s->sink : p; }
+
+// mark_slots (infer.rs:1770-1779).
+void mark_slots(nh_session* s, int p0, int end) {
+    for (int p = p0; p < end; ++p) {
+        const int sl = slot_of(s, p);
+        if ((int)s->slot_pos.size() <= sl) s->slot_pos.resize(sl + 1, -1);
+        s->slot_pos[sl] = p;
+    }
+}
+
+bool live(const nh_session* s, int p) {
+    const int sl = slot_of(s, p);
+    return sl < (int)s->slot_pos.size() && s->slot_pos[sl] == p;
+}
+
+// The span's keys for a feed ending at `end` (key_ranges, infer.rs:1781-1826):
+// the live runs of [0, sink) and [max(end - ring, sink), end), and per row
+// the reference's own run count, which it asserts stays within KEY_RUNS
+// (16, infer.rs:1760,1806-1808).
+int span_keys(const nh_session* s, const nh::Dims& D, const std::vector<nh::LayerDev>& layers, int p0, int end,
+              nh::KeySpan* K) {
+    *K = nh::KeySpan{};
+    K->end = end;
+    const int b0 = std::max(end - s->ring, s->sink);
+    auto scan = [&](int lo, int hi) -> int {
+        int a = -1;
+        for (int p = lo; p <= hi; ++p) {
+            const bool ok = p < hi && live(s, p);
+            if (ok && a < 0) a = p;
+            if (!ok && a >= 0) {
+                if (K->nrun == nh::SPAN_RUNS) return fail(NH_EINVAL, "attention span: too many runs of live keys");
+                K->lo[K->nrun] = a, K->hi[K->nrun] = p, ++K->nrun, a = -1;
+            }
+        }
+        return NH_OK;
+    };
+    if (int rc = scan(0, std::min(s->sink, end))) return rc;
+    if (int rc = scan(std::max(b0, std::min(s->sink, end)), end)) return rc;
+    // the reference's runs per query row: its coarse ranges cut by liveness
+    std::vector<int> windows;
+    for (const auto& L : layers)
+        if (std::find(windows.begin(), windows.end(), L.window) == windows.end()) windows.push_back(L.window);
+    for (int pos = p0; pos < end; ++pos)
+        for (int w : windows) {
+            const int lo = (w > 0 && pos + 1 > w) ? pos + 1 - w : 0;
+            const int ranges[2][2] = {{lo, std::max(lo, std::min(s->sink, pos + 1))},
+                                      {std::min(b0, pos + 1), pos + 1}};
+            int runs = 0;
+            for (const auto& r : ranges) {
+                bool open = false;
+                for (int p = r[0]; p < r[1]; ++p) {
+                    const bool ok = live(s, p);
+                    if (ok && !open) ++runs;
+                    open = ok;
+                }
+            }
+            if (runs > 16) return fail(NH_EINVAL, "attention span: a query sees more than 16 key runs");
+        }
+    (void)D;
+    return NH_OK;
+}
+
+// Rows an output mode returns for a feed of t tokens (chunk.rs:331-335).
+int out_rows_of(int outputs, int t) {
+    return outputs == NH_OUT_NONE ? 0 : (outputs == NH_OUT_ALL_LOGITS || outputs == NH_OUT_HIDDEN) ? t : 1;
+}
+
+int out_width(const nh_session* s, int outputs) {
+    return (outputs == NH_OUT_HIDDEN || outputs == NH_OUT_LAST_HIDDEN) ? s->dims.d : s->dims.out_rows;
+}
+
 // One feed of t <= 32 tokens at positions s->len ..: step_native for one
-// token, chunk_job for more (forward_native, infer.rs:1105-1132); the head
-// of the last row when `logits`.
-int feed(nh_session* s, int t, bool logits, hipStream_t st) {
+// token, chunk_job for more (forward_native, infer.rs:1105-1132); `outputs`
+// picks what the rows give (chunk.rs:331-353, step.rs:715-729), written to
+// `out` (device, rows x width, or null to keep only the session's copies).
+int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
     const nh_model* m = s->m;
-    const nh::Dims& D = s->dims;
     const nh::SessDev& S = s->S;
     const int p0 = s->len;
+    nh::Dims D = s->dims;
+    D.hist_lo = p0 - s->hrows;
+    D.rope_prev = t == 1 && s->rope_n > 0;
+    D.sink = s->sink;
+    D.ring = s->ring;
+    mark_slots(s, p0, p0 + t);
+    nh::KeySpan span{};
+    const nh::KeySpan* sp = nullptr;
+    if (s->ring > 0) {
+        if (int rc = span_keys(s, D, m->layers, p0, p0 + t, &span)) return rc;
+        sp = &span;
+    }
     NH_TRY(nh::fwd_begin(D, m->glob, S, m->begin, p0, t, st), "feed begin");
     if (t == 1 && D.sites > 1 && nh::gemv_batchable(m->ekv.data(), D.sites)) {
         // every site's key | value product in one launch
@@ -448,16 +547,92 @@ int feed(nh_session* s, int t, bool logits, hipStream_t st) {
             NH_TRY(nh::fwd_dec_attn(D, S, m->layers[l], l, p0, m->out[l]->m.bits, st), "decode attention");
         } else {
             NH_TRY(nh::fwd_units(D, S, m->layers[l], l, p0, t, st), "units");
-            NH_TRY(nh::fwd_attend(D, S, m->layers[l], l, p0, t, st), "attend");
-            NH_TRY(nh::fwd_attn_out(D, S, m->layers[l], p0, t, m->out[l]->m.bits, st), "attention out");
+            NH_TRY(nh::fwd_attend(D, S, m->layers[l], l, p0, t, sp, st), "attend");
+            NH_TRY(nh::fwd_attn_out(D, S, m->layers[l], p0, t, m->out[l]->m.bits, sp, st), "attention out");
         }
         NH_TRY(product(m->out[l], &s->a_att, t, S.o, D.d, st), "out");
     }
-    const nh::LayerDev* last = D.layers > 0 ? &m->layers[D.layers - 1] : nullptr;
-    NH_TRY(nh::fwd_layer(D, m->glob, S, last, nullptr, t - 1, 1, 0, m->head_bits, st), "head input");
-    if (logits) NH_TRY(product(m->head, &s->a_in, 1, S.logits, D.out_rows, st), "head");
+    // the last layer's post block, the lane mean and final norm of the rows
+    // the outputs want, then the head (head_logits per row, decode combine)
+    const int rows = out_rows_of(outputs, t), row0 = t - rows;
+    const int d = D.d, Gd = (d + nh::GROUP - 1) / nh::GROUP;
+    if (rows > 0) {
+        const nh::LayerDev* last = D.layers > 0 ? &m->layers[D.layers - 1] : nullptr;
+        NH_TRY(nh::fwd_layer(D, m->glob, S, last, nullptr, row0, rows, 0, m->head_bits, st), "head input");
+        const bool logits = outputs == NH_OUT_LAST_LOGITS || outputs == NH_OUT_ALL_LOGITS;
+        for (int i = 0; i < rows && logits; ++i) {
+            nh_qact a = s->a_in;
+            a.d_xq += (size_t)i * Gd * nh::GROUP;
+            a.d_sx += (size_t)i * Gd;
+            float* y = (outputs == NH_OUT_ALL_LOGITS && out) ? out + (size_t)i * D.out_rows : S.logits;
+            NH_TRY(product(m->head, &a, 1, y, D.out_rows, st), "head");
+            if (i == rows - 1 && y != S.logits)
+                NH_TRY(hipMemcpyAsync(S.logits, y, (size_t)D.out_rows * 4, hipMemcpyDeviceToDevice, st), "logits");
+        }
+        if (out && !logits)
+            NH_TRY(hipMemcpyAsync(out, S.hid, (size_t)rows * d * 4, hipMemcpyDeviceToDevice, st), "hidden");
+        if (out && outputs == NH_OUT_LAST_LOGITS)
+            NH_TRY(hipMemcpyAsync(out, S.logits, (size_t)D.out_rows * 4, hipMemcpyDeviceToDevice, st), "logits");
+        NH_TRY(hipMemcpyAsync(S.last_hid, S.hid + (size_t)(rows - 1) * d, (size_t)d * 4, hipMemcpyDeviceToDevice, st),
+               "last hidden");
+        s->have_logits = logits;
+        s->have_hidden = true;
+    } else {
+        s->have_logits = false;
+    }
+    // the host mirrors: the history rows and their trim (chunk.rs:319-329),
+    // the RoPE list and its trim (rope_rows, infer.rs:1740-1745)
     s->len = p0 + t;
-    s->have_logits = logits;
+    const int keep = D.taps - 1 + nh::ROLLBACK;
+    s->hrows += t;
+    if (s->hrows > 2 * keep) s->hrows = keep;
+    s->rope_n += t;
+    if (s->rope_n > 2 * (nh::ROLLBACK + 1)) s->rope_n = nh::ROLLBACK + 1;
+    return rows;
+}
+
+// Model::forward_native (infer.rs:1105-1132) over host token ids: chunks of
+// 32, a one-token chunk as a step, LastLogits / LastHidden from the last
+// chunk only.  Returns the rows written.
+int forward_ids(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, hipStream_t st) {
+    NH_TRY(hipMemcpyAsync(s->S.tokens + s->len, toks, (size_t)n * 4, hipMemcpyHostToDevice, st), "tokens");
+    NH_TRY(hipStreamSynchronize(st), "tokens");
+    s->toks.resize(s->len);
+    s->toks.insert(s->toks.end(), toks, toks + n);
+    const int width = out_width(s, outputs);
+    int rows = 0;
+    for (int i = 0; i < n; i += nh::FWD_ROWS) {
+        const int t = std::min(nh::FWD_ROWS, n - i);
+        const bool last = i + t == n;
+        const int want =
+            (!last && (outputs == NH_OUT_LAST_LOGITS || outputs == NH_OUT_LAST_HIDDEN)) ? NH_OUT_NONE : outputs;
+        const int r = feed(s, t, want, out ? out + (size_t)rows * width : nullptr, st);
+        if (r < 0) {
+            // The device caches hold part of the feed (the reference would
+            // have panicked): the session starts over rather than keep them.
+            const std::string msg = nh_last_error();
+            nh_session_reset(s);
+            return fail(r, msg + " (the session was reset)");
+        }
+        rows += r;
+    }
+    return rows;
+}
+
+int check_feed(nh_session* s, const uint32_t* toks, int n, int outputs) {
+    if (!s || (n > 0 && !toks) || n < 0) return fail(NH_EINVAL, "bad arguments");
+    if (outputs < NH_OUT_NONE || outputs > NH_OUT_LAST_HIDDEN) return fail(NH_EINVAL, "unknown outputs mode");
+    if (!nh::ready()) return fail(NH_ESTATE, "nh_init has not been called");
+    if (s->len + n > s->dims.cap) return fail(NH_EINVAL, "the tokens do not fit the session's capacity");
+    for (int i = 0; i < n; ++i)
+        if (toks[i] >= (uint32_t)s->dims.vocab) return fail(NH_EINVAL, "token id outside the vocabulary");
+    return NH_OK;
+}
+
+int check_out(const nh_session* s, int n, int outputs, const float* out, int64_t out_cap) {
+    const int rows = n == 0 ? 0 : out_rows_of(outputs, n);
+    if (out && (int64_t)rows * out_width(s, outputs) > out_cap)
+        return fail(NH_ESMALL, "the output buffer is too small");
     return NH_OK;
 }
 
@@ -520,14 +695,16 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     for (int n = 1; n <= cap; ++n) mc = std::max(mc, key_chunk_count(n, D.nkv));
     D.max_chunks = mc;
     const size_t d = D.d, L = D.layers, c = cap, E = D.sites, R = nh::FWD_ROWS, AR = nh::ACT_ROWS;
+    const size_t half = D.qk / 2;
     const int Gd = (D.d + nh::GROUP - 1) / nh::GROUP, Ga = (D.nh * D.vd + nh::GROUP - 1) / nh::GROUP;
     Layout Y;
     const size_t o_xs = Y.take(R * 4 * d * 4), o_u = Y.take(R * d * 4), o_x1 = Y.take(R * d * 4);
     const size_t o_p = Y.take(R * 64 * 4), o_proj = Y.take(R * D.nq * 4), o_q = Y.take(R * D.nh * D.qk * 4);
     const size_t o_o = Y.take(R * d * 4), o_ekv = Y.take(E * R * 2 * d * 4), o_ev = Y.take(E * R * d * 4);
     const size_t o_lg = Y.take(round_up(D.out_rows, nh::PANEL_ROWS) * 4);
-    const size_t o_rc = Y.take(R * (D.qk / 2) * 4), o_rs = Y.take(R * (D.qk / 2) * 4);
-    const size_t o_rpc = Y.take(D.qk / 2 * 4), o_rps = Y.take(D.qk / 2 * 4), o_tok = Y.take(c * 4);
+    const size_t o_rc = Y.take(R * half * 4), o_rs = Y.take(R * half * 4);
+    const size_t o_rrc = Y.take(nh::ROPE_RING * half * 4), o_rrs = Y.take(nh::ROPE_RING * half * 4);
+    const size_t o_hid = Y.take(R * d * 4), o_lh = Y.take(d * 4), o_tok = Y.take(c * 4);
     const size_t o_po = Y.take(R * D.nh * mc * D.vd * 4), o_pm = Y.take(R * D.nh * mc * 4),
                  o_ps = Y.take(R * D.nh * mc * 4);
     const size_t o_hist = Y.take(L * D.hist_slots * D.W * 4);
@@ -545,13 +722,15 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
         delete s;
         return fail(NH_ENOMEM, std::string("session allocation: ") + hipGetErrorString(e));
     }
+    s->bytes = Y.size;
     uint8_t* b = (uint8_t*)s->d_buf;
     nh::SessDev& S = s->S;
     S.xs = (float*)(b + o_xs), S.u = (float*)(b + o_u), S.x1 = (float*)(b + o_x1), S.p = (float*)(b + o_p);
     S.proj = (float*)(b + o_proj), S.qbuf = (float*)(b + o_q), S.o = (float*)(b + o_o);
     S.ekv = (float*)(b + o_ekv), S.evals = (float*)(b + o_ev), S.logits = (float*)(b + o_lg);
     S.rope_c = (float*)(b + o_rc), S.rope_s = (float*)(b + o_rs), S.tokens = (uint32_t*)(b + o_tok);
-    S.rope_pc = (float*)(b + o_rpc), S.rope_ps = (float*)(b + o_rps);
+    S.rope_rc = (float*)(b + o_rrc), S.rope_rs = (float*)(b + o_rrs);
+    S.hid = (float*)(b + o_hid), S.last_hid = (float*)(b + o_lh);
     S.po = (float*)(b + o_po), S.pm = (float*)(b + o_pm), S.psum = (float*)(b + o_ps);
     S.hist = (float*)(b + o_hist), S.k8 = (int8_t*)(b + o_k8), S.ks = (float*)(b + o_ks);
     S.v8t = (int8_t*)(b + o_v8), S.vs = (float*)(b + o_vs), S.ev8 = (int8_t*)(b + o_e8), S.evs = (float*)(b + o_es);
@@ -590,23 +769,150 @@ int nh_session_len(const nh_session* s) {
 int nh_session_reset(nh_session* s) {
     if (!s) return fail(NH_EINVAL, "null session");
     s->len = 0;
+    s->have_logits = s->have_hidden = false;
+    s->hrows = s->rope_n = 0;
+    s->sink = s->ring = 0;
+    s->slot_pos.clear();
+    s->toks.clear();
+    return NH_OK;
+}
+
+int nh_session_clone(const nh_session* s, void* stream, nh_session** out) {
+    if (!s || !out) return fail(NH_EINVAL, "null argument");
+    *out = nullptr;
+    nh_session* c = nullptr;
+    if (int rc = nh_session_new(s->m, s->dims.cap, &c)) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    hipError_t e = hipMemcpyAsync(c->d_buf, s->d_buf, s->bytes, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        delete c;
+        return hip_fail(e, "session clone");
+    }
+    c->len = s->len;
+    c->have_logits = s->have_logits;
+    c->have_hidden = s->have_hidden;
+    c->hrows = s->hrows;
+    c->rope_n = s->rope_n;
+    c->sink = s->sink;
+    c->ring = s->ring;
+    c->slot_pos = s->slot_pos;
+    c->toks = s->toks;
+    *out = c;
+    return NH_OK;
+}
+
+int nh_session_set_attend(nh_session* s, int sink, int ring) {
+    if (!s || sink < 0 || ring < 0) return fail(NH_EINVAL, "bad arguments");
+    // A shorter ring would give two rows of a 32-token chunk one KV slot (the
+    // reference's team races on it) and could leave a row no key at all (its
+    // attend_head_ref panics on step_by(0)).
+    if (ring > 0 && ring < nh::FWD_ROWS) return fail(NH_EINVAL, "an attention ring shorter than a 32-token chunk");
+    s->sink = ring > 0 ? sink : 0;
+    s->ring = ring;
+    return NH_OK;
+}
+
+int nh_session_rollback(nh_session* s, int n) {
+    if (!s || n < 0) return fail(NH_EINVAL, "bad arguments");
+    if (n > nh::ROLLBACK) return fail(NH_EINVAL, "rollback of more than 32 positions");
+    if (n > s->len) return fail(NH_EINVAL, "rollback past the start of the session");
+    if (n == 0) return NH_OK;
+    s->len -= n;
+    s->hrows = std::max(0, s->hrows - n);
+    s->rope_n = std::max(0, s->rope_n - n);
+    s->toks.resize(s->len);
     s->have_logits = false;
     return NH_OK;
 }
 
-int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* stream) {
-    if (!s || (n > 0 && !toks) || n < 0) return fail(NH_EINVAL, "bad arguments");
+int nh_session_rewind_zeroed(nh_session* s, int len) {
+    if (!s || len < 0) return fail(NH_EINVAL, "bad arguments");
+    if (len < s->len) {
+        s->len = len;
+        s->toks.resize(len);
+        s->have_logits = false;
+    }
+    s->hrows = 0;
+    s->rope_n = 0;
+    return NH_OK;
+}
+
+int nh_session_last_hidden(const nh_session* s, float* h, void* stream) {
+    if (!s || !h) return fail(NH_EINVAL, "bad arguments");
+    if (!s->have_hidden) return fail(NH_EINVAL, "no hidden state yet (no feed has returned outputs)");
+    NH_TRY(hipMemcpyAsync(h, s->S.last_hid, (size_t)s->dims.d * 4, hipMemcpyDeviceToDevice, (hipStream_t)stream),
+           "last hidden");
+    return NH_OK;
+}
+
+int nh_session_head_logits(nh_session* s, float* logits, void* stream) {
+    if (!s || !logits) return fail(NH_EINVAL, "bad arguments");
     if (!nh::ready()) return fail(NH_ESTATE, "nh_init has not been called");
-    if (s->len + n > s->dims.cap) return fail(NH_EINVAL, "the tokens do not fit the session's capacity");
-    for (int i = 0; i < n; ++i)
-        if (toks[i] >= (uint32_t)s->dims.vocab) return fail(NH_EINVAL, "token id outside the vocabulary");
-    if (n == 0) return NH_OK;
+    if (!s->have_hidden) return fail(NH_EINVAL, "no hidden state yet (no feed has returned outputs)");
     hipStream_t st = (hipStream_t)stream;
-    NH_TRY(hipMemcpyAsync(s->S.tokens + s->len, toks, (size_t)n * 4, hipMemcpyHostToDevice, st), "tokens");
-    NH_TRY(hipStreamSynchronize(st), "tokens");
-    for (int i = 0; i < n; i += nh::FWD_ROWS) {
-        const int t = std::min(nh::FWD_ROWS, n - i);
-        if (int rc = feed(s, t, i + t == n, st)) return rc;
+    const nh::Dims& D = s->dims;
+    nh_qact a = s->a_in;
+    a.bits = s->m->head_bits;
+    NH_TRY(nh::launch_act_prep(s->S.last_hid, 1, D.d, a.groups, s->m->head_bits, nullptr, a.d_xq, a.d_sx, st),
+           "head A8");
+    NH_TRY(product(s->m->head, &a, 1, logits, D.out_rows, st), "head");
+    return NH_OK;
+}
+
+int nh_session_head_logits_sparse(nh_session* s, const uint32_t* ids, int n, float* logits, void* stream) {
+    if (!s || !logits || n < 0 || (n > 0 && !ids)) return fail(NH_EINVAL, "bad arguments");
+    if (!nh::ready()) return fail(NH_ESTATE, "nh_init has not been called");
+    if (!s->have_hidden) return fail(NH_EINVAL, "no hidden state yet (no feed has returned outputs)");
+    hipStream_t st = (hipStream_t)stream;
+    const nh::Dims& D = s->dims;
+    nh_qact a = s->a_in;
+    a.rows = 1;
+    a.bits = s->m->head_bits;
+    NH_TRY(nh::launch_act_prep(s->S.last_hid, 1, D.d, a.groups, s->m->head_bits, nullptr, a.d_xq, a.d_sx, st),
+           "head A8");
+    return nh_head_logits_sparse(s->m->head, &a, ids, n, D.out_rows, logits, stream);
+}
+
+int nh_forward_outputs(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, int64_t out_cap,
+                       void* stream) {
+    if (int rc = check_feed(s, toks, n, outputs)) return rc;
+    if (int rc = check_out(s, n, outputs, out, out_cap)) return rc;
+    if (n == 0) return 0;
+    return forward_ids(s, toks, n, outputs, out, (hipStream_t)stream);
+}
+
+int nh_prefill(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, int64_t out_cap, void* stream) {
+    if (int rc = check_feed(s, toks, n, outputs)) return rc;
+    if (int rc = check_out(s, n, outputs, out, out_cap)) return rc;
+    // prefill_native (infer.rs:1078-1101): with a span and a slot map, the
+    // first position in max(end - ring, sink) .. len whose slot another
+    // position holds now starts a re-feed with the conv history zeroed
+    const int pos = s->len, end = pos + n;
+    if (s->ring > 0 && !s->slot_pos.empty()) {
+        for (int p = std::max(end - s->ring, s->sink); p < pos; ++p) {
+            if (live(s, p)) continue;
+            std::vector<uint32_t> refeed(s->toks.begin() + p, s->toks.begin() + pos);
+            refeed.insert(refeed.end(), toks, toks + n);
+            if (int rc = check_out(s, (int)refeed.size(), outputs, out, out_cap)) return rc;
+            nh_session_rewind_zeroed(s, p);
+            return forward_ids(s, refeed.data(), (int)refeed.size(), outputs, out, (hipStream_t)stream);
+        }
+    }
+    if (n == 0) return 0;
+    return forward_ids(s, toks, n, outputs, out, (hipStream_t)stream);
+}
+
+int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* stream) {
+    if (int rc = check_feed(s, toks, n, NH_OUT_LAST_LOGITS)) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (n == 0) {
+        // nothing fed: the logits of the last position, when the session has them
+        if (!logits) return NH_OK;
+        if (!s->have_logits) return fail(NH_EINVAL, "no tokens and no logits of an earlier feed");
+    } else {
+        const int r = forward_ids(s, toks, n, NH_OUT_LAST_LOGITS, nullptr, st);
+        if (r < 0) return r;
     }
     if (logits)
         NH_TRY(hipMemcpyAsync(logits, s->S.logits, (size_t)s->dims.out_rows * 4, hipMemcpyDeviceToDevice, st),
@@ -623,7 +929,8 @@ int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, v
     const int len0 = s->len;
     for (int i = 0; i < steps; ++i) {
         NH_TRY(nh::fwd_argmax(s->S.logits, s->dims.out_rows, s->S.tokens + s->len, st), "argmax");
-        if (int rc = feed(s, 1, true, st)) return rc;
+        const int r = feed(s, 1, NH_OUT_LAST_LOGITS, nullptr, st);
+        if (r < 0) return r;
     }
     if (logits)
         NH_TRY(hipMemcpyAsync(logits, s->S.logits, (size_t)s->dims.out_rows * 4, hipMemcpyDeviceToDevice, st),
@@ -631,6 +938,8 @@ int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, v
     if (steps > 0) {
         NH_TRY(hipMemcpyAsync(out, s->S.tokens + len0, (size_t)steps * 4, hipMemcpyDeviceToHost, st), "tokens");
         NH_TRY(hipStreamSynchronize(st), "tokens");
+        s->toks.resize(len0);
+        s->toks.insert(s->toks.end(), out, out + steps);
     }
     return NH_OK;
 }

@@ -20,6 +20,9 @@ LIB_PATH = os.path.join(HERE, "libneedle_hip.so")
 GROUP = 128
 NEG = np.frombuffer(np.uint32(0xF149F2CA).tobytes(), dtype=np.float32)[0]
 
+# Outputs (crates/needle-engine/src/model.rs:150-160)
+OUT_NONE, OUT_LAST_LOGITS, OUT_ALL_LOGITS, OUT_HIDDEN, OUT_LAST_HIDDEN = range(5)
+
 # Every exported symbol of include/needle_hip.h, with (restype, argtypes).
 P = C.c_void_p
 I = C.c_int
@@ -62,6 +65,15 @@ SIGNATURES = {
     "nh_session_len": (I, [P]),
     "nh_session_reset": (I, [P]),
     "nh_forward": (I, [P, P, I, P, P]),
+    "nh_forward_outputs": (I, [P, P, I, I, P, C.c_int64, P]),
+    "nh_prefill": (I, [P, P, I, I, P, C.c_int64, P]),
+    "nh_session_clone": (I, [P, P, P]),
+    "nh_session_set_attend": (I, [P, I, I]),
+    "nh_session_rollback": (I, [P, I]),
+    "nh_session_rewind_zeroed": (I, [P, I]),
+    "nh_session_last_hidden": (I, [P, P, P]),
+    "nh_session_head_logits": (I, [P, P, P]),
+    "nh_session_head_logits_sparse": (I, [P, P, I, P, P]),
     "nh_generate_greedy": (I, [P, I, P, P, P]),
     "nh_normal": (I, [C.c_uint32, C.c_uint32, C.c_uint64, P]),
     "nh_split": (I, [C.c_uint32, C.c_uint32, P]),
@@ -385,6 +397,11 @@ class Model:
     def __init__(self, h):
         self.h = h
         self.out_rows = _check(_lib.nh_model_out_rows(h))
+        w = C.c_void_p()
+        _check(_lib.nh_model_weights(h, C.byref(w)))
+        words = np.zeros(49, dtype=np.uint32)
+        _check(_lib.nh_weights_header(w.value, _hptr(words), 49))
+        self.d_model = int(words[7])  # the header's d_model word (cact.rs:80-118)
 
     @property
     def weights(self) -> "QWeights":
@@ -414,14 +431,16 @@ class Model:
 
 
 class Session:
-    """Session (crates/needle-engine/src/model.rs:55-69): one sequence's
+    """Session (crates/needle-engine/src/model.rs:55-121): one sequence's
     decoding state (KV caches, tap and engram histories) in HBM."""
 
-    def __init__(self, model: Model, cap: int):
+    def __init__(self, model: Model, cap: int, handle=None):
         self.model = model
-        h = C.c_void_p()
-        _check(_lib.nh_session_new(model.h, int(cap), C.byref(h)))
-        self.h = h.value
+        if handle is None:
+            h = C.c_void_p()
+            _check(_lib.nh_session_new(model.h, int(cap), C.byref(h)))
+            handle = h.value
+        self.h = handle
         self.cap = cap
 
     def __len__(self):
@@ -430,15 +449,70 @@ class Session:
     def reset(self):
         _check(_lib.nh_session_reset(self.h))
 
-    def forward(self, tokens, stream=None) -> torch.Tensor:
-        """Model::forward with Outputs::LastLogits (model.rs:304-306) as
-        forward_native feeds it (infer.rs:1105-1132): chunks of 32 tokens
-        (chunk_job), a single token as a step; the last token's logits
-        [out_rows] (device)."""
+    def _width(self, outputs):
+        return self.model.d_model if outputs in (OUT_HIDDEN, OUT_LAST_HIDDEN) else self.model.out_rows
+
+    def _feed(self, fn, tokens, outputs, stream):
         toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(-1))
-        logits = torch.empty(self.model.out_rows, dtype=torch.float32, device="cuda")
-        _check(_lib.nh_forward(self.h, _hptr(toks), toks.size, _dptr(logits), _stream(stream)))
-        return logits
+        # a prefill may re-feed up to the session's length before the tokens
+        rows = (toks.size + (len(self) if fn is _lib.nh_prefill else 0)) if outputs in (OUT_ALL_LOGITS, OUT_HIDDEN) \
+            else (1 if outputs != OUT_NONE else 0)
+        width = self._width(outputs)
+        out = torch.empty(max(rows, 1) * width, dtype=torch.float32, device="cuda")
+        r = _check(fn(self.h, _hptr(toks), toks.size, int(outputs), _dptr(out), out.numel(), _stream(stream)))
+        return out[:r * width].view(r, width)
+
+    def forward(self, tokens, outputs: int | None = None, stream=None) -> torch.Tensor:
+        """Model::forward (model.rs:304-306) as forward_native feeds it
+        (infer.rs:1105-1132): chunks of 32 tokens (chunk_job), a single token
+        as a step.  Without `outputs`: the last token's logits [out_rows];
+        with an Outputs mode: the rows it returns, [rows][width] (device)."""
+        if outputs is None:
+            toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(-1))
+            logits = torch.empty(self.model.out_rows, dtype=torch.float32, device="cuda")
+            _check(_lib.nh_forward(self.h, _hptr(toks), toks.size, _dptr(logits), _stream(stream)))
+            return logits
+        return self._feed(_lib.nh_forward_outputs, tokens, outputs, stream)
+
+    def prefill(self, tokens, outputs: int = OUT_LAST_LOGITS, stream=None) -> torch.Tensor:
+        """Model::prefill on the native path (prefill_native, infer.rs:1078-1101)."""
+        return self._feed(_lib.nh_prefill, tokens, outputs, stream)
+
+    def clone(self, stream=None) -> "Session":
+        """Session::clone (model.rs:53-55)."""
+        h = C.c_void_p()
+        _check(_lib.nh_session_clone(self.h, _stream(stream), C.byref(h)))
+        return Session(self.model, self.cap, handle=h.value)
+
+    def set_attend(self, sink: int, ring: int):
+        """Session::attend = Some((sink, ring)) (model.rs:62-66); ring 0: None."""
+        _check(_lib.nh_session_set_attend(self.h, int(sink), int(ring)))
+
+    def rollback(self, n: int):
+        """Session::rollback (model.rs:81-113)."""
+        _check(_lib.nh_session_rollback(self.h, int(n)))
+
+    def rewind_zeroed(self, length: int):
+        """Session::rewind_zeroed (model.rs:115-121)."""
+        _check(_lib.nh_session_rewind_zeroed(self.h, int(length)))
+
+    def last_hidden(self, stream=None) -> torch.Tensor:
+        """NatState::last_hidden (infer.rs:996-998)."""
+        h = torch.empty(self.model.d_model, dtype=torch.float32, device="cuda")
+        _check(_lib.nh_session_last_hidden(self.h, _dptr(h), _stream(stream)))
+        return h
+
+    def head_logits(self, stream=None) -> torch.Tensor:
+        """Model::head_logits (infer.rs:1135-1141) of the last hidden state."""
+        out = torch.empty(self.model.out_rows, dtype=torch.float32, device="cuda")
+        _check(_lib.nh_session_head_logits(self.h, _dptr(out), _stream(stream)))
+        return out
+
+    def head_logits_sparse(self, ids: torch.Tensor, stream=None) -> torch.Tensor:
+        """Model::head_logits_sparse (infer.rs:1145-1166) of the last hidden state."""
+        out = torch.empty(self.model.out_rows, dtype=torch.float32, device="cuda")
+        _check(_lib.nh_session_head_logits_sparse(self.h, _dptr(ids), ids.numel(), _dptr(out), _stream(stream)))
+        return out
 
     def generate_greedy(self, steps: int, stream=None):
         """The greedy loop of generate (crates/needle-engine/src/generate.rs:87-139)

@@ -512,9 +512,12 @@ nf_session* nf_session_clone(const nf_model* m, const nf_session* s) {
 
 size_t nf_session_len(const nf_session* s) { return s->len; }
 
-/* Session::attend (model.rs:62-66): ring 0 is None. */
+/* Session::attend (model.rs:62-66): ring 0 is None.  A ring shorter than a
+ * 32-token chunk is refused: two rows of one chunk would share a KV slot
+ * (the reference's members race on it) and a row could see no key at all
+ * (attend_head_ref's step_by(0) panics). */
 int nf_session_set_attend(nf_session* s, size_t sink, size_t ring) {
-    if (ring > 0 && sink + ring > s->cap) return -1;
+    if (ring > 0 && ring < 32) return -1;
     s->sink = sink;
     s->ring = ring;
     return 0;

@@ -305,7 +305,7 @@ class Session:
     def set_attend(self, sink: int, ring: int):
         """Session::attend = Some((sink, ring)) (ring 0: None)."""
         if _lib().nf_session_set_attend(self.s, int(sink), int(ring)) != 0:
-            raise ValueError("attention span past the capacity")
+            raise ValueError("attention ring shorter than a 32-token chunk")
 
     def rollback(self, n: int):
         if _lib().nf_session_rollback(self.f.m, self.s, int(n)) != 0:

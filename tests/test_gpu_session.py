@@ -1,0 +1,224 @@
+"""GPU: the session operations of the model boundary against the oracle doing
+the same operations on the same archive (bit-identical at every step).
+
+- Outputs (crates/needle-engine/src/model.rs:150-160): None, LastLogits,
+  AllLogits, Hidden, LastHidden over prompts of several chunks;
+- Session::rollback / rewind_zeroed / clone (model.rs:81-121,
+  infer.rs:1039-1071), including a rollback across the history trim;
+- Session::attend = (sink, ring) with the KV slot ring and the slot map
+  (infer.rs:1749-1826), stale slots after a rollback and prefill_native's
+  re-feed (infer.rs:1078-1101), stepwise and in chunks, a ring shorter than
+  the sequence;
+- the session heads: last_hidden, head_logits, head_logits_sparse
+  (infer.rs:1135-1166, agent.rs:398-409);
+- the conv tap counts 1, 2, 4, 6 (the exact and the clamped unit kernels),
+  with a one-token prompt and a prompt past one chunk;
+- a geometry with more taps than the kernels take is refused at load.
+"""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as o
+from oracle import cact, forward
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 2e-3
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def archive(g, seed):
+    ts, _ = cact.needle3_tensors(g, seed=seed, kind=lambda n: ("cq", 4) if n == "embedding" else ("random", 4))
+    return cact.pack(ts, g.header())
+
+
+def same(label, got, want, stats):
+    got = np.asarray(got, dtype=np.float32)
+    want = np.asarray(want, dtype=np.float32)
+    assert got.shape == want.shape, (label, got.shape, want.shape)
+    stats["n"] = stats.get("n", 0) + 1
+    if want.size == 0:
+        stats["exact"] = stats.get("exact", 0) + 1
+        return
+    assert np.isfinite(got).all() and np.isfinite(want).all(), label
+    scale = max(float(np.abs(want).max()), 1e-30)
+    err = float(np.abs(got - want).max()) / scale
+    stats["max_rel"] = max(stats.get("max_rel", 0.0), err)
+    stats["exact"] = stats.get("exact", 0) + int(np.array_equal(got.view(np.uint32), want.view(np.uint32)))
+    assert err <= REL_TOL, (label, err)
+
+
+class Pair:
+    """A device session and an oracle session driven by the same script."""
+
+    def __init__(self, nh, data, cap):
+        self.f = forward.Forward(data)
+        self.m = nh.Model.from_archive(data)
+        self.g, self.o = self.m.session(cap), self.f.session(cap)
+        self.stats = {}
+
+    def fwd(self, toks, outputs=forward.OUT_LAST_LOGITS, label="forward"):
+        got = self.g.forward(toks, outputs).cpu().numpy()
+        same(label, got, self.o.forward(toks, outputs), self.stats)
+        return got
+
+    def prefill(self, toks, outputs=forward.OUT_LAST_LOGITS, label="prefill"):
+        got = self.g.prefill(toks, outputs).cpu().numpy()
+        same(label, got, self.o.prefill(toks, outputs), self.stats)
+        return got
+
+    def steps(self, toks, outputs=forward.OUT_LAST_LOGITS, label="step"):
+        for i, t in enumerate(toks):
+            self.fwd([int(t)], outputs, f"{label} {i}")
+
+    def rollback(self, n):
+        self.g.rollback(n)
+        self.o.rollback(n)
+        assert len(self.g) == len(self.o)
+
+    def rewind_zeroed(self, n):
+        self.g.rewind_zeroed(n)
+        self.o.rewind_zeroed(n)
+        assert len(self.g) == len(self.o)
+
+    def attend(self, sink, ring):
+        self.g.set_attend(sink, ring)
+        self.o.set_attend(sink, ring)
+
+    def clone(self):
+        c = Pair.__new__(Pair)
+        c.f, c.m, c.stats = self.f, self.m, self.stats
+        c.g, c.o = self.g.clone(), self.o.clone()
+        return c
+
+    def heads(self, ids):
+        h = self.o.last_hidden()
+        same("last_hidden", self.g.last_hidden().cpu().numpy(), h, self.stats)
+        same("head_logits", self.g.head_logits().cpu().numpy(), self.f.head_logits(h), self.stats)
+        dev_ids = torch.from_numpy(np.asarray(ids, dtype=np.int32)).cuda()
+        same("head_logits_sparse", self.g.head_logits_sparse(dev_ids).cpu().numpy(),
+             self.f.head_logits_sparse(h, ids), self.stats)
+
+    def done(self, label):
+        say(f"{label}: {self.stats['exact']}/{self.stats['n']} bit-identical, "
+            f"max rel {self.stats.get('max_rel', 0.0):.3g}")
+        assert self.stats["exact"] == self.stats["n"], self.stats
+
+
+SMALL = dict(vocab=300, num_layers=3, engram_slots=64, engram_sites=(1,), global_layers=(1,), sliding_window=8)
+
+
+def test_outputs_modes(nh):
+    say("Outputs modes over a 40-token prompt (32 + 8) and steps")
+    data = archive(cact.Geometry(**SMALL), seed=51)
+    toks = o.random_tokens(40, 300, seed=51)
+    for mode in (forward.OUT_NONE, forward.OUT_LAST_LOGITS, forward.OUT_ALL_LOGITS, forward.OUT_HIDDEN,
+                 forward.OUT_LAST_HIDDEN):
+        p = Pair(nh, data, 64)
+        got = p.fwd(toks, mode, f"mode {mode} prompt")
+        rows = {forward.OUT_NONE: 0, forward.OUT_ALL_LOGITS: 40, forward.OUT_HIDDEN: 40}.get(mode, 1)
+        assert got.shape[0] == rows
+        p.steps(o.random_tokens(3, 300, seed=52), mode, f"mode {mode} step")
+        if mode != forward.OUT_NONE:
+            p.heads([0, 7, 150, 299])
+        p.done(f"outputs mode {mode}")
+
+
+def test_rollback_clone_rewind(nh):
+    say("rollback (across the history trim), clone, rewind_zeroed")
+    data = archive(cact.Geometry(**SMALL), seed=52)
+    p = Pair(nh, data, 160)
+    p.fwd(o.random_tokens(60, 300, seed=53))
+    p.steps(o.random_tokens(25, 300, seed=54))
+    p.rollback(25)
+    p.steps(o.random_tokens(4, 300, seed=55), label="after rollback")
+    p.rollback(3)
+    p.rollback(1)
+    c = p.clone()
+    p.fwd(o.random_tokens(9, 300, seed=56), label="original")
+    c.fwd(o.random_tokens(33, 300, seed=57), label="clone")
+    c.steps(o.random_tokens(2, 300, seed=58), label="clone step")
+    p.rewind_zeroed(50)
+    p.fwd(o.random_tokens(40, 300, seed=59), label="after rewind")
+    p.steps(o.random_tokens(2, 300, seed=60), label="after rewind step")
+    p.heads([3, 4, 5])
+    p.done("rollback / clone / rewind")
+    with pytest.raises(nh.NeedleHipError, match="32"):
+        p.g.rollback(33)
+
+
+@pytest.mark.parametrize("stepwise", [True, False])
+def test_attention_span(nh, stepwise):
+    say(f"attention span (sink 6, ring 32), {'steps' if stepwise else 'chunks'}, with rollbacks and prefill")
+    data = archive(cact.Geometry(**SMALL), seed=61)
+    p = Pair(nh, data, 160)
+    p.attend(6, 32)
+    toks = o.random_tokens(70, 300, seed=62)
+    if stepwise:
+        p.steps(toks[:40])
+    else:
+        p.fwd(toks[:40])
+    p.rollback(5)  # leaves stale slots
+    p.steps(toks[40:43], label="after rollback")
+    p.prefill(toks[43:50], label="prefill re-feed")
+    p.rollback(2)
+    p.prefill(toks[50:70], forward.OUT_ALL_LOGITS, label="prefill all rows")
+    p.steps(o.random_tokens(3, 300, seed=63), label="tail")
+    p.heads([1, 2, 3])
+    p.done(f"attention span {'steps' if stepwise else 'chunks'}")
+    with pytest.raises(nh.NeedleHipError, match="shorter than a 32-token chunk"):
+        p.g.set_attend(6, 16)
+
+
+def test_attention_span_long(nh):
+    say("attention span over 300 positions (sink 20, ring 256: two key chunks), chunks and steps")
+    g = cact.Geometry(vocab=300, num_layers=2, engram_slots=64, engram_sites=(1,), global_layers=(0,),
+                      sliding_window=64)
+    p = Pair(nh, archive(g, seed=64), 320)
+    p.attend(20, 256)
+    p.fwd(o.random_tokens(290, 300, seed=65))
+    p.steps(o.random_tokens(6, 300, seed=66))
+    p.done("attention span long")
+
+
+@pytest.mark.parametrize("taps", [1, 2, 4, 6])
+def test_conv_taps(nh, taps):
+    say(f"qkv conv taps {taps}: a one-token prompt, steps, a 40-token prompt, steps")
+    g = cact.Geometry(vocab=300, num_layers=3, engram_slots=64, engram_sites=(1,), global_layers=(1,),
+                      sliding_window=8, qkv_conv_taps=taps)
+    data = archive(g, seed=70 + taps)
+    p = Pair(nh, data, 96)
+    p.fwd(o.random_tokens(1, 300, seed=71))
+    p.steps(o.random_tokens(5, 300, seed=72))
+    p.fwd(o.random_tokens(40, 300, seed=73))
+    p.steps(o.random_tokens(3, 300, seed=74))
+    p.done(f"taps {taps}")
+
+
+def test_too_many_taps_refused(nh):
+    say("an archive with 9 conv taps is refused, naming the limit")
+    g = cact.Geometry(vocab=300, num_layers=2, engram_slots=64, engram_sites=(1,), global_layers=(1,),
+                      sliding_window=8, qkv_conv_taps=9)
+    with pytest.raises(nh.NeedleHipError, match="at most 8"):
+        nh.Model.from_archive(archive(g, seed=79))
+    torch.cuda.synchronize()
+
+
+def test_forward_empty(nh):
+    say("forward of no tokens")
+    data = archive(cact.Geometry(**SMALL), seed=80)
+    m = nh.Model.from_archive(data)
+    s = m.session(16)
+    with pytest.raises(nh.NeedleHipError, match="no tokens"):
+        s.forward([])
+    a = s.forward([5, 6]).cpu().numpy()
+    b = s.forward([]).cpu().numpy()  # the logits the session holds
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert s.forward([], forward.OUT_HIDDEN).shape[0] == 0

@@ -402,7 +402,7 @@ def visible_changes(f, feed, pos, sink, ring, n):
     alt[pos] = (int(toks[pos]) + 1) % 300
     outs = []
     for tt in (toks, alt):
-        s = f.session(64)
+        s = f.session(n + 16)
         s.set_attend(sink, ring)
         outs.append(feed(s, tt))
     return not np.array_equal(bits(outs[0]), bits(outs[1]))
@@ -410,7 +410,7 @@ def visible_changes(f, feed, pos, sink, ring, n):
 
 def test_attention_span_receptive_field():
     f = model("one")
-    sink, ring, n = 4, 8, 30
+    sink, ring, n = 4, 32, 80
 
     def stepwise(s, tt):
         for t in tt[:-1]:
@@ -418,11 +418,14 @@ def test_attention_span_receptive_field():
         return s.forward([int(tt[-1])])
 
     def chunk(s, tt):
-        return s.forward(tt)
+        return s.forward(tt)  # 32 + 32 + 16
 
+    probe = [0, 2, 3, 4, 5, 20, 46, 47, 48, 49, 60, 79]
     for feed in (stepwise, chunk):
-        seen = [p for p in range(n) if visible_changes(f, feed, p, sink, ring, n)]
-        assert seen == list(range(sink)) + list(range(n - ring, n)), (feed.__name__, seen)
+        seen = [p for p in probe if visible_changes(f, feed, p, sink, ring, n)]
+        assert seen == [p for p in probe if p < sink or p >= n - ring], (feed.__name__, seen)
+    with pytest.raises(ValueError):
+        f.session(64).set_attend(4, 16)  # a ring shorter than a chunk
 
 
 def test_attention_span_wide_is_no_span():
@@ -440,37 +443,38 @@ def test_attention_span_wide_is_no_span():
 
 def test_stale_slots_are_skipped_and_prefill_refeeds():
     f = model("one")
-    sink, ring = 4, 8
-    toks = o.random_tokens(20, 300, seed=43)
+    sink, ring = 4, 32
+    toks = o.random_tokens(60, 300, seed=43)
 
     def after_rollback(tt, new):
-        s = f.session(64)
+        s = f.session(96)
         s.set_attend(sink, ring)
         for t in tt:
             s.forward([int(t)], forward.OUT_NONE)
-        s.rollback(3)  # positions 17..19 keep slots 9..11 (were 9..11... of 10, 11)
+        s.rollback(3)  # 57..59 keep slots 25..27 (positions 25..27 had them)
         return s, s.forward([new])
 
     s0, base = after_rollback(toks, 5)
-    # position 10 and 11's slots now hold 18 and 19: invisible
-    for p, seen in ((10, False), (11, False), (12, True), (2, True), (16, True)):
+    # the step at 57 sees the sink and 26..57 of the ring, less 26 and 27,
+    # whose slots the dropped positions 58 and 59 hold
+    for p, seen in ((25, False), (26, False), (27, False), (28, True), (2, True), (56, True)):
         alt = toks.copy()
         alt[p] = (int(toks[p]) + 1) % 300
         _, got = after_rollback(alt, 5)
         assert (not np.array_equal(bits(got), bits(base))) == seen, p
-    # prefill finds position 10 stale and re-feeds 10..16 and the new token
-    s = f.session(64)
+    # prefill finds position 26 stale and re-feeds 26..56 and the new token
+    s = f.session(96)
     s.set_attend(sink, ring)
     for t in toks:
         s.forward([int(t)], forward.OUT_NONE)
     s.rollback(3)
     got = s.prefill([5])
-    fresh = f.session(64)
+    fresh = f.session(96)
     fresh.set_attend(sink, ring)
-    for t in toks[:10]:
+    for t in toks[:26]:
         fresh.forward([int(t)], forward.OUT_NONE)
-    want = fresh.forward(np.concatenate([toks[10:17], [5]]))
-    assert len(s) == 18 and np.array_equal(bits(got), bits(want))
+    want = fresh.forward(np.concatenate([toks[26:57], [5]]))
+    assert len(s) == 58 and np.array_equal(bits(got), bits(want))
 
 
 # ---------------------------------------------------------------- outputs
