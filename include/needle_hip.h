@@ -227,6 +227,13 @@ int nh_session_rollback(nh_session* s, int n);
  * positions len.. as the engine's context-overflow re-feed does: the KV cache
  * keeps what it holds, the conv history and the RoPE state start over. */
 int nh_session_rewind_zeroed(nh_session* s, int len);
+/* No reference counterpart (a test hook): the polls a bounded in-kernel
+ * wait makes before it gives up (default 1 << 20, about 30 ms).  A wait
+ * that gives up lets its kernel end and marks the session; the next call
+ * that synchronizes (nh_forward*, nh_prefill, nh_generate_greedy) returns
+ * NH_EDEVICE and resets the session.  0 makes every such wait give up at
+ * once, for tests of that path. */
+int nh_session_debug_spin_limit(nh_session* s, int limit);
 /* NatState::last_hidden (infer.rs:996-998) into DEVICE h[d_model]. */
 int nh_session_last_hidden(const nh_session* s, float* h, void* stream);
 /* Model::head_logits (infer.rs:1135-1141) of the session's last hidden state
@@ -245,6 +252,10 @@ int nh_session_head_logits_sparse(nh_session* s, const uint32_t* ids, int n, flo
  * (DEVICE, out_rows floats, or NULL) receives the last token's; with n = 0
  * they are the logits the session already holds (NH_EINVAL without any). */
 int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* stream);
+/* generate::argmax (crates/needle-engine/src/generate.rs:42-50) on the
+ * device: the first index of the maximum of DEVICE x[n] into DEVICE dst[0];
+ * NaNs never win, and a NaN x[0] gives 0, as the reference's loop does. */
+int nh_argmax(const float* x, int n, uint32_t* dst, void* stream);
 /* The greedy loop of generate (crates/needle-engine/src/generate.rs:87-139)
  * at temperature 0, on the device: `steps` times argmax of the current
  * logits (generate.rs:42-50, the first maximum), then a step on that token.

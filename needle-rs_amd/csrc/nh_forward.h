@@ -32,6 +32,8 @@ constexpr int ROLLBACK = 32;        // ROLLBACK (crates/needle-engine/src/model.
 constexpr int ROPE_RING = 128;      // RoPE rows kept by position (the reference's list holds at most 66)
 constexpr int DG_MAX_TAPS = 8;      // conv taps the unit kernels are written for
 constexpr int SPAN_RUNS = 24;       // runs of live positions an attention span passes to a feed
+constexpr int STATUS_SPIN = 1;      // a bounded in-kernel wait gave up (SessDev::status)
+constexpr int SPIN_LIMIT = 1 << 20; // polls of a bounded wait (~64 cycles each, ~30 ms)
 
 struct Dims {
     int d, nh, nkv, qk, vd, lanes, taps, layers;
@@ -45,6 +47,7 @@ struct Dims {
     int cap;    // session positions
     int vcap;   // row stride of the transposed int8 values: cap + 4 rounded up to 16
     int max_chunks;  // attention chunks a position can need
+    int spin_limit;  // polls of an in-kernel wait before it gives up (SPIN_LIMIT)
     // per-feed state, set by the host before each feed
     int hist_lo;     // the first position the conv history still holds (LayerState::hist,
                      // crates/needle-engine/src/infer.rs:968-980): older rows read as zero
@@ -123,6 +126,7 @@ struct SessDev {
     int8_t* xq_eng;   // [sites][ACT_ROWS][G(d)][128] the engram rows
     float* sx_eng;
     int32_t* argmax;  // scratch of the greedy pick
+    int32_t* status;  // STATUS_* bits set by a kernel that gave up a wait; the host reads and clears it
 };
 
 // A CQ matrix read by rows (the embedding, the engram tables).

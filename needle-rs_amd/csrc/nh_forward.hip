@@ -492,12 +492,21 @@ __device__ __forceinline__ float dot16_t(const float* xT, const float* yT, int p
 // A barrier among the mix8 wavefronts only (the other wavefronts go on):
 // lane 0 of each adds its arrival to an LDS counter and waits for `target`
 // arrivals.  LDS operations of a wavefront complete in order, so the
-// wavefront's earlier LDS writes are visible once its arrival is.
-__device__ __forceinline__ void mixer_sync(int* count, int target) {
+// wavefront's earlier LDS writes are visible once its arrival is.  The wait
+// is bounded: after `limit` polls the wavefront records STATUS_SPIN in the
+// session's status word and goes on, so the kernel always ends (the host
+// reports the failure at its next synchronization).
+__device__ __forceinline__ void mixer_sync(int* count, int target, int limit, int32_t* status) {
     if ((threadIdx.x & 63) == 0) {
         __hip_atomic_fetch_add(count, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-        while (__hip_atomic_load(count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+        for (int polls = 0; __hip_atomic_load(count, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target;
+             ++polls) {
+            if (polls >= limit) {
+                __hip_atomic_fetch_or(status, STATUS_SPIN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
             __builtin_amdgcn_s_sleep(1);
+        }
     }
     __builtin_amdgcn_wave_barrier();
 }
@@ -661,7 +670,7 @@ __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int l
 
 // The Hadamard MLP and mHC write of layer P (step.rs:600-705); returns this
 // thread's max |new lane value| (for the next layer's mHC read).
-__device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, LayerShared& sh) {
+__device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, const OutRegs& q, LayerShared& sh) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
     // mix8 runs on waves 4..7 (threads 256..511), beside cond_weights on wave 0
     const bool mixer = t >= MIX_T && t < 2 * MIX_T;
@@ -695,7 +704,7 @@ __device__ float layer_out(const Dims& D, const LayerDev& P, const OutRegs& q, L
     if (wave == 0) cond_weights(sh, d, lane, sh.wk);
     if (mixer) {
         mix8_t(mu, sh.kp[0], sh.A, sh.B);
-        mixer_sync(&sh.mix_count, MIX_T / 64);
+        mixer_sync(&sh.mix_count, MIX_T / 64, D.spin_limit, S.status);
         mix8_n(mu, sh.B, sh.kp[1], sh.C, HADA_NB);
     }
     __syncthreads();
@@ -991,7 +1000,7 @@ __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, Laye
     if constexpr (has_prev) store_out(D, qo, sh);
     __syncthreads();
     if constexpr (has_next && has_prev) qi = load_in(D, R, N);
-    if constexpr (has_prev) m = layer_out(D, P, qo, sh);
+    if constexpr (has_prev) m = layer_out(D, S, P, qo, sh);
     // the wavefronts' maxima of |xs| for the mHC read
     m = wave_max(m);
     if (lane == 0) sh.red[wave] = m;
@@ -1926,13 +1935,16 @@ hipError_t fwd_dec_attn(const Dims& D, const SessDev& S, const LayerDev& L, int 
 
 // ----------------------------------------------------------------- argmax
 // argmax (crates/needle-engine/src/generate.rs:42-50): the first maximum.
-// Each thread keeps the first maximum of its strided share (all its loads
-// issued first); a wavefront's first maximum is the smallest index among
+// The reference's loop keeps index 0 when x[0] is NaN (nothing compares
+// greater) and otherwise never moves to a NaN, so NaNs are skipped and a
+// NaN first element gives 0.  Each thread keeps the first maximum of its
+// strided share (all its loads issued first); a wavefront's first maximum is the smallest index among
 // the lanes holding the wavefront's maximum (two DPP reductions), and the
 // same again over the wavefronts' results.
 __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, uint32_t* __restrict__ dst) {
     constexpr int PER = 16;  // elements per thread read in one batch
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const float x0 = x[0];
     float best = -__builtin_inff();
     int bi = n;
     for (int base = 0; base < n; base += 1024 * PER) {
@@ -1942,7 +1954,8 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
 #pragma unroll
         for (int k = 0; k < PER; ++k) {
             const int i = base + k * 1024 + t;
-            if (i < n && (bi == n || v[k] > best)) {
+            // a NaN is never greater than the best so far: it never wins
+            if (i < n && v[k] == v[k] && (bi == n || v[k] > best)) {
                 best = v[k];
                 bi = i;
             }
@@ -1962,7 +1975,8 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
         const int ix = lane < 16 ? si[min(lane, 15)] : 0x7fffffff;
         const float m = wave_max(v);
         const int first = __ockl_wfred_min_i32(v == m && ix != 0x7fffffff ? ix : 0x7fffffff);
-        if (lane == 0) dst[0] = (uint32_t)(first < n ? first : 0);
+        // with x[0] NaN nothing is greater than x[best = 0]: the reference keeps 0
+        if (lane == 0) dst[0] = (uint32_t)(first < n && x0 == x0 ? first : 0);
     }
 }
 

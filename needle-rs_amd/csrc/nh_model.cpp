@@ -591,12 +591,27 @@ int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
     return rows;
 }
 
+// The session's status word (bounded in-kernel waits that gave up, as far
+// as the stream has run): synchronizes the stream; an error when set (the
+// word is cleared and the session reset, its caches being unreliable).
+int check_status(nh_session* s, hipStream_t st) {
+    int32_t status = 0;
+    NH_TRY(hipMemcpyAsync(&status, s->S.status, 4, hipMemcpyDeviceToHost, st), "status");
+    NH_TRY(hipStreamSynchronize(st), "status");
+    if (status == 0) return NH_OK;
+    const int32_t zero = 0;
+    NH_TRY(hipMemcpyAsync(s->S.status, &zero, 4, hipMemcpyHostToDevice, st), "status");
+    NH_TRY(hipStreamSynchronize(st), "status");
+    nh_session_reset(s);
+    return fail(NH_EDEVICE, "a bounded wait in the layer kernel gave up (the session was reset)");
+}
+
 // Model::forward_native (infer.rs:1105-1132) over host token ids: chunks of
 // 32, a one-token chunk as a step, LastLogits / LastHidden from the last
 // chunk only.  Returns the rows written.
 int forward_ids(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, hipStream_t st) {
     NH_TRY(hipMemcpyAsync(s->S.tokens + s->len, toks, (size_t)n * 4, hipMemcpyHostToDevice, st), "tokens");
-    NH_TRY(hipStreamSynchronize(st), "tokens");
+    if (int rc = check_status(s, st)) return rc;
     s->toks.resize(s->len);
     s->toks.insert(s->toks.end(), toks, toks + n);
     const int width = out_width(s, outputs);
@@ -714,7 +729,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     const size_t o_xi = Y.take(AR * Gd * nh::GROUP), o_si = Y.take(AR * Gd * 4);
     const size_t o_xa = Y.take(AR * Ga * nh::GROUP), o_sa = Y.take(AR * Ga * 4);
     const size_t o_xe = Y.take(E * AR * Gd * nh::GROUP), o_se = Y.take(E * AR * Gd * 4);
-    const size_t o_am = Y.take(16);
+    const size_t o_am = Y.take(16), o_st = Y.take(16);
     hipError_t e = hipMalloc(&s->d_buf, Y.size);
     if (e == hipSuccess) e = hipMemset(s->d_buf, 0, Y.size);
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -738,6 +753,8 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     S.xq_att = (int8_t*)(b + o_xa), S.sx_att = (float*)(b + o_sa);
     S.xq_eng = (int8_t*)(b + o_xe), S.sx_eng = (float*)(b + o_se);
     S.argmax = (int32_t*)(b + o_am);
+    S.status = (int32_t*)(b + o_st);
+    D.spin_limit = nh::SPIN_LIMIT;
     auto view = [](int8_t* xq, float* sx, int in_dim, int groups) {
         nh_qact a{};
         a.cap_rows = nh::ACT_ROWS;
@@ -799,6 +816,12 @@ int nh_session_clone(const nh_session* s, void* stream, nh_session** out) {
     c->slot_pos = s->slot_pos;
     c->toks = s->toks;
     *out = c;
+    return NH_OK;
+}
+
+int nh_session_debug_spin_limit(nh_session* s, int limit) {
+    if (!s || limit < 0) return fail(NH_EINVAL, "bad arguments");
+    s->dims.spin_limit = limit > 0 ? limit : 0;
     return NH_OK;
 }
 
@@ -920,6 +943,13 @@ int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* 
     return NH_OK;
 }
 
+int nh_argmax(const float* x, int n, uint32_t* dst, void* stream) {
+    if (!x || !dst || n <= 0) return fail(NH_EINVAL, "bad arguments");
+    if (!nh::ready()) return fail(NH_ESTATE, "nh_init has not been called");
+    NH_TRY(nh::fwd_argmax(x, n, dst, (hipStream_t)stream), "argmax");
+    return NH_OK;
+}
+
 int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, void* stream) {
     if (!s || steps < 0 || (steps > 0 && !out)) return fail(NH_EINVAL, "bad arguments");
     if (!nh::ready()) return fail(NH_ESTATE, "nh_init has not been called");
@@ -937,11 +967,10 @@ int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, v
                "logits");
     if (steps > 0) {
         NH_TRY(hipMemcpyAsync(out, s->S.tokens + len0, (size_t)steps * 4, hipMemcpyDeviceToHost, st), "tokens");
-        NH_TRY(hipStreamSynchronize(st), "tokens");
         s->toks.resize(len0);
         s->toks.insert(s->toks.end(), out, out + steps);
     }
-    return NH_OK;
+    return check_status(s, st);
 }
 
 }  // extern "C"

@@ -70,11 +70,13 @@ SIGNATURES = {
     "nh_session_clone": (I, [P, P, P]),
     "nh_session_set_attend": (I, [P, I, I]),
     "nh_session_rollback": (I, [P, I]),
+    "nh_session_debug_spin_limit": (I, [P, I]),
     "nh_session_rewind_zeroed": (I, [P, I]),
     "nh_session_last_hidden": (I, [P, P, P]),
     "nh_session_head_logits": (I, [P, P, P]),
     "nh_session_head_logits_sparse": (I, [P, P, I, P, P]),
     "nh_generate_greedy": (I, [P, I, P, P, P]),
+    "nh_argmax": (I, [P, I, P, P]),
     "nh_normal": (I, [C.c_uint32, C.c_uint32, C.c_uint64, P]),
     "nh_split": (I, [C.c_uint32, C.c_uint32, P]),
 }
@@ -488,6 +490,10 @@ class Session:
         """Session::attend = Some((sink, ring)) (model.rs:62-66); ring 0: None."""
         _check(_lib.nh_session_set_attend(self.h, int(sink), int(ring)))
 
+    def debug_spin_limit(self, limit: int):
+        """Test hook: the polls a bounded in-kernel wait makes before giving up."""
+        _check(_lib.nh_session_debug_spin_limit(self.h, int(limit)))
+
     def rollback(self, n: int):
         """Session::rollback (model.rs:81-113)."""
         _check(_lib.nh_session_rollback(self.h, int(n)))
@@ -540,6 +546,13 @@ def head_logits(embedding: QMat, h: torch.Tensor, out_rows: int) -> torch.Tensor
     """Model::head_logits (crates/needle-engine/src/infer.rs:1135-1141)."""
     a = QAct.new(h, 1, h.numel(), embedding.act_bits())
     return embedding.matmul(a)[0, :out_rows]
+
+
+def argmax(x: torch.Tensor, stream=None) -> int:
+    """generate::argmax (crates/needle-engine/src/generate.rs:42-50) on the device."""
+    dst = torch.zeros(1, dtype=torch.int32, device="cuda")
+    _check(_lib.nh_argmax(_dptr(x), x.numel(), _dptr(dst), _stream(stream)))
+    return int(dst.item())
 
 
 def codebook(bits: int) -> np.ndarray:

@@ -302,3 +302,18 @@ def test_repeatable(nh):
     y1 = q.matmul(a).cpu().numpy()
     y2 = q.matmul(a).cpu().numpy()
     assert bits_equal(y1, y2)
+
+
+def test_device_argmax_rule(nh):
+    """generate::argmax on the device: the first maximum, NaNs never win, a NaN
+    first element gives 0 (the reference's loop), over cases that cross the
+    kernel's thread, wavefront and batch boundaries."""
+    from test_oracle_numerics import argmax_cases
+    cases = argmax_cases()
+    rng = np.random.default_rng(5)
+    big = rng.normal(size=40000).astype(np.float32)
+    big[[5, 1029, 33000]] = np.float32(9.0)
+    big[[3, 20000]] = np.float32(np.nan)
+    cases.append(big)
+    for x in cases:
+        assert nh.argmax(torch.from_numpy(x).cuda()) == o.argmax(x)

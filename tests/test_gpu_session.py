@@ -222,3 +222,19 @@ def test_forward_empty(nh):
     b = s.forward([]).cpu().numpy()  # the logits the session holds
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     assert s.forward([], forward.OUT_HIDDEN).shape[0] == 0
+
+
+def test_bounded_wait_gives_up_and_reports(nh):
+    say("the layer kernel's bounded wait: a spin limit of 0 forced from the host")
+    data = archive(cact.Geometry(**SMALL), seed=81)
+    m = nh.Model.from_archive(data)
+    s = m.session(32)
+    s.debug_spin_limit(0)  # every mixer wait gives up at once; the kernels still end
+    s.forward([1, 2])  # layers 1 and 2 (and the head's input) run the wait
+    with pytest.raises(nh.NeedleHipError, match="gave up"):
+        s.forward([3])  # reported at the next synchronization
+    assert len(s) == 0  # reset
+    s.debug_spin_limit(1 << 20)
+    got = s.forward([5, 6, 7]).cpu().numpy()
+    want = forward.Forward(data).session(32).feed([5, 6, 7])
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

@@ -309,3 +309,33 @@ def test_qlinear_merge():
     y = lin.matmul(a)
     cols = np.concatenate([p.matmul(a) for p in parts], axis=1)
     assert np.array_equal(y, cols)
+
+
+def argmax_ref(x):
+    """generate::argmax (crates/needle-engine/src/generate.rs:42-50) as written."""
+    best = 0
+    for i, v in enumerate(x):
+        if v > x[best]:
+            best = i
+    return best
+
+
+def argmax_cases():
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    rng = np.random.default_rng(17)
+    base = rng.normal(size=5000).astype(np.float32)
+    cases = [base.copy()]
+    for spots in ([0], [1], [3000], [0, 4999], list(range(0, 5000, 7))):
+        c = base.copy()
+        c[spots] = nan
+        cases.append(c)
+    ties = np.zeros(3000, np.float32)
+    ties[[17, 1800, 2999]] = 2.0
+    cases += [ties, np.full(100, -inf, np.float32), np.array([nan, nan, 3.0], np.float32),
+              np.array([-inf, nan, -inf], np.float32), np.array([1.0, inf, nan, inf], np.float32)]
+    return cases
+
+
+def test_argmax_rule():
+    for x in argmax_cases():
+        assert o.argmax(x) == argmax_ref(list(x))
