@@ -112,6 +112,11 @@ int nh_qact_download(const nh_qact* a, int8_t* xq, uint64_t xq_bytes, float* sx,
  * else the prefill combine (qlinear.rs:353-363) with block = t < rows/4*4
  * (qlinear.rs:397). */
 int nh_matmul(const nh_qmat* w, const nh_qact* a, float* y, int ldy, int col0, void* stream);
+/* QLinear::apply (qlinear.rs:555-557): y[rows][out] = the products of w
+ * with QAct::new(x, rows, in_dim, act_bits) (DEVICE x[rows][in_dim] f32,
+ * DEVICE y), the decode combine for one row, the prefill combine for more.
+ * The activation staging is allocated and released on `stream` by the call. */
+int nh_qlinear_apply(const nh_qmat* w, const float* x, int rows, float* y, void* stream);
 /* The prefill combine with one block flag per token (1: (norm*cbs)*sx,
  * 0: norm*(cbs*sx)): a batched feed of several <=32-token chunks gives
  * each token its in-chunk flag (crates/needle-engine/src/infer.rs:1105-1132). */

@@ -604,6 +604,48 @@ static int check_pair(const nh_qmat* w, const nh_qact* a) {
     return NH_OK;
 }
 
+// QLinear::apply's two steps over a staging activation (xq, sx) of
+// `cap_rows` rows: A8 of x, then the product (decode combine for one row,
+// prefill combine for more) into y[rows][out].
+static int apply_into(const nh_qmat* w, const float* x, int rows, float* y, int8_t* xq, float* sx, int cap_rows,
+                      hipStream_t st) {
+    nh_qact a{};
+    a.cap_rows = cap_rows;
+    a.rows = rows;
+    a.in_dim = w->m.in_dim;
+    a.groups = w->m.groups;
+    a.bits = w->m.bits;
+    a.d_xq = xq;
+    a.d_sx = sx;
+    NH_HIP(launch_act_prep(x, rows, a.in_dim, a.groups, a.bits, nullptr, xq, sx, st), "apply: act_prep");
+    hipError_t e = rows == 1 ? launch_gemv(w, &a, y, 0, nullptr, st)
+                             : launch_gemm(w, &a, nullptr, y, w->m.out, 0, nullptr, st);
+    NH_HIP(e, "apply: product");
+    return NH_OK;
+}
+
+static int check_apply(const nh_qmat* w, const float* x, int rows, const float* y) {
+    if (int rc = check_ready()) return rc;
+    if (!w || !x || !y) return fail(NH_EINVAL, "null argument");
+    if (rows <= 0) return fail(NH_EINVAL, "no rows");
+    if (w->m.groups > 32) return fail(NH_EINVAL, "in_dim above 4096 is not supported");
+    return NH_OK;
+}
+
+int nh_qlinear_apply(const nh_qmat* w, const float* x, int rows, float* y, void* stream) {
+    if (int rc = check_apply(w, x, rows, y)) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    const int cap = (rows + ACT_PAD - 1) / ACT_PAD * ACT_PAD;
+    const size_t nx = (size_t)cap * w->m.groups * GROUP, ns = (size_t)cap * w->m.groups;
+    void* buf = nullptr;
+    NH_HIP(hipMallocAsync(&buf, nx + ns * 4, st), "apply: staging allocation");
+    const int rc = apply_into(w, x, rows, y, (int8_t*)buf, (float*)((uint8_t*)buf + nx), cap, st);
+    const hipError_t e = hipFreeAsync(buf, st);
+    if (rc != NH_OK) return rc;
+    NH_HIP(e, "apply: staging release");
+    return NH_OK;
+}
+
 int nh_matmul(const nh_qmat* w, const nh_qact* a, float* y, int ldy, int col0, void* stream) {
     if (int rc = check_pair(w, a)) return rc;
     if (!y) return fail(NH_EINVAL, "null output");

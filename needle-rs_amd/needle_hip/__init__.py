@@ -45,6 +45,7 @@ SIGNATURES = {
     "nh_qact_rows": (I, [P]),
     "nh_qact_download": (I, [P, P, C.c_uint64, P, C.c_uint64]),
     "nh_matmul": (I, [P, P, P, I, I, P]),
+    "nh_qlinear_apply": (I, [P, P, I, P, P]),
     "nh_matmul_flags": (I, [P, P, P, P, I, I, P]),
     "nh_single_rows": (I, [P, P, P, I, P, P]),
     "nh_head_logits_sparse": (I, [P, P, P, I, I, P, P]),
@@ -319,8 +320,12 @@ class QLinear:
     def rows_into(self, a: QAct, y: torch.Tensor, ldy: int, stream=None):
         self.fused.matmul_into(a, y, ldy, 0, stream)
 
-    def apply(self, x: torch.Tensor, rows: int) -> torch.Tensor:
-        return self.matmul(QAct.new(x, rows, self.in_dim, self.act_bits()))
+    def apply(self, x: torch.Tensor, rows: int, stream=None) -> torch.Tensor:
+        """QLinear::apply (qlinear.rs:555-557): A8 of x [rows][in_dim] and the
+        products, in one call (nh_qlinear_apply)."""
+        y = torch.empty((rows, self.out), dtype=torch.float32, device="cuda")
+        _check(_lib.nh_qlinear_apply(self.fused.h, _dptr(x), int(rows), _dptr(y), _stream(stream)))
+        return y
 
     def bytes(self) -> int:
         return self.fused.bytes()

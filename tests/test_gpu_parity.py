@@ -261,6 +261,12 @@ def test_qlinear_fused_qkvg(nh):
         y = lin.matmul(nh.QAct.new(dev(x), M, K)).cpu().numpy()
         want = olin.matmul(o.OQAct.new(x, M, K))
         assert bits_equal(y, want), report(y, want)
+    # QLinear::apply (qlinear.rs:555-557): A8 and the products in one call
+    for M in (1, 3, 70):
+        x = o.seeded_normals([M * K], 9 + M)[0]
+        y = lin.apply(dev(x), M).cpu().numpy()
+        want = olin.matmul(o.OQAct.new(x, M, K))
+        assert bits_equal(y, want), report(y, want)
 
 
 def test_edge_cases(nh):
