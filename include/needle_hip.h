@@ -117,6 +117,16 @@ int nh_matmul(const nh_qmat* w, const nh_qact* a, float* y, int ldy, int col0, v
  * DEVICE y), the decode combine for one row, the prefill combine for more.
  * The activation staging is allocated and released on `stream` by the call. */
 int nh_qlinear_apply(const nh_qmat* w, const float* x, int rows, float* y, void* stream);
+/* No counterpart in the reference: nh_qlinear_apply for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  It allocates nothing: the activation staging is a
+ * static device array of 270,336 bytes that each GPU the library runs on
+ * holds until the process ends.  At most 64 rows and in_dim <= 4096 (32
+ * groups); larger inputs return NH_EINVAL.  Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU (other streams,
+ * threads or processes) race and must be serialized by the caller.
+ * nh_init must have been called for the current device. */
+int nh_qlinear_apply_static(const nh_qmat* w, const float* x, int rows, float* y, void* stream);
 /* The prefill combine with one block flag per token (1: (norm*cbs)*sx,
  * 0: norm*(cbs*sx)): a batched feed of several <=32-token chunks gives
  * each token its in-chunk flag (crates/needle-engine/src/infer.rs:1105-1132). */

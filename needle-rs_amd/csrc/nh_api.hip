@@ -32,6 +32,19 @@ static float g_cb4[16];
 static float g_cbs4;
 static std::mutex g_init_mu;
 
+// The staging of nh_qlinear_apply_static: one A8 activation of up to
+// STATIC_ROWS rows and 32 groups (int8 codes, then the f32 scales).  Each
+// GPU holds its own copy from the library's load to the end of the process.
+// In host code `scratch` is only a handle for hipGetSymbolAddress; its
+// device address, one per device, is g_scratch[device], set by nh_init.
+constexpr int STATIC_ROWS = ACT_PAD;
+constexpr int STATIC_GROUPS = 32;
+constexpr size_t SCRATCH_XQ = (size_t)STATIC_ROWS * STATIC_GROUPS * GROUP;
+constexpr size_t SCRATCH_BYTES = SCRATCH_XQ + (size_t)STATIC_ROWS * STATIC_GROUPS * 4;
+static __device__ __align__(256) uint8_t scratch[SCRATCH_BYTES];
+constexpr int MAX_DEVICES = 64;
+static void* g_scratch[MAX_DEVICES];
+
 void set_error(const std::string& msg) { g_err = msg; }
 
 int device_cus() { return g_cus > 0 ? g_cus : 1; }
@@ -392,6 +405,15 @@ int nh_init(int device) {
     NH_HIP(hipSetDevice(device), "hipSetDevice");
     NH_HIP(hipDeviceGetAttribute(&g_cus, hipDeviceAttributeMultiprocessorCount, device), "hipDeviceGetAttribute");
     if (!ensure_tables()) return fail(NH_EDEVICE, "no v_perm table pair reproduces the int8 codebook");
+    if (device < MAX_DEVICES) {
+        // this device's copy of the static staging, with the device current
+        std::lock_guard<std::mutex> lk(g_init_mu);
+        if (!g_scratch[device]) {
+            void* p = nullptr;
+            NH_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+            g_scratch[device] = p;
+        }
+    }
     g_device = device;
     return NH_OK;
 }
@@ -644,6 +666,19 @@ int nh_qlinear_apply(const nh_qmat* w, const float* x, int rows, float* y, void*
     if (rc != NH_OK) return rc;
     NH_HIP(e, "apply: staging release");
     return NH_OK;
+}
+
+int nh_qlinear_apply_static(const nh_qmat* w, const float* x, int rows, float* y, void* stream) {
+    if (int rc = check_apply(w, x, rows, y)) return rc;
+    if (rows > STATIC_ROWS) return fail(NH_EINVAL, "nh_qlinear_apply_static takes at most 64 rows");
+    int dev = -1;
+    NH_HIP(hipGetDevice(&dev), "hipGetDevice");
+    void* p = dev >= 0 && dev < MAX_DEVICES ? g_scratch[dev] : nullptr;
+    if (!p) return fail(NH_ESTATE, "nh_init has not been called for the current device");
+    // Nothing in the staging needs to start at zero: act_prep writes the
+    // rows' codes and scales, and the products store no padding row.
+    return apply_into(w, x, rows, y, (int8_t*)p, (float*)((uint8_t*)p + SCRATCH_XQ), STATIC_ROWS,
+                      (hipStream_t)stream);
 }
 
 int nh_matmul(const nh_qmat* w, const nh_qact* a, float* y, int ldy, int col0, void* stream) {

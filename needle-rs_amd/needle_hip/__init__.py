@@ -46,6 +46,7 @@ SIGNATURES = {
     "nh_qact_download": (I, [P, P, C.c_uint64, P, C.c_uint64]),
     "nh_matmul": (I, [P, P, P, I, I, P]),
     "nh_qlinear_apply": (I, [P, P, I, P, P]),
+    "nh_qlinear_apply_static": (I, [P, P, I, P, P]),
     "nh_matmul_flags": (I, [P, P, P, P, I, I, P]),
     "nh_single_rows": (I, [P, P, P, I, P, P]),
     "nh_head_logits_sparse": (I, [P, P, P, I, I, P, P]),
@@ -325,6 +326,12 @@ class QLinear:
         products, in one call (nh_qlinear_apply)."""
         y = torch.empty((rows, self.out), dtype=torch.float32, device="cuda")
         _check(_lib.nh_qlinear_apply(self.fused.h, _dptr(x), int(rows), _dptr(y), _stream(stream)))
+        return y
+
+    def apply_static(self, x: torch.Tensor, rows: int, y: torch.Tensor, stream=None) -> torch.Tensor:
+        """nh_qlinear_apply_static: QLinear::apply into a caller's y [rows][out]
+        with no allocation (a per-GPU static staging; at most 64 rows)."""
+        _check(_lib.nh_qlinear_apply_static(self.fused.h, _dptr(x), int(rows), _dptr(y), _stream(stream)))
         return y
 
     def bytes(self) -> int:
