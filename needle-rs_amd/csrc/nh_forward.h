@@ -26,8 +26,9 @@ constexpr int MAX_TABLES = 16;
 constexpr int ENGRAM_TAPS = 4;      // ENGRAM_CONV_TAPS (config.rs:10)
 constexpr int ATT_CHUNK_MAX = 256;  // key_chunks never makes a chunk longer
 constexpr int ATT_THREADS = 256;
-constexpr int FWD_ROWS = 32;        // token rows of one feed (a prompt chunk, infer.rs:1105-1132)
-constexpr int ACT_ROWS = 64;        // rows of an A8 buffer (the GEMM reads whole 64-token tiles)
+constexpr int FWD_ROWS = 32;        // token rows of one prompt chunk (infer.rs:1105-1132)
+constexpr int BATCH_ROWS = 512;     // token rows of one feed: whole chunks of a prompt fed together
+constexpr int ACT_ROWS = BATCH_ROWS;  // rows of an A8 buffer (a multiple of the GEMM's 64-token tiles)
 constexpr int ROLLBACK = 32;        // ROLLBACK (crates/needle-engine/src/model.rs:181-183)
 constexpr int ROPE_RING = 128;      // RoPE rows kept by position (the reference's list holds at most 66)
 constexpr int DG_MAX_TAPS = 8;      // conv taps the unit kernels are written for
@@ -89,7 +90,7 @@ struct Globals {
 };
 
 // One session's state, all device memory.  Row buffers hold the rows of
-// the current feed (FWD_ROWS at most); activations feed the products.
+// the current feed (BATCH_ROWS at most); activations feed the products.
 struct SessDev {
     float* xs;        // [rows][4][d] residual lanes
     float* u;         // [rows][d] mHC read of the layer
@@ -127,6 +128,7 @@ struct SessDev {
     float* sx_eng;
     int32_t* argmax;  // scratch of the greedy pick
     int32_t* status;  // STATUS_* bits set by a kernel that gave up a wait; the host reads and clears it
+    uint8_t* flags;   // [rows] the prefill combine's block flag of each row of the feed
 };
 
 // A CQ matrix read by rows (the embedding, the engram tables).
@@ -143,7 +145,11 @@ struct BeginArgs {
     int eng_bits[MAX_SITES];  // code width of each site's key | value matrix
 };
 
-// Launchers (nh_forward.hip).  A feed is rows p0 .. p0 + t - 1 (t <= 32).
+// Launchers (nh_forward.hip).  A feed is rows p0 .. p0 + t - 1: one token
+// (a decode step), one prompt chunk (t <= 32), or several whole chunks of
+// at least two tokens each fed together (t <= BATCH_ROWS, chunk c = rows
+// 32c .. 32c + 31): every row keeps its chunk's semantics (the block flag of
+// its products, nested key chunking, sincosf RoPE rows).
 // The start of a feed: the embedding rows into the lanes, the RoPE rows, and
 // per engram site the hashed table rows as A8 rows.
 hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const BeginArgs& B, int p0, int t,
@@ -160,7 +166,9 @@ hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int lay
 // `span`: the keys of a session with an attention span (null: none).
 hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t,
                       const KeySpan* span, hipStream_t s);
-hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int p0, int t, int out_bits,
+// Also writes the tap history of a feed of several chunks (there the units
+// leave it: a row could overwrite a ring slot another row still reads).
+hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, int out_bits,
                         const KeySpan* span, hipStream_t s);
 // One decode token's units, attention, gate and A8 in one launch (the three
 // launches above for a single row), for positions whose keys form one chunk

@@ -150,6 +150,12 @@ __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, Beg
     const int per_row = Gd * (1 + D.sites);
     if (wave < t * per_row) {
         const int i = wave / per_row, r = wave % per_row, pos = p0 + i;
+        if (r == 0 && lane == 0) {
+            // the block flag of row i: its place in its 32-token chunk below
+            // the chunk's length rounded down to 4 (qlinear.rs:397)
+            const int tc = min(FWD_ROWS, t - (i & ~(FWD_ROWS - 1)));
+            S.flags[i] = (i & (FWD_ROWS - 1)) < tc / 4 * 4;
+        }
         if (r < Gd) {
             const uint32_t tok = S.tokens[pos];
             float v0, v1;
@@ -237,7 +243,7 @@ __device__ __forceinline__ int8_t group_quant32(float v, float& s) {
 __global__ __launch_bounds__(1024) void k_engram_hist(Dims D, Globals G, SessDev S, int p0) {
     const int e = blockIdx.x, i = blockIdx.y, k = threadIdx.x, d = D.d, pos = p0 + i;
     const bool on = k < d;
-    const float* kv = S.ekv + (size_t)e * FWD_ROWS * 2 * d;
+    const float* kv = S.ekv + (size_t)e * BATCH_ROWS * 2 * d;
     float s;
     const int8_t q = group_quant32(on ? kv[(size_t)i * 2 * d + d + k] : 0.0f, s);
     const int gs = d / 32;
@@ -264,7 +270,7 @@ __global__ __launch_bounds__(1024) void k_engram_hist(Dims D, Globals G, SessDev
         const float tw = on ? G.etaps[((size_t)e * ENGRAM_TAPS + j) * d + k] : 0.0f;
         dst = __builtin_fmaf(tw, qs * (float)q8, dst);
     }
-    if (on) S.evals[((size_t)e * FWD_ROWS + i) * d + k] = dst;
+    if (on) S.evals[((size_t)e * BATCH_ROWS + i) * d + k] = dst;
 }
 
 hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, int p0, int t, hipStream_t s) {
@@ -772,8 +778,8 @@ __device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const
     const int td = min(t, d - 1);
     q.norm = N.norm_in[td];
     const bool site = N.site >= 0;
-    const float* kp = site ? S.ekv + (size_t)N.site * FWD_ROWS * 2 * d : S.proj;
-    const float* ep = site ? S.evals + (size_t)N.site * FWD_ROWS * d : S.proj + d;
+    const float* kp = site ? S.ekv + (size_t)N.site * BATCH_ROWS * 2 * d : S.proj;
+    const float* ep = site ? S.evals + (size_t)N.site * BATCH_ROWS * d : S.proj + d;
     q.kr = kp[td];
     q.ev = ep[td];
     // Phi8 rows: wavefront w >= 1 holds row w - 1, and row w + PHI_B - 1
@@ -1189,7 +1195,7 @@ __global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, Lay
         u = unit_load<TAPS, EXACT>(D, S, layer, pos, row, start, vdim, vh * vd, vd, L.v_taps, L.k_norm, i);
     }
     if (unit >= nh + 2 * nkv) return;
-    const float v = unit_finish<TAPS, EXACT>(D, S, layer, pos, start, len, u, unit < nh + nkv, i, true);
+    const float v = unit_finish<TAPS, EXACT>(D, S, layer, pos, start, len, u, unit < nh + nkv, i, t <= FWD_ROWS);
     if (unit < nh) {
         if (i < qk) S.qbuf[(size_t)row * qd + start + i] = v;
     } else {
@@ -1560,10 +1566,18 @@ hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int la
 
 // The chunk merge (infer.rs:1990-2006), the head gate
 // (att / (nexp(-gate) + 1), step.rs:558-572) and A8 of the heads.
-__global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, int p0, int rows, int out_bits,
-                                                 KeySpan KS, int span) {
+__global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, int layer, int p0, int rows,
+                                                 int out_bits, KeySpan KS, int span) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, vd = D.vd, K = D.nh * vd;
     const int row = blockIdx.x, pos = p0 + row, Ga = (K + GROUP - 1) / GROUP;
+    // A feed of several chunks: the tap history of its last rows (the units
+    // have read every earlier row by now; only the rows the ring keeps are
+    // written, so no two rows share a slot)
+    if (rows > FWD_ROWS && row >= rows - D.hist_slots) {
+        float* h = S.hist + ((size_t)layer * D.hist_slots + pos % D.hist_slots) * D.W;
+        const float* src = S.proj + (size_t)row * D.nq;
+        for (int k = t; k < D.W; k += LT) h[k] = src[k];
+    }
     __shared__ float att[FWD_MAX_D];
     const int n = key_count(D, KS, span != 0, L.window, pos);
     int count, chunk;
@@ -1598,10 +1612,10 @@ __global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, 
     }
 }
 
-hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int p0, int t, int out_bits,
+hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, int out_bits,
                         const KeySpan* span, hipStream_t s) {
-    hipLaunchKernelGGL(k_attn_out, dim3(t), dim3(LT), 0, s, D, S, L, p0, t, out_bits, span ? *span : KeySpan{},
-                       span ? 1 : 0);
+    hipLaunchKernelGGL(k_attn_out, dim3(t), dim3(LT), 0, s, D, S, L, layer, p0, t, out_bits,
+                       span ? *span : KeySpan{}, span ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -118,7 +118,7 @@ struct nh_model {
     void* d_small = nullptr;
 
     ~nh_model() {
-        if (d_small) hipFree(d_small);
+        if (d_small) (void)hipFree(d_small);
         delete head;
         nh_weights_free(w);
     }
@@ -146,7 +146,7 @@ struct nh_session {
     std::vector<nh_qact> a_eng;
 
     ~nh_session() {
-        if (d_buf) hipFree(d_buf);
+        if (d_buf) (void)hipFree(d_buf);
     }
 };
 
@@ -365,7 +365,7 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
                                  nullptr);
         }
         if (e == hipSuccess) e = hipDeviceSynchronize();
-        hipFree(rows);
+        (void)hipFree(rows);
         NH_TRY(e, "Phi8");
     }
 
@@ -424,9 +424,11 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
 // One product over the feed's rows: the decode combine for one row, the
 // prefill combine (block = i < t / 4 * 4) for more (QMat::matmul_into,
 // qlinear.rs:468-487).
-hipError_t product(const nh_qmat* w, nh_qact* a, int rows, float* y, int ldy, hipStream_t st) {
+// `flags`: the block flag of each row when they come from several chunks
+// (null: one chunk, block = i < t / 4 * 4).
+hipError_t product(const nh_qmat* w, nh_qact* a, int rows, float* y, int ldy, const uint8_t* flags, hipStream_t st) {
     a->rows = rows;
-    return rows == 1 ? nh::launch_gemv(w, a, y, 0, nullptr, st) : nh::launch_gemm(w, a, nullptr, y, ldy, 0, nullptr, st);
+    return rows == 1 ? nh::launch_gemv(w, a, y, 0, nullptr, st) : nh::launch_gemm(w, a, flags, y, ldy, 0, nullptr, st);
 }
 
 // slot_of (crates/needle-engine/src/infer.rs:1749-1756).
@@ -502,14 +504,21 @@ int out_width(const nh_session* s, int outputs) {
     return (outputs == NH_OUT_HIDDEN || outputs == NH_OUT_LAST_HIDDEN) ? s->dims.d : s->dims.out_rows;
 }
 
-// One feed of t <= 32 tokens at positions s->len ..: step_native for one
-// token, chunk_job for more (forward_native, infer.rs:1105-1132); `outputs`
-// picks what the rows give (chunk.rs:331-353, step.rs:715-729), written to
-// `out` (device, rows x width, or null to keep only the session's copies).
+// One feed at positions s->len ..: step_native for one token, chunk_job for
+// a chunk of up to 32 (forward_native, infer.rs:1105-1132), or several whole
+// chunks of at least two tokens each (t <= BATCH_ROWS) as one pass through
+// the layers with each row keeping its chunk's arithmetic (chunk c = rows
+// 32c ..: its rows' block flags, nested key chunks and sincosf RoPE rows;
+// the causal keys of a row do not depend on how the prompt was cut).
+// `outputs` picks what the rows give (chunk.rs:331-353, step.rs:715-729),
+// written to `out` (device, rows x width, or null to keep only the
+// session's copies); for several chunks the Last* modes mean the last
+// chunk's last row, All* every row.
 int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
     const nh_model* m = s->m;
     const nh::SessDev& S = s->S;
     const int p0 = s->len;
+    const uint8_t* flags = t > nh::FWD_ROWS ? S.flags : nullptr;
     nh::Dims D = s->dims;
     D.hist_lo = p0 - s->hrows;
     D.rope_prev = t == 1 && s->rope_n > 0;
@@ -530,27 +539,28 @@ int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
         for (int e = 0; e < D.sites; ++e) {
             s->a_eng[e].rows = 1;
             acts[e] = &s->a_eng[e];
-            ys[e] = S.ekv + (size_t)e * nh::FWD_ROWS * 2 * D.d;
+            ys[e] = S.ekv + (size_t)e * nh::BATCH_ROWS * 2 * D.d;
         }
         NH_TRY(nh::launch_gemv_batch(m->ekv.data(), acts, ys, D.sites, st), "engram kv");
     } else {
         for (int e = 0; e < D.sites; ++e)
-            NH_TRY(product(m->ekv[e], &s->a_eng[e], t, S.ekv + (size_t)e * nh::FWD_ROWS * 2 * D.d, 2 * D.d, st),
+            NH_TRY(product(m->ekv[e], &s->a_eng[e], t, S.ekv + (size_t)e * nh::BATCH_ROWS * 2 * D.d, 2 * D.d, flags,
+                           st),
                    "engram kv");
     }
     NH_TRY(nh::fwd_engram_hist(D, m->glob, S, p0, t, st), "engram history");
     for (int l = 0; l < D.layers; ++l) {
         const nh::LayerDev* prev = l > 0 ? &m->layers[l - 1] : nullptr;
         NH_TRY(nh::fwd_layer(D, m->glob, S, prev, &m->layers[l], 0, t, m->qkvg[l]->m.bits, 0, st), "layer");
-        NH_TRY(product(m->qkvg[l], &s->a_in, t, S.proj, D.nq, st), "q|k|v|gate");
+        NH_TRY(product(m->qkvg[l], &s->a_in, t, S.proj, D.nq, flags, st), "q|k|v|gate");
         if (t == 1 && nh::dec_group_fits(D, p0, m->layers[l].window)) {
             NH_TRY(nh::fwd_dec_attn(D, S, m->layers[l], l, p0, m->out[l]->m.bits, st), "decode attention");
         } else {
             NH_TRY(nh::fwd_units(D, S, m->layers[l], l, p0, t, st), "units");
             NH_TRY(nh::fwd_attend(D, S, m->layers[l], l, p0, t, sp, st), "attend");
-            NH_TRY(nh::fwd_attn_out(D, S, m->layers[l], p0, t, m->out[l]->m.bits, sp, st), "attention out");
+            NH_TRY(nh::fwd_attn_out(D, S, m->layers[l], l, p0, t, m->out[l]->m.bits, sp, st), "attention out");
         }
-        NH_TRY(product(m->out[l], &s->a_att, t, S.o, D.d, st), "out");
+        NH_TRY(product(m->out[l], &s->a_att, t, S.o, D.d, flags, st), "out");
     }
     // the last layer's post block, the lane mean and final norm of the rows
     // the outputs want, then the head (head_logits per row, decode combine)
@@ -565,7 +575,7 @@ int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
             a.d_xq += (size_t)i * Gd * nh::GROUP;
             a.d_sx += (size_t)i * Gd;
             float* y = (outputs == NH_OUT_ALL_LOGITS && out) ? out + (size_t)i * D.out_rows : S.logits;
-            NH_TRY(product(m->head, &a, 1, y, D.out_rows, st), "head");
+            NH_TRY(product(m->head, &a, 1, y, D.out_rows, nullptr, st), "head");
             if (i == rows - 1 && y != S.logits)
                 NH_TRY(hipMemcpyAsync(S.logits, y, (size_t)D.out_rows * 4, hipMemcpyDeviceToDevice, st), "logits");
         }
@@ -580,14 +590,18 @@ int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
     } else {
         s->have_logits = false;
     }
-    // the host mirrors: the history rows and their trim (chunk.rs:319-329),
-    // the RoPE list and its trim (rope_rows, infer.rs:1740-1745)
+    // the host mirrors, chunk by chunk: the history rows and their trim
+    // (chunk.rs:319-329), the RoPE list and its trim (rope_rows,
+    // infer.rs:1740-1745)
     s->len = p0 + t;
     const int keep = D.taps - 1 + nh::ROLLBACK;
-    s->hrows += t;
-    if (s->hrows > 2 * keep) s->hrows = keep;
-    s->rope_n += t;
-    if (s->rope_n > 2 * (nh::ROLLBACK + 1)) s->rope_n = nh::ROLLBACK + 1;
+    for (int c = 0; c < t; c += nh::FWD_ROWS) {
+        const int tc = std::min(nh::FWD_ROWS, t - c);
+        s->hrows += tc;
+        if (s->hrows > 2 * keep) s->hrows = keep;
+        s->rope_n += tc;
+        if (s->rope_n > 2 * (nh::ROLLBACK + 1)) s->rope_n = nh::ROLLBACK + 1;
+    }
     return rows;
 }
 
@@ -616,8 +630,13 @@ int forward_ids(nh_session* s, const uint32_t* toks, int n, int outputs, float* 
     s->toks.insert(s->toks.end(), toks, toks + n);
     const int width = out_width(s, outputs);
     int rows = 0;
-    for (int i = 0; i < n; i += nh::FWD_ROWS) {
-        const int t = std::min(nh::FWD_ROWS, n - i);
+    for (int i = 0; i < n;) {
+        // whole chunks of 32 together while every chunk has two tokens or
+        // more (a one-token chunk is a step) and no attention span (a span's
+        // slot map changes chunk by chunk)
+        int t = std::min(nh::FWD_ROWS, n - i);
+        if (s->ring == 0 && t > 1)
+            while (t < nh::BATCH_ROWS && i + t < n && n - (i + t) > 1) t += std::min(nh::FWD_ROWS, n - (i + t));
         const bool last = i + t == n;
         const int want =
             (!last && (outputs == NH_OUT_LAST_LOGITS || outputs == NH_OUT_LAST_HIDDEN)) ? NH_OUT_NONE : outputs;
@@ -630,6 +649,7 @@ int forward_ids(nh_session* s, const uint32_t* toks, int n, int outputs, float* 
             return fail(r, msg + " (the session was reset)");
         }
         rows += r;
+        i += t;
     }
     return rows;
 }
@@ -709,7 +729,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     int mc = 1;
     for (int n = 1; n <= cap; ++n) mc = std::max(mc, key_chunk_count(n, D.nkv));
     D.max_chunks = mc;
-    const size_t d = D.d, L = D.layers, c = cap, E = D.sites, R = nh::FWD_ROWS, AR = nh::ACT_ROWS;
+    const size_t d = D.d, L = D.layers, c = cap, E = D.sites, R = nh::BATCH_ROWS, AR = nh::ACT_ROWS;
     const size_t half = D.qk / 2;
     const int Gd = (D.d + nh::GROUP - 1) / nh::GROUP, Ga = (D.nh * D.vd + nh::GROUP - 1) / nh::GROUP;
     Layout Y;
@@ -729,7 +749,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     const size_t o_xi = Y.take(AR * Gd * nh::GROUP), o_si = Y.take(AR * Gd * 4);
     const size_t o_xa = Y.take(AR * Ga * nh::GROUP), o_sa = Y.take(AR * Ga * 4);
     const size_t o_xe = Y.take(E * AR * Gd * nh::GROUP), o_se = Y.take(E * AR * Gd * 4);
-    const size_t o_am = Y.take(16), o_st = Y.take(16);
+    const size_t o_am = Y.take(16), o_st = Y.take(16), o_fl = Y.take(R);
     hipError_t e = hipMalloc(&s->d_buf, Y.size);
     if (e == hipSuccess) e = hipMemset(s->d_buf, 0, Y.size);
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -754,6 +774,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     S.xq_eng = (int8_t*)(b + o_xe), S.sx_eng = (float*)(b + o_se);
     S.argmax = (int32_t*)(b + o_am);
     S.status = (int32_t*)(b + o_st);
+    S.flags = (uint8_t*)(b + o_fl);
     D.spin_limit = nh::SPIN_LIMIT;
     auto view = [](int8_t* xq, float* sx, int in_dim, int groups) {
         nh_qact a{};
@@ -879,7 +900,7 @@ int nh_session_head_logits(nh_session* s, float* logits, void* stream) {
     a.bits = s->m->head_bits;
     NH_TRY(nh::launch_act_prep(s->S.last_hid, 1, D.d, a.groups, s->m->head_bits, nullptr, a.d_xq, a.d_sx, st),
            "head A8");
-    NH_TRY(product(s->m->head, &a, 1, logits, D.out_rows, st), "head");
+    NH_TRY(product(s->m->head, &a, 1, logits, D.out_rows, nullptr, st), "head");
     return NH_OK;
 }
 
