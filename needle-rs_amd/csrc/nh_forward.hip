@@ -139,11 +139,11 @@ __device__ __forceinline__ int window_lo(int window, int p0) {
 // then per engram site e and group g the hashed row of table g
 // (engram_native, infer.rs:1261-1275) dequantized and rotated (QMat::row),
 // A8-prepared as group g of the site's activation row i (QAct::new over the
-// concatenated rows); missing rows are zeros.  The last wave: the RoPE rows
-// (rope_rows, infer.rs:1716-1747): for one token right after the newest
-// row the reference still keeps (D.rope_prev, the host's mirror of its
-// list) the angle-addition recurrence from that row, else sincosf(freq *
-// pos) per row; every row also goes to the ring of recent rows.
+// concatenated rows); missing rows are zeros.  The last t waves: the RoPE
+// rows (rope_rows, infer.rs:1716-1747), one row each: for one token right
+// after the newest row the reference still keeps (D.rope_prev, the host's
+// mirror of its list) the angle-addition recurrence from that row, else
+// sincosf(freq * pos); every row also goes to the ring of recent rows.
 __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, BeginArgs B, int p0, int t) {
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     const int Gd = (D.d + GROUP - 1) / GROUP;
@@ -190,8 +190,8 @@ __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, Beg
             const size_t unit = ((size_t)e * ACT_ROWS + i) * Gd + g;
             a8_group(v0, v1, lane, B.eng_bits[e], S.xq_eng + unit * GROUP, S.sx_eng + unit);
         }
-    } else if (wave == t * per_row) {
-        const int half = D.qk / 2;
+    } else if (wave < t * per_row + t) {
+        const int half = D.qk / 2, i = wave - t * per_row;
         if (lane < half) {
             if (t == 1 && D.rope_prev) {
                 const size_t prev = (size_t)((p0 + ROPE_RING - 1) % ROPE_RING) * half + lane;
@@ -203,12 +203,12 @@ __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, Beg
                 S.rope_rc[(size_t)(p0 % ROPE_RING) * half + lane] = c;
                 S.rope_rs[(size_t)(p0 % ROPE_RING) * half + lane] = sn;
             } else {
-                for (int i = 0; i < t; ++i) {
-                    double sv, cv;
-                    sincos((double)(G.freq[lane] * (float)(p0 + i)), &sv, &cv);
-                    const float c = (float)cv, sn = (float)sv;
-                    S.rope_c[i * half + lane] = c;
-                    S.rope_s[i * half + lane] = sn;
+                double sv, cv;
+                sincos((double)(G.freq[lane] * (float)(p0 + i)), &sv, &cv);
+                const float c = (float)cv, sn = (float)sv;
+                S.rope_c[i * half + lane] = c;
+                S.rope_s[i * half + lane] = sn;
+                if (i + ROPE_RING >= t) {  // the rows the ring keeps (no two share a slot)
                     S.rope_rc[(size_t)((p0 + i) % ROPE_RING) * half + lane] = c;
                     S.rope_rs[(size_t)((p0 + i) % ROPE_RING) * half + lane] = sn;
                 }
@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, Beg
 hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const BeginArgs& B, int p0, int t,
                      hipStream_t s) {
     const int Gd = (D.d + GROUP - 1) / GROUP;
-    const int waves = t * Gd * (1 + D.sites) + 1;
+    const int waves = t * Gd * (1 + D.sites) + t;
     hipLaunchKernelGGL(k_begin, dim3((waves + 3) / 4), dim3(256), 0, s, D, G, S, B, p0, t);
     return hipGetLastError();
 }
@@ -1553,11 +1553,207 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     }
 }
 
+// LDS writes of a wavefront visible to its other lanes (its LDS operations
+// complete in order; the fence waits for them and keeps the compiler from
+// moving accesses across).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+}
+
+// attend_head_ref for all the query heads that share a kv head: one
+// workgroup per (row, kv head, key chunk) stages the chunk's key rows,
+// scales and value columns once (as k_attend does), then wavefront h
+// computes query head h of the group: the int8 query, the scores (key i of
+// the chunk on lane i % 64), the chunk max, chunk_exp with the reference's
+// sum order (lanes 0-7 run the eight lane-class chains), the weights and
+// 21-bit digits, and the exact integer P.V with lane = value dimension.
+constexpr int AG_WAVES = 8;  // query heads per kv head this kernel takes
+constexpr int AG_T = AG_WAVES * 64;
+
+__global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerDev L, int layer, int p0, int rows) {
+    const int row = blockIdx.x / D.nkv, kvh = blockIdx.x % D.nkv, ci = blockIdx.y, t = threadIdx.x;
+    const int wave = t >> 6, lane = t & 63, pos = p0 + row;
+    const int nkv = D.nkv, qk = D.qk, vd = D.vd, hpg = D.nh / nkv;
+    const int lo = window_lo(L.window, pos), n = pos + 1 - lo;
+    int count, chunk;
+    key_chunks(n, nkv, rows > 1, count, chunk);
+    if (ci >= count) return;
+    const int c0 = ci * chunk, len = min(chunk, n - c0), blocked = len / 4 * 4, slot0 = lo + c0;
+    const int sh = slot0 & 3, base = slot0 - sh, cols = sh + len;
+    __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][ATT_KPITCH];
+    __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][ATT_PITCH];
+    __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
+    __shared__ alignas(16) int8_t q8[AG_WAVES][MAX_HEAD_DIM];
+    __shared__ float sc[AG_WAVES][ATT_CHUNK_MAX];
+    __shared__ alignas(16) int8_t dig[AG_WAVES][3][ATT_PITCH];
+    const size_t lc = (size_t)layer * D.cap;
+    const int hw = min(wave, hpg - 1), hh = kvh * hpg + hw;
+    // every load first (unconditional, at clamped in-range addresses)
+    const float qv = S.qbuf[((size_t)row * D.nh + hh) * qk + min(lane, qk - 1)];
+    constexpr int KR = ATT_CHUNK_MAX * 4 / AG_T, VR = (MAX_HEAD_DIM * ATT_VDW + AG_T - 1) / AG_T;
+    const int rq = qk / 16, vdw = (cols + 3) / 4;
+    uint4 kr[KR];
+    uint32_t vw[VR];
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+        const int e = t + r * AG_T, i = min(e >> 2, len - 1), c = min(e & 3, rq - 1);
+        kr[r] = reinterpret_cast<const uint4*>(S.k8 + ((lc + slot0 + i) * nkv + kvh) * qk)[c];
+    }
+    float ksr, vsr;
+    {
+        const int i = min(t, len - 1);
+        ksr = S.ks[(lc + slot0 + i) * nkv + kvh];
+        vsr = S.vs[(lc + slot0 + i) * nkv + kvh];
+    }
+    const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
+#pragma unroll
+    for (int r = 0; r < VR; ++r) {
+        const int e = t + r * AG_T, dm = min(e / ATT_VDW, vd - 1), k = min(e % ATT_VDW, vdw - 1);
+        vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
+    }
+    // the query of this wavefront's head
+    const float s = wave_quant_scale(lane < qk ? qv : 0.0f);
+    if (lane < qk) q8[wave][lane] = quant_one(qv, 1.0f / s);
+    const float qs = s * bits_f32(0x3e13cd3au);
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+        const int e = t + r * AG_T, i = e >> 2, c = e & 3;
+        if (i < len && c < rq) reinterpret_cast<uint4*>(ks8[i])[c] = kr[r];
+    }
+    if (t < len) {
+        kss[t] = ksr;
+        vss[t] = vsr;
+    }
+#pragma unroll
+    for (int r = 0; r < VR; ++r) {
+        const int e = t + r * AG_T, dm = e / ATT_VDW, k = e % ATT_VDW;
+        if (dm < vd && k < vdw) {
+            if (4 * k + 3 < cols) {
+                reinterpret_cast<uint32_t*>(vs8[dm])[k] = vw[r];
+            } else {
+#pragma unroll
+                for (int b = 0; b < 4; ++b)
+                    if (4 * k + b < cols) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
+            }
+        }
+    }
+    __syncthreads();
+    if (wave >= hpg) return;
+    float* scw = sc[wave];
+    float mx = -__builtin_inff();
+    {
+        uint4 qw[MAX_HEAD_DIM / 16];
+#pragma unroll
+        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) qw[c] = reinterpret_cast<const uint4*>(q8[wave])[c];
+        for (int i = lane; i < len; i += 64) {
+            int dot = 0;
+#pragma unroll
+            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
+                if (c < rq) {
+                    const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
+                    dot = __builtin_amdgcn_sdot4((int)kv.x, (int)qw[c].x, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)kv.y, (int)qw[c].y, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)kv.z, (int)qw[c].z, dot, false);
+                    dot = __builtin_amdgcn_sdot4((int)kv.w, (int)qw[c].w, dot, false);
+                }
+            const float ksc = kss[i];
+            const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
+            scw[i] = sv;
+            mx = fmaxf(mx, sv);
+        }
+    }
+    mx = wave_max(mx);
+    for (int i = lane; i < len; i += 64) scw[i] = i < blocked ? nexp(scw[i] - mx) : lexpf(scw[i] - mx);
+    wave_lds_sync();
+    float sum;
+    {
+        // chunk_exp's order (infer.rs:2222-2279): a[k] over the 8-blocks'
+        // first halves plus a trailing 4-block, b[k] over their second
+        // halves (lane 4 hi + k), then t = a + b, (t0 + t1) + (t2 + t3)
+        float acc = 0.0f;
+        const int nb8 = len / 8;
+        if (lane < 8) {
+            const int k = lane & 3, hi = lane >> 2;
+            const float* col = &scw[hi * 4 + k];
+            int b = 0;
+            for (; b + 8 <= nb8; b += 8) {
+                float v[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[j] = col[(b + j) * 8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc += v[j];
+            }
+            for (; b < nb8; ++b) acc += col[b * 8];
+            if (hi == 0 && len - nb8 * 8 >= 4) acc += scw[nb8 * 8 + k];
+        }
+        const float tk = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
+                                                                                       0x104, 0xF, 0xF, false));
+        const int ti = __builtin_bit_cast(int, tk);
+        const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x00, 0xF, 0xF, false));
+        const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x55, 0xF, 0xF, false));
+        const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xAA, 0xF, 0xF, false));
+        const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xFF, 0xF, 0xF, false));
+        sum = (t0 + t1) + (t2 + t3);
+        int i = blocked;
+        if (len - i >= 2) {
+            sum = (scw[i] + sum) + scw[i + 1];
+            i += 2;
+        }
+        if (len - i == 1) sum += scw[i];
+    }
+    float wmax = 0.0f;
+    for (int i = lane; i < len; i += 64) {
+        const float w = scw[i] * vss[i];
+        scw[i] = w;
+        wmax = fmaxf(wmax, w);
+    }
+    wmax = wave_max(wmax);
+    const float qwt = bits_f32(0x49fffff8u) / wmax;
+    int8_t(*dg)[ATT_PITCH] = dig[wave];
+    for (int i = lane; i < len; i += 64) {
+        const int32_t wq = (int32_t)roundf(scw[i] * qwt);
+        dg[0][sh + i] = (int8_t)(wq >> 14);
+        dg[1][sh + i] = (int8_t)((wq >> 7) & 127);
+        dg[2][sh + i] = (int8_t)(wq & 127);
+    }
+    // zero digits in the first dword before the keys and the last one past them
+    if (lane < 4) {
+        const int j0 = lane, j1 = cols + lane;
+        if (j0 < sh) dg[0][j0] = dg[1][j0] = dg[2][j0] = 0;
+        if (j1 < (cols + 3) / 4 * 4) dg[0][j1] = dg[1][j1] = dg[2][j1] = 0;
+    }
+    wave_lds_sync();
+    const float cw = wmax * bits_f32(0x35000004u);
+    const size_t pi = ((size_t)row * D.nh + hh) * D.max_chunks + ci;
+    if (lane < vd) {
+        // exact integer P.V over the chunk, four keys per sdot4
+        const int* vrow = reinterpret_cast<const int*>(vs8[lane]);
+        const int* d0 = reinterpret_cast<const int*>(dg[0]);
+        const int* d1 = reinterpret_cast<const int*>(dg[1]);
+        const int* d2 = reinterpret_cast<const int*>(dg[2]);
+        int a = 0, b = 0, c = 0;
+        for (int k = 0; 4 * k < cols; ++k) {
+            const int v = vrow[k];
+            a = __builtin_amdgcn_sdot4(d0[k], v, a, false);
+            b = __builtin_amdgcn_sdot4(d1[k], v, b, false);
+            c = __builtin_amdgcn_sdot4(d2[k], v, c, false);
+        }
+        S.po[pi * vd + lane] = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
+    }
+    if (lane == 0) {
+        S.pm[pi] = mx;
+        S.psum[pi] = sum;
+    }
+}
+
 hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t,
                       const KeySpan* span, hipStream_t s) {
     if (span)
         hipLaunchKernelGGL(k_attend<true>, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer, p0,
                            t, *span);
+    else if (D.nh / D.nkv <= AG_WAVES)
+        hipLaunchKernelGGL(k_attend_group, dim3(t * D.nkv, D.max_chunks), dim3(AG_T), 0, s, D, S, L, layer, p0, t);
     else
         hipLaunchKernelGGL(k_attend<false>, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer,
                            p0, t, KeySpan{});
