@@ -1,10 +1,12 @@
 """Benchmark: W4A8 decode GEMV (K=2048, N=8192, one token) on one MI355X.
 
-A step is one GEMV launch (the decode combine over one CQ-W4 matrix).  The
-timed region replays a HIP graph that sweeps `--copies` distinct weight
-copies (>= 64 => > 512 MiB, so bytes come from HBM, not the 256 MiB
-Infinity Cache), bracketed by torch.cuda.synchronize() and timed with HIP
-events on the stream the kernels run on.  Algorithmic bytes per launch =
+A step is one sweep of the decode GEMV over `--copies` distinct HBM-resident
+weight copies (>= 64 => > 512 MiB, so bytes come from HBM, not the 256 MiB
+Infinity Cache): `copies` dependent launches of the full K=2048 N=8192
+product, captured once as a HIP graph.  Exactly `--steps` replays are
+timed, bracketed by torch.cuda.synchronize() and timed with HIP events on
+the stream the kernels run on; `value` is the algorithmic bytes of one
+launch over the mean time of one launch.  Algorithmic bytes per launch =
 codes N*K/2 + norms N*(K/128)*2 + int8 activations K + scales (K/128)*4 +
 f32 output N*4 = 8,685,632 B.
 
@@ -28,6 +30,47 @@ sys.path.insert(0, os.path.join(ROOT, "needle-rs_amd"))
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 K, N, GROUP = 2048, 8192, 128
+# The published Needle 3's vocabulary (its logits are [t, 8192]): with it the
+# Config::default geometry (20 layers, d 768) has 121M parameters.
+NEEDLE3_VOCAB = 8192
+
+
+def host_cpu() -> str:
+    """The host's CPU model, as /proc/cpuinfo names it."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def logits_err(got, want):
+    """(bit-identical, max |got - want|, that over max |want|) of two logit rows."""
+    import numpy as np
+
+    got = np.asarray(got, dtype=np.float32)
+    want = np.asarray(want, dtype=np.float32)
+    d = float(np.abs(got - want).max())
+    return bool(np.array_equal(got.view(np.uint32), want.view(np.uint32))), d, d / max(float(np.abs(want).max()), 1e-30)
+
+
+class ErrStats:
+    def __init__(self):
+        self.n = self.exact = 0
+        self.abs = self.rel = 0.0
+
+    def add(self, got, want):
+        e, a, r = logits_err(got, want)
+        self.n += 1
+        self.exact += int(e)
+        self.abs = max(self.abs, a)
+        self.rel = max(self.rel, r)
+
+    def json(self):
+        return {"logit_rows_compared": self.n, "bit_identical": self.exact, "max_abs": float(f"{self.abs:.3g}"),
+                "max_rel": float(f"{self.rel:.3g}")}
 
 
 def progress(msg: str):
@@ -91,8 +134,7 @@ def gpu_gemv(args, nh, torch):
         for m in mats:
             m.matmul_into(a, y, N, 0)
 
-    reps = max(1, args.steps // args.copies)
-    warm = max(1, args.warmup // args.copies)
+    reps, warm = max(1, args.steps), max(1, args.warmup)
     ms_sweep = time_graph(sweep, reps, warm, torch)
     ms_launch = ms_sweep / len(mats)
     # sanity: the graph's result equals an eager launch (no oracle here)
@@ -104,8 +146,8 @@ def gpu_gemv(args, nh, torch):
         raise SystemExit("non-finite GEMV output")
     nbytes = algorithmic_bytes(1, K, N)
     gbs = nbytes / (ms_launch * 1e-3) / 1e9
-    return {"ms_launch": ms_launch, "gbs": gbs, "bytes": nbytes, "launches": reps * len(mats), "x": x,
-            "packed": packed, "norms": norms, "G": G, "a": a}
+    return {"ms_launch": ms_launch, "ms_sweep": ms_sweep, "gbs": gbs, "bytes": nbytes, "launches": reps * len(mats),
+            "x": x, "packed": packed, "norms": norms, "G": G, "a": a}
 
 
 def gpu_gemv_steady(gpu, copies, nh, torch):
@@ -171,7 +213,7 @@ def gpu_sweeps(nh, torch):
 def needle3_products(nh, torch):
     """Secondary line: the CQ-W4 x A8 products of the Needle-3 forward at its
     default geometry (crates/needle-core/src/config.rs:61-100: d 768, 20
-    layers, vocab 16384, q|k|v|gate 576+96+128+768, 5 engram sites), with
+    layers, vocab 8192, q|k|v|gate 576+96+128+768, 5 engram sites), with
     random-init weights 0.02*N(0,1) packed to CQ-W4 and fused as QWeights
     holds them (crates/needle-engine/src/weights.rs:480-495).
 
@@ -185,7 +227,7 @@ def needle3_products(nh, torch):
     head once."""
     import numpy as np
 
-    d, layers, vocab, sites, chunk, seq = 768, 20, 16384, 5, 32, 512
+    d, layers, vocab, sites, chunk, seq = 768, 20, NEEDLE3_VOCAB, 5, 32, 512
     parts = (576, 96, 128, 768)
     seed = [1000]
 
@@ -251,7 +293,7 @@ DECODE_PROMPT, DECODE_STEPS = 118, 64
 
 def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
     """The full Needle-3 decode (crates/needle-core/src/config.rs:61-100:
-    20 layers, d 768, vocab 16384, 5 engram sites) from random-init weights
+    20 layers, d 768, 5 engram sites; vocab 8192, 121M parameters) from random-init weights
     0.02*N(0,1) through CQ-W4 (needle_hip.archive.random_needle3, seed 0):
     a prompt of 118 uniform random token ids fed as forward_native feeds it
     (chunks of 32 through chunk_job), then 64 greedy decode steps on the
@@ -268,7 +310,7 @@ def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
     from needle_hip import archive
 
     t0 = time.perf_counter()
-    data = archive.random_needle3(nh, seed=0)
+    data = archive.random_needle3(nh, archive.Needle3(vocab=NEEDLE3_VOCAB), seed=0)
     build_s = time.perf_counter() - t0
     model = nh.Model.from_archive(data)
     vocab = model.out_rows
@@ -309,24 +351,32 @@ def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
         import oracle as o
         from oracle import forward
 
+        # The oracle fed the same prompt and the device's picks; the device
+        # re-fed step by step (outside the timed runs) so that every step's
+        # logits can be compared.  Only the oracle's time counts for its rate.
         f = forward.Forward(data)
         ses = f.session(DECODE_PROMPT + DECODE_STEPS)
+        err = ErrStats()
+        sess.reset()
         t1 = time.perf_counter()
         last = ses.feed(prompt)
         t_prompt = time.perf_counter() - t1
-        agree, steps, t2 = 0, 0, time.perf_counter()
+        err.add(sess.forward(prompt).cpu().numpy(), last)
+        agree, steps, t_dec = 0, 0, 0.0
         for t in picks:
             agree += int(int(np.argmax(last)) == int(t))
+            t2 = time.perf_counter()
             last = ses.step(int(t))
+            t_dec += time.perf_counter() - t2
+            err.add(sess.forward([int(t)]).cpu().numpy(), last)
             steps += 1
-            if time.perf_counter() - t2 >= cpu_seconds:
+            if t_dec >= cpu_seconds:
                 break
-        t_dec = time.perf_counter() - t2
         out["cpu_baseline"] = {"value": round(steps / t_dec, 2), "unit": "tok/s", "cores": o.default_threads(),
-                               "kind": "port",
+                               "cpu": host_cpu(), "kind": "port",
                                "sample": f"the oracle's step_native: the 118-token prompt ({t_prompt:.1f} s), then "
                                          f"{steps} of the 64 decode steps fed the device's picks ({t_dec:.1f} s)"}
-        out["parity"] = {"greedy_picks_checked": steps, "oracle_argmax_agrees": agree}
+        out["parity"] = {"greedy_picks_checked": steps, "oracle_argmax_agrees": agree, **err.json()}
         out["gpu_over_cpu"] = round(out["decode_tok_s"] / out["cpu_baseline"]["value"], 1)
     return out
 
@@ -350,7 +400,7 @@ def needle3_prefill(nh, torch, cpu_seconds: float, with_cpu: bool):
 
     from needle_hip import archive
 
-    data = archive.random_needle3(nh, seed=0)
+    data = archive.random_needle3(nh, archive.Needle3(vocab=NEEDLE3_VOCAB), seed=0)
     model = nh.Model.from_archive(data)
     rng = np.random.default_rng(1)
     seqs = [rng.integers(0, model.out_rows, PREFILL_LEN).astype(np.uint32) for _ in range(PREFILL_SEQS)]
@@ -382,8 +432,9 @@ def needle3_prefill(nh, torch, cpu_seconds: float, with_cpu: bool):
         from oracle import forward
 
         f = forward.Forward(data)
+        err = ErrStats()
         tokens, agree, whole, t0 = 0, 0, 0, time.perf_counter()
-        for q, pick in zip(seqs, picks):
+        for q, pick, got in zip(seqs, picks, last):
             ses = f.session(PREFILL_LEN)
             lg = None
             for i in range(0, PREFILL_LEN, 32):
@@ -394,14 +445,15 @@ def needle3_prefill(nh, torch, cpu_seconds: float, with_cpu: bool):
             if len(ses) == PREFILL_LEN:
                 whole += 1
                 agree += int(int(np.argmax(lg)) == pick)
+                err.add(got.cpu().numpy(), lg)
             if time.perf_counter() - t0 >= cpu_seconds:
                 break
         el = time.perf_counter() - t0
         out["cpu_baseline"] = {"value": round(tokens / el, 1), "unit": "tok/s", "cores": o.default_threads(),
-                               "kind": "port",
+                               "cpu": host_cpu(), "kind": "port",
                                "sample": f"the oracle's chunk_job over {tokens} tokens of the same sequences "
                                          f"({el:.1f} s)"}
-        out["parity"] = {"sequences_checked": whole, "oracle_argmax_agrees": agree}
+        out["parity"] = {"sequences_checked": whole, "oracle_argmax_agrees": agree, **err.json()}
         out["gpu_over_cpu"] = round(out["prefill_tok_s"] / out["cpu_baseline"]["value"], 1)
     return out
 
@@ -451,7 +503,8 @@ def cpu_baseline(gpu, seconds: float):
         if el >= seconds or calls >= 2000:
             break
     per = el / calls
-    return {"value": round(gpu["bytes"] / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": round(gpu["bytes"] / per / 1e9, 3), "unit": "GB/s", "cores": threads, "cpu": host_cpu(),
+            "kind": "port",
             "sample": f"{calls} full K=2048 N=8192 decode GEMVs over {el:.1f} s (one weight copy, host-resident)",
             "ms_per_call": round(per * 1e3, 3)}
 
@@ -459,8 +512,8 @@ def cpu_baseline(gpu, seconds: float):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=12800)
-    ap.add_argument("--warmup", type=int, default=640)
+    ap.add_argument("--steps", type=int, default=200, help="timed sweeps of the copies (graph replays)")
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--copies", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -505,7 +558,7 @@ def main():
         return
     gpu = gpu_gemv(args, nh, torch)
     progress(f"decode GEMV: {gpu['ms_launch'] * 1e3:.3f} us per launch")
-    steps = gpu["launches"]
+    steps = args.steps
     line = {
         "metric": "W4A8 GEMV HBM GB/s (K=2048, N=8192, decode combine)",
         "value": round(gpu["gbs"], 2),
@@ -513,7 +566,7 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": args.warmup,
-        "ms_per_step": round(gpu["ms_launch"], 6),
+        "ms_per_step": round(gpu["ms_sweep"], 6),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -521,7 +574,9 @@ def main():
         "data": "synthetic seeded: W=0.02*N(0,1) (threefry, seed 0) through CQ-W4 group 128; x=N(0,1)",
         "config": {"workload": "single W4A8 decode GEMV, K=2048 N=8192 M=1, rotating "
                                f"{args.copies} HBM-resident weight copies", "K": K, "N": N, "M": 1,
-                   "copies": args.copies, "bytes_per_launch": gpu["bytes"]},
+                   "copies": args.copies, "bytes_per_launch": gpu["bytes"],
+                   "step": f"one sweep of {args.copies} dependent launches, one per weight copy",
+                   "us_per_launch": round(gpu["ms_launch"] * 1e3, 4), "launches_timed": gpu["launches"]},
         "roofline": {"bound": "hbm", "achieved": round(gpu["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gpu["gbs"] / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic("gemv_decode_k2048_n8192_pmc.md")},
