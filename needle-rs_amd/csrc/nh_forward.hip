@@ -282,11 +282,12 @@ hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, in
 
 // -------------------------------------------------------------- the layer
 // One workgroup of 1024 threads per token row; thread t owns element t of
-// every d- and hada_n-long vector (d <= 1024 = hada_n) and elements
-// t + 1024 k of the 4 d residual lanes.  Every global read is issued at the
-// start: the Kronecker factors (widened to f32) and the cond_v / cond_u
-// tables land in LDS, the elementwise weights and this wavefront's Phi8
-// rows in registers.  The short serial chains (dot16 over d, the gates) run
+// every d- and hada_n-long vector (d <= 1024 = hada_n), and element t of each
+// of the 4 residual lanes, in registers.  Every global read is issued at the
+// start: the Kronecker factors and cond_v land in LDS, the elementwise
+// weights, the thread's cond_u column and its wavefront's Phi8 rows in
+// registers.  The LDS footprint stays under half a CU's, so two rows of a
+// batched feed run on a CU side by side.  The short serial chains (dot16 over d, the gates) run
 // in every wavefront that needs their result, so no barrier is spent on
 // handing it out.
 namespace {
@@ -306,19 +307,23 @@ constexpr int TP_H = FWD_MAX_D / 4 + 4;
 constexpr int TP_C = FWD_MAX_D / 4 + 8;
 
 struct LayerShared {
-    float xs[MHC_LANES * FWD_MAX_D];
     float x2[FWD_MAX_D];
     float h[FWD_MAX_D];
-    alignas(16) float A[HADA_N];
-    alignas(16) float B[HADA_NB * BT_STRIDE];
+    // The MLP's buffers are dead once its last pass is read; the mHC write
+    // then fills the transposed lanes over them.
+    union {
+        struct {
+            alignas(16) float A[HADA_N];
+            alignas(16) float B[HADA_NB * BT_STRIDE];
+            alignas(16) uint32_t kp[6][HADA_NB / 2 * KP_PITCH];  // Kronecker factors as f16 pairs, pair-major
+        };
+        alignas(16) float tX[16 * TP_X];
+    };
     alignas(16) float C[HADA_N];
-    alignas(16) uint32_t kp[6][HADA_NB / 2 * KP_PITCH];  // Kronecker factors as f16 pairs, pair-major
     alignas(16) int8_t nx8[MHC_LANES * FWD_MAX_D];
     alignas(16) uint16_t cvT[4 * COND_RANK * TP_C];
-    alignas(16) uint16_t cond_u[COND_RANK * HADA_N];
     alignas(16) float tA[16 * TP_D];
     alignas(16) float tB[16 * TP_D];
-    alignas(16) float tX[16 * TP_X];
     alignas(16) float hT[4 * TP_H];
     float red[LT / 64];
     float p[64];
@@ -544,8 +549,8 @@ __device__ __forceinline__ float block_rinv_all(const float* xT, int pitch, int 
 // The previous layer's inputs and weights a thread needs, read up front.
 // The LDS tables go out as one list of 16-byte chunks, up to STAGE_PER per
 // thread: [0, 768) the six Kronecker factors (128 each), then cond_v
-// (d chunks), then cond_u (1024).
-constexpr int STAGE_PER = 3;
+// (d chunks); cond_u follows them, one 16-byte column per thread.
+constexpr int STAGE_PER = 2;
 
 // f16 weights stay raw bits (one per register) until their use:
 // converting or packing them on arrival would make the wave wait for each
@@ -555,18 +560,21 @@ struct OutRegs {
     uint32_t pn, ph, d1, d2, b2, d3, d4;
     int p1, p2;
     uint4 st[STAGE_PER];
+    uint4 cu;  // cond_u [k][t], k < 8, as f16 pairs
 };
 
 __device__ __forceinline__ OutRegs load_out(const Dims& D, const Globals& G, const SessDev& S, const LayerDev& P,
                                             LayerShared& sh) {
     const int t = threadIdx.x, d = D.d;
     OutRegs q{};
-    const int kron_n = 6 * HADA_N / 8, cv_n = d * COND_RANK / 8, cu_n = COND_RANK * HADA_N / 8;
+    const int kron_n = 6 * HADA_N / 8, cv_n = d * COND_RANK / 8;
+    static_assert(STAGE_PER * LT >= 6 * HADA_N / 8 + FWD_MAX_D * COND_RANK / 8, "the stage loads cover the tables");
 #pragma unroll
     for (int r = 0; r < STAGE_PER; ++r) {
-        const int e = min(t + r * LT, kron_n + cv_n + cu_n - 1);
+        const int e = min(t + r * LT, kron_n + cv_n - 1);
         q.st[r] = reinterpret_cast<const uint4*>(P.stage)[e];
     }
+    q.cu = reinterpret_cast<const uint4*>(P.stage)[kron_n + cv_n + t];
     // (unconditional loads: threads past d read element d - 1 and ignore it)
     const int td = min(t, d - 1);
     q.o = S.o[td];
@@ -594,7 +602,7 @@ __device__ __forceinline__ float h2f_late(uint32_t b) {
 
 __device__ __forceinline__ void store_out(const Dims& D, const OutRegs& q, LayerShared& sh) {
     const int t = threadIdx.x;
-    const int kron_n = 6 * HADA_N / 8, cv_n = D.d * COND_RANK / 8, cu_n = COND_RANK * HADA_N / 8;
+    const int kron_n = 6 * HADA_N / 8, cv_n = D.d * COND_RANK / 8;
 #pragma unroll
     for (int r = 0; r < STAGE_PER; ++r) {
         const int e = t + r * LT;
@@ -616,8 +624,6 @@ __device__ __forceinline__ void store_out(const Dims& D, const OutRegs& q, Layer
                 dst[(2 * k) * TP_C] = (uint16_t)(w[k] & 0xffffu);
                 dst[(2 * k + 1) * TP_C] = (uint16_t)(w[k] >> 16);
             }
-        } else if (e < kron_n + cv_n + cu_n) {
-            reinterpret_cast<uint4*>(sh.cond_u)[e - kron_n - cv_n] = q.st[r];
         }
     }
     if (t < D.d) put_t(sh.tA, TP_D, t, q.o);
@@ -674,9 +680,11 @@ __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int l
     if (lane < 8) wk[lane] = e * inv;
 }
 
-// The Hadamard MLP and mHC write of layer P (step.rs:600-705); returns this
-// thread's max |new lane value| (for the next layer's mHC read).
-__device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, const OutRegs& q, LayerShared& sh) {
+// The Hadamard MLP and mHC write of layer P (step.rs:600-705): xl holds the
+// thread's element of the 4 lanes (t < d) and gets the new ones; returns
+// this thread's max |new lane value| (for the next layer's mHC read).
+__device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, const OutRegs& q, LayerShared& sh,
+                           float (&xl)[MHC_LANES]) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
     // mix8 runs on waves 4..7 (threads 256..511), beside cond_weights on wave 0
     const bool mixer = t >= MIX_T && t < 2 * MIX_T;
@@ -716,8 +724,10 @@ __device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, c
     __syncthreads();
     {
         float cond = 1.0f;
+        const uint32_t cw[4] = {q.cu.x, q.cu.y, q.cu.z, q.cu.w};
 #pragma unroll
-        for (int k = 0; k < COND_RANK; ++k) cond = __builtin_fmaf(h2f(sh.cond_u[k * HADA_N + t]), sh.wk[k], cond);
+        for (int k = 0; k < COND_RANK; ++k)
+            cond = __builtin_fmaf(h2f((uint16_t)(cw[k >> 1] >> (16 * (k & 1)))), sh.wk[k], cond);
         float zs = __builtin_fmaf(sh.C[q.p1], cond * h2f_late(q.d2), h2f_late(q.b2));
         zs = zs / (nexp(-zs) + 1.0f);
         sh.A[t] = zs;
@@ -742,13 +752,13 @@ __device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, c
         const float y = (x2 + sh.C[t] * h2f_late(q.d4)) - q.u;
         float old[MHC_LANES];
 #pragma unroll
-        for (int b = 0; b < MHC_LANES; ++b) old[b] = sh.xs[b * d + t];
+        for (int b = 0; b < MHC_LANES; ++b) old[b] = xl[b];
 #pragma unroll
         for (int a = 0; a < MHC_LANES; ++a) {
             float v = y * hpost[a];
 #pragma unroll
             for (int b = 0; b < MHC_LANES; ++b) v = __builtin_fmaf(old[b], hres[a * MHC_LANES + b], v);
-            sh.xs[a * d + t] = v;
+            xl[a] = v;
             put_t(sh.tX, TP_X, a * d + t, v);
             m = fmaxf(m, fabsf(v));
         }
@@ -768,8 +778,12 @@ struct InRegs {
     uint4 r0[PHI_CHUNKS], r1[PHI_CHUNKS];
 };
 
+__device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InRegs& q);
+
+// PHI: the Phi8 rows too (else layer_in reads them itself).
+template <bool PHI>
 __device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const LayerDev& N) {
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d, nc = MHC_LANES * d;
+    const int t = threadIdx.x, d = D.d;
     // Unconditional loads at clamped addresses (threads, rows and chunks
     // past the ranges read an in-range element and ignore it; a layer
     // without an engram site reads the projection row instead, which
@@ -782,6 +796,12 @@ __device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const
     const float* ep = site ? S.evals + (size_t)N.site * BATCH_ROWS * d : S.proj + d;
     q.kr = kp[td];
     q.ev = ep[td];
+    if constexpr (PHI) load_phi(D, N, q);
+    return q;
+}
+
+__device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InRegs& q) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nc = MHC_LANES * D.d;
     // Phi8 rows: wavefront w >= 1 holds row w - 1, and row w + PHI_B - 1
     // while that is below 24; wavefront 0, which runs the first chain of the
     // MLP right after these loads are issued, holds none, so it never waits
@@ -807,7 +827,6 @@ __device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const
         q.ps0 = N.phi_s[w0];
         q.ps1 = N.phi_s[w1];
     }
-    return q;
 }
 
 __device__ __forceinline__ int dot_row(const uint4* r, const int8_t* x8, int per, int lane) {
@@ -828,13 +847,17 @@ __device__ __forceinline__ int dot_row(const uint4* r, const int8_t* x8, int per
 }
 
 // The mHC read, engram gate, input norm and A8 of layer N
-// (step.rs:400-479).  `m` is this thread's max |xs| (its share of the
-// lanes); the lanes are in LDS behind a barrier.  The post and residual
+// (step.rs:400-479).  xl holds the thread's element of the 4 lanes (t < d);
+// their transposed copy and the wavefronts' maxima of |xs| are in LDS
+// behind a barrier.  The post and residual
 // gates of the layer (hpost, the Sinkhorn hres) are computed beside its
 // units, off this kernel's path.
-__device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, const InRegs& q, int in_bits,
-                         LayerShared& sh) {
+template <bool LATE_PHI>
+__device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, InRegs q, int in_bits,
+                         LayerShared& sh, const float (&xl)[MHC_LANES]) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d, nc = MHC_LANES * d;
+    // (the Phi8 rows read now land while wavefront 0 runs the norm chain)
+    if constexpr (LATE_PHI) load_phi(D, N, q);
     // every wavefront: r = rinv(dot16(xs)), the amax over the wavefronts'
     // maxima of |xs| (rounding is monotonic, so max_i |xs_i r| =
     // max_i |xs_i| r for r > 0), then the int8 lanes
@@ -846,7 +869,10 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, con
         m = m * r;
         const float sx = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
         const float inv = 1.0f / sx;
-        for (int i = t; i < nc; i += LT) sh.nx8[i] = quant_one(sh.xs[i] * r, inv);
+        if (t < d) {
+#pragma unroll
+            for (int b = 0; b < MHC_LANES; ++b) sh.nx8[b * d + t] = quant_one(xl[b] * r, inv);
+        }
         if (t == 0) sh.r_sx = sx;
     }
     __syncthreads();
@@ -878,9 +904,9 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, con
     }
     float u = 0.0f, x1 = 0.0f;
     if (t < d) {
-        u = sh.xs[t] * hp[0];
+        u = xl[0] * hp[0];
 #pragma unroll
-        for (int b = 1; b < MHC_LANES; ++b) u = __builtin_fmaf(sh.xs[b * d + t], hp[b], u);
+        for (int b = 1; b < MHC_LANES; ++b) u = __builtin_fmaf(xl[b], hp[b], u);
         x1 = u;
         put_t(sh.tA, TP_D, t, x1);
         if (N.site >= 0) put_t(sh.tB, TP_D, t, q.kr);
@@ -933,11 +959,12 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, con
 
 // The head's input (step.rs:706-728, chunk.rs:331-347): lane mean, zcn with
 // the f32 final norm into `hid`, A8 into activation row `arow`.
-__device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_bits, int arow, LayerShared& sh) {
+__device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_bits, int arow, LayerShared& sh,
+                        const float (&xl)[MHC_LANES]) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
     float mean = 0.0f;
     if (t < d) {
-        mean = (((sh.xs[t] + sh.xs[d + t]) + sh.xs[2 * d + t]) + sh.xs[3 * d + t]) * 0.25f;
+        mean = (((xl[0] + xl[1]) + xl[2]) + xl[3]) * 0.25f;
         put_t(sh.tA, TP_D, t, mean);
     }
     __syncthreads();
@@ -961,8 +988,11 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
 
 }  // namespace
 
-template <bool PREV, bool NEXT>
-__global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int row0,
+// BATCH (a feed of several rows): two rows per CU (at most 64 VGPRs), so
+// the next layer's Phi8 rows are read at the start of the mHC read instead
+// of beside the MLP.
+template <bool PREV, bool NEXT, bool BATCH>
+__global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 1))) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int row0,
                                               int in_bits, int head_bits) {
     constexpr bool has_prev = PREV, has_next = NEXT;
     __shared__ LayerShared sh;
@@ -980,10 +1010,12 @@ __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, Laye
     R.evals += (size_t)row * d;
     R.xq_in += (size_t)row * Gd * GROUP;
     R.sx_in += (size_t)row * Gd;
-    // every global read first, then the LDS stores
-    float xv[MHC_LANES];
+    // every global read first, then the LDS stores; thread t < d holds
+    // element t of each lane
+    const int td = min(t, d - 1);
+    float xl[MHC_LANES];
 #pragma unroll
-    for (int k = 0; k < MHC_LANES; ++k) xv[k] = R.xs[min(t + k * LT, nc - 1)];
+    for (int k = 0; k < MHC_LANES; ++k) xl[k] = R.xs[k * d + td];
     OutRegs qo;
     if constexpr (has_prev) qo = load_out(D, G, R, P, sh);
     InRegs qi;
@@ -992,21 +1024,25 @@ __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, Laye
     // go now.  With one they go after the first barrier: the Phi8 rows are
     // half the kernel's bytes and are not needed before the mHC read, so
     // they stay out of the way of the tables the MLP waits for.
-    if constexpr (has_next && !has_prev) qi = load_in(D, R, N);
+    if constexpr (has_next && !has_prev) qi = load_in<!BATCH>(D, R, N);
     if constexpr (!has_next) fnorm = G.final_norm[min(t, d - 1)];
     float m = 0.0f;
     if (t == 0) sh.mix_count = 0;
+    // With a previous layer the lanes' transposed copy is written by its
+    // mHC write (over the MLP's buffers, which store_out fills now).
+    if constexpr (!has_prev) {
+        if (t < d) {
 #pragma unroll
-    for (int k = 0; k < MHC_LANES; ++k)
-        if (t + k * LT < nc) {
-            sh.xs[t + k * LT] = xv[k];
-            put_t(sh.tX, TP_X, t + k * LT, xv[k]);
-            m = fmaxf(m, fabsf(xv[k]));
+            for (int k = 0; k < MHC_LANES; ++k) {
+                put_t(sh.tX, TP_X, k * d + t, xl[k]);
+                m = fmaxf(m, fabsf(xl[k]));
+            }
         }
+    }
     if constexpr (has_prev) store_out(D, qo, sh);
     __syncthreads();
-    if constexpr (has_next && has_prev) qi = load_in(D, R, N);
-    if constexpr (has_prev) m = layer_out(D, S, P, qo, sh);
+    if constexpr (has_next && has_prev) qi = load_in<!BATCH>(D, R, N);
+    if constexpr (has_prev) m = layer_out(D, S, P, qo, sh, xl);
     // the wavefronts' maxima of |xs| for the mHC read
     m = wave_max(m);
     if (lane == 0) sh.red[wave] = m;
@@ -1015,31 +1051,41 @@ __global__ __launch_bounds__(LT) void k_layer(Dims D, Globals G, SessDev S, Laye
     // stores issued earlier would sit in the memory counter ahead of loads
     // that are waited for)
     if constexpr (has_next)
-        layer_in(D, R, N, qi, in_bits, sh);
+        layer_in<BATCH>(D, R, N, qi, in_bits, sh, xl);
     else
-        head_in(D, S, fnorm, head_bits, blockIdx.x, sh);  // row i - row0
+        head_in(D, S, fnorm, head_bits, blockIdx.x, sh, xl);  // row i - row0
     if constexpr (has_prev) {
+        if (t < d) {
 #pragma unroll
-        for (int k = 0; k < MHC_LANES; ++k)
-            if (t + k * LT < nc) R.xs[t + k * LT] = sh.xs[t + k * LT];
+            for (int k = 0; k < MHC_LANES; ++k) R.xs[k * d + t] = xl[k];
+        }
     }
+}
+
+template <bool BATCH>
+static void launch_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev,
+                         const LayerDev* next, int row0, int rows, int in_bits, int head_bits, hipStream_t s) {
+    const LayerDev none{};
+    if (prev && next)
+        hipLaunchKernelGGL((k_layer<true, true, BATCH>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, *next, row0,
+                           in_bits, head_bits);
+    else if (next)
+        hipLaunchKernelGGL((k_layer<false, true, BATCH>), dim3(rows), dim3(LT), 0, s, D, G, S, none, *next, row0,
+                           in_bits, head_bits);
+    else if (prev)
+        hipLaunchKernelGGL((k_layer<true, false, BATCH>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, none, row0,
+                           in_bits, head_bits);
+    else
+        hipLaunchKernelGGL((k_layer<false, false, BATCH>), dim3(rows), dim3(LT), 0, s, D, G, S, none, none, row0,
+                           in_bits, head_bits);
 }
 
 hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
                      int row0, int rows, int in_bits, int head_bits, hipStream_t s) {
-    const LayerDev none{};
-    if (prev && next)
-        hipLaunchKernelGGL((k_layer<true, true>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, *next, row0, in_bits,
-                           head_bits);
-    else if (next)
-        hipLaunchKernelGGL((k_layer<false, true>), dim3(rows), dim3(LT), 0, s, D, G, S, none, *next, row0, in_bits,
-                           head_bits);
-    else if (prev)
-        hipLaunchKernelGGL((k_layer<true, false>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, none, row0, in_bits,
-                           head_bits);
+    if (rows > 1)
+        launch_layer<true>(D, G, S, prev, next, row0, rows, in_bits, head_bits, s);
     else
-        hipLaunchKernelGGL((k_layer<false, false>), dim3(rows), dim3(LT), 0, s, D, G, S, none, none, row0, in_bits,
-                           head_bits);
+        launch_layer<false>(D, G, S, prev, next, row0, rows, in_bits, head_bits, s);
     return hipGetLastError();
 }
 

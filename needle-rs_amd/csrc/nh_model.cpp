@@ -298,8 +298,9 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
         for (size_t i = 0; i < v.size(); ++i) b[i] = f32_to_f16(v[i]);
         return A.put(b.data(), b.size() * 2);
     };
-    // The tables the layer kernel stages into LDS, as one block per layer:
-    // the six Kronecker factors, cond_v [d][8], cond_u [8][hada_n] (f16).
+    // The tables of the layer kernel, as one block per layer: the six
+    // Kronecker factors and cond_v [d][8] (staged into LDS), then cond_u
+    // by column, [hada_n][8] (f16; thread t reads its column's 16 bytes).
     std::vector<size_t> stage(D.layers);
     for (int l = 0; l < D.layers; ++l) {
         for (int k = 0; k < nh::SMALL_KINDS; ++k) off[l].t[k] = put16(sm.layer[l][k]);
@@ -311,7 +312,8 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
         const auto& cv = sm.layer[l][nh::S_COND_V];
         blk.insert(blk.end(), cv.begin(), cv.begin() + (size_t)D.d * nh::COND_RANK);
         const auto& cu = sm.layer[l][nh::S_COND_U];
-        blk.insert(blk.end(), cu.begin(), cu.begin() + (size_t)nh::COND_RANK * nh::HADA_N);
+        for (int t = 0; t < nh::HADA_N; ++t)
+            for (int k = 0; k < nh::COND_RANK; ++k) blk.push_back(cu[(size_t)k * nh::HADA_N + t]);
         stage[l] = put16(blk);
         off[l].phi_q = A.reserve((size_t)nh::MHC_COLS * nc);
         off[l].phi_s = A.reserve(nh::MHC_COLS * 4);
