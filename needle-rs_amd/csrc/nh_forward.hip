@@ -109,7 +109,7 @@ __device__ __forceinline__ float wave_quant_scale(float v) {
 // key_chunks (infer.rs:2093-2101): the chunk count and length of n keys,
 // at least k = 2 NATIVE_TEAM / nkv chunks past 64 k keys, or 1 for a
 // feed's rows (nested, infer.rs:1888).
-__device__ __forceinline__ void key_chunks(int n, int nkv, bool nested, int& count, int& size) {
+__host__ __device__ inline void key_chunks(int n, int nkv, bool nested, int& count, int& size) {
     int k = 2 * NATIVE_TEAM / nkv;
     if (k < 1 || nested) k = 1;
     int c = (n + 255) / 256;
@@ -127,7 +127,7 @@ __device__ __forceinline__ int slot_of(const Dims& D, int p) {
     return (D.ring > 0 && p >= D.sink) ? (p - D.sink) % D.ring + D.sink : p;
 }
 
-__device__ __forceinline__ int window_lo(int window, int p0) {
+__host__ __device__ inline int window_lo(int window, int p0) {
     return (window > 0 && p0 + 1 > window) ? p0 + 1 - window : 0;
 }
 
@@ -1609,16 +1609,24 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 // attend_head_ref for all the query heads that share a kv head: one
 // workgroup per (row, kv head, key chunk) stages the chunk's key rows,
-// scales and value columns once (as k_attend does), then wavefront h
-// computes query head h of the group: the int8 query, the scores (key i of
-// the chunk on lane i % 64), the chunk max, chunk_exp with the reference's
-// sum order (lanes 0-7 run the eight lane-class chains), the weights and
-// 21-bit digits, and the exact integer P.V with lane = value dimension.
-constexpr int AG_WAVES = 8;  // query heads per kv head this kernel takes
+// scales and value columns once (as k_attend does).  The two integer dot
+// products run on the matrix cores, since an int32 sum is the same in any
+// order: the scores of every head against 16 keys are one
+// v_mfma_i32_16x16x64_i8 (A = the heads' int8 queries, B = the key rows),
+// and P.V is a product of the three 7-bit digit planes of every head (A,
+// rows plane * 8 + head) with the value columns (B), 64 keys per step.
+// Between them wavefront h runs query head h's float steps as the reference
+// orders them: the chunk max, chunk_exp with its sum order (lanes 0-7 run
+// the eight lane-class chains), the weights and the 21-bit digits.
+constexpr int AG_WAVES = 8;   // query heads per kv head this kernel takes
 constexpr int AG_T = AG_WAVES * 64;
+constexpr int AG_COLS = 320;  // value / digit columns: 3 alignment + 256 keys, in whole 64-column steps
+constexpr int AG_KPL = ATT_CHUNK_MAX / 64;  // keys per lane in the head steps
+constexpr int AG_TP = ATT_CHUNK_MAX / 8 + 4;  // a lane class's exps (16-byte rows, room for the trailing 4-block)
 
 __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerDev L, int layer, int p0, int rows) {
-    const int row = blockIdx.x / D.nkv, kvh = blockIdx.x % D.nkv, ci = blockIdx.y, t = threadIdx.x;
+    // the longest rows first
+    const int row = rows - 1 - (int)blockIdx.x / D.nkv, kvh = blockIdx.x % D.nkv, ci = blockIdx.y, t = threadIdx.x;
     const int wave = t >> 6, lane = t & 63, pos = p0 + row;
     const int nkv = D.nkv, qk = D.qk, vd = D.vd, hpg = D.nh / nkv;
     const int lo = window_lo(L.window, pos), n = pos + 1 - lo;
@@ -1628,11 +1636,13 @@ __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerD
     const int c0 = ci * chunk, len = min(chunk, n - c0), blocked = len / 4 * 4, slot0 = lo + c0;
     const int sh = slot0 & 3, base = slot0 - sh, cols = sh + len;
     __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][ATT_KPITCH];
-    __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][ATT_PITCH];
+    __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][AG_COLS];
     __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
     __shared__ alignas(16) int8_t q8[AG_WAVES][MAX_HEAD_DIM];
-    __shared__ float sc[AG_WAVES][ATT_CHUNK_MAX];
-    __shared__ alignas(16) int8_t dig[AG_WAVES][3][ATT_PITCH];
+    __shared__ float qsc[AG_WAVES];
+    __shared__ alignas(16) float sc[AG_WAVES][8 * AG_TP];
+    __shared__ alignas(16) int8_t dig[AG_WAVES][3][AG_COLS];
+    __shared__ int32_t pv[3][AG_WAVES][MAX_HEAD_DIM];
     const size_t lc = (size_t)layer * D.cap;
     const int hw = min(wave, hpg - 1), hh = kvh * hpg + hw;
     // every load first (unconditional, at clamped in-range addresses)
@@ -1658,10 +1668,11 @@ __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerD
         const int e = t + r * AG_T, dm = min(e / ATT_VDW, vd - 1), k = min(e % ATT_VDW, vdw - 1);
         vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
     }
-    // the query of this wavefront's head
+    // the int8 query of this wavefront's head, zero past qk (the key rows'
+    // bytes there are not staged)
     const float s = wave_quant_scale(lane < qk ? qv : 0.0f);
-    if (lane < qk) q8[wave][lane] = quant_one(qv, 1.0f / s);
-    const float qs = s * bits_f32(0x3e13cd3au);
+    q8[wave][lane] = lane < qk ? quant_one(qv, 1.0f / s) : (int8_t)0;
+    if (lane == 0) qsc[wave] = s * bits_f32(0x3e13cd3au);
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
         const int e = t + r * AG_T, i = e >> 2, c = e & 3;
@@ -1685,111 +1696,149 @@ __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerD
         }
     }
     __syncthreads();
-    if (wave >= hpg) return;
-    float* scw = sc[wave];
-    float mx = -__builtin_inff();
-    {
-        uint4 qw[MAX_HEAD_DIM / 16];
-#pragma unroll
-        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) qw[c] = reinterpret_cast<const uint4*>(q8[wave])[c];
-        for (int i = lane; i < len; i += 64) {
-            int dot = 0;
-#pragma unroll
-            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
-                if (c < rq) {
-                    const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
-                    dot = __builtin_amdgcn_sdot4((int)kv.x, (int)qw[c].x, dot, false);
-                    dot = __builtin_amdgcn_sdot4((int)kv.y, (int)qw[c].y, dot, false);
-                    dot = __builtin_amdgcn_sdot4((int)kv.z, (int)qw[c].z, dot, false);
-                    dot = __builtin_amdgcn_sdot4((int)kv.w, (int)qw[c].w, dot, false);
-                }
+    const int mr = lane & 15, mq = lane >> 4;  // MFMA lane: row / column mr, 16-byte k-block mq
+    // scores: key tile kt (16 keys) per MFMA, tiles split over the wavefronts;
+    // lane (mq, mr) gets heads 4 mq + v against key 16 kt + mr
+    for (int kt = wave; kt * 16 < len; kt += AG_WAVES) {
+        const v4i a = mr < AG_WAVES ? *reinterpret_cast<const v4i*>(&q8[mr][16 * mq]) : v4i{0, 0, 0, 0};
+        const v4i b = *reinterpret_cast<const v4i*>(&ks8[kt * 16 + mr][16 * mq]);
+        const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+        const int i = kt * 16 + mr;
+        if (i < len) {
             const float ksc = kss[i];
-            const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
-            scw[i] = sv;
-            mx = fmaxf(mx, sv);
-        }
-    }
-    mx = wave_max(mx);
-    for (int i = lane; i < len; i += 64) scw[i] = i < blocked ? nexp(scw[i] - mx) : lexpf(scw[i] - mx);
-    wave_lds_sync();
-    float sum;
-    {
-        // chunk_exp's order (infer.rs:2222-2279): a[k] over the 8-blocks'
-        // first halves plus a trailing 4-block, b[k] over their second
-        // halves (lane 4 hi + k), then t = a + b, (t0 + t1) + (t2 + t3)
-        float acc = 0.0f;
-        const int nb8 = len / 8;
-        if (lane < 8) {
-            const int k = lane & 3, hi = lane >> 2;
-            const float* col = &scw[hi * 4 + k];
-            int b = 0;
-            for (; b + 8 <= nb8; b += 8) {
-                float v[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = col[(b + j) * 8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc += v[j];
+            for (int v = 0; v < 4; ++v) {
+                const int h = 4 * mq + v;
+                if (h < hpg) {
+                    const float qs = qsc[h];
+                    sc[h][i] = i < blocked ? (ksc * (float)d[v]) * qs : (ksc * qs) * (float)d[v];
+                }
             }
-            for (; b < nb8; ++b) acc += col[b * 8];
-            if (hi == 0 && len - nb8 * 8 >= 4) acc += scw[nb8 * 8 + k];
         }
-        const float tk = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
-                                                                                       0x104, 0xF, 0xF, false));
-        const int ti = __builtin_bit_cast(int, tk);
-        const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x00, 0xF, 0xF, false));
-        const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x55, 0xF, 0xF, false));
-        const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xAA, 0xF, 0xF, false));
-        const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xFF, 0xF, 0xF, false));
-        sum = (t0 + t1) + (t2 + t3);
-        int i = blocked;
-        if (len - i >= 2) {
-            sum = (scw[i] + sum) + scw[i + 1];
-            i += 2;
+    }
+    __syncthreads();
+    float mx = -__builtin_inff(), sum = 0.0f, cw = 0.0f;
+    if (wave < hpg) {
+        // key i = lane + 64 j of the head in register e[j]: score, exp, weight
+        float* scw = sc[wave];
+        float e[AG_KPL];
+#pragma unroll
+        for (int j = 0; j < AG_KPL; ++j) {
+            const int i = lane + 64 * j;
+            e[j] = i < len ? scw[i] : -__builtin_inff();
+            mx = fmaxf(mx, e[j]);
         }
-        if (len - i == 1) sum += scw[i];
-    }
-    float wmax = 0.0f;
-    for (int i = lane; i < len; i += 64) {
-        const float w = scw[i] * vss[i];
-        scw[i] = w;
-        wmax = fmaxf(wmax, w);
-    }
-    wmax = wave_max(wmax);
-    const float qwt = bits_f32(0x49fffff8u) / wmax;
-    int8_t(*dg)[ATT_PITCH] = dig[wave];
-    for (int i = lane; i < len; i += 64) {
-        const int32_t wq = (int32_t)roundf(scw[i] * qwt);
-        dg[0][sh + i] = (int8_t)(wq >> 14);
-        dg[1][sh + i] = (int8_t)((wq >> 7) & 127);
-        dg[2][sh + i] = (int8_t)(wq & 127);
-    }
-    // zero digits in the first dword before the keys and the last one past them
-    if (lane < 4) {
-        const int j0 = lane, j1 = cols + lane;
-        if (j0 < sh) dg[0][j0] = dg[1][j0] = dg[2][j0] = 0;
-        if (j1 < (cols + 3) / 4 * 4) dg[0][j1] = dg[1][j1] = dg[2][j1] = 0;
-    }
-    wave_lds_sync();
-    const float cw = wmax * bits_f32(0x35000004u);
-    const size_t pi = ((size_t)row * D.nh + hh) * D.max_chunks + ci;
-    if (lane < vd) {
-        // exact integer P.V over the chunk, four keys per sdot4
-        const int* vrow = reinterpret_cast<const int*>(vs8[lane]);
-        const int* d0 = reinterpret_cast<const int*>(dg[0]);
-        const int* d1 = reinterpret_cast<const int*>(dg[1]);
-        const int* d2 = reinterpret_cast<const int*>(dg[2]);
-        int a = 0, b = 0, c = 0;
-        for (int k = 0; 4 * k < cols; ++k) {
-            const int v = vrow[k];
-            a = __builtin_amdgcn_sdot4(d0[k], v, a, false);
-            b = __builtin_amdgcn_sdot4(d1[k], v, b, false);
-            c = __builtin_amdgcn_sdot4(d2[k], v, c, false);
+        mx = wave_max(mx);
+#pragma unroll
+        for (int j = 0; j < AG_KPL; ++j) {
+            const int i = lane + 64 * j;
+            if (i < len) e[j] = i < blocked ? nexp(e[j] - mx) : lexpf(e[j] - mx);
         }
-        S.po[pi * vd + lane] = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
+        // the exps by lane class, key i at (i % 8) * AG_TP + i / 8 (over the
+        // scores, which this wavefront has read)
+#pragma unroll
+        for (int j = 0; j < AG_KPL; ++j) {
+            const int i = lane + 64 * j;
+            if (i < len) scw[(i & 7) * AG_TP + (i >> 3)] = e[j];
+        }
+        wave_lds_sync();
+        {
+            // chunk_exp's order (infer.rs:2222-2279): a[k] over the 8-blocks'
+            // first halves plus a trailing 4-block, b[k] over their second
+            // halves (lane 4 hi + k), then t = a + b, (t0 + t1) + (t2 + t3)
+            float acc = 0.0f;
+            const int nb8 = len / 8;
+            if (lane < 8) {
+                const float4* tr = reinterpret_cast<const float4*>(scw + lane * AG_TP);
+                float v[ATT_CHUNK_MAX / 8];
+#pragma unroll
+                for (int q = 0; q < ATT_CHUNK_MAX / 32; ++q) {
+                    const float4 x = tr[q];
+                    v[4 * q] = x.x;
+                    v[4 * q + 1] = x.y;
+                    v[4 * q + 2] = x.z;
+                    v[4 * q + 3] = x.w;
+                }
+#pragma unroll
+                for (int b = 0; b < ATT_CHUNK_MAX / 8; ++b) acc = b < nb8 ? acc + v[b] : acc;
+                if (lane < 4 && len - nb8 * 8 >= 4) acc += scw[lane * AG_TP + nb8];
+            }
+            const float tk = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                                 0, __builtin_bit_cast(int, acc), 0x104, 0xF, 0xF, false));
+            const int ti = __builtin_bit_cast(int, tk);
+            const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x00, 0xF, 0xF, false));
+            const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x55, 0xF, 0xF, false));
+            const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xAA, 0xF, 0xF, false));
+            const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xFF, 0xF, 0xF, false));
+            sum = (t0 + t1) + (t2 + t3);
+            int i = blocked;
+            if (len - i >= 2) {
+                sum = (scw[(i & 7) * AG_TP + (i >> 3)] + sum) + scw[((i + 1) & 7) * AG_TP + ((i + 1) >> 3)];
+                i += 2;
+            }
+            if (len - i == 1) sum += scw[(i & 7) * AG_TP + (i >> 3)];
+        }
+        float wmax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < AG_KPL; ++j) {
+            const int i = lane + 64 * j;
+            if (i < len) {
+                e[j] = e[j] * vss[i];
+                wmax = fmaxf(wmax, e[j]);
+            }
+        }
+        wmax = wave_max(wmax);
+        const float qwt = bits_f32(0x49fffff8u) / wmax;
+        int8_t(*dg)[AG_COLS] = dig[wave];
+#pragma unroll
+        for (int j = 0; j < AG_KPL; ++j) {
+            const int i = lane + 64 * j;
+            if (i < len) {
+                const int32_t wq = (int32_t)roundf(e[j] * qwt);
+                dg[0][sh + i] = (int8_t)(wq >> 14);
+                dg[1][sh + i] = (int8_t)((wq >> 7) & 127);
+                dg[2][sh + i] = (int8_t)(wq & 127);
+            }
+        }
+        // zero digits before the keys and from their end to the last step's
+        if (lane < sh) dg[0][lane] = dg[1][lane] = dg[2][lane] = 0;
+        const int j1 = cols + lane;
+        if (j1 < (cols + 63) / 64 * 64) dg[0][j1] = dg[1][j1] = dg[2][j1] = 0;
+        cw = wmax * bits_f32(0x35000004u);
     }
-    if (lane == 0) {
-        S.pm[pi] = mx;
-        S.psum[pi] = sum;
+    __syncthreads();
+    // P.V: row tile rt (rows plane * 8 + head) x value-dimension tile dt per
+    // job, 64 columns per step
+    {
+        const int ndt = (vd + 15) / 16, nsteps = (cols + 63) / 64;
+        for (int job = wave; job < 2 * ndt; job += AG_WAVES) {
+            const int rt = job / ndt, dt = job % ndt;
+            const int R = rt * 16 + mr, j = R >> 3, h = R & 7, dm = min(dt * 16 + mr, MAX_HEAD_DIM - 1);
+            v4i acc = {0, 0, 0, 0};
+            for (int st = 0; st < nsteps; ++st) {
+                const int c = st * 64 + 16 * mq;
+                const v4i a = j < 3 ? *reinterpret_cast<const v4i*>(&dig[h][j][c]) : v4i{0, 0, 0, 0};
+                const v4i b = *reinterpret_cast<const v4i*>(&vs8[dm][c]);
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int R2 = rt * 16 + 4 * mq + v, j2 = R2 >> 3;
+                if (j2 < 3) pv[j2][R2 & 7][dt * 16 + mr] = acc[v];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave < hpg) {
+        const size_t pi = ((size_t)row * D.nh + hh) * D.max_chunks + ci;
+        if (lane < vd) {
+            const int a = pv[0][wave][lane], b = pv[1][wave][lane], c = pv[2][wave][lane];
+            S.po[pi * vd + lane] = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
+        }
+        if (lane == 0) {
+            S.pm[pi] = mx;
+            S.psum[pi] = sum;
+        }
     }
 }
 
@@ -1798,8 +1847,17 @@ hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int la
     if (span)
         hipLaunchKernelGGL(k_attend<true>, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer, p0,
                            t, *span);
-    else if (D.nh / D.nkv <= AG_WAVES)
-        hipLaunchKernelGGL(k_attend_group, dim3(t * D.nkv, D.max_chunks), dim3(AG_T), 0, s, D, S, L, layer, p0, t);
+    else if (D.nh / D.nkv <= AG_WAVES) {
+        // the most chunks a row of the feed needs
+        int most = 1;
+        for (int i = 0; i < t; ++i) {
+            const int pos = p0 + i, n = pos + 1 - window_lo(L.window, pos);
+            int count, chunk;
+            key_chunks(n, D.nkv, t > 1, count, chunk);
+            most = count > most ? count : most;
+        }
+        hipLaunchKernelGGL(k_attend_group, dim3(t * D.nkv, most), dim3(AG_T), 0, s, D, S, L, layer, p0, t);
+    }
     else
         hipLaunchKernelGGL(k_attend<false>, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer,
                            p0, t, KeySpan{});

@@ -240,3 +240,14 @@ def test_prefill_full_needle3(nh):
     say("the full Needle-3 geometry: a 37-token prompt (32 + 5) then 2 steps")
     g = cact.Geometry()
     run_feed(nh, archive(g, seed=45), o.random_tokens(37, g.vocab, seed=13), 48, "needle3 prompt", then_steps=2)
+
+
+@pytest.mark.parametrize("heads,kv,qk,vd", [(8, 2, 32, 48), (8, 1, 48, 32), (6, 3, 16, 20)])
+def test_head_geometries(nh, heads, kv, qk, vd):
+    say(f"{heads} heads over {kv} kv heads, qk {qk}, vd {vd}: a 300-token prompt (rows past 256 keys attend in 2 "
+        f"chunks), a chunk, steps")
+    g = cact.Geometry(vocab=300, num_layers=2, num_heads=heads, num_kv_heads=kv, qk_head_dim=qk, v_head_dim=vd,
+                      engram_slots=64, engram_sites=(1,), global_layers=(0,), sliding_window=40)
+    data = archive(g, seed=46 + heads + qk)
+    m, s = run_feed(nh, data, o.random_tokens(300, g.vocab, seed=14), 340, f"heads {heads}/{kv} qk {qk} vd {vd}",
+                    then_steps=3)
