@@ -1119,7 +1119,7 @@ __device__ __forceinline__ float sinkhorn_lane(float z, int lane) {
 // The post and residual gates of the layer (step.rs:636-660), written
 // after the 24 mHC projections of a row: hpost[j] = 2 sigmoid(p_post[j]
 // a_post + off_j + b_post[j]) at 24, hres = sinkhorn64(fma(p_res, a_res,
-// b_res)) at 28.  One wavefront, beside the units.
+// b_res)) at 28.  One wavefront, beside the attention output of the row.
 __device__ __forceinline__ void post_gates(float* p, const LayerDev& L, int lane) {
     const int k = lane & 15;
     const float z = __builtin_fmaf(p[2 * MHC_LANES + k], L.a_res, L.b_res[k]);
@@ -1205,21 +1205,17 @@ __device__ __forceinline__ float unit_finish(const Dims& D, const SessDev& S, in
     return v;
 }
 
-// Blocks 0 .. t-1: row i's units, one wavefront per unit (q heads, k heads,
+// Block i: row i's units, one wavefront per unit (q heads, k heads,
 // v heads; step.rs:481-556, chunk.rs:202-253), lane = element: the causal
 // conv over the row and the pre-tap rows before it (fma from the newest
 // back; a row before position 0 contributes fma(w, 0, v)), then for q and
 // k the head zcn16 and RoPE, and for k and v the int8 cache append.  Rows
 // of the same feed are read from the projection, earlier ones from the
 // history ring; the row's pre-tap values go to the ring at a slot no row of
-// the feed reads.  Blocks t .. 2t-1: the row's post gates.
+// the feed reads.
 template <int TAPS, bool EXACT>
 __global__ __launch_bounds__(MAX_UNITS * 64) void k_units(Dims D, SessDev S, LayerDev L, int layer, int p0, int t) {
     const int unit = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), i = threadIdx.x & 63;
-    if ((int)blockIdx.x >= t) {
-        if (unit == 0) post_gates(S.p + (size_t)(blockIdx.x - t) * 64, L, i);
-        return;
-    }
     const int row = blockIdx.x, pos = p0 + row;
     const int nh = D.nh, nkv = D.nkv, qk = D.qk, vd = D.vd;
     const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd;
@@ -1270,7 +1266,7 @@ hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int lay
     const int units = D.nh + 2 * D.nkv;
     switch (D.taps) {
 #define NH_UNITS(TP, EX) \
-    hipLaunchKernelGGL((k_units<TP, EX>), dim3(2 * t), dim3(units * 64), 0, s, D, S, L, layer, p0, t)
+    hipLaunchKernelGGL((k_units<TP, EX>), dim3(t), dim3(units * 64), 0, s, D, S, L, layer, p0, t)
         case 1: NH_UNITS(1, true); break;
         case 2: NH_UNITS(2, true); break;
         case 3: NH_UNITS(3, true); break;
@@ -1878,6 +1874,9 @@ __global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, 
         const float* src = S.proj + (size_t)row * D.nq;
         for (int k = t; k < D.W; k += LT) h[k] = src[k];
     }
+    // the row's post gates on the last wavefront (past the heads' elements
+    // when nh vd <= 960)
+    if (wave == LT / 64 - 1 && K <= LT - 64) post_gates(S.p + (size_t)row * 64, L, lane);
     __shared__ float att[FWD_MAX_D];
     const int n = key_count(D, KS, span != 0, L.window, pos);
     int count, chunk;
@@ -1910,6 +1909,7 @@ __global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, 
         a8_group(q0 < K ? att[q0] : 0.0f, q1 < K ? att[q1] : 0.0f, lane, out_bits,
                  S.xq_att + ((size_t)row * Ga + g) * GROUP, S.sx_att + (size_t)row * Ga + g);
     }
+    if (wave == LT / 64 - 1 && K > LT - 64) post_gates(S.p + (size_t)row * 64, L, lane);
 }
 
 hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, int out_bits,
