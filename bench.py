@@ -119,6 +119,28 @@ def time_graph(fn_sweep, reps: int, warmup: int, torch):
     return start.elapsed_time(end) / reps
 
 
+def launch_floors(args, nh, torch):
+    """What bounds one dependent launch of the GEMV's size: µs per launch, in the same graph replay of
+    `copies` launches over distinct buffers, for a one-element fill (the launch itself), a write of the
+    GEMV's algorithmic bytes, a copy of them (read + write), and the GEMV."""
+    nbytes = algorithmic_bytes(1, K, N)
+    n4 = nbytes // 4
+    tiny = [torch.empty(1, device="cuda") for _ in range(args.copies)]
+    dst = [torch.empty(n4, device="cuda") for _ in range(args.copies)]
+    src = [torch.ones(n4, device="cuda") for _ in range(args.copies)]
+
+    def us(sweep):
+        return round(time_graph(sweep, max(1, args.steps), max(1, args.warmup), torch) / args.copies * 1e3, 4)
+
+    out = {"bytes": nbytes, "launches_per_replay": args.copies,
+           "fill_1_float_us": us(lambda: [x.fill_(1.0) for x in tiny]),
+           "fill_bytes_us": us(lambda: [x.fill_(1.0) for x in dst]),
+           "copy_bytes_us": us(lambda: [d.copy_(s_) for d, s_ in zip(dst, src)])}
+    del tiny, dst, src
+    out["gemv_us"] = round(gpu_gemv(args, nh, torch)["ms_launch"] * 1e3, 4)
+    return out
+
+
 def gpu_gemv(args, nh, torch):
     G = K // GROUP
     w, x = nh.seeded_normals([N * K, K], 0)
@@ -223,11 +245,12 @@ def needle3_products(nh, torch):
     engram key|value at each site, q|k|v|gate (RMSNorm fused into its A8
     prep) and out per layer, the tied head over the whole embedding; every
     product behind its A8 prep.  Prefill, per 512-token sequence
-    (infer/chunk.rs:197,274,350): the same products per 32-token chunk, the
-    head once."""
+    (infer/chunk.rs:197,274,350): the same products, each over all 512 rows
+    at once as the forward feeds a prompt's whole 32-token chunks together,
+    the head once."""
     import numpy as np
 
-    d, layers, vocab, sites, chunk, seq = 768, 20, NEEDLE3_VOCAB, 5, 32, 512
+    d, layers, vocab, sites, seq = 768, 20, NEEDLE3_VOCAB, 5, 512
     parts = (576, 96, 128, 768)
     seed = [1000]
 
@@ -241,7 +264,7 @@ def needle3_products(nh, torch):
     qkvg = [nh.QLinear([mat(n, d) for n in parts]) for _ in range(layers)]
     outp = [mat(d, parts[3]) for _ in range(layers)]
     ekv = [nh.QLinear([mat(d, d), mat(d, d)]) for _ in range(sites)]
-    xs = nh.seeded_normals([chunk * d], 77)[0]
+    xs = nh.seeded_normals([seq * d], 77)[0]
     x = torch.from_numpy(xs).cuda()
     ns = torch.from_numpy(np.float16(1.0 + 0.1 * xs[:d]).view(np.uint16).astype(np.int16)).cuda()
     nq = sum(parts)
@@ -267,11 +290,10 @@ def needle3_products(nh, torch):
         a1.prep(x, 1, ns)
         head.matmul_into(a1, y1["h"], vocab, 0)
 
-    ac, yc = nh.QAct(chunk, d), buffers(chunk)
+    ac, yc = nh.QAct(seq, d), buffers(seq)
 
     def sequence():
-        for _ in range(seq // chunk):
-            products(chunk, ac, yc)
+        products(seq, ac, yc)
         a1.prep(x, 1, ns)
         head.matmul_into(a1, y1["h"], vocab, 0)
 
@@ -279,7 +301,8 @@ def needle3_products(nh, torch):
     pre_ms = time_graph(sequence, 10, 2, torch)
     launches = 2 * (sites + 2 * layers + 1)
     return {"workload": "Needle-3 CQ-W4 x A8 products only (random-init weights; attention, mHC, engram conv and "
-                        "MLP not included): decode per token, prefill per 512-token sequence in 32-token chunks",
+                        "MLP not included): decode per token; prefill per 512-token sequence, each product over "
+                        "the sequence's 512 rows at once (the forward feeds whole 32-token chunks together)",
             "products_only": True, "launches_per_token": launches,
             "decode_us_per_token": round(dec_ms * 1e3, 2),
             "decode_products_tok_s": round(1e3 / dec_ms, 1),
@@ -335,8 +358,8 @@ def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
     prompt_ms = min(a for a, _ in runs)
     decode_ms = min(b for _, b in runs)
     layers = 20
-    out = {"workload": "Needle-3 random-init decode: 118 random prompt tokens (32-token chunks), then 64 greedy "
-                       "steps on the device",
+    out = {"workload": "Needle-3 random-init decode: 118 random prompt tokens fed together (32-token chunks "
+                       "32 + 32 + 32 + 22, each with its own block flags), then 64 greedy steps on the device",
            "prompt_tokens": DECODE_PROMPT, "decode_steps": DECODE_STEPS,
            "decode_tok_s": round(DECODE_STEPS * 1e3 / decode_ms, 1),
            "decode_ms_per_token": round(decode_ms / DECODE_STEPS, 4),
@@ -421,8 +444,9 @@ def needle3_prefill(nh, torch, cpu_seconds: float, with_cpu: bool):
             runs.append(ev0.elapsed_time(ev1))
     ms = min(runs)
     picks = [int(torch.argmax(x).item()) for x in last]
-    out = {"workload": "Needle-3 random-init prefill: 16 sequences x 512 random tokens, one at a time, 32-token "
-                       "chunks on the W4A8 GEMM",
+    out = {"workload": "Needle-3 random-init prefill: 16 sequences x 512 random tokens, one at a time, each fed "
+                       "as its 16 whole 32-token chunks together (512 rows per layer launch, the products as "
+                       "M=512 W4A8 GEMMs)",
            "sequences": PREFILL_SEQS, "tokens_per_sequence": PREFILL_LEN,
            "prefill_tok_s": round(PREFILL_SEQS * PREFILL_LEN * 1e3 / ms, 1),
            "ms_per_sequence": round(ms / PREFILL_SEQS, 3), "runs": len(runs)}
@@ -523,6 +547,8 @@ def main():
     ap.add_argument("--gemm-shape", default="", metavar="M,K,N",
                     help="only run one prefill product shape, eagerly (for GEMM profiles)")
     ap.add_argument("--launches", type=int, default=200, help="launches for --gemm-shape")
+    ap.add_argument("--floors", action="store_true",
+                    help="only time the single-launch floors beside the GEMV (launch, write, copy)")
     ap.add_argument("--needle3-only", action="store_true",
                     help="only run the Needle-3 decode and prefill lines (for model profiles)")
     args = ap.parse_args()
@@ -551,6 +577,9 @@ def main():
     torch.cuda.synchronize()
     if args.gemm_shape:
         print(json.dumps(gemm_shape(args.gemm_shape, args.launches, nh, torch)))
+        return
+    if args.floors:
+        print(json.dumps(launch_floors(args, nh, torch)))
         return
     if args.needle3_only:
         print(json.dumps({"needle3_decode": needle3_decode(nh, torch, args.cpu_seconds * 2, not args.no_cpu),
