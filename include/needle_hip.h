@@ -249,7 +249,7 @@ int nh_session_rewind_zeroed(nh_session* s, int len);
  * NH_EDEVICE and resets the session.  0 makes every such wait give up at
  * once, for tests of that path. */
 int nh_session_debug_spin_limit(nh_session* s, int limit);
-/* NatState::last_hidden (infer.rs:996-998) into DEVICE h[d_model]. */
+/* NatState::last_hidden (infer.rs:1014-1016) into DEVICE h[d_model]. */
 int nh_session_last_hidden(const nh_session* s, float* h, void* stream);
 /* Model::head_logits (infer.rs:1135-1141) of the session's last hidden state
  * into DEVICE logits[out_rows]. */

@@ -515,7 +515,7 @@ class Session:
         _check(_lib.nh_session_rewind_zeroed(self.h, int(length)))
 
     def last_hidden(self, stream=None) -> torch.Tensor:
-        """NatState::last_hidden (infer.rs:996-998)."""
+        """NatState::last_hidden (infer.rs:1014-1016)."""
         h = torch.empty(self.model.d_model, dtype=torch.float32, device="cuda")
         _check(_lib.nh_session_last_hidden(self.h, _dptr(h), _stream(stream)))
         return h
