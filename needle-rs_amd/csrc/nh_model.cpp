@@ -988,12 +988,15 @@ int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, v
     if (logits)
         NH_TRY(hipMemcpyAsync(logits, s->S.logits, (size_t)s->dims.out_rows * 4, hipMemcpyDeviceToDevice, st),
                "logits");
-    if (steps > 0) {
+    if (steps > 0)
         NH_TRY(hipMemcpyAsync(out, s->S.tokens + len0, (size_t)steps * 4, hipMemcpyDeviceToHost, st), "tokens");
+    // (the picks are read on the host once the stream has synchronized)
+    if (int rc = check_status(s, st)) return rc;
+    if (steps > 0) {
         s->toks.resize(len0);
         s->toks.insert(s->toks.end(), out, out + steps);
     }
-    return check_status(s, st);
+    return NH_OK;
 }
 
 }  // extern "C"

@@ -238,3 +238,32 @@ def test_bounded_wait_gives_up_and_reports(nh):
     got = s.forward([5, 6, 7]).cpu().numpy()
     want = forward.Forward(data).session(32).feed([5, 6, 7])
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_greedy_picks_into_pinned_memory(nh):
+    say("greedy picks into pinned host memory (C ABI), then a rollback and a prefill whose re-feed replays them")
+    import ctypes
+
+    data = archive(cact.Geometry(**SMALL), seed=82)
+    p = Pair(nh, data, 96)
+    p.attend(4, 32)
+    want = p.fwd(o.random_tokens(40, 300, seed=83))
+    steps = 12
+    out = torch.zeros(steps, dtype=torch.int32, pin_memory=True)
+    logits = torch.empty(p.m.out_rows, dtype=torch.float32, device="cuda")
+    rc = nh._lib.nh_generate_greedy(p.g.h, steps, ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(logits.data_ptr()),
+                                    None)
+    assert rc == 0, nh._lib.nh_last_error()
+    picks = out.numpy().astype(np.uint32)
+    for i, t in enumerate(picks):
+        assert int(t) == int(np.argmax(want)), (i, int(t))
+        want = p.o.forward([int(t)])
+    same("greedy logits", logits.cpu().numpy(), np.asarray(want).reshape(-1), p.stats)
+    assert len(p.g) == len(p.o) == 52
+    # positions 47..51 held slots 15..19; after the rollback a 3-token prefill
+    # (end 50) sees 18 and 19 as stale and re-feeds from 18 through the
+    # greedy picks at 40..46
+    p.rollback(5)
+    p.prefill(o.random_tokens(3, 300, seed=84), label="prefill re-feed over greedy picks")
+    p.steps(o.random_tokens(2, 300, seed=85), label="after re-feed")
+    p.done("greedy picks into pinned memory")
