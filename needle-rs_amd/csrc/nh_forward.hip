@@ -975,6 +975,7 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
             const float h = __builtin_fmaf(tt, fnorm, tt);
             sh.x2[t] = h;
             S.hid[(size_t)arow * d + t] = h;
+            if (arow == (int)gridDim.x - 1) S.last_hid[t] = h;  // NatState::last_hidden: the last row returned
         }
     }
     __syncthreads();
@@ -1631,14 +1632,24 @@ __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerD
     if (ci >= count) return;
     const int c0 = ci * chunk, len = min(chunk, n - c0), blocked = len / 4 * 4, slot0 = lo + c0;
     const int sh = slot0 & 3, base = slot0 - sh, cols = sh + len;
-    __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][ATT_KPITCH];
     __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][AG_COLS];
     __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
     __shared__ alignas(16) int8_t q8[AG_WAVES][MAX_HEAD_DIM];
     __shared__ float qsc[AG_WAVES];
-    __shared__ alignas(16) float sc[AG_WAVES][8 * AG_TP];
-    __shared__ alignas(16) int8_t dig[AG_WAVES][3][AG_COLS];
-    __shared__ int32_t pv[3][AG_WAVES][MAX_HEAD_DIM];
+    // The key rows are read by the score products only; the scores, digits
+    // and P.V sums then take their space (three blocks fit on a CU).
+    __shared__ union {
+        alignas(16) int8_t ks8[ATT_CHUNK_MAX][ATT_KPITCH];
+        struct {
+            alignas(16) float sc[AG_WAVES][8 * AG_TP];
+            alignas(16) int8_t dig[AG_WAVES][3][AG_COLS];
+            int32_t pv[3][AG_WAVES][MAX_HEAD_DIM];
+        };
+    } lds;
+    auto& ks8 = lds.ks8;
+    auto& sc = lds.sc;
+    auto& dig = lds.dig;
+    auto& pv = lds.pv;
     const size_t lc = (size_t)layer * D.cap;
     const int hw = min(wave, hpg - 1), hh = kvh * hpg + hw;
     // every load first (unconditional, at clamped in-range addresses)
@@ -1693,13 +1704,24 @@ __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerD
     }
     __syncthreads();
     const int mr = lane & 15, mq = lane >> 4;  // MFMA lane: row / column mr, 16-byte k-block mq
-    // scores: key tile kt (16 keys) per MFMA, tiles split over the wavefronts;
-    // lane (mq, mr) gets heads 4 mq + v against key 16 kt + mr
-    for (int kt = wave; kt * 16 < len; kt += AG_WAVES) {
-        const v4i a = mr < AG_WAVES ? *reinterpret_cast<const v4i*>(&q8[mr][16 * mq]) : v4i{0, 0, 0, 0};
-        const v4i b = *reinterpret_cast<const v4i*>(&ks8[kt * 16 + mr][16 * mq]);
-        const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
-        const int i = kt * 16 + mr;
+    // scores: key tile kt (16 keys) per MFMA, tiles split over the wavefronts
+    // (at most KT per wavefront); lane (mq, mr) gets heads 4 mq + v against
+    // key 16 kt + mr, kept in registers until every key row has been read
+    constexpr int KT = ATT_CHUNK_MAX / 16 / AG_WAVES;
+    v4i dk[KT];
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+        const int kt = wave + j * AG_WAVES;
+        if (kt * 16 < len) {
+            const v4i a = mr < AG_WAVES ? *reinterpret_cast<const v4i*>(&q8[mr][16 * mq]) : v4i{0, 0, 0, 0};
+            const v4i b = *reinterpret_cast<const v4i*>(&ks8[kt * 16 + mr][16 * mq]);
+            dk[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, v4i{0, 0, 0, 0}, 0, 0, 0);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+        const int i = (wave + j * AG_WAVES) * 16 + mr;
         if (i < len) {
             const float ksc = kss[i];
 #pragma unroll
@@ -1707,7 +1729,7 @@ __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerD
                 const int h = 4 * mq + v;
                 if (h < hpg) {
                     const float qs = qsc[h];
-                    sc[h][i] = i < blocked ? (ksc * (float)d[v]) * qs : (ksc * qs) * (float)d[v];
+                    sc[h][i] = i < blocked ? (ksc * (float)dk[j][v]) * qs : (ksc * qs) * (float)dk[j][v];
                 }
             }
         }

@@ -585,8 +585,7 @@ int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
             NH_TRY(hipMemcpyAsync(out, S.hid, (size_t)rows * d * 4, hipMemcpyDeviceToDevice, st), "hidden");
         if (out && outputs == NH_OUT_LAST_LOGITS)
             NH_TRY(hipMemcpyAsync(out, S.logits, (size_t)D.out_rows * 4, hipMemcpyDeviceToDevice, st), "logits");
-        NH_TRY(hipMemcpyAsync(S.last_hid, S.hid + (size_t)(rows - 1) * d, (size_t)d * 4, hipMemcpyDeviceToDevice, st),
-               "last hidden");
+        // (the head's input kernel writes the last row's hidden state to S.last_hid as well)
         s->have_logits = logits;
         s->have_hidden = true;
     } else {
