@@ -267,3 +267,58 @@ def test_greedy_picks_into_pinned_memory(nh):
     p.prefill(o.random_tokens(3, 300, seed=84), label="prefill re-feed over greedy picks")
     p.steps(o.random_tokens(2, 300, seed=85), label="after re-feed")
     p.done("greedy picks into pinned memory")
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_random_session_scripts(nh, seed):
+    """A seeded random script of feeds (every Outputs mode, lengths across the
+    chunk and batch boundaries), prefills, single steps, rollbacks within the
+    last feeds, clones, rewinds and, for some seeds, an attention span; every
+    result bit-identical to the oracle running the same script."""
+    rng = np.random.default_rng(1000 + seed)
+    geoms = [SMALL, dict(vocab=300, num_layers=2, engram_slots=64, engram_sites=(0,), global_layers=(0,),
+                         sliding_window=48, qkv_conv_taps=4)]
+    g = cact.Geometry(**geoms[seed % 2])
+    data = archive(g, seed=90 + seed)
+    cap = 260
+    p = Pair(nh, data, cap)
+    if seed == 1:
+        p.attend(int(rng.integers(2, 9)), int(rng.choice([32, 48, 64])))
+    since = 0  # positions fed since the last rollback or rewind (what a rollback may drop)
+    hidden = False
+    say(f"random session script, seed {seed}")
+    for op in range(40):
+        kind = rng.choice(["feed", "prefill", "steps", "rollback", "clone", "rewind", "heads"],
+                          p=[0.3, 0.15, 0.2, 0.15, 0.07, 0.05, 0.08])
+        room = cap - len(p.g)
+        if kind in ("feed", "prefill"):
+            n = int(rng.choice([1, 2, 5, 31, 32, 33, 64, 70, 97]))
+            if n > room:
+                continue
+            mode = int(rng.integers(0, 5))
+            toks = rng.integers(0, 300, n).astype(np.uint32)
+            (p.fwd if kind == "feed" else p.prefill)(toks, mode, f"{kind} {n} mode {mode} at op {op}")
+            since += n
+            hidden = hidden or mode != forward.OUT_NONE
+        elif kind == "steps":
+            n = int(rng.integers(1, 5))
+            if n > room:
+                continue
+            p.steps(rng.integers(0, 300, n), forward.OUT_LAST_LOGITS, f"step at op {op}")
+            since += n
+            hidden = True
+        elif kind == "rollback":
+            n = int(min(since, rng.integers(1, 33)))
+            if n < 1:
+                continue
+            p.rollback(n)
+            since -= n
+        elif kind == "clone":
+            p = p.clone()
+        elif kind == "rewind":
+            length = int(rng.integers(0, len(p.g) + 1))
+            p.rewind_zeroed(length)
+            since = 0
+        elif kind == "heads" and hidden:
+            p.heads(rng.integers(0, 300, 5))
+    p.done(f"random session script {seed}")
