@@ -1091,49 +1091,22 @@ hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const La
 }
 
 // ------------------------------------------------------------------ units
-// A 64-bit value from another lane of the same 16-lane row (DPP control
-// CTRL applied to both halves).
-template <int CTRL>
-__device__ __forceinline__ double dpp64(double x) {
-    const uint64_t u = __builtin_bit_cast(uint64_t, x);
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, 0xF, 0xF, false);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, 0xF, 0xF, false);
-    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-
 // sinkhorn64 (infer.rs:2501-2528) by 16 lanes, lane = 4 r + c holding
 // e[r][c]: row sums ((e0 + e1) + (e2 + e3)), column sums
-// ((e[c] + e[4 + c]) + (e[8 + c] + e[12 + c])), 20 rounds, in f64.  The
-// row's values come by quad broadcasts; the column's by rotations of the
-// 16-lane row by 4, 8 and 12 lanes, each carrying its source row, so the
-// sum takes them in row order.
+// ((e[c] + e[4 + c]) + (e[8 + c] + e[12 + c])), 20 rounds, in f64.
 __device__ __forceinline__ float sinkhorn_lane(float z, int lane) {
-    const int r = (lane >> 2) & 3;
-    const int zi = __builtin_bit_cast(int, z);
-    const float z0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, zi, 0x00, 0xF, 0xF, false));
-    const float z1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, zi, 0x55, 0xF, 0xF, false));
-    const float z2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, zi, 0xAA, 0xF, 0xF, false));
-    const float z3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, zi, 0xFF, 0xF, 0xF, false));
+    const int r = (lane >> 2) & 3, c = lane & 3;
+    const float z0 = __shfl(z, 4 * r, 64), z1 = __shfl(z, 4 * r + 1, 64), z2 = __shfl(z, 4 * r + 2, 64),
+                z3 = __shfl(z, 4 * r + 3, 64);
     const double m = (double)fmaxf(fmaxf(z0, z1), fmaxf(z2, z3));
     double e = exp((double)z - m);
-    // the source rows of the three rotations
-    const int r1 = __builtin_amdgcn_update_dpp(0, r, 0x124, 0xF, 0xF, false);
-    const int r2 = __builtin_amdgcn_update_dpp(0, r, 0x128, 0xF, 0xF, false);
     for (int it = 0; it < 20; ++it) {
         {
-            const double a0 = dpp64<0x00>(e), a1 = dpp64<0x55>(e), a2 = dpp64<0xAA>(e), a3 = dpp64<0xFF>(e);
+            const double a0 = __shfl(e, 4 * r, 64), a1 = __shfl(e, 4 * r + 1, 64), a2 = __shfl(e, 4 * r + 2, 64),
+                         a3 = __shfl(e, 4 * r + 3, 64);
             const double inv = 1.0 / ((a0 + a1) + (a2 + a3));
             e *= inv;
         }
-        {
-            const double v1 = dpp64<0x124>(e), v2 = dpp64<0x128>(e), v3 = dpp64<0x12C>(e);
-            auto row = [&](int k) { return r == k ? e : r1 == k ? v1 : r2 == k ? v2 : v3; };
-            const double inv = 1.0 / ((row(0) + row(1)) + (row(2) + row(3)));
-            e *= inv;
-        }
-    }
-    return (float)e;
-}
         {
             const double a0 = __shfl(e, c, 64), a1 = __shfl(e, 4 + c, 64), a2 = __shfl(e, 8 + c, 64),
                          a3 = __shfl(e, 12 + c, 64);
