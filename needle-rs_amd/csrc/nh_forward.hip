@@ -683,8 +683,9 @@ __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int l
 // The Hadamard MLP and mHC write of layer P (step.rs:600-705): xl holds the
 // thread's element of the 4 lanes (t < d) and gets the new ones; returns
 // this thread's max |new lane value| (for the next layer's mHC read).
+template <typename AfterMlp>
 __device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, const OutRegs& q, LayerShared& sh,
-                           float (&xl)[MHC_LANES]) {
+                           float (&xl)[MHC_LANES], AfterMlp after_mlp) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
     // mix8 runs on waves 4..7 (threads 256..511), beside cond_weights on wave 0
     const bool mixer = t >= MIX_T && t < 2 * MIX_T;
@@ -743,6 +744,7 @@ __device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, c
     __syncthreads();
     if (mixer) mix8_n(mu, sh.B, sh.kp[5], sh.C, d / HADA_NB / 8 * 8);
     __syncthreads();
+    after_mlp();
     // The mHC write: y = (x2 + t3 * d4) - u; lane a = y hpost[a] + sum_b
     // hres[a][b] old[b] as an fma chain over b.
     float m = 0.0f;
@@ -1043,7 +1045,11 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     if constexpr (has_prev) store_out(D, qo, sh);
     __syncthreads();
     if constexpr (has_next && has_prev) qi = load_in<!BATCH>(D, R, N);
-    if constexpr (has_prev) m = layer_out(D, S, P, qo, sh, xl);
+    // (batched: the Phi8 rows are read once the MLP's registers are free)
+    if constexpr (has_prev)
+        m = layer_out(D, S, P, qo, sh, xl, [&]() __attribute__((always_inline)) {
+            if constexpr (has_next && BATCH) load_phi(D, N, qi);
+        });
     // the wavefronts' maxima of |xs| for the mHC read
     m = wave_max(m);
     if (lane == 0) sh.red[wave] = m;
@@ -1052,7 +1058,7 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     // stores issued earlier would sit in the memory counter ahead of loads
     // that are waited for)
     if constexpr (has_next)
-        layer_in<BATCH>(D, R, N, qi, in_bits, sh, xl);
+        layer_in<BATCH && !has_prev>(D, R, N, qi, in_bits, sh, xl);
     else
         head_in(D, S, fnorm, head_bits, blockIdx.x, sh, xl);  // row i - row0
     if constexpr (has_prev) {
