@@ -1959,15 +1959,16 @@ hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int 
 // and the history ring).  With no cross-block data the group's A8 runs in
 // the block.  One more block computes the row's post gates.
 constexpr int DG_HEAD_T = 256;
+constexpr int DG_THREADS = 1024;  // 16 wavefronts: the attention's HP * 256 threads, the rest stage keys
 
 constexpr int DG_PITCH = ATT_CHUNK_MAX + 8;      // value / digit row: 3 alignment bytes + 256 slots + dword tail
 constexpr int DG_KPITCH = MAX_HEAD_DIM + 16;     // key row (80 bytes: 8 rows cover the 32 banks)
 constexpr int DG_VDW = (ATT_CHUNK_MAX + 3 + 3) / 4;  // value dwords per column (alignment offset + slots)
 
 template <int HP, int TAPS, bool EXACT>
-__global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S, LayerDev L, int layer, int p0,
-                                                              int out_bits) {
-    constexpr int NT = HP * DG_HEAD_T;
+__global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, LayerDev L, int layer, int p0,
+                                                          int out_bits) {
+    constexpr int NT = HP * DG_HEAD_T;  // the attention's threads (the rest only stage keys)
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int nh = D.nh, nkv = D.nkv, qk = D.qk, vd = D.vd, group = nh / nkv;
     const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd;
@@ -1982,6 +1983,7 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
     // boundary of the cache row): column index j = i + sh for key i
     const int sh = lo & 3, base = lo - sh;
     const int h = t / DG_HEAD_T, u = t % DG_HEAD_T, hw = u >> 6;  // head, thread and wavefront in it
+    const bool attends = t < NT;  // (wave-uniform)
     __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][DG_KPITCH];  // key rows by slot - lo
     __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][DG_PITCH];    // value columns by slot - base
     __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
@@ -1992,51 +1994,55 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
     __shared__ float s_qs[HP], s_sum[HP];
     __shared__ float att[HP * MAX_HEAD_DIM];
     const size_t lc = (size_t)layer * D.cap;
-    // The unit inputs first: queries on waves 0 .. HP-1, the new key and
-    // value on the next two.
-    // (The role is made wave-uniform for the compiler, so the loads sit
-    // under a scalar branch and nothing waits for them before the stream.)
-    // Waves past the units load the value unit's inputs too and ignore
-    // them.  The role is wave-uniform (scalar branches, each with constant
-    // argument fields: selecting the fields by role would copy the
-    // argument struct to scratch).
-    const int role = __builtin_amdgcn_readfirstlane(wave < HP ? 0 : wave - HP + 1);  // 0 q, 1 k, 2 v, 3+ none
+    // Waves 0 .. HP-1 load the query units' inputs, the next two those of
+    // the new key and value, and the rest (the staging waves) the keys
+    // before the position: int8 rows (16-byte chunks), scales and value
+    // dwords.  A wavefront's loads land at about a kilobyte per thousand
+    // cycles, so the units' few loads are kept apart from the keys' and
+    // the keys' are spread over many wavefronts.  The role is wave-uniform
+    // (scalar branches, each with constant argument fields: selecting the
+    // fields by role would copy the argument struct to scratch); within a
+    // role the loads are unconditional, at clamped in-range addresses (a
+    // load under a lane condition gets waited for at the branch's end), and
+    // what lies past the keys is never stored.
+    const int role = __builtin_amdgcn_readfirstlane(wave < HP ? 0 : min(wave - HP + 1, 3));  // 0 q, 1 k, 2 v, 3 keys
+    constexpr int NS = DG_THREADS - (HP + 2) * 64;  // staging threads
+    constexpr int KR = (ATT_CHUNK_MAX * 4 + NS - 1) / NS, VR = (MAX_HEAD_DIM * DG_VDW + NS - 1) / NS,
+                  SR = (ATT_CHUNK_MAX + NS - 1) / NS;
+    const int nold = n - 1, rq = qk / 16, vdw = (sh + nold + 3) / 4, ts = t - (HP + 2) * 64;
     UnitIn ui;
-    if (role == 0)
+    u32x4 kr[KR];  // (a native vector: an array of HIP's uint4 is kept on the stack)
+    uint32_t vw[VR];
+    float ksr[SR], vsr[SR];
+    if (role == 0) {
         ui = unit_load<TAPS, EXACT>(D, S, layer, p0, 0, (hh0 + wave) * qk, qd, (hh0 + wave) * qk, qk, L.q_taps,
                                     L.q_norm, lane);
-    else if (role == 1)
+    } else if (role == 1) {
         ui = unit_load<TAPS, EXACT>(D, S, layer, p0, 0, qd + kvh * qk, kd, kvh * qk, qk, L.k_taps, L.k_norm, lane);
-    else
+    } else if (role == 2) {
         ui = unit_load<TAPS, EXACT>(D, S, layer, p0, 0, qd + kd + kvh * vd, vdim, kvh * vd, vd, L.v_taps, L.k_norm,
                                     lane);
-    // The keys before the position: int8 rows (16-byte chunks), scales and
-    // value dwords, all in flight at once, stored to LDS after the units.
-    constexpr int KR = ATT_CHUNK_MAX * 4 / NT, VR = (MAX_HEAD_DIM * DG_VDW + NT - 1) / NT;
-    const int nold = n - 1, rq = qk / 16, vdw = (sh + nold + 3) / 4;
-    uint4 kr[KR];
-    uint32_t vw[VR];
-    float ksr = 0.0f, vsr = 0.0f;
-    // (unconditional loads at clamped in-range addresses; what lies past
-    // the keys is never stored)
+    } else {
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
-        const int e = t + r * NT, i = min(e >> 2, n - 1), c = min(e & 3, rq - 1);
-        kr[r] = reinterpret_cast<const uint4*>(S.k8 + ((lc + lo + i) * nkv + kvh) * qk)[c];
-    }
-    {
-        const int i = min(t, n - 1);
-        ksr = S.ks[(lc + lo + i) * nkv + kvh];
-        vsr = S.vs[(lc + lo + i) * nkv + kvh];
+        for (int r = 0; r < KR; ++r) {
+            const int e = ts + r * NS, i = min(e >> 2, n - 1), c = min(e & 3, rq - 1);
+            kr[r] = reinterpret_cast<const u32x4*>(S.k8 + ((lc + lo + i) * nkv + kvh) * qk)[c];
+        }
+#pragma unroll
+        for (int r = 0; r < SR; ++r) {
+            const int i = min(ts + r * NS, n - 1);
+            ksr[r] = S.ks[(lc + lo + i) * nkv + kvh];
+            vsr[r] = S.vs[(lc + lo + i) * nkv + kvh];
+        }
+        const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
+#pragma unroll
+        for (int r = 0; r < VR; ++r) {
+            const int e = ts + r * NS, dm = min(e / DG_VDW, vd - 1), k = min(e % DG_VDW, max(vdw - 1, 0));
+            vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
+        }
     }
     // the head gate of this thread's P.V output (head h, dimension u / 4)
-    const float gate = S.proj[D.W + (hh0 + h) * vd + min(u >> 2, vd - 1)];
-    const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
-#pragma unroll
-    for (int r = 0; r < VR; ++r) {
-        const int e = t + r * NT, dm = min(e / DG_VDW, vd - 1), k = min(e % DG_VDW, max(vdw - 1, 0));
-        vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
-    }
+    const float gate = S.proj[D.W + (hh0 + min(h, HP - 1)) * vd + min(u >> 2, vd - 1)];
     // the units
     if (wave < HP) {
         const float v = unit_finish<TAPS, EXACT>(D, S, layer, p0, (hh0 + wave) * qk, qk, ui, true, lane, true);
@@ -2067,36 +2073,42 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
             vss[n - 1] = s;
             if (owner) S.vs[(lc + p0) * nkv + kvh] = s;
         }
-    }
+    } else {
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
-        const int e = t + r * NT, i = e >> 2, c = e & 3;
-        if (i < nold && c < rq) reinterpret_cast<uint4*>(ks8[i])[c] = kr[r];
-    }
-    if (t < nold) {
-        kss[t] = ksr;
-        vss[t] = vsr;
-    }
-    // value bytes of keys 0 .. nold - 1 (columns sh .. sh + nold - 1); the
-    // bytes before sh and past the keys meet zero digits
+        for (int r = 0; r < KR; ++r) {
+            const int e = ts + r * NS, i = e >> 2, c = e & 3;
+            if (i < nold && c < rq) reinterpret_cast<u32x4*>(ks8[i])[c] = kr[r];
+        }
 #pragma unroll
-    for (int r = 0; r < VR; ++r) {
-        const int e = t + r * NT, dm = e / DG_VDW, k = e % DG_VDW;
-        if (dm < vd && k < vdw) {
-            if (4 * k + 3 < sh + nold) {
-                reinterpret_cast<uint32_t*>(vs8[dm])[k] = vw[r];
-            } else {
+        for (int r = 0; r < SR; ++r) {
+            const int i = ts + r * NS;
+            if (i < nold) {
+                kss[i] = ksr[r];
+                vss[i] = vsr[r];
+            }
+        }
+        // value bytes of keys 0 .. nold - 1 (columns sh .. sh + nold - 1);
+        // the bytes before sh and past the keys meet zero digits
 #pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    if (4 * k + b < sh + nold) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
+        for (int r = 0; r < VR; ++r) {
+            const int e = ts + r * NS, dm = e / DG_VDW, k = e % DG_VDW;
+            if (dm < vd && k < vdw) {
+                if (4 * k + 3 < sh + nold) {
+                    reinterpret_cast<uint32_t*>(vs8[dm])[k] = vw[r];
+                } else {
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        if (4 * k + b < sh + nold) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
+                }
             }
         }
     }
     __syncthreads();
-    // attend_head_ref over the one chunk, one head per 256 threads
-    const float qs = s_qs[h];
-    float mx = -__builtin_inff();
-    {
+    // attend_head_ref over the one chunk, one head per 256 threads (the
+    // staging waves only meet the barriers)
+    float mx = -__builtin_inff(), wmax = 0.0f;
+    if (attends) {
+        const float qs = s_qs[h];
         uint4 qv[MAX_HEAD_DIM / 16];
 #pragma unroll
         for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) qv[c] = reinterpret_cast<const uint4*>(q8[h])[c];
@@ -2116,14 +2128,16 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
             sc[h][i] = sv;
             mx = fmaxf(mx, sv);
         }
+        mx = wave_max(mx);
+        if (lane == 0) red[h][hw] = mx;
     }
-    mx = wave_max(mx);
-    if (lane == 0) red[h][hw] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
-    for (int i = u; i < n; i += DG_HEAD_T) sc[h][i] = i < blocked ? nexp(sc[h][i] - mx) : lexpf(sc[h][i] - mx);
+    if (attends) {
+        mx = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
+        for (int i = u; i < n; i += DG_HEAD_T) sc[h][i] = i < blocked ? nexp(sc[h][i] - mx) : lexpf(sc[h][i] - mx);
+    }
     __syncthreads();
-    if (hw == 0) {
+    if (attends && hw == 0) {
         // lane 4 hi + k sums sc[8 b + 4 hi + k] over b in order, the loads
         // of a batch of 8 issued ahead of its adds
         float acc = 0.0f;
@@ -2162,31 +2176,34 @@ __global__ __launch_bounds__(HP * DG_HEAD_T) void k_dec_group(Dims D, SessDev S,
         if (lane == 0) s_sum[h] = sum;
     }
     __syncthreads();
-    float wmax = 0.0f;
-    for (int i = u; i < n; i += DG_HEAD_T) {
-        const float w = sc[h][i] * vss[i];
-        sc[h][i] = w;
-        wmax = fmaxf(wmax, w);
-    }
-    wmax = wave_max(wmax);
-    if (lane == 0) red[h][hw] = wmax;
-    __syncthreads();
-    wmax = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
-    const float qw = bits_f32(0x49fffff8u) / wmax;
-    for (int i = u; i < n; i += DG_HEAD_T) {
-        const int32_t wq = (int32_t)roundf(sc[h][i] * qw);
-        dig[h][0][sh + i] = (int8_t)(wq >> 14);
-        dig[h][1][sh + i] = (int8_t)((wq >> 7) & 127);
-        dig[h][2][sh + i] = (int8_t)(wq & 127);
-    }
-    // zero digits in the first dword before the keys and the last one past them
-    if (u < 4) {
-        const int j0 = u, j1 = sh + n + u;
-        if (j0 < sh) dig[h][0][j0] = dig[h][1][j0] = dig[h][2][j0] = 0;
-        if (j1 < (sh + n + 3) / 4 * 4) dig[h][0][j1] = dig[h][1][j1] = dig[h][2][j1] = 0;
+    if (attends) {
+        for (int i = u; i < n; i += DG_HEAD_T) {
+            const float w = sc[h][i] * vss[i];
+            sc[h][i] = w;
+            wmax = fmaxf(wmax, w);
+        }
+        wmax = wave_max(wmax);
+        if (lane == 0) red[h][hw] = wmax;
     }
     __syncthreads();
-    {
+    if (attends) {
+        wmax = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
+        const float qw = bits_f32(0x49fffff8u) / wmax;
+        for (int i = u; i < n; i += DG_HEAD_T) {
+            const int32_t wq = (int32_t)roundf(sc[h][i] * qw);
+            dig[h][0][sh + i] = (int8_t)(wq >> 14);
+            dig[h][1][sh + i] = (int8_t)((wq >> 7) & 127);
+            dig[h][2][sh + i] = (int8_t)(wq & 127);
+        }
+        // zero digits in the first dword before the keys and the last one past them
+        if (u < 4) {
+            const int j0 = u, j1 = sh + n + u;
+            if (j0 < sh) dig[h][0][j0] = dig[h][1][j0] = dig[h][2][j0] = 0;
+            if (j1 < (sh + n + 3) / 4 * 4) dig[h][0][j1] = dig[h][1][j1] = dig[h][2][j1] = 0;
+        }
+    }
+    __syncthreads();
+    if (attends) {
         // exact integer P.V: four columns per sdot4, 16 per thread step
         const float cw = wmax * bits_f32(0x35000004u);
         const int dm = u >> 2, part = u & 3, cols = sh + n;
@@ -2255,7 +2272,7 @@ hipError_t fwd_dec_attn(const Dims& D, const SessDev& S, const LayerDev& L, int 
     const int hp = GROUP / D.vd, blocks = D.nh / hp + 1;
     // exact tap counts 1..4, clamped loads up to DG_MAX_TAPS otherwise
 #define NH_DG(HP, TP, EX)                                                                                        \
-    hipLaunchKernelGGL((k_dec_group<HP, TP, EX>), dim3(blocks), dim3(HP * DG_HEAD_T), 0, s, D, S, L, layer, p0, \
+    hipLaunchKernelGGL((k_dec_group<HP, TP, EX>), dim3(blocks), dim3(DG_THREADS), 0, s, D, S, L, layer, p0,     \
                        out_bits)
 #define NH_DG_TAPS(HP)                          \
     switch (D.taps) {                           \
