@@ -1100,23 +1100,42 @@ hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const La
 // sinkhorn64 (infer.rs:2501-2528) by 16 lanes, lane = 4 r + c holding
 // e[r][c]: row sums ((e0 + e1) + (e2 + e3)), column sums
 // ((e[c] + e[4 + c]) + (e[8 + c] + e[12 + c])), 20 rounds, in f64.
+// A double moved across lanes by one DPP pattern (both halves).
+template <int CTRL>
+__device__ __forceinline__ double dpp64(double x) {
+    const unsigned long long b = __builtin_bit_cast(unsigned long long, x);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, (unsigned long long)(unsigned)lo | ((unsigned long long)(unsigned)hi << 32));
+}
+
 __device__ __forceinline__ float sinkhorn_lane(float z, int lane) {
-    const int r = (lane >> 2) & 3, c = lane & 3;
+    const int r = (lane >> 2) & 3;
     const float z0 = __shfl(z, 4 * r, 64), z1 = __shfl(z, 4 * r + 1, 64), z2 = __shfl(z, 4 * r + 2, 64),
                 z3 = __shfl(z, 4 * r + 3, 64);
     const double m = (double)fmaxf(fmaxf(z0, z1), fmaxf(z2, z3));
     double e = exp((double)z - m);
+    // Both sums are (x0 + x1) + (x2 + x3) over the row's (column's)
+    // elements in order.  A row's lanes are a quad: lane c gets element
+    // c ^ j from quad permutes j = 1, 2, 3, and since IEEE addition is
+    // commutative, (y0 + y1) + (y2 + y3) over them is the same sum in every
+    // lane.  A column's elements sit 4 lanes apart: rotations by 4, 8, 12
+    // within the 16 lanes bring rows r +- 1, r +- 2, r -+ 1, so the sum
+    // pairs (w0 + w1) + (w2 + w3) when row r and the first rotation's row
+    // differ in bit 0 only, else (w0 + w3) + (w1 + w2); the first
+    // rotation's row comes from rotating r itself.
+    const int r1 = __builtin_amdgcn_update_dpp(0, r, 0x124, 0xF, 0xF, false);
+    const bool pair01 = (r ^ r1) == 1;
     for (int it = 0; it < 20; ++it) {
         {
-            const double a0 = __shfl(e, 4 * r, 64), a1 = __shfl(e, 4 * r + 1, 64), a2 = __shfl(e, 4 * r + 2, 64),
-                         a3 = __shfl(e, 4 * r + 3, 64);
-            const double inv = 1.0 / ((a0 + a1) + (a2 + a3));
+            const double y1 = dpp64<0xB1>(e), y2 = dpp64<0x4E>(e), y3 = dpp64<0x1B>(e);
+            const double inv = 1.0 / ((e + y1) + (y2 + y3));
             e *= inv;
         }
         {
-            const double a0 = __shfl(e, c, 64), a1 = __shfl(e, 4 + c, 64), a2 = __shfl(e, 8 + c, 64),
-                         a3 = __shfl(e, 12 + c, 64);
-            const double inv = 1.0 / ((a0 + a1) + (a2 + a3));
+            const double w1 = dpp64<0x124>(e), w2 = dpp64<0x128>(e), w3 = dpp64<0x12C>(e);
+            const double sa = (e + w1) + (w2 + w3), sb = (e + w3) + (w1 + w2);
+            const double inv = 1.0 / (pair01 ? sa : sb);
             e *= inv;
         }
     }
@@ -1889,9 +1908,13 @@ hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int la
 }
 
 // The chunk merge (infer.rs:1990-2006), the head gate
-// (att / (nexp(-gate) + 1), step.rs:558-572) and A8 of the heads.
+// (att / (nexp(-gate) + 1), step.rs:558-572) and A8 of the heads: wavefront
+// g merges the two halves of A8 group g (elements 128 g + lane and
+// 128 g + 64 + lane) and quantizes them, so no wavefront waits for another;
+// the last wavefront computes the row's post gates meanwhile.
 __global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, int layer, int p0, int rows,
                                                  int out_bits, KeySpan KS, int span) {
+    static_assert((FWD_MAX_D + GROUP - 1) / GROUP < LT / 64, "the A8 groups leave the last wavefront free");
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, vd = D.vd, K = D.nh * vd;
     const int row = blockIdx.x, pos = p0 + row, Ga = (K + GROUP - 1) / GROUP;
     // A feed of several chunks: the tap history of its last rows (the units
@@ -1902,15 +1925,17 @@ __global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, 
         const float* src = S.proj + (size_t)row * D.nq;
         for (int k = t; k < D.W; k += LT) h[k] = src[k];
     }
-    // the row's post gates on the last wavefront (past the heads' elements
-    // when nh vd <= 960)
-    if (wave == LT / 64 - 1 && K <= LT - 64) post_gates(S.p + (size_t)row * 64, L, lane);
-    __shared__ float att[FWD_MAX_D];
+    if (wave == LT / 64 - 1) {
+        post_gates(S.p + (size_t)row * 64, L, lane);
+        return;
+    }
+    if (wave >= Ga) return;
     const int n = key_count(D, KS, span != 0, L.window, pos);
     int count, chunk;
     key_chunks(n, D.nkv, rows > 1, count, chunk);
-    if (t < K) {
-        const int hh = t / vd, i = t % vd;
+    auto merged = [&](int q) -> float {
+        if (q >= K) return 0.0f;
+        const int hh = q / vd, i = q % vd;
         const size_t base = ((size_t)row * D.nh + hh) * D.max_chunks;
         float out;
         if (count == 1) {
@@ -1928,16 +1953,10 @@ __global__ __launch_bounds__(LT) void k_attn_out(Dims D, SessDev S, LayerDev L, 
             const float inv = 1.0f / total;
             out = acc * inv;
         }
-        att[t] = out / (nexp(-S.proj[(size_t)row * D.nq + D.W + t]) + 1.0f);
-    }
-    __syncthreads();
-    const int groups = (K + GROUP - 1) / GROUP;
-    for (int g = wave; g < groups; g += LT / 64) {
-        const int q0 = g * GROUP + lane, q1 = q0 + 64;
-        a8_group(q0 < K ? att[q0] : 0.0f, q1 < K ? att[q1] : 0.0f, lane, out_bits,
-                 S.xq_att + ((size_t)row * Ga + g) * GROUP, S.sx_att + (size_t)row * Ga + g);
-    }
-    if (wave == LT / 64 - 1 && K > LT - 64) post_gates(S.p + (size_t)row * 64, L, lane);
+        return out / (nexp(-S.proj[(size_t)row * D.nq + D.W + q]) + 1.0f);
+    };
+    const float v0 = merged(wave * GROUP + lane), v1 = merged(wave * GROUP + 64 + lane);
+    a8_group(v0, v1, lane, out_bits, S.xq_att + ((size_t)row * Ga + wave) * GROUP, S.sx_att + (size_t)row * Ga + wave);
 }
 
 hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, int out_bits,
