@@ -1971,12 +1971,13 @@ hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int 
 // position's keys form a single chunk (key_chunks gives one chunk below
 // 64 k keys; the arithmetic of k_units, k_attend and k_attn_out for one
 // row).  Block g owns the heads of A8 group g (GROUP / vd heads sharing one
-// kv head), 256 threads per head; the keys' int8 rows, scales and values
-// are staged in LDS up front.  The waves of the heads' query units and of
-// the kv head's new key and value compute them first (the same values in
-// every block of the kv group; its first block appends them to the cache
-// and the history ring).  With no cross-block data the group's A8 runs in
-// the block.  One more block computes the row's post gates.
+// kv head): 16 wavefronts, the attention on 256 threads per head.  The
+// waves of the heads' query units and of the kv head's new key and value
+// compute them first (the same values in every block of the kv group; its
+// first block appends them to the cache and the history ring) while the
+// other waves stage the keys' int8 rows, scales and values in LDS.  With no
+// cross-block data the group's A8 runs in the block.  One more block
+// computes the row's post gates.
 constexpr int DG_HEAD_T = 256;
 constexpr int DG_THREADS = 1024;  // 16 wavefronts: the attention's HP * 256 threads, the rest stage keys
 
