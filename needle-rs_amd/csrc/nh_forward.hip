@@ -1646,58 +1646,74 @@ constexpr int AG_COLS = 320;  // value / digit columns: 3 alignment + 256 keys, 
 constexpr int AG_KPL = ATT_CHUNK_MAX / 64;  // keys per lane in the head steps
 constexpr int AG_TP = ATT_CHUNK_MAX / 8 + 4;  // a lane class's exps (16-byte rows, room for the trailing 4-block)
 
-__global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerDev L, int layer, int p0, int rows) {
+// RP rows per workgroup (RP = 2: two consecutive rows whose keys, chunks
+// and window agree, which the launch checks for the whole feed): the
+// chunk is staged once by all RP * 512 threads, then row rr's 8 wavefronts
+// (threads rr * 512 ...) run its scores, head steps and P.V; a feed with an
+// odd count of rows leaves the last workgroup's second row empty.
+template <int RP>
+__global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP == 2 ? 8 : 1))) void k_attend_group(
+    Dims D, SessDev S, LayerDev L, int layer, int p0, int rows) {
+    constexpr int NTT = AG_T * RP;
     // the longest rows first
-    const int row = rows - 1 - (int)blockIdx.x / D.nkv, kvh = blockIdx.x % D.nkv, ci = blockIdx.y, t = threadIdx.x;
-    const int wave = t >> 6, lane = t & 63, pos = p0 + row;
+    const int tb = threadIdx.x, rr = tb / AG_T, t = tb % AG_T;
+    const int rowA = rows - 1 - RP * ((int)blockIdx.x / D.nkv), kvh = blockIdx.x % D.nkv, ci = blockIdx.y;
+    const int row = rowA - rr;
+    const bool live = RP == 1 || row >= 0;  // (wave-uniform)
+    const int wave = t >> 6, lane = t & 63, posA = p0 + rowA, pos = p0 + (live ? row : 0);
     const int nkv = D.nkv, qk = D.qk, vd = D.vd, hpg = D.nh / nkv;
-    const int lo = window_lo(L.window, pos), n = pos + 1 - lo;
+    // the staged range is row A's (the block's rows share lo and the chunking)
+    const int lo = window_lo(L.window, posA), nA = posA + 1 - lo, n = pos + 1 - lo;
     int count, chunk;
-    key_chunks(n, nkv, rows > 1, count, chunk);
+    key_chunks(nA, nkv, rows > 1, count, chunk);
     if (ci >= count) return;
-    const int c0 = ci * chunk, len = min(chunk, n - c0), blocked = len / 4 * 4, slot0 = lo + c0;
-    const int sh = slot0 & 3, base = slot0 - sh, cols = sh + len;
+    const int c0 = ci * chunk, lenA = min(chunk, nA - c0), slot0 = lo + c0;
+    const int len = live ? min(chunk, n - c0) : 0, blocked = len / 4 * 4;
+    const int sh = slot0 & 3, base = slot0 - sh, colsA = sh + lenA, cols = sh + len;
     __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][AG_COLS];
     __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
-    __shared__ alignas(16) int8_t q8[AG_WAVES][MAX_HEAD_DIM];
-    __shared__ float qsc[AG_WAVES];
+    __shared__ alignas(16) int8_t q8s[RP][AG_WAVES][MAX_HEAD_DIM];
+    __shared__ float qscs[RP][AG_WAVES];
     // The key rows are read by the score products only; the scores, digits
-    // and P.V sums then take their space (three blocks fit on a CU).
+    // and P.V sums then take their space (three one-row blocks or two
+    // two-row blocks fit on a CU).
     __shared__ union {
         alignas(16) int8_t ks8[ATT_CHUNK_MAX][ATT_KPITCH];
         struct {
-            alignas(16) float sc[AG_WAVES][8 * AG_TP];
-            alignas(16) int8_t dig[AG_WAVES][3][AG_COLS];
-            int32_t pv[3][AG_WAVES][MAX_HEAD_DIM];
+            alignas(16) float sc[RP][AG_WAVES][8 * AG_TP];
+            alignas(16) int8_t dig[RP][AG_WAVES][3][AG_COLS];
+            int32_t pv[RP][3][AG_WAVES][MAX_HEAD_DIM];
         };
     } lds;
     auto& ks8 = lds.ks8;
-    auto& sc = lds.sc;
-    auto& dig = lds.dig;
-    auto& pv = lds.pv;
+    auto& sc = lds.sc[rr];
+    auto& dig = lds.dig[rr];
+    auto& pv = lds.pv[rr];
+    auto& q8 = q8s[rr];
+    auto& qsc = qscs[rr];
     const size_t lc = (size_t)layer * D.cap;
     const int hw = min(wave, hpg - 1), hh = kvh * hpg + hw;
     // every load first (unconditional, at clamped in-range addresses)
-    const float qv = S.qbuf[((size_t)row * D.nh + hh) * qk + min(lane, qk - 1)];
-    constexpr int KR = ATT_CHUNK_MAX * 4 / AG_T, VR = (MAX_HEAD_DIM * ATT_VDW + AG_T - 1) / AG_T;
-    const int rq = qk / 16, vdw = (cols + 3) / 4;
+    const float qv = S.qbuf[((size_t)(live ? row : 0) * D.nh + hh) * qk + min(lane, qk - 1)];
+    constexpr int KR = ATT_CHUNK_MAX * 4 / NTT, VR = (MAX_HEAD_DIM * ATT_VDW + NTT - 1) / NTT;
+    const int rq = qk / 16, vdw = (colsA + 3) / 4;
     uint4 kr[KR];
     uint32_t vw[VR];
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
-        const int e = t + r * AG_T, i = min(e >> 2, len - 1), c = min(e & 3, rq - 1);
+        const int e = tb + r * NTT, i = min(e >> 2, lenA - 1), c = min(e & 3, rq - 1);
         kr[r] = reinterpret_cast<const uint4*>(S.k8 + ((lc + slot0 + i) * nkv + kvh) * qk)[c];
     }
     float ksr, vsr;
     {
-        const int i = min(t, len - 1);
+        const int i = min(tb, lenA - 1);
         ksr = S.ks[(lc + slot0 + i) * nkv + kvh];
         vsr = S.vs[(lc + slot0 + i) * nkv + kvh];
     }
     const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
 #pragma unroll
     for (int r = 0; r < VR; ++r) {
-        const int e = t + r * AG_T, dm = min(e / ATT_VDW, vd - 1), k = min(e % ATT_VDW, vdw - 1);
+        const int e = tb + r * NTT, dm = min(e / ATT_VDW, vd - 1), k = min(e % ATT_VDW, vdw - 1);
         vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
     }
     // the int8 query of this wavefront's head, zero past qk (the key rows'
@@ -1707,23 +1723,23 @@ __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerD
     if (lane == 0) qsc[wave] = s * bits_f32(0x3e13cd3au);
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
-        const int e = t + r * AG_T, i = e >> 2, c = e & 3;
-        if (i < len && c < rq) reinterpret_cast<uint4*>(ks8[i])[c] = kr[r];
+        const int e = tb + r * NTT, i = e >> 2, c = e & 3;
+        if (i < lenA && c < rq) reinterpret_cast<uint4*>(ks8[i])[c] = kr[r];
     }
-    if (t < len) {
-        kss[t] = ksr;
-        vss[t] = vsr;
+    if (tb < lenA) {
+        kss[tb] = ksr;
+        vss[tb] = vsr;
     }
 #pragma unroll
     for (int r = 0; r < VR; ++r) {
-        const int e = t + r * AG_T, dm = e / ATT_VDW, k = e % ATT_VDW;
+        const int e = tb + r * NTT, dm = e / ATT_VDW, k = e % ATT_VDW;
         if (dm < vd && k < vdw) {
-            if (4 * k + 3 < cols) {
+            if (4 * k + 3 < colsA) {
                 reinterpret_cast<uint32_t*>(vs8[dm])[k] = vw[r];
             } else {
 #pragma unroll
                 for (int b = 0; b < 4; ++b)
-                    if (4 * k + b < cols) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
+                    if (4 * k + b < colsA) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
             }
         }
     }
@@ -1761,7 +1777,7 @@ __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerD
     }
     __syncthreads();
     float mx = -__builtin_inff(), sum = 0.0f, cw = 0.0f;
-    if (wave < hpg) {
+    if (live && wave < hpg) {
         // key i = lane + 64 j of the head in register e[j]: score, exp, weight
         float* scw = sc[wave];
         float e[AG_KPL];
@@ -1852,7 +1868,7 @@ __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerD
     __syncthreads();
     // P.V: row tile rt (rows plane * 8 + head) x value-dimension tile dt per
     // job, 64 columns per step
-    {
+    if (live) {
         const int ndt = (vd + 15) / 16, nsteps = (cols + 63) / 64;
         for (int job = wave; job < 2 * ndt; job += AG_WAVES) {
             const int rt = job / ndt, dt = job % ndt;
@@ -1872,7 +1888,7 @@ __global__ __launch_bounds__(AG_T) void k_attend_group(Dims D, SessDev S, LayerD
         }
     }
     __syncthreads();
-    if (wave < hpg) {
+    if (live && wave < hpg) {
         const size_t pi = ((size_t)row * D.nh + hh) * D.max_chunks + ci;
         if (lane < vd) {
             const int a = pv[0][wave][lane], b = pv[1][wave][lane], c = pv[2][wave][lane];
@@ -1899,7 +1915,21 @@ hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int la
             key_chunks(n, D.nkv, t > 1, count, chunk);
             most = count > most ? count : most;
         }
-        hipLaunchKernelGGL(k_attend_group, dim3(t * D.nkv, most), dim3(AG_T), 0, s, D, S, L, layer, p0, t);
+        // consecutive rows whose window start and chunking agree share a
+        // workgroup (every pair of the feed, else none)
+        bool pairs = t > 1;
+        for (int i = t - 1; i > 0 && pairs; i -= 2) {
+            const int pa = p0 + i, pb = pa - 1, la = window_lo(L.window, pa), lb = window_lo(L.window, pb);
+            int ca, sa, cb, sb;
+            key_chunks(pa + 1 - la, D.nkv, true, ca, sa);
+            key_chunks(pb + 1 - lb, D.nkv, true, cb, sb);
+            pairs = la == lb && ca == cb && sa == sb;
+        }
+        if (pairs)
+            hipLaunchKernelGGL(k_attend_group<2>, dim3((t + 1) / 2 * D.nkv, most), dim3(2 * AG_T), 0, s, D, S, L,
+                               layer, p0, t);
+        else
+            hipLaunchKernelGGL(k_attend_group<1>, dim3(t * D.nkv, most), dim3(AG_T), 0, s, D, S, L, layer, p0, t);
     }
     else
         hipLaunchKernelGGL(k_attend<false>, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer,
