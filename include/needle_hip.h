@@ -244,10 +244,13 @@ int nh_session_rollback(nh_session* s, int n);
 int nh_session_rewind_zeroed(nh_session* s, int len);
 /* No reference counterpart (a test hook): the polls a bounded in-kernel
  * wait makes before it gives up (default 1 << 20, about 30 ms).  A wait
- * that gives up lets its kernel end and marks the session; the next call
- * that synchronizes (nh_forward*, nh_prefill, nh_generate_greedy) returns
- * NH_EDEVICE and resets the session.  0 makes every such wait give up at
- * once, for tests of that path. */
+ * that gives up lets its kernel end and marks the session.  Each feed ends
+ * by queueing a copy of that mark to pinned host memory; the first
+ * nh_forward*, nh_prefill or nh_generate_greedy call made after the stream
+ * has passed the copy (any call after a synchronization, and
+ * nh_generate_greedy itself, which waits for its own) returns NH_EDEVICE
+ * and resets the session.  No call waits for earlier work to check it.
+ * 0 makes every such wait give up at once, for tests of that path. */
 int nh_session_debug_spin_limit(nh_session* s, int limit);
 /* NatState::last_hidden (infer.rs:1014-1016) into DEVICE h[d_model]. */
 int nh_session_last_hidden(const nh_session* s, float* h, void* stream);

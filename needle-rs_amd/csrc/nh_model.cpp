@@ -144,8 +144,15 @@ struct nh_session {
     std::vector<uint32_t> toks;
     nh_qact a_in{}, a_att{};
     std::vector<nh_qact> a_eng;
+    // The status word as the stream last copied it (pinned), behind
+    // ev_status; pending while that copy has not been read.
+    int32_t* h_status = nullptr;
+    hipEvent_t ev_status = nullptr;
+    bool status_pending = false;
 
     ~nh_session() {
+        if (ev_status) (void)hipEventDestroy(ev_status);
+        if (h_status) (void)hipHostFree(h_status);
         if (d_buf) (void)hipFree(d_buf);
     }
 };
@@ -606,14 +613,21 @@ int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
     return rows;
 }
 
-// The session's status word (bounded in-kernel waits that gave up, as far
-// as the stream has run): synchronizes the stream; an error when set (the
-// word is cleared and the session reset, its caches being unreliable).
-int check_status(nh_session* s, hipStream_t st) {
-    int32_t status = 0;
-    NH_TRY(hipMemcpyAsync(&status, s->S.status, 4, hipMemcpyDeviceToHost, st), "status");
-    NH_TRY(hipStreamSynchronize(st), "status");
-    if (status == 0) return NH_OK;
+// The session's status word (bounded in-kernel waits that gave up).  A call
+// that feeds ends by queueing a copy of the word to pinned host memory and
+// an event behind it (post_status); the next call reads that copy if the
+// event has completed (wait: waits for it) and otherwise leaves the check
+// to a later call, so a feed never waits for the previous one's work.  A
+// failure is reported by the first call made after the stream has passed
+// the copy (any call after a synchronization).  An error when set (the word
+// is cleared and the session reset, its caches being unreliable).
+int check_status(nh_session* s, hipStream_t st, bool wait) {
+    if (!s->status_pending) return NH_OK;
+    const hipError_t q = wait ? hipEventSynchronize(s->ev_status) : hipEventQuery(s->ev_status);
+    if (q == hipErrorNotReady) return NH_OK;
+    NH_TRY(q, "status");
+    s->status_pending = false;
+    if (*s->h_status == 0) return NH_OK;
     const int32_t zero = 0;
     NH_TRY(hipMemcpyAsync(s->S.status, &zero, 4, hipMemcpyHostToDevice, st), "status");
     NH_TRY(hipStreamSynchronize(st), "status");
@@ -621,12 +635,19 @@ int check_status(nh_session* s, hipStream_t st) {
     return fail(NH_EDEVICE, "a bounded wait in the layer kernel gave up (the session was reset)");
 }
 
+int post_status(nh_session* s, hipStream_t st) {
+    NH_TRY(hipMemcpyAsync(s->h_status, s->S.status, 4, hipMemcpyDeviceToHost, st), "status");
+    NH_TRY(hipEventRecord(s->ev_status, st), "status");
+    s->status_pending = true;
+    return NH_OK;
+}
+
 // Model::forward_native (infer.rs:1105-1132) over host token ids: chunks of
 // 32, a one-token chunk as a step, LastLogits / LastHidden from the last
 // chunk only.  Returns the rows written.
 int forward_ids(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, hipStream_t st) {
+    if (int rc = check_status(s, st, false)) return rc;
     NH_TRY(hipMemcpyAsync(s->S.tokens + s->len, toks, (size_t)n * 4, hipMemcpyHostToDevice, st), "tokens");
-    if (int rc = check_status(s, st)) return rc;
     s->toks.resize(s->len);
     s->toks.insert(s->toks.end(), toks, toks + n);
     const int width = out_width(s, outputs);
@@ -652,6 +673,7 @@ int forward_ids(nh_session* s, const uint32_t* toks, int n, int outputs, float* 
         rows += r;
         i += t;
     }
+    if (int rc = post_status(s, st)) return rc;
     return rows;
 }
 
@@ -753,6 +775,8 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     const size_t o_am = Y.take(16), o_st = Y.take(16), o_fl = Y.take(R);
     hipError_t e = hipMalloc(&s->d_buf, Y.size);
     if (e == hipSuccess) e = hipMemset(s->d_buf, 0, Y.size);
+    if (e == hipSuccess) e = hipHostMalloc((void**)&s->h_status, sizeof(int32_t), hipHostMallocDefault);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&s->ev_status, hipEventDisableTiming);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         delete s;
@@ -989,8 +1013,9 @@ int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, v
                "logits");
     if (steps > 0)
         NH_TRY(hipMemcpyAsync(out, s->S.tokens + len0, (size_t)steps * 4, hipMemcpyDeviceToHost, st), "tokens");
-    // (the picks are read on the host once the stream has synchronized)
-    if (int rc = check_status(s, st)) return rc;
+    // (the picks are read on the host once the stream has passed the status copy)
+    if (int rc = post_status(s, st)) return rc;
+    if (int rc = check_status(s, st, true)) return rc;
     if (steps > 0) {
         s->toks.resize(len0);
         s->toks.insert(s->toks.end(), out, out + steps);

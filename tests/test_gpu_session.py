@@ -231,8 +231,9 @@ def test_bounded_wait_gives_up_and_reports(nh):
     s = m.session(32)
     s.debug_spin_limit(0)  # every mixer wait gives up at once; the kernels still end
     s.forward([1, 2])  # layers 1 and 2 (and the head's input) run the wait
+    torch.cuda.synchronize()  # the stream has passed the feed's status copy
     with pytest.raises(nh.NeedleHipError, match="gave up"):
-        s.forward([3])  # reported at the next synchronization
+        s.forward([3])  # reported by the first call after that
     assert len(s) == 0  # reset
     s.debug_spin_limit(1 << 20)
     got = s.forward([5, 6, 7]).cpu().numpy()
