@@ -2043,6 +2043,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
     __shared__ float red[HP][DG_HEAD_T / 64];
     __shared__ float s_qs[HP], s_sum[HP];
     __shared__ float att[HP * MAX_HEAD_DIM];
+    __shared__ float gden[HP * MAX_HEAD_DIM];  // exp(-gate) + 1 of output hh0 * vd + j
     const size_t lc = (size_t)layer * D.cap;
     // Waves 0 .. HP-1 load the query units' inputs, the next two those of
     // the new key and value, and the rest (the staging waves) the keys
@@ -2091,14 +2092,16 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
             vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
         }
     }
-    // the head gate of this thread's P.V output (head h, dimension u / 4)
-    const float gate = S.proj[D.W + (hh0 + min(h, HP - 1)) * vd + min(u >> 2, vd - 1)];
+    // the head gates of the group's HP * vd = GROUP outputs, one per thread
+    // of the query waves, whose units finish well before the staging
+    const float gate = S.proj[D.W + hh0 * vd + min(t, HP * vd - 1)];
     // the units
     if (wave < HP) {
         const float v = unit_finish<TAPS, EXACT>(D, S, layer, p0, (hh0 + wave) * qk, qk, ui, true, lane, true);
         const float s = wave_quant_scale(lane < qk ? v : 0.0f);
         if (lane < qk) q8[wave][lane] = quant_one(v, 1.0f / s);
         if (lane == 0) s_qs[wave] = s * bits_f32(0x3e13cd3au);
+        if (t < HP * vd) gden[t] = nexp(-gate) + 1.0f;
     } else if (wave == HP) {
         const float v = unit_finish<TAPS, EXACT>(D, S, layer, p0, qd + kvh * qk, qk, ui, true, lane, owner);
         const float s = wave_quant_scale(lane < qk ? v : 0.0f);
@@ -2163,16 +2166,18 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
 #pragma unroll
         for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) qv[c] = reinterpret_cast<const uint4*>(q8[h])[c];
         for (int i = u; i < n; i += DG_HEAD_T) {
-            int dot = 0;
+            // (four partial integer sums: exact in any order)
+            int dp[4] = {0, 0, 0, 0};
 #pragma unroll
             for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
                 if (c < rq) {
                     const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
-                    dot = __builtin_amdgcn_sdot4((int)kv.x, (int)qv[c].x, dot, false);
-                    dot = __builtin_amdgcn_sdot4((int)kv.y, (int)qv[c].y, dot, false);
-                    dot = __builtin_amdgcn_sdot4((int)kv.z, (int)qv[c].z, dot, false);
-                    dot = __builtin_amdgcn_sdot4((int)kv.w, (int)qv[c].w, dot, false);
+                    dp[0] = __builtin_amdgcn_sdot4((int)kv.x, (int)qv[c].x, dp[0], false);
+                    dp[1] = __builtin_amdgcn_sdot4((int)kv.y, (int)qv[c].y, dp[1], false);
+                    dp[2] = __builtin_amdgcn_sdot4((int)kv.z, (int)qv[c].z, dp[2], false);
+                    dp[3] = __builtin_amdgcn_sdot4((int)kv.w, (int)qv[c].w, dp[3], false);
                 }
+            const int dot = (dp[0] + dp[1]) + (dp[2] + dp[3]);
             const float ksc = kss[i];
             const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
             sc[h][i] = sv;
@@ -2226,7 +2231,9 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
         if (lane == 0) s_sum[h] = sum;
     }
     __syncthreads();
+    float inv_sum = 0.0f;
     if (attends) {
+        inv_sum = 1.0f / s_sum[h];  // (its latency overlaps the weights)
         for (int i = u; i < n; i += DG_HEAD_T) {
             const float w = sc[h][i] * vss[i];
             sc[h][i] = w;
@@ -2292,9 +2299,8 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
         c = quad_sum_i32(c);
         if (dm < vd && part == 0) {
             const float po = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
-            const float inv = 1.0f / s_sum[h];
-            const float out = po * inv;
-            att[h * vd + dm] = out / (nexp(-gate) + 1.0f);
+            const float out = po * inv_sum;
+            att[h * vd + dm] = out / gden[h * vd + dm];
         }
     }
     __syncthreads();
