@@ -52,6 +52,14 @@ __device__ __forceinline__ float lane_xor(float v, int h, int lane) {
     }
 }
 
+// A raw buffer resource over `bytes` bytes at p (gfx9 descriptor word 3):
+// loads through it take a scalar base and 32-bit lane offsets (no 64-bit
+// address arithmetic per lane), and read zero past the range.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, size_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)(bytes < 0xffffffffu ? bytes : 0xffffffffu),
+                                             0x00020000);
+}
+
 // A streamed 16-byte load (read once, non-temporal hint).
 __device__ __forceinline__ uint4 load_stream(const uint4* p) {
     u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));

@@ -1655,18 +1655,39 @@ template <int RP>
 __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP == 2 ? 8 : 1))) void k_attend_group(
     Dims D, SessDev S, LayerDev L, int layer, int p0, int rows) {
     constexpr int NTT = AG_T * RP;
-    // the longest rows first
     const int tb = threadIdx.x, rr = tb / AG_T, t = tb % AG_T;
-    const int rowA = rows - 1 - RP * ((int)blockIdx.x / D.nkv), kvh = blockIdx.x % D.nkv, ci = blockIdx.y;
+    // The block's parameters (three divisions by runtime values) are worked
+    // out once, by wavefront 0, and handed over through LDS: ~200 scalar
+    // instructions per wavefront would otherwise queue on the CU's scalar
+    // unit for every resident wavefront before any load is issued.  The
+    // longest rows first; the staged range is row A's (the block's rows
+    // share lo and the chunking).
+    __shared__ int prm[6];
+    if (tb < 64) {
+        const int pr = (int)blockIdx.x / D.nkv, rA = rows - 1 - RP * pr, pA = p0 + rA;
+        const int l0 = window_lo(L.window, pA);
+        int cnt, chk;
+        key_chunks(pA + 1 - l0, D.nkv, rows > 1, cnt, chk);
+        if (tb == 0) {
+            prm[0] = rA;
+            prm[1] = (int)blockIdx.x - pr * D.nkv;
+            prm[2] = l0;
+            prm[3] = cnt;
+            prm[4] = chk;
+            prm[5] = D.nh / D.nkv;
+        }
+    }
+    __syncthreads();
+    const int rowA = __builtin_amdgcn_readfirstlane(prm[0]), kvh = __builtin_amdgcn_readfirstlane(prm[1]);
+    const int lo = __builtin_amdgcn_readfirstlane(prm[2]), count = __builtin_amdgcn_readfirstlane(prm[3]);
+    const int chunk = __builtin_amdgcn_readfirstlane(prm[4]), hpg = __builtin_amdgcn_readfirstlane(prm[5]);
+    const int ci = blockIdx.y;
+    if (ci >= count) return;
     const int row = rowA - rr;
     const bool live = RP == 1 || row >= 0;  // (wave-uniform)
     const int wave = t >> 6, lane = t & 63, posA = p0 + rowA, pos = p0 + (live ? row : 0);
-    const int nkv = D.nkv, qk = D.qk, vd = D.vd, hpg = D.nh / nkv;
-    // the staged range is row A's (the block's rows share lo and the chunking)
-    const int lo = window_lo(L.window, posA), nA = posA + 1 - lo, n = pos + 1 - lo;
-    int count, chunk;
-    key_chunks(nA, nkv, rows > 1, count, chunk);
-    if (ci >= count) return;
+    const int nkv = D.nkv, qk = D.qk, vd = D.vd;
+    const int nA = posA + 1 - lo, n = pos + 1 - lo;
     const int c0 = ci * chunk, lenA = min(chunk, nA - c0), slot0 = lo + c0;
     const int len = live ? min(chunk, n - c0) : 0, blocked = len / 4 * 4;
     const int sh = slot0 & 3, base = slot0 - sh, colsA = sh + lenA, cols = sh + len;
@@ -1697,24 +1718,31 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
     const float qv = S.qbuf[((size_t)(live ? row : 0) * D.nh + hh) * qk + min(lane, qk - 1)];
     constexpr int KR = ATT_CHUNK_MAX * 4 / NTT, VR = (MAX_HEAD_DIM * ATT_VDW + NTT - 1) / NTT;
     const int rq = qk / 16, vdw = (colsA + 3) / 4;
-    uint4 kr[KR];
+    // buffer resources over the chunk's key rows (this kv head's, from
+    // slot0), their scales and the value columns (from base)
+    const int kstride = nkv * qk;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(S.k8 + (lc + slot0) * kstride + kvh * qk, (size_t)lenA * kstride);
+    const __amdgpu_buffer_rsrc_t rks = make_rsrc(S.ks + (lc + slot0) * nkv + kvh, (size_t)lenA * nkv * 4);
+    const __amdgpu_buffer_rsrc_t rvs = make_rsrc(S.vs + (lc + slot0) * nkv + kvh, (size_t)lenA * nkv * 4);
+    const __amdgpu_buffer_rsrc_t rv =
+        make_rsrc(S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base, (size_t)vd * D.vcap);
+    u32x4 kr[KR];
     uint32_t vw[VR];
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
         const int e = tb + r * NTT, i = min(e >> 2, lenA - 1), c = min(e & 3, rq - 1);
-        kr[r] = reinterpret_cast<const uint4*>(S.k8 + ((lc + slot0 + i) * nkv + kvh) * qk)[c];
+        kr[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, __mul24(i, kstride) + c * 16, 0, 0));
     }
     float ksr, vsr;
     {
         const int i = min(tb, lenA - 1);
-        ksr = S.ks[(lc + slot0 + i) * nkv + kvh];
-        vsr = S.vs[(lc + slot0 + i) * nkv + kvh];
+        ksr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rks, __mul24(i, nkv) * 4, 0, 0));
+        vsr = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rvs, __mul24(i, nkv) * 4, 0, 0));
     }
-    const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
 #pragma unroll
     for (int r = 0; r < VR; ++r) {
         const int e = tb + r * NTT, dm = min(e / ATT_VDW, vd - 1), k = min(e % ATT_VDW, vdw - 1);
-        vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
+        vw[r] = __builtin_amdgcn_raw_buffer_load_b32(rv, __mul24(dm, D.vcap) + k * 4, 0, 0);
     }
     // the int8 query of this wavefront's head, zero past qk (the key rows'
     // bytes there are not staged)
@@ -1724,7 +1752,7 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
         const int e = tb + r * NTT, i = e >> 2, c = e & 3;
-        if (i < lenA && c < rq) reinterpret_cast<uint4*>(ks8[i])[c] = kr[r];
+        if (i < lenA && c < rq) reinterpret_cast<u32x4*>(ks8[i])[c] = kr[r];
     }
     if (tb < lenA) {
         kss[tb] = ksr;

@@ -86,12 +86,6 @@ __host__ __device__ constexpr int gemm_act_bytes() {
     return BM * GC * 128;
 }
 
-// A raw buffer resource over `bytes` bytes at p (gfx9 descriptor word 3).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, size_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, (int)(bytes < 0xffffffffu ? bytes : 0xffffffffu),
-                                             0x00020000);
-}
-
 // One group's A fragments as held in registers: the int8 fragments
 // themselves (halves 0 and 1), or (W4) the 4-bit code pieces they expand
 // from, expanded right before use.
