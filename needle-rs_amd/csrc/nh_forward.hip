@@ -1646,11 +1646,12 @@ constexpr int AG_COLS = 320;  // value / digit columns: 3 alignment + 256 keys, 
 constexpr int AG_KPL = ATT_CHUNK_MAX / 64;  // keys per lane in the head steps
 constexpr int AG_TP = ATT_CHUNK_MAX / 8 + 4;  // a lane class's exps (16-byte rows, room for the trailing 4-block)
 
-// RP rows per workgroup (RP = 2: two consecutive rows whose keys, chunks
-// and window agree, which the launch checks for the whole feed): the
+// RP rows per workgroup (RP = 2: two consecutive rows whose window start
+// and chunk ranges agree, which the launch checks for the whole feed): the
 // chunk is staged once by all RP * 512 threads, then row rr's 8 wavefronts
-// (threads rr * 512 ...) run its scores, head steps and P.V; a feed with an
-// odd count of rows leaves the last workgroup's second row empty.
+// (threads rr * 512 ...) run its scores, head steps and P.V over its own
+// keys, a prefix of the staged ones; a feed with an odd count of rows
+// leaves the last workgroup's second row empty.
 template <int RP>
 __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP == 2 ? 8 : 1))) void k_attend_group(
     Dims D, SessDev S, LayerDev L, int layer, int p0, int rows) {
@@ -1944,14 +1945,15 @@ hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int la
             most = count > most ? count : most;
         }
         // consecutive rows whose window start and chunking agree share a
-        // workgroup (every pair of the feed, else none)
+        // workgroup (every pair of the feed, else none); rows of one chunk
+        // each agree whatever its length (the chunk is all their keys)
         bool pairs = t > 1;
         for (int i = t - 1; i > 0 && pairs; i -= 2) {
             const int pa = p0 + i, pb = pa - 1, la = window_lo(L.window, pa), lb = window_lo(L.window, pb);
             int ca, sa, cb, sb;
             key_chunks(pa + 1 - la, D.nkv, true, ca, sa);
             key_chunks(pb + 1 - lb, D.nkv, true, cb, sb);
-            pairs = la == lb && ca == cb && sa == sb;
+            pairs = la == lb && ca == cb && (ca == 1 || sa == sb);
         }
         if (pairs)
             hipLaunchKernelGGL(k_attend_group<2>, dim3((t + 1) / 2 * D.nkv, most), dim3(2 * AG_T), 0, s, D, S, L,
