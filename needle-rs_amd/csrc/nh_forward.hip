@@ -1656,7 +1656,9 @@ template <int RP>
 __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP == 2 ? 8 : 1))) void k_attend_group(
     Dims D, SessDev S, LayerDev L, int layer, int p0, int rows) {
     constexpr int NTT = AG_T * RP;
-    const int tb = threadIdx.x, rr = tb / AG_T, t = tb % AG_T;
+    // (the row half and the wavefront are wave-uniform: in scalar registers,
+    // so the lengths and bounds derived from them are too)
+    const int tb = threadIdx.x, rr = __builtin_amdgcn_readfirstlane(tb / AG_T), t = tb % AG_T;
     // The block's parameters (three divisions by runtime values) are worked
     // out once, by wavefront 0, and handed over through LDS: ~200 scalar
     // instructions per wavefront would otherwise queue on the CU's scalar
@@ -1686,7 +1688,8 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
     if (ci >= count) return;
     const int row = rowA - rr;
     const bool live = RP == 1 || row >= 0;  // (wave-uniform)
-    const int wave = t >> 6, lane = t & 63, posA = p0 + rowA, pos = p0 + (live ? row : 0);
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63, posA = p0 + rowA,
+              pos = p0 + (live ? row : 0);
     const int nkv = D.nkv, qk = D.qk, vd = D.vd;
     const int nA = posA + 1 - lo, n = pos + 1 - lo;
     const int c0 = ci * chunk, lenA = min(chunk, nA - c0), slot0 = lo + c0;
@@ -1837,18 +1840,23 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
             float acc = 0.0f;
             const int nb8 = len / 8;
             if (lane < 8) {
+                // the class's first nb8 exps in order, four per 16-byte read
+                // (nb8 is wave-uniform: scalar loop bounds, no selects)
                 const float4* tr = reinterpret_cast<const float4*>(scw + lane * AG_TP);
-                float v[ATT_CHUNK_MAX / 8];
-#pragma unroll
-                for (int q = 0; q < ATT_CHUNK_MAX / 32; ++q) {
-                    const float4 x = tr[q];
-                    v[4 * q] = x.x;
-                    v[4 * q + 1] = x.y;
-                    v[4 * q + 2] = x.z;
-                    v[4 * q + 3] = x.w;
+                int b = 0;
+                for (; b + 4 <= nb8; b += 4) {
+                    const float4 x = tr[b >> 2];
+                    acc += x.x;
+                    acc += x.y;
+                    acc += x.z;
+                    acc += x.w;
                 }
-#pragma unroll
-                for (int b = 0; b < ATT_CHUNK_MAX / 8; ++b) acc = b < nb8 ? acc + v[b] : acc;
+                if (b < nb8) {
+                    const float4 x = tr[b >> 2];
+                    acc += x.x;
+                    if (b + 1 < nb8) acc += x.y;
+                    if (b + 2 < nb8) acc += x.z;
+                }
                 if (lane < 4 && len - nb8 * 8 >= 4) acc += scw[lane * AG_TP + nb8];
             }
             const float tk = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
