@@ -1642,7 +1642,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // the eight lane-class chains), the weights and the 21-bit digits.
 constexpr int AG_WAVES = 8;   // query heads per kv head this kernel takes
 constexpr int AG_T = AG_WAVES * 64;
-constexpr int AG_COLS = 320;  // value / digit columns: 3 alignment + 256 keys, in whole 64-column steps
+constexpr int AG_COLS = 320;  // value / digit columns: 15 alignment + 256 keys, in whole 64-column steps
 constexpr int AG_KPL = ATT_CHUNK_MAX / 64;  // keys per lane in the head steps
 constexpr int AG_TP = ATT_CHUNK_MAX / 8 + 4;  // a lane class's exps (16-byte rows, room for the trailing 4-block)
 
@@ -1694,7 +1694,9 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
     const int nA = posA + 1 - lo, n = pos + 1 - lo;
     const int c0 = ci * chunk, lenA = min(chunk, nA - c0), slot0 = lo + c0;
     const int len = live ? min(chunk, n - c0) : 0, blocked = len / 4 * 4;
-    const int sh = slot0 & 3, base = slot0 - sh, colsA = sh + lenA, cols = sh + len;
+    // value columns and digits from slot base = slot0 rounded down to 16
+    // bytes (column j = key + sh)
+    const int sh = slot0 & 15, base = slot0 - sh, colsA = sh + lenA, cols = sh + len;
     __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][AG_COLS];
     __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
     __shared__ alignas(16) int8_t q8s[RP][AG_WAVES][MAX_HEAD_DIM];
@@ -1720,8 +1722,9 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
     const int hw = min(wave, hpg - 1), hh = kvh * hpg + hw;
     // every load first (unconditional, at clamped in-range addresses)
     const float qv = S.qbuf[((size_t)(live ? row : 0) * D.nh + hh) * qk + min(lane, qk - 1)];
-    constexpr int KR = ATT_CHUNK_MAX * 4 / NTT, VR = (MAX_HEAD_DIM * ATT_VDW + NTT - 1) / NTT;
-    const int rq = qk / 16, vdw = (colsA + 3) / 4;
+    constexpr int VQ = AG_COLS / 16;  // 16-byte value chunks per column
+    constexpr int KR = ATT_CHUNK_MAX * 4 / NTT, VR = (MAX_HEAD_DIM * VQ + NTT - 1) / NTT;
+    const int rq = qk / 16, vq = (colsA + 15) / 16;
     // buffer resources over the chunk's key rows (this kv head's, from
     // slot0), their scales and the value columns (from base)
     const int kstride = nkv * qk;
@@ -1730,8 +1733,7 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
     const __amdgpu_buffer_rsrc_t rvs = make_rsrc(S.vs + (lc + slot0) * nkv + kvh, (size_t)lenA * nkv * 4);
     const __amdgpu_buffer_rsrc_t rv =
         make_rsrc(S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base, (size_t)vd * D.vcap);
-    u32x4 kr[KR];
-    uint32_t vw[VR];
+    u32x4 kr[KR], vw[VR];
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
         const int e = tb + r * NTT, i = min(e >> 2, lenA - 1), c = min(e & 3, rq - 1);
@@ -1745,8 +1747,8 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
     }
 #pragma unroll
     for (int r = 0; r < VR; ++r) {
-        const int e = tb + r * NTT, dm = min(e / ATT_VDW, vd - 1), k = min(e % ATT_VDW, vdw - 1);
-        vw[r] = __builtin_amdgcn_raw_buffer_load_b32(rv, __mul24(dm, D.vcap) + k * 4, 0, 0);
+        const int e = tb + r * NTT, dm = min(e / VQ, vd - 1), k = min(e % VQ, vq - 1);
+        vw[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, __mul24(dm, D.vcap) + k * 16, 0, 0));
     }
     // the int8 query of this wavefront's head, zero past qk (the key rows'
     // bytes there are not staged)
@@ -1762,18 +1764,12 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
         kss[tb] = ksr;
         vss[tb] = vsr;
     }
+    // whole chunks: the bytes before column sh and past the keys meet zero
+    // digits in P.V
 #pragma unroll
     for (int r = 0; r < VR; ++r) {
-        const int e = tb + r * NTT, dm = e / ATT_VDW, k = e % ATT_VDW;
-        if (dm < vd && k < vdw) {
-            if (4 * k + 3 < colsA) {
-                reinterpret_cast<uint32_t*>(vs8[dm])[k] = vw[r];
-            } else {
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    if (4 * k + b < colsA) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
-            }
-        }
+        const int e = tb + r * NTT, dm = e / VQ, k = e % VQ;
+        if (dm < vd && k < vq) reinterpret_cast<u32x4*>(vs8[dm])[k] = vw[r];
     }
     __syncthreads();
     const int mr = lane & 15, mq = lane >> 4;  // MFMA lane: row / column mr, 16-byte k-block mq
