@@ -242,6 +242,35 @@ def test_prefill_full_needle3(nh):
     run_feed(nh, archive(g, seed=45), o.random_tokens(37, g.vocab, seed=13), 48, "needle3 prompt", then_steps=2)
 
 
+@pytest.mark.parametrize("window", [0, 24])
+def test_prefill_feeds_at_offsets(nh, window):
+    # Feeds of 37, 63, 2, 200 and 1 tokens in one session (positions 0, 37,
+    # 100, 102, 302): odd and even row counts, feeds that start mid-session,
+    # rows of one key chunk and of two (past 256 keys), and a one-token step.
+    # With every layer global the feed attention pairs consecutive rows in a
+    # workgroup where their chunks allow: the odd feeds leave the last
+    # workgroup's second row empty, and the 200-row feed pairs rows across
+    # the 256-key boundary ((258, 257) keys: two chunks of 144 each).  A
+    # window makes consecutive rows start at different keys, so those layers
+    # keep one row per workgroup.
+    say(f"feeds of 37, 63, 2, 200 and 1 tokens at positions 0 .. 302, window {window}")
+    g = cact.Geometry(vocab=300, num_layers=2, engram_slots=64, engram_sites=(1,),
+                      global_layers=(0, 1) if window == 0 else (0,), sliding_window=max(window, 8))
+    data = archive(g, seed=61 + window)
+    f = forward.Forward(data)
+    m = nh.Model.from_archive(data)
+    s, os_ = m.session(320), f.session(320)
+    toks = o.random_tokens(303, g.vocab, seed=62)
+    stats = {}
+    at = 0
+    for n in (37, 63, 2, 200, 1):
+        part = toks[at:at + n]
+        compare(f"feed of {n} at {at}", s.forward(part).cpu().numpy(), os_.feed(part), stats)
+        at += n
+    say(f"window {window}: {stats['exact']}/{stats['steps']} feeds bit-identical, max rel {stats['max_rel']:.3g}")
+    assert stats["exact"] == stats["steps"], stats
+
+
 @pytest.mark.parametrize("heads,kv,qk,vd", [(8, 2, 32, 48), (8, 1, 48, 32), (6, 3, 16, 20)])
 def test_head_geometries(nh, heads, kv, qk, vd):
     say(f"{heads} heads over {kv} kv heads, qk {qk}, vd {vd}: a 300-token prompt (rows past 256 keys attend in 2 "
