@@ -36,6 +36,18 @@ namespace nh {
 
 __device__ __forceinline__ int swz(int tok, int b) { return b ^ (tok & 7); }
 
+// The per-product operands of one launch; blockIdx.y picks the product
+// (the products of a launch share shape, code tables and token rows).
+constexpr int GEMM_BATCH_MAX = 8;
+struct GemmSrcs {
+    const uint4* w8[GEMM_BATCH_MAX];
+    const uint2* codes[GEMM_BATCH_MAX];
+    const uint16_t* norms[GEMM_BATCH_MAX];
+    const uint4* xq[GEMM_BATCH_MAX];
+    const float* sx[GEMM_BATCH_MAX];
+    float* y[GEMM_BATCH_MAX];
+};
+
 // The int8 A-fragment copy of a tiled code matrix: one wavefront per
 // (16-row tile, group).  Lane L = 16 q + r holds row r's k-block q of each
 // 64-wide half: the 8-byte code pieces of chunks l = q / 2 (half 0) and
@@ -100,10 +112,15 @@ struct AFrag<true> {
 
 template <int BM, int NW, int GC, bool GENERAL, bool DBG, bool W4>
 __global__ __launch_bounds__(64 * NW, DBG ? 1 : 2) void k_gemm(
-    const uint4* __restrict__ w8, const uint2* __restrict__ codes, Lut lut, const uint16_t* __restrict__ norms,
-    const uint4* __restrict__ xq, const float* __restrict__ sx, const uint8_t* __restrict__ block, int blocked,
-    float* __restrict__ y, int ldy, int col0, int vec_store, int32_t* __restrict__ dbg, int out, int out_alloc,
-    int cap_rows, int M, int G, float cbs, int panels, int items) {
+    GemmSrcs src, Lut lut, const uint8_t* __restrict__ block, int blocked, int ldy, int col0, int vec_store,
+    int32_t* __restrict__ dbg, int out, int out_alloc, int cap_rows, int M, int G, float cbs, int panels, int items) {
+    const int mb = blockIdx.y;
+    const uint4* __restrict__ w8 = src.w8[mb];
+    const uint2* __restrict__ codes = src.codes[mb];
+    const uint16_t* __restrict__ norms = src.norms[mb];
+    const uint4* __restrict__ xq = src.xq[mb];
+    const float* __restrict__ sx = src.sx[mb];
+    float* __restrict__ y = src.y[mb];
     constexpr int T = 64 * NW;
     constexpr int ROWS = 16 * NW;
     constexpr int TT = BM / 16;  // token tiles per wavefront
@@ -392,13 +409,20 @@ static int occupancy(K kern, int threads, size_t lds) {
     return n;
 }
 
+// n same-shaped products (w[i] x a[i] into y[i]) in one launch.
+struct GemmSet {
+    const nh_qmat* const* w;
+    const nh_qact* const* a;
+    float* const* y;
+    int n;
+};
+
 template <int BM, int NW, int GC, bool GENERAL, bool W4>
-static hipError_t run(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
-                      int32_t* dbg, hipStream_t s) {
+static hipError_t run(const GemmSet& g, const uint8_t* block, int ldy, int col0, int32_t* dbg, hipStream_t s) {
     constexpr int ROWS = 16 * NW;
-    const QMatMeta& m = w->m;
+    const QMatMeta& m = g.w[0]->m;
     const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
-    const int M = a->rows;
+    const int M = g.a[0]->rows;
     const int panels = (m.out_pad + ROWS - 1) / ROWS;
     const int ttiles = (M + BM - 1) / BM;
     const int items = panels * ttiles;
@@ -414,39 +438,50 @@ static hipError_t run(const nh_qmat* w, const nh_qact* a, const uint8_t* block, 
         if (e != hipSuccess) return e;
         per_cu = occupancy(k_gemm<BM, NW, GC, GENERAL, false, W4>, 64 * NW, lds);
     }
-    // Persistent grid: at most one resident wave of workgroups, each taking
-    // the same number of items.
+    // Persistent grid: at most one resident wave of workgroups over all the
+    // launch's products, each taking the same number of items.
     const int slots = device_cus() * per_cu;
-    const int rounds = (items + slots - 1) / slots;
+    const int rounds = (g.n * items + slots - 1) / slots;
     const int grid = (items + rounds - 1) / rounds;
-    const int vec = ((uintptr_t)y % 16 == 0 && ldy % 4 == 0 && col0 % 4 == 0) ? 1 : 0;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(64 * NW), lds, s, w->d_w8, (const uint2*)w->d_codes, lut, w->d_norms,
-                       (const uint4*)a->d_xq, a->d_sx, block, M / 4 * 4, y, ldy, col0, vec, dbg, m.out,
-                       (m.out + PANEL_ROWS - 1) / PANEL_ROWS * PANEL_ROWS, a->cap_rows, M, m.groups, m.cbs, panels,
-                       items);
+    GemmSrcs src{};
+    int vec = ldy % 4 == 0 && col0 % 4 == 0;
+    for (int i = 0; i < g.n; ++i) {
+        src.w8[i] = (const uint4*)g.w[i]->d_w8;
+        src.codes[i] = (const uint2*)g.w[i]->d_codes;
+        src.norms[i] = g.w[i]->d_norms;
+        src.xq[i] = (const uint4*)g.a[i]->d_xq;
+        src.sx[i] = g.a[i]->d_sx;
+        src.y[i] = g.y[i];
+        vec &= (uintptr_t)g.y[i] % 16 == 0;
+    }
+    hipLaunchKernelGGL(kern, dim3(grid, g.n), dim3(64 * NW), lds, s, src, lut, block, M / 4 * 4, ldy, col0, vec, dbg,
+                       m.out, (m.out + PANEL_ROWS - 1) / PANEL_ROWS * PANEL_ROWS, g.a[0]->cap_rows, M, m.groups,
+                       m.cbs, panels, items);
     return hipGetLastError();
 }
 
 // BM-token tiles on NW wavefronts with the largest chunk (3, 4, 2 or 1
 // groups) that divides G.
 template <int BM, int NW, bool W4>
-static hipError_t run_gc(bool general, const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy,
-                         int col0, int32_t* dbg, hipStream_t s) {
-    const int G = w->m.groups;
-#define NH_GEMM_GC(GCV)                                                                   \
-    if (G % GCV == 0)                                                                     \
-        return general ? run<BM, NW, GCV, true, W4>(w, a, block, y, ldy, col0, dbg, s) \
-                       : run<BM, NW, GCV, false, W4>(w, a, block, y, ldy, col0, dbg, s);
+static hipError_t run_gc(bool general, const GemmSet& g, const uint8_t* block, int ldy, int col0, int32_t* dbg,
+                         hipStream_t s) {
+    const int G = g.w[0]->m.groups;
+#define NH_GEMM_GC(GCV)                                                               \
+    if (G % GCV == 0)                                                                 \
+        return general ? run<BM, NW, GCV, true, W4>(g, block, ldy, col0, dbg, s) \
+                       : run<BM, NW, GCV, false, W4>(g, block, ldy, col0, dbg, s);
     NH_GEMM_GC(3)
     NH_GEMM_GC(4)
     NH_GEMM_GC(2)
 #undef NH_GEMM_GC
-    return general ? run<BM, NW, 1, true, W4>(w, a, block, y, ldy, col0, dbg, s)
-                   : run<BM, NW, 1, false, W4>(w, a, block, y, ldy, col0, dbg, s);
+    return general ? run<BM, NW, 1, true, W4>(g, block, ldy, col0, dbg, s)
+                   : run<BM, NW, 1, false, W4>(g, block, ldy, col0, dbg, s);
 }
 
-hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
-                       int32_t* dbg, hipStream_t s) {
+static hipError_t gemm_dispatch(const GemmSet& g, const uint8_t* block, int ldy, int col0, int32_t* dbg,
+                                hipStream_t s) {
+    const nh_qmat* w = g.w[0];
+    const nh_qact* a = g.a[0];
     // Tokens past rows / 4 * 4 (or flagged) take the remainder combine.
     const bool general = block != nullptr || a->rows % 4 != 0;
     // Activation buffers hold whole multiples of ACT_PAD token rows, so
@@ -462,13 +497,35 @@ hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block,
     // bound by the weight stream, so it reads the 4-bit codes (half the
     // bytes of the int8 copy) and expands them in the kernel.
     const int M = a->rows, cus = device_cus(), out_pad = w->m.out_pad;
-    auto items = [&](int rows, int bm) { return (long)((out_pad + rows - 1) / rows) * ((M + bm - 1) / bm); };
+    // (items over all the launch's products)
+    auto items = [&](int rows, int bm) { return (long)g.n * ((out_pad + rows - 1) / rows) * ((M + bm - 1) / bm); };
     if (M > 48 && items(64, 64) >= cus)
-        return general ? run<64, 4, 1, true, false>(w, a, block, y, ldy, col0, dbg, s)
-                       : run<64, 4, 1, false, false>(w, a, block, y, ldy, col0, dbg, s);
-    if (M > 16 && items(64, 32) >= cus) return run_gc<32, 4, false>(general, w, a, block, y, ldy, col0, dbg, s);
-    if (M <= 16 && w->m.bits == 4) return run_gc<16, 2, true>(general, w, a, block, y, ldy, col0, dbg, s);
-    return run_gc<16, 2, false>(general, w, a, block, y, ldy, col0, dbg, s);
+        return general ? run<64, 4, 1, true, false>(g, block, ldy, col0, dbg, s)
+                       : run<64, 4, 1, false, false>(g, block, ldy, col0, dbg, s);
+    if (M > 16 && items(64, 32) >= cus) return run_gc<32, 4, false>(general, g, block, ldy, col0, dbg, s);
+    if (M <= 16 && w->m.bits == 4) return run_gc<16, 2, true>(general, g, block, ldy, col0, dbg, s);
+    return run_gc<16, 2, false>(general, g, block, ldy, col0, dbg, s);
+}
+
+hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
+                       int32_t* dbg, hipStream_t s) {
+    const GemmSet g{&w, &a, &y, 1};
+    return gemm_dispatch(g, block, ldy, col0, dbg, s);
+}
+
+bool gemm_batchable(const nh_qmat* const* w, const nh_qact* const* a, int n) {
+    if (n < 1 || n > GEMM_BATCH_MAX || !gemv_batchable(w, n)) return false;
+    for (int i = 1; i < n; ++i)
+        if (w[i]->m.in_dim != w[0]->m.in_dim || a[i]->rows != a[0]->rows || a[i]->cap_rows != a[0]->cap_rows ||
+            a[i]->bits != a[0]->bits)
+            return false;
+    return true;
+}
+
+hipError_t launch_gemm_batch(const nh_qmat* const* w, const nh_qact* const* a, float* const* y, int n,
+                             const uint8_t* block, int ldy, hipStream_t s) {
+    const GemmSet g{w, a, y, n};
+    return gemm_dispatch(g, block, ldy, 0, nullptr, s);
 }
 
 }  // namespace nh

@@ -144,6 +144,11 @@ hipError_t launch_gemv(const nh_qmat* w, const nh_qact* a, float* y, int col0, i
 hipError_t launch_expand_w8(const nh_qmat* w, hipStream_t s);
 hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
                        int32_t* dbg_totals, hipStream_t s);
+// Same-shaped prefill products in one launch (blockIdx.y picks the product):
+// gemv_batchable matrices, activations of equal rows, width and capacity.
+bool gemm_batchable(const nh_qmat* const* w, const nh_qact* const* a, int n);
+hipError_t launch_gemm_batch(const nh_qmat* const* w, const nh_qact* const* a, float* const* y, int n,
+                             const uint8_t* block, int ldy, hipStream_t s);
 hipError_t launch_single_rows(const nh_qmat* w, const nh_qact* a, const uint32_t* ids, int n, float* out,
                               float* scatter_logits, int scatter_n, hipStream_t s);
 hipError_t launch_fill(float* p, float v, int n, hipStream_t s);

@@ -552,10 +552,21 @@ int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
         }
         NH_TRY(nh::launch_gemv_batch(m->ekv.data(), acts, ys, D.sites, st), "engram kv");
     } else {
-        for (int e = 0; e < D.sites; ++e)
-            NH_TRY(product(m->ekv[e], &s->a_eng[e], t, S.ekv + (size_t)e * nh::BATCH_ROWS * 2 * D.d, 2 * D.d, flags,
-                           st),
-                   "engram kv");
+        // several rows: every site's product in one GEMM launch when they
+        // share shape and tables, else one launch each
+        const nh_qact* acts[nh::MAX_SITES];
+        float* ys[nh::MAX_SITES];
+        for (int e = 0; e < D.sites; ++e) {
+            s->a_eng[e].rows = t;
+            acts[e] = &s->a_eng[e];
+            ys[e] = S.ekv + (size_t)e * nh::BATCH_ROWS * 2 * D.d;
+        }
+        if (t > 1 && D.sites > 1 && nh::gemm_batchable(m->ekv.data(), acts, D.sites)) {
+            NH_TRY(nh::launch_gemm_batch(m->ekv.data(), acts, ys, D.sites, flags, 2 * D.d, st), "engram kv");
+        } else {
+            for (int e = 0; e < D.sites; ++e)
+                NH_TRY(product(m->ekv[e], &s->a_eng[e], t, ys[e], 2 * D.d, flags, st), "engram kv");
+        }
     }
     NH_TRY(nh::fwd_engram_hist(D, m->glob, S, p0, t, st), "engram history");
     for (int l = 0; l < D.layers; ++l) {
