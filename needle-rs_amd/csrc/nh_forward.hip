@@ -243,17 +243,34 @@ __device__ __forceinline__ int8_t group_quant32(float v, float& s) {
 __global__ __launch_bounds__(1024) void k_engram_hist(Dims D, Globals G, SessDev S, int p0) {
     const int e = blockIdx.x, i = blockIdx.y, k = threadIdx.x, d = D.d, pos = p0 + i;
     const bool on = k < d;
+    const int kc = on ? k : 0;
     const float* kv = S.ekv + (size_t)e * BATCH_ROWS * 2 * d;
-    float s;
-    const int8_t q = group_quant32(on ? kv[(size_t)i * 2 * d + d + k] : 0.0f, s);
     const int gs = d / 32;
     int8_t* ev8 = S.ev8 + (size_t)e * D.cap * d;
     float* evs = S.evs + (size_t)e * D.cap * gs;
+    // Every load first, at clamped in-range addresses: the row's value and,
+    // per tap, both sources of its row (the value, for a row of this feed;
+    // the int8 history and its scale, for an earlier one) and the tap
+    // weight; the taps then pick theirs.
+    const float v0 = kv[(size_t)i * 2 * d + d + kc];
+    float kvj[ENGRAM_TAPS], hsj[ENGRAM_TAPS], twj[ENGRAM_TAPS];
+    int8_t h8j[ENGRAM_TAPS];
+#pragma unroll
+    for (int j = 0; j < ENGRAM_TAPS; ++j) {
+        const int pj = max(pos - j * D.dilation, 0);
+        kvj[j] = kv[(size_t)max(pj - p0, 0) * 2 * d + d + kc];
+        hsj[j] = evs[(size_t)pj * gs + kc / 32];
+        h8j[j] = ev8[(size_t)pj * d + kc];
+        twj[j] = G.etaps[((size_t)e * ENGRAM_TAPS + j) * d + kc];
+    }
+    float s;
+    const int8_t q = group_quant32(on ? v0 : 0.0f, s);
     if (on) {
         ev8[(size_t)pos * d + k] = q;
         if ((k & 31) == 0) evs[(size_t)pos * gs + k / 32] = s;
     }
     float dst = 0.0f;
+#pragma unroll
     for (int j = 0; j < ENGRAM_TAPS; ++j) {
         if (pos < j * D.dilation) break;
         const int pj = pos - j * D.dilation;
@@ -262,12 +279,12 @@ __global__ __launch_bounds__(1024) void k_engram_hist(Dims D, Globals G, SessDev
         if (j == 0) {
             qs = s, q8 = q;
         } else if (pj >= p0) {
-            q8 = group_quant32(on ? kv[(size_t)(pj - p0) * 2 * d + d + k] : 0.0f, qs);
+            q8 = group_quant32(on ? kvj[j] : 0.0f, qs);
         } else {
-            qs = on ? evs[(size_t)pj * gs + k / 32] : 0.0f;
-            q8 = on ? ev8[(size_t)pj * d + k] : 0;
+            qs = on ? hsj[j] : 0.0f;
+            q8 = on ? h8j[j] : 0;
         }
-        const float tw = on ? G.etaps[((size_t)e * ENGRAM_TAPS + j) * d + k] : 0.0f;
+        const float tw = on ? twj[j] : 0.0f;
         dst = __builtin_fmaf(tw, qs * (float)q8, dst);
     }
     if (on) S.evals[((size_t)e * BATCH_ROWS + i) * d + k] = dst;
