@@ -1647,8 +1647,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 }
 
 // attend_head_ref for all the query heads that share a kv head: one
-// workgroup per (row, kv head, key chunk) stages the chunk's key rows,
-// scales and value columns once (as k_attend does).  The two integer dot
+// workgroup per (row or pair of rows, kv head, key chunk) stages the
+// chunk's key rows, scales and value columns once (as k_attend does).  The two integer dot
 // products run on the matrix cores, since an int32 sum is the same in any
 // order: the scores of every head against 16 keys are one
 // v_mfma_i32_16x16x64_i8 (A = the heads' int8 queries, B = the key rows),
