@@ -391,7 +391,9 @@ struct Held {
 
 int fuse(std::initializer_list<nh_qmat*> parts, nh_qmat** h) {
     std::vector<nh_qmat*> v(parts);
-    return nh_qlinear_new(v.data(), (int)v.size(), h);
+    const int rc = nh_qlinear_new(v.data(), (int)v.size(), h);
+    if (rc == NH_OK) (*h)->resident = true;  // a model's weights
+    return rc;
 }
 
 }  // namespace
@@ -474,6 +476,7 @@ int nh::load_archive(const uint8_t* bytes, uint64_t n, nh_weights** out, nh::Arc
     int rc = NH_OK;
     auto put = [&](size_t i, nh_qmat** h) {
         if (rc == NH_OK) rc = upload(bytes, plan.recs[i], h);
+        if (rc == NH_OK) (*h)->resident = true;  // a model's weights
         return rc == NH_OK;
     };
     if (put(plan.embedding, &wts->embedding)) {

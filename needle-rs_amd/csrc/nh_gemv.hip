@@ -28,7 +28,10 @@ namespace nh {
 // it replaces one workgroup per tile (8 tiles per workgroup).
 constexpr int STREAM_WG_PER_CU = 4;
 
-template <int GPS, int S, int BITS, bool DBG>
+// NT: the code loads carry the non-temporal hint (a matrix read once per
+// sweep of more than the caches hold); without it (a resident matrix, read
+// again at every token) their lines stay cached.
+template <int GPS, int S, int BITS, bool DBG, bool NT>
 __device__ __forceinline__ void gemv_tile(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
                                           const uint4* __restrict__ xq, const float* __restrict__ sx,
                                           float* __restrict__ y, int32_t* __restrict__ dbg, int out, int G, float cbs,
@@ -55,9 +58,10 @@ __device__ __forceinline__ void gemv_tile(const void* __restrict__ codes, const 
     for (int j = 0; j < GPS; ++j) {
         // Groups past G (when S * GPS > G) reload group 0; never used.
         const int g = g0 + j < G ? g0 + j : 0;
-        if constexpr (BITS == 4)
-            c[j] = load_stream(reinterpret_cast<const uint4*>(codes) + ((size_t)(tile * G + g) * 64 + lane));
-        else
+        if constexpr (BITS == 4) {
+            const uint4* p = reinterpret_cast<const uint4*>(codes) + ((size_t)(tile * G + g) * 64 + lane);
+            c[j] = NT ? load_stream(p) : *p;
+        } else
             c[j] = reinterpret_cast<const uint2*>(codes)[(size_t)(tile * G + g) * 64 + lane];
         nb[j] = norms[(size_t)n * G + g];
         sxv[j] = sx[g];
@@ -101,21 +105,21 @@ __device__ __forceinline__ void gemv_tile(const void* __restrict__ codes, const 
     if (y && l == 0 && n < out) y[n] = u;
 }
 
-template <int GPS, int S, int BITS, bool DBG>
+template <int GPS, int S, int BITS, bool DBG, bool NT>
 __global__ __launch_bounds__(S * 64) void k_gemv(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
                                                  const uint4* __restrict__ xq, const float* __restrict__ sx,
                                                  float* __restrict__ y, int32_t* __restrict__ dbg, int out, int G,
                                                  float cbs, Lut lut) {
-    gemv_tile<GPS, S, BITS, DBG>(codes, norms, xq, sx, y, dbg, out, G, cbs, lut, blockIdx.x);
+    gemv_tile<GPS, S, BITS, DBG, NT>(codes, norms, xq, sx, y, dbg, out, G, cbs, lut, blockIdx.x);
 }
 
 // Several same-shaped products in one launch (blockIdx.y picks the member),
 // e.g. the engram key | value products of every site.
-template <int GPS, int S, int BITS>
+template <int GPS, int S, int BITS, bool NT>
 __global__ __launch_bounds__(S * 64) void k_gemv_batch(GemvBatch b, int out, int G, float cbs, Lut lut) {
     const int e = blockIdx.y;
-    gemv_tile<GPS, S, BITS, false>(b.codes[e], b.norms[e], b.xq[e], b.sx[e], b.y[e], nullptr, out, G, cbs, lut,
-                                   blockIdx.x);
+    gemv_tile<GPS, S, BITS, false, NT>(b.codes[e], b.norms[e], b.xq[e], b.sx[e], b.y[e], nullptr, out, G, cbs, lut,
+                                       blockIdx.x);
 }
 
 // The same product for very tall matrices (4-bit): a persistent grid of a
@@ -197,12 +201,10 @@ static hipError_t run(const nh_qmat* w, const nh_qact* a, float* y, int32_t* dbg
                            (const uint4*)a->d_xq, a->d_sx, y, m.out, m.groups, m.cbs, lut, tiles);
         return hipGetLastError();
     }
-    if (dbg)
-        hipLaunchKernelGGL((k_gemv<GPS, S, BITS, true>), grid, block, 0, s, w->d_codes, w->d_norms,
-                           (const uint4*)a->d_xq, a->d_sx, y, dbg, m.out, m.groups, m.cbs, lut);
-    else
-        hipLaunchKernelGGL((k_gemv<GPS, S, BITS, false>), grid, block, 0, s, w->d_codes, w->d_norms,
-                           (const uint4*)a->d_xq, a->d_sx, y, dbg, m.out, m.groups, m.cbs, lut);
+    auto kern = dbg ? k_gemv<GPS, S, BITS, true, true>
+                    : w->resident ? k_gemv<GPS, S, BITS, false, false> : k_gemv<GPS, S, BITS, false, true>;
+    hipLaunchKernelGGL(kern, grid, block, 0, s, w->d_codes, w->d_norms, (const uint4*)a->d_xq, a->d_sx, y, dbg, m.out,
+                       m.groups, m.cbs, lut);
     return hipGetLastError();
 }
 
@@ -233,8 +235,8 @@ template <int GPS, int S, int BITS>
 static hipError_t run_batch(const nh_qmat* w, const GemvBatch& b, int n, hipStream_t s) {
     const QMatMeta& m = w->m;
     const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
-    hipLaunchKernelGGL((k_gemv_batch<GPS, S, BITS>), dim3(m.out_pad / TILE_ROWS, n), dim3(S * 64), 0, s, b, m.out,
-                       m.groups, m.cbs, lut);
+    auto kern = w->resident ? k_gemv_batch<GPS, S, BITS, false> : k_gemv_batch<GPS, S, BITS, true>;
+    hipLaunchKernelGGL(kern, dim3(m.out_pad / TILE_ROWS, n), dim3(S * 64), 0, s, b, m.out, m.groups, m.cbs, lut);
     return hipGetLastError();
 }
 

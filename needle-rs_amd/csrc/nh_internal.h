@@ -58,6 +58,10 @@ struct nh_qmat {
     // and group, [half][lane][16 bytes] (k_expand_w8).
     uint4* d_w8 = nullptr;
     float* d_fsel = nullptr;
+    // Read again at every token (a loaded model's weights): the decode
+    // product's code loads then keep their lines cached instead of streaming
+    // them past (the default, for matrices swept once).
+    bool resident = false;
     // Host copy of the archive-layout codes and norms (fusion, download).
     std::vector<uint8_t> h_packed;   // out x groups*64
     std::vector<uint16_t> h_norms;   // out x groups

@@ -421,6 +421,7 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
     }
     m->head = new nh_qmat();
     m->head->m = emb->m;
+    m->head->resident = true;
     m->head->m.out = D.out_rows;
     m->head->m.out_pad = (int)round_up(D.out_rows, nh::TILE_ROWS);
     m->head->d_codes = emb->d_codes;
