@@ -2091,7 +2091,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
     __shared__ alignas(16) int8_t q8[HP][MAX_HEAD_DIM];
     __shared__ float sc[HP][ATT_CHUNK_MAX];
     __shared__ alignas(16) int8_t dig[HP][3][DG_PITCH];
-    __shared__ float red[HP][DG_HEAD_T / 64];
+    __shared__ float red[HP][DG_HEAD_T / 64], wred[HP][DG_HEAD_T / 64];
     __shared__ float s_qs[HP], s_sum[HP];
     __shared__ float att[HP * MAX_HEAD_DIM];
     __shared__ float gden[HP * MAX_HEAD_DIM];  // exp(-gate) + 1 of output hh0 * vd + j
@@ -2239,66 +2239,64 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
     }
     __syncthreads();
     if (attends) {
+        // the exps (kept in sc for the sum) and the max of the value
+        // weights w = p * vscale, which the digits need and the sum does not
         mx = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
-        for (int i = u; i < n; i += DG_HEAD_T) sc[h][i] = i < blocked ? nexp(sc[h][i] - mx) : lexpf(sc[h][i] - mx);
-    }
-    __syncthreads();
-    if (attends && hw == 0) {
-        // lane 4 hi + k sums sc[8 b + 4 hi + k] over b in order, the loads
-        // of a batch of 8 issued ahead of its adds
-        float acc = 0.0f;
-        const int nb8 = n / 8;
-        if (lane < 8) {
-            const int k = lane & 3, hi = lane >> 2;
-            const float* col = &sc[h][hi * 4 + k];
-            int b = 0;
-            for (; b + 8 <= nb8; b += 8) {
-                float v[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) v[j] = col[(b + j) * 8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) acc += v[j];
-            }
-            for (; b < nb8; ++b) acc += col[b * 8];
-            if (hi == 0 && n - nb8 * 8 >= 4) acc += sc[h][nb8 * 8 + k];
-        }
-        // t[k] = a[k] + b[k] (lane 4 + k brought to lane k by a DPP row
-        // shift), then (t0 + t1) + (t2 + t3) by quad broadcasts: exact in
-        // lane 0, which alone uses it
-        const float tk = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, acc),
-                                                                                       0x104, 0xF, 0xF, false));
-        const int ti = __builtin_bit_cast(int, tk);
-        const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x00, 0xF, 0xF, false));
-        const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x55, 0xF, 0xF, false));
-        const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xAA, 0xF, 0xF, false));
-        const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xFF, 0xF, 0xF, false));
-        float sum = (t0 + t1) + (t2 + t3);
-        int i = blocked;
-        if (n - i >= 2) {
-            sum = (sc[h][i] + sum) + sc[h][i + 1];
-            i += 2;
-        }
-        if (n - i == 1) sum += sc[h][i];
-        if (lane == 0) s_sum[h] = sum;
-    }
-    __syncthreads();
-    float inv_sum = 0.0f;
-    if (attends) {
-        inv_sum = 1.0f / s_sum[h];  // (its latency overlaps the weights)
         for (int i = u; i < n; i += DG_HEAD_T) {
-            const float w = sc[h][i] * vss[i];
-            sc[h][i] = w;
-            wmax = fmaxf(wmax, w);
+            const float e = i < blocked ? nexp(sc[h][i] - mx) : lexpf(sc[h][i] - mx);
+            sc[h][i] = e;
+            wmax = fmaxf(wmax, e * vss[i]);
         }
         wmax = wave_max(wmax);
-        if (lane == 0) red[h][hw] = wmax;
+        if (lane == 0) wred[h][hw] = wmax;
     }
     __syncthreads();
     if (attends) {
-        wmax = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
+        if (hw == 0) {
+            // lane 4 hi + k sums sc[8 b + 4 hi + k] over b in order, the
+            // loads of a batch of 8 issued ahead of its adds
+            float acc = 0.0f;
+            const int nb8 = n / 8;
+            if (lane < 8) {
+                const int k = lane & 3, hi = lane >> 2;
+                const float* col = &sc[h][hi * 4 + k];
+                int b = 0;
+                for (; b + 8 <= nb8; b += 8) {
+                    float v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = col[(b + j) * 8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc += v[j];
+                }
+                for (; b < nb8; ++b) acc += col[b * 8];
+                if (hi == 0 && n - nb8 * 8 >= 4) acc += sc[h][nb8 * 8 + k];
+            }
+            // t[k] = a[k] + b[k] (lane 4 + k brought to lane k by a DPP row
+            // shift), then (t0 + t1) + (t2 + t3) by quad broadcasts: exact in
+            // lane 0, which alone uses it
+            const float tk = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                                 0, __builtin_bit_cast(int, acc), 0x104, 0xF, 0xF, false));
+            const int ti = __builtin_bit_cast(int, tk);
+            const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x00, 0xF, 0xF, false));
+            const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x55, 0xF, 0xF, false));
+            const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xAA, 0xF, 0xF, false));
+            const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xFF, 0xF, 0xF, false));
+            float sum = (t0 + t1) + (t2 + t3);
+            int i = blocked;
+            if (n - i >= 2) {
+                sum = (sc[h][i] + sum) + sc[h][i + 1];
+                i += 2;
+            }
+            if (n - i == 1) sum += sc[h][i];
+            if (lane == 0) s_sum[h] = sum;
+        }
+        // the 21-bit digits of the weights, beside the sum (wave 0 joins
+        // once its sum is done); w is recomputed from the same two factors
+        wmax = fmaxf(fmaxf(wred[h][0], wred[h][1]), fmaxf(wred[h][2], wred[h][3]));
         const float qw = bits_f32(0x49fffff8u) / wmax;
         for (int i = u; i < n; i += DG_HEAD_T) {
-            const int32_t wq = (int32_t)roundf(sc[h][i] * qw);
+            const float w = sc[h][i] * vss[i];
+            const int32_t wq = (int32_t)roundf(w * qw);
             dig[h][0][sh + i] = (int8_t)(wq >> 14);
             dig[h][1][sh + i] = (int8_t)((wq >> 7) & 127);
             dig[h][2][sh + i] = (int8_t)(wq & 127);
@@ -2313,6 +2311,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
     __syncthreads();
     if (attends) {
         // exact integer P.V: four columns per sdot4, 16 per thread step
+        const float inv_sum = 1.0f / s_sum[h];
         const float cw = wmax * bits_f32(0x35000004u);
         const int dm = u >> 2, part = u & 3, cols = sh + n;
         int a = 0, b = 0, c = 0;
