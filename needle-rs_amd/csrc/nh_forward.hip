@@ -791,23 +791,28 @@ __device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, c
 constexpr int PHI_CHUNKS = MHC_LANES * FWD_MAX_D / 16 / 64;
 constexpr int PHI_B = LT / 64 - 1;  // wavefronts holding Phi8 rows
 static_assert(2 * PHI_B >= MHC_COLS, "two Phi8 rows per wavefront cover the 24 rows");
+// PC: the 1 KB chunks a Phi8 row has (its 4 d int8 / 1024), fixed at compile
+// time so a narrower model holds no registers for chunks it never reads (3
+// at d = 768: 24 VGPRs instead of 32, which the 64-VGPR batched kernel needs).
+template <int PC>
 struct InRegs {
     uint32_t norm;
     float kr, ev, ps0, ps1;
-    uint4 r0[PHI_CHUNKS], r1[PHI_CHUNKS];
+    uint4 r0[PC], r1[PC];
 };
 
-__device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InRegs& q);
+template <int PC>
+__device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InRegs<PC>& q);
 
 // PHI: the Phi8 rows too (else layer_in reads them itself).
-template <bool PHI>
-__device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const LayerDev& N) {
+template <bool PHI, int PC>
+__device__ __forceinline__ InRegs<PC> load_in(const Dims& D, const SessDev& S, const LayerDev& N) {
     const int t = threadIdx.x, d = D.d;
     // Unconditional loads at clamped addresses (threads, rows and chunks
     // past the ranges read an in-range element and ignore it; a layer
     // without an engram site reads the projection row instead, which
     // nothing else here reads).
-    InRegs q;
+    InRegs<PC> q;
     const int td = min(t, d - 1);
     q.norm = N.norm_in[td];
     const bool site = N.site >= 0;
@@ -819,7 +824,8 @@ __device__ __forceinline__ InRegs load_in(const Dims& D, const SessDev& S, const
     return q;
 }
 
-__device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InRegs& q) {
+template <int PC>
+__device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InRegs<PC>& q) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nc = MHC_LANES * D.d;
     // Phi8 rows: wavefront w >= 1 holds row w - 1, and row w + PHI_B - 1
     // while that is below 24; wavefront 0, which runs the first chain of the
@@ -836,7 +842,7 @@ __device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InReg
         const uint4* row0 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)w0 * nc);
         const uint4* row1 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)w1 * nc);
 #pragma unroll
-        for (int j = 0; j < PHI_CHUNKS; ++j) {
+        for (int j = 0; j < PC; ++j) {
             if (64 * j < per) {
                 const int c = min(lane + 64 * j, per - 1);
                 q.r0[j] = row0[c];
@@ -848,11 +854,12 @@ __device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InReg
     }
 }
 
+template <int PC>
 __device__ __forceinline__ int dot_row(const uint4* r, const int8_t* x8, int per, int lane) {
     const uint4* xv = reinterpret_cast<const uint4*>(x8);
     int acc = 0;
 #pragma unroll
-    for (int j = 0; j < PHI_CHUNKS; ++j) {
+    for (int j = 0; j < PC; ++j) {
         const int i = lane + 64 * j;
         if (i < per) {
             const uint4 b = xv[i];
@@ -871,8 +878,8 @@ __device__ __forceinline__ int dot_row(const uint4* r, const int8_t* x8, int per
 // behind a barrier.  The post and residual
 // gates of the layer (hpost, the Sinkhorn hres) are computed beside its
 // units, off this kernel's path.
-template <bool LATE_PHI>
-__device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, InRegs q, int in_bits,
+template <bool LATE_PHI, int PC>
+__device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, InRegs<PC> q, int in_bits,
                          LayerShared& sh, const float (&xl)[MHC_LANES]) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d, nc = MHC_LANES * d;
     // (the Phi8 rows read now land while wavefront 0 runs the norm chain)
@@ -900,10 +907,10 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, InR
         const float sx = sh.r_sx;
         const int per = nc / 16;
         if (wave >= 1) {
-            const int acc = dot_row(q.r0, sh.nx8, per, lane);
+            const int acc = dot_row<PC>(q.r0, sh.nx8, per, lane);
             if (lane == 0) sh.p[wave - 1] = (sx * q.ps0) * (float)acc;
             if (wave - 1 + PHI_B < MHC_COLS) {
-                const int acc1 = dot_row(q.r1, sh.nx8, per, lane);
+                const int acc1 = dot_row<PC>(q.r1, sh.nx8, per, lane);
                 if (lane == 0) sh.p[wave - 1 + PHI_B] = (sx * q.ps1) * (float)acc1;
             }
         }
@@ -1011,7 +1018,7 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
 // BATCH (a feed of several rows): two rows per CU (at most 64 VGPRs), so
 // the next layer's Phi8 rows are read at the start of the mHC read instead
 // of beside the MLP.
-template <bool PREV, bool NEXT, bool BATCH>
+template <bool PREV, bool NEXT, bool BATCH, int PC>
 __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 1))) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int row0,
                                               int in_bits, int head_bits) {
     constexpr bool has_prev = PREV, has_next = NEXT;
@@ -1038,13 +1045,13 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     for (int k = 0; k < MHC_LANES; ++k) xl[k] = R.xs[k * d + td];
     OutRegs qo;
     if constexpr (has_prev) qo = load_out(D, G, R, P, sh);
-    InRegs qi;
+    InRegs<PC> qi;
     float fnorm = 0.0f;
     // Without a previous layer nothing else loads: the next layer's reads
     // go now.  With one they go after the first barrier: the Phi8 rows are
     // half the kernel's bytes and are not needed before the mHC read, so
     // they stay out of the way of the tables the MLP waits for.
-    if constexpr (has_next && !has_prev) qi = load_in<!BATCH>(D, R, N);
+    if constexpr (has_next && !has_prev) qi = load_in<!BATCH, PC>(D, R, N);
     if constexpr (!has_next) fnorm = G.final_norm[min(t, d - 1)];
     float m = 0.0f;
     if (t == 0) sh.mix_count = 0;
@@ -1061,7 +1068,7 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     }
     if constexpr (has_prev) store_out(D, qo, sh);
     __syncthreads();
-    if constexpr (has_next && has_prev) qi = load_in<!BATCH>(D, R, N);
+    if constexpr (has_next && has_prev) qi = load_in<!BATCH, PC>(D, R, N);
     // (batched: the Phi8 rows are read once the MLP's registers are free)
     if constexpr (has_prev)
         m = layer_out(D, S, P, qo, sh, xl, [&]() __attribute__((always_inline)) {
@@ -1075,7 +1082,7 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     // stores issued earlier would sit in the memory counter ahead of loads
     // that are waited for)
     if constexpr (has_next)
-        layer_in<BATCH && !has_prev>(D, R, N, qi, in_bits, sh, xl);
+        layer_in<BATCH && !has_prev, PC>(D, R, N, qi, in_bits, sh, xl);
     else
         head_in(D, S, fnorm, head_bits, blockIdx.x, sh, xl);  // row i - row0
     if constexpr (has_prev) {
@@ -1086,30 +1093,38 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     }
 }
 
-template <bool BATCH>
+template <bool BATCH, int PC>
 static void launch_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev,
                          const LayerDev* next, int row0, int rows, int in_bits, int head_bits, hipStream_t s) {
     const LayerDev none{};
     if (prev && next)
-        hipLaunchKernelGGL((k_layer<true, true, BATCH>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, *next, row0,
+        hipLaunchKernelGGL((k_layer<true, true, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, *next, row0,
                            in_bits, head_bits);
     else if (next)
-        hipLaunchKernelGGL((k_layer<false, true, BATCH>), dim3(rows), dim3(LT), 0, s, D, G, S, none, *next, row0,
+        hipLaunchKernelGGL((k_layer<false, true, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, none, *next, row0,
                            in_bits, head_bits);
     else if (prev)
-        hipLaunchKernelGGL((k_layer<true, false, BATCH>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, none, row0,
+        hipLaunchKernelGGL((k_layer<true, false, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, none, row0,
                            in_bits, head_bits);
     else
-        hipLaunchKernelGGL((k_layer<false, false, BATCH>), dim3(rows), dim3(LT), 0, s, D, G, S, none, none, row0,
+        hipLaunchKernelGGL((k_layer<false, false, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, none, none, row0,
                            in_bits, head_bits);
 }
 
 hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
                      int row0, int rows, int in_bits, int head_bits, hipStream_t s) {
-    if (rows > 1)
-        launch_layer<true>(D, G, S, prev, next, row0, rows, in_bits, head_bits, s);
-    else
-        launch_layer<false>(D, G, S, prev, next, row0, rows, in_bits, head_bits, s);
+    // A feed's 64-VGPR kernel sized for a Phi8 row of at most three 1 KB
+    // chunks (d <= 768: no spills) or of four.  The one-row kernel has no
+    // register cap and keeps the four-chunk form (measured no faster with
+    // three).
+    if (rows > 1) {
+        if (MHC_LANES * D.d <= 3 * 1024)
+            launch_layer<true, 3>(D, G, S, prev, next, row0, rows, in_bits, head_bits, s);
+        else
+            launch_layer<true, PHI_CHUNKS>(D, G, S, prev, next, row0, rows, in_bits, head_bits, s);
+    } else {
+        launch_layer<false, PHI_CHUNKS>(D, G, S, prev, next, row0, rows, in_bits, head_bits, s);
+    }
     return hipGetLastError();
 }
 
