@@ -36,19 +36,29 @@ __device__ __forceinline__ void gemv_tile(const void* __restrict__ codes, const 
                                           const uint4* __restrict__ xq, const float* __restrict__ sx,
                                           float* __restrict__ y, int32_t* __restrict__ dbg, int out, int G, float cbs,
                                           Lut lut, int tile) {
-    static_assert(S * 64 >= GPS * S * 8, "one thread per activation uint4");
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
     const int r = lane >> 2, l = lane & 3;
     const int n = tile * TILE_ROWS + r;
     const int g0 = wave * GPS;
 
-    // The token's activations (G * 128 bytes) go to LDS once per workgroup;
-    // their load is issued first so waiting for it does not wait for the
-    // code stream behind it.
-    __shared__ uint4 xs[GPS * S * 8];
-    uint4 xv = make_uint4(0, 0, 0, 0);
-    if (threadIdx.x < G * 8) xv = xq[threadIdx.x];
+    // The token's activations, issued ahead of the code stream.  With one
+    // group per wavefront a lane reads its decode lane's 32 bytes itself (the
+    // 16 rows' lanes with the same l share them: one 128-byte span per
+    // wavefront, an L2 hit after the first workgroup) and no barrier waits
+    // for the slowest wavefront; with more, the G * 128 bytes go to LDS once
+    // per workgroup (two direct reads per group measured slower there).
+    constexpr bool DIRECT = GPS == 1;
+    static_assert(DIRECT || S * 64 >= GPS * S * 8, "one thread per activation uint4");
+    __shared__ uint4 xs[DIRECT ? 1 : GPS * S * 8];
+    uint4 xa[GPS], xb[GPS], xv = make_uint4(0, 0, 0, 0);
+    if constexpr (DIRECT) {
+        const int g = g0 < G ? g0 : 0;
+        xa[0] = xq[(g * 4 + l) * 2];
+        xb[0] = xq[(g * 4 + l) * 2 + 1];
+    } else if (threadIdx.x < G * 8) {
+        xv = xq[threadIdx.x];
+    }
     // A lane's chunk: 16 bytes (4-bit: 32 codes) or 8 (2-bit: 32 codes).
     using Chunk = typename std::conditional<BITS == 4, uint4, uint2>::type;
     Chunk c[GPS];
@@ -66,18 +76,28 @@ __device__ __forceinline__ void gemv_tile(const void* __restrict__ codes, const 
         nb[j] = norms[(size_t)n * G + g];
         sxv[j] = sx[g];
     }
-    if (threadIdx.x < G * 8) xs[threadIdx.x] = xv;
-    __syncthreads();
+    if constexpr (!DIRECT) {
+        if (threadIdx.x < G * 8) xs[threadIdx.x] = xv;
+        __syncthreads();
+    }
     float lf[GPS], sc[GPS];
 #pragma unroll
     for (int j = 0; j < GPS; ++j) {
-        const int g = g0 + j < G ? g0 + j : 0;
-        const uint4* xp = xs + (g * 4 + l) * 2;
+        uint4 x0, x1;
+        if constexpr (DIRECT) {
+            x0 = xa[j];
+            x1 = xb[j];
+        } else {
+            const int g = g0 + j < G ? g0 + j : 0;
+            const uint4* xp = xs + (g * 4 + l) * 2;
+            x0 = xp[0];
+            x1 = xp[1];
+        }
         int isum;
         if constexpr (BITS == 4)
-            isum = dot_chunk(c[j], xp[0], xp[1], lut);
+            isum = dot_chunk(c[j], x0, x1, lut);
         else
-            isum = dot_chunk2(c[j], xp[0], xp[1], lut.a_lo);
+            isum = dot_chunk2(c[j], x0, x1, lut.a_lo);
         if (DBG && n < out && g0 + j < G) dbg[((size_t)n * G + g0 + j) * 4 + l] = isum;
         lf[j] = (float)isum;
         sc[j] = (sxv[j] * cbs) * f16_bits_to_f32(nb[j]);
