@@ -271,6 +271,17 @@ def test_prefill_feeds_at_offsets(nh, window):
     assert stats["exact"] == stats["steps"], stats
 
 
+def test_widest_model(nh):
+    # d = 1024, the widest the layer kernel takes: a Phi8 row is four 1 KB
+    # chunks per wavefront, the layer kernel's form that narrower models
+    # (three chunks or fewer) do not use
+    say("d_model 1024: a 100-token prompt (three whole chunks together, then a 4-token chunk), steps")
+    g = cact.Geometry(vocab=300, d_model=1024, num_layers=2, engram_slots=64, engram_sites=(1,), global_layers=(0,),
+                      sliding_window=48)
+    data = archive(g, seed=61)
+    run_feed(nh, data, o.random_tokens(100, g.vocab, seed=15), 140, "d_model 1024", then_steps=3)
+
+
 @pytest.mark.parametrize("heads,kv,qk,vd", [(8, 2, 32, 48), (8, 1, 48, 32), (6, 3, 16, 20)])
 def test_head_geometries(nh, heads, kv, qk, vd):
     say(f"{heads} heads over {kv} kv heads, qk {qk}, vd {vd}: a 300-token prompt (rows past 256 keys attend in 2 "
