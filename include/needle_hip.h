@@ -200,7 +200,8 @@ int nh_session_new(const nh_model* m, int cap, nh_session** s);
 int nh_session_free(nh_session* s);
 /* Session::len (model.rs:72-74). */
 int nh_session_len(const nh_session* s);
-/* Back to an empty session (Model::session again, without reallocating). */
+/* Back to an empty session (Model::session again, without reallocating):
+ * no attention span, no cell tracking. */
 int nh_session_reset(nh_session* s);
 /* Outputs (crates/needle-engine/src/model.rs:150-160): what a feed returns. */
 #define NH_OUT_NONE 0        /* nothing: the head is not run */
@@ -215,24 +216,57 @@ int nh_session_reset(nh_session* s);
  * (infer/chunk.rs:331-353).  `out` is DEVICE memory for out_cap floats (or
  * NULL); returns the rows written (ForwardOut::rows), NH_ESMALL when they do
  * not fit.  The session keeps the last returned row's hidden state
- * (NatState::last_hidden) and, for the logits modes, its logits.  On a
- * failure after the first chunk the session is reset. */
+ * (NatState::last_hidden) and, for the logits modes, its logits.  Argument
+ * errors (bad ids, capacity, a small buffer) leave the session untouched;
+ * any failure once feeding has begun (a span the slot map cannot express, a
+ * launch error) resets it to empty, keeping its attention span. */
 int nh_forward_outputs(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, int64_t out_cap,
                        void* stream);
+/* Model::forward_cells (model.rs:330-345): nh_forward_outputs that also
+ * returns ForwardOut::cells, the feed's per-depth cells [n][L+1][d_model]
+ * (L layers): the lane mean (((x0 + x1) + x2) + x3) * 0.25 of the residual
+ * lanes after the embedding (depth 0) and after each layer's mHC write, as
+ * the native drivers record them (infer/step.rs:240-243,672-714,
+ * infer/chunk.rs:69-70,310, lane_mean infer.rs:1707-1711).  `cells` is
+ * DEVICE memory for cells_cap floats (NULL: the cells go only to a tracking
+ * session's store); NH_ESMALL when they do not fit.  Returns the rows of
+ * `out` as nh_forward_outputs does. */
+int nh_forward_cells(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, int64_t out_cap,
+                     float* cells, int64_t cells_cap, void* stream);
+/* Session::cells = Some(vec![]) (on) or None (off) (model.rs:60-62): a
+ * tracking session appends the cells of every nh_forward, nh_forward_outputs,
+ * nh_forward_cells and nh_generate_greedy feed to its store (step.rs:730-732,
+ * chunk.rs:353-355), which rollback, rewind_zeroed and a prefill re-feed
+ * truncate to the session's length (model.rs:108-110,118-121,
+ * infer.rs:1096-1099).  nh_prefill appends none: prefill_native runs its
+ * feeds with want_cells = false (infer.rs:1089,1100).  Tracking starts at an
+ * empty session (NH_EINVAL otherwise); the first call allocates the store,
+ * cap x (L+1) x d_model floats in HBM.  nh_session_reset turns it off. */
+int nh_session_track_cells(nh_session* s, int on);
+/* The number of cell rows a tracking session holds (Session::cells.len() /
+ * ((L+1) d_model)); NH_EINVAL when it does not track them. */
+int nh_session_cell_rows(const nh_session* s);
+/* Rows row0 .. row0 + n - 1 of a tracking session's cells into DEVICE
+ * dst[n][L+1][d_model]; returns n. */
+int nh_session_cells(const nh_session* s, int row0, int n, float* dst, void* stream);
 /* Model::prefill on the native path (prefill_native, infer.rs:1078-1101):
  * with an attention span, a position in max(end - ring, sink) .. len whose KV
  * slot another position holds now starts a re-feed from there with the
  * conv history zeroed; else as nh_forward_outputs. */
 int nh_prefill(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, int64_t out_cap, void* stream);
 /* Session::clone (model.rs:53-55): a new session with a copy of every cache
- * (one device-to-device copy on `stream`, then a synchronization). */
+ * (one device-to-device copy on `stream`, then a synchronization).  A source
+ * whose bounded wait gave up and has not been reported yet is refused
+ * (NH_EDEVICE; the source's next feed reports it). */
 int nh_session_clone(const nh_session* s, void* stream, nh_session** out);
 /* Session::attend = Some((sink, ring)) (model.rs:62-66; ring 0: None): every
  * query sees the first `sink` positions and the last `ring`; positions past
  * the sink share `ring` KV slots (slot_of, infer.rs:1749-1756) and a slot map
  * (mark_slots / key_ranges, infer.rs:1770-1826) skips a position whose slot
- * another has taken since.  A ring must be 0 or at least 32 (a shorter one
- * would give two rows of a 32-token chunk one slot). */
+ * another has taken since.  Any ring is taken; with a ring shorter than 32 a
+ * feed longer than the ring is refused (NH_EINVAL, the session untouched):
+ * two rows of its chunk would share a KV slot, where the reference's team
+ * members race, and a row could see no key at all. */
 int nh_session_set_attend(nh_session* s, int sink, int ring);
 /* Session::rollback (model.rs:81-113, NatState::rollback infer.rs:1053-1071):
  * drop the last n <= 32 positions without recomputing; the KV slots and the
@@ -252,6 +286,12 @@ int nh_session_rewind_zeroed(nh_session* s, int len);
  * and resets the session.  No call waits for earlier work to check it.
  * 0 makes every such wait give up at once, for tests of that path. */
 int nh_session_debug_spin_limit(nh_session* s, int limit);
+/* No reference counterpart (a test hook for the failure path): the
+ * `after`-th feed from now (each nh_forward* / nh_prefill chunk group or
+ * greedy step counts one) fails with NH_EDEVICE before it launches anything,
+ * as a feed does whose attention span the slot map cannot express; 0 turns
+ * it off. */
+int nh_session_debug_fail_feed(nh_session* s, int after);
 /* NatState::last_hidden (infer.rs:1014-1016) into DEVICE h[d_model]. */
 int nh_session_last_hidden(const nh_session* s, float* h, void* stream);
 /* Model::head_logits (infer.rs:1135-1141) of the session's last hidden state
@@ -279,7 +319,8 @@ int nh_argmax(const float* x, int n, uint32_t* dst, void* stream);
  * logits (generate.rs:42-50, the first maximum), then a step on that token.
  * The picked ids land in HOST `out` at the end (one synchronization); the
  * last step's logits in `logits` (DEVICE, or NULL).  No stop token: the
- * caller cuts at EOS. */
+ * caller cuts at EOS.  A step that fails resets the session to empty
+ * (keeping its attention span), as a failed nh_forward_outputs does. */
 int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, void* stream);
 
 /* ---- seeded inputs (host) ---------------------------------------------- */

@@ -371,7 +371,7 @@ using namespace nh;
 
 extern "C" {
 
-int nh_version(void) { return 100; }
+int nh_version(void) { return 101; }
 
 int nh_codebook(int bits, float* out) {
     if (!out) return fail(NH_EINVAL, "null output");

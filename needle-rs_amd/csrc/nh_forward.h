@@ -77,6 +77,7 @@ struct LayerDev {
     float ga;             // sigmoid(attn_gate), f32 expf on the host
     float b_pre[4], b_post[4], b_res[16];
     int site;             // engram site gating this layer, or -1
+    int index;            // the layer's index (its post block writes cell depth index + 1)
     int lane;             // l % lanes
     int window;           // sliding window (0: attends to every position)
 };
@@ -129,6 +130,8 @@ struct SessDev {
     int32_t* argmax;  // scratch of the greedy pick
     int32_t* status;  // STATUS_* bits set by a kernel that gave up a wait; the host reads and clears it
     uint8_t* flags;   // [rows] the prefill combine's block flag of each row of the feed
+    float* cells;     // [rows][layers + 1][d] the feed's cells (lane means after the embedding
+                      // and after each layer's mHC write), or null when not wanted; set per feed
 };
 
 // A CQ matrix read by rows (the embedding, the engram tables).
@@ -157,11 +160,12 @@ hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const Be
 hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, int p0, int t, hipStream_t s);
 // The per-layer boundary for rows row0 .. row0 + rows - 1: the Hadamard MLP
 // and mHC write of layer `prev` (null: none, the lanes hold the embedding
-// rows), then the mHC read, engram gate, input norm and A8 of layer `next`
-// (null: the head's lane mean and final norm into hid row i - row0 and its
-// A8 into activation row i - row0).
+// rows; with S.cells its lane means go to cell depth prev->index + 1), then
+// the mHC read, engram gate, input norm and A8 of layer `next` (null: for
+// rows i >= row0 + head_row0, the head's lane mean and final norm into hid
+// row i - row0 - head_row0 and its A8 into that activation row).
 hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
-                     int row0, int rows, int in_bits, int head_bits, hipStream_t s);
+                     int row0, int rows, int in_bits, int head_bits, hipStream_t s, int head_row0 = 0);
 hipError_t fwd_units(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t, hipStream_t s);
 // `span`: the keys of a session with an attention span (null: none).
 hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int t,

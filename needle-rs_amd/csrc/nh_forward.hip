@@ -166,9 +166,17 @@ __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, Beg
             const float scale = __builtin_sqrtf((float)D.d);
             const int i0 = r * GROUP + lane, i1 = i0 + 64;
             float* xs = S.xs + (size_t)i * MHC_LANES * D.d;
+            const float e0 = v0 * scale, e1 = v1 * scale;
             for (int b = 0; b < MHC_LANES; ++b) {
-                if (i0 < D.d) xs[b * D.d + i0] = v0 * scale;
-                if (i1 < D.d) xs[b * D.d + i1] = v1 * scale;
+                if (i0 < D.d) xs[b * D.d + i0] = e0;
+                if (i1 < D.d) xs[b * D.d + i1] = e1;
+            }
+            if (S.cells) {
+                // cell depth 0: the lane mean of the four embedding lanes
+                // (step.rs:240-243, chunk.rs:69-70, lane_mean infer.rs:1707-1711)
+                float* c = S.cells + (size_t)i * (D.layers + 1) * D.d;
+                if (i0 < D.d) c[i0] = (((e0 + e0) + e0) + e0) * 0.25f;
+                if (i1 < D.d) c[i1] = (((e1 + e1) + e1) + e1) * 0.25f;
             }
         } else {
             const int e = (r - Gd) / Gd, g = (r - Gd) % Gd;
@@ -1001,7 +1009,8 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
             const float h = __builtin_fmaf(tt, fnorm, tt);
             sh.x2[t] = h;
             S.hid[(size_t)arow * d + t] = h;
-            if (arow == (int)gridDim.x - 1) S.last_hid[t] = h;  // NatState::last_hidden: the last row returned
+            // NatState::last_hidden: the last row returned (the launch's last block)
+            if (blockIdx.x == gridDim.x - 1) S.last_hid[t] = h;
         }
     }
     __syncthreads();
@@ -1020,7 +1029,7 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
 // of beside the MLP.
 template <bool PREV, bool NEXT, bool BATCH, int PC>
 __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 1))) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int row0,
-                                              int in_bits, int head_bits) {
+                                              int in_bits, int head_bits, int head_row0) {
     constexpr bool has_prev = PREV, has_next = NEXT;
     __shared__ LayerShared sh;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, d = D.d, nc = MHC_LANES * d;
@@ -1083,47 +1092,53 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     // that are waited for)
     if constexpr (has_next)
         layer_in<BATCH && !has_prev, PC>(D, R, N, qi, in_bits, sh, xl);
-    else
-        head_in(D, S, fnorm, head_bits, blockIdx.x, sh, xl);  // row i - row0
+    else if ((int)blockIdx.x >= head_row0)  // (uniform over the block)
+        head_in(D, S, fnorm, head_bits, blockIdx.x - head_row0, sh, xl);  // row i - row0 - head_row0
     if constexpr (has_prev) {
         if (t < d) {
 #pragma unroll
             for (int k = 0; k < MHC_LANES; ++k) R.xs[k * d + t] = xl[k];
+            // the cell of layer P: the lane mean after its mHC write
+            // (step.rs:672-694, chunk.rs:310, lane_mean infer.rs:1707-1711)
+            if (S.cells)
+                S.cells[((size_t)row * (D.layers + 1) + P.index + 1) * d + t] =
+                    (((xl[0] + xl[1]) + xl[2]) + xl[3]) * 0.25f;
         }
     }
 }
 
 template <bool BATCH, int PC>
 static void launch_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev,
-                         const LayerDev* next, int row0, int rows, int in_bits, int head_bits, hipStream_t s) {
+                         const LayerDev* next, int row0, int rows, int in_bits, int head_bits, int head_row0,
+                         hipStream_t s) {
     const LayerDev none{};
     if (prev && next)
         hipLaunchKernelGGL((k_layer<true, true, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, *next, row0,
-                           in_bits, head_bits);
+                           in_bits, head_bits, head_row0);
     else if (next)
         hipLaunchKernelGGL((k_layer<false, true, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, none, *next, row0,
-                           in_bits, head_bits);
+                           in_bits, head_bits, head_row0);
     else if (prev)
         hipLaunchKernelGGL((k_layer<true, false, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, none, row0,
-                           in_bits, head_bits);
+                           in_bits, head_bits, head_row0);
     else
         hipLaunchKernelGGL((k_layer<false, false, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, none, none, row0,
-                           in_bits, head_bits);
+                           in_bits, head_bits, head_row0);
 }
 
 hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
-                     int row0, int rows, int in_bits, int head_bits, hipStream_t s) {
+                     int row0, int rows, int in_bits, int head_bits, hipStream_t s, int head_row0) {
     // A feed's 64-VGPR kernel sized for a Phi8 row of at most three 1 KB
     // chunks (d <= 768: no spills) or of four.  The one-row kernel has no
     // register cap and keeps the four-chunk form (measured no faster with
     // three).
     if (rows > 1) {
         if (MHC_LANES * D.d <= 3 * 1024)
-            launch_layer<true, 3>(D, G, S, prev, next, row0, rows, in_bits, head_bits, s);
+            launch_layer<true, 3>(D, G, S, prev, next, row0, rows, in_bits, head_bits, head_row0, s);
         else
-            launch_layer<true, PHI_CHUNKS>(D, G, S, prev, next, row0, rows, in_bits, head_bits, s);
+            launch_layer<true, PHI_CHUNKS>(D, G, S, prev, next, row0, rows, in_bits, head_bits, head_row0, s);
     } else {
-        launch_layer<false, PHI_CHUNKS>(D, G, S, prev, next, row0, rows, in_bits, head_bits, s);
+        launch_layer<false, PHI_CHUNKS>(D, G, S, prev, next, row0, rows, in_bits, head_bits, head_row0, s);
     }
     return hipGetLastError();
 }

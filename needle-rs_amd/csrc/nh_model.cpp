@@ -149,10 +149,18 @@ struct nh_session {
     int32_t* h_status = nullptr;
     hipEvent_t ev_status = nullptr;
     bool status_pending = false;
+    // Session::cells (model.rs:60-62): when tracked, the cell rows the feeds
+    // appended, [ncells][layers + 1][d] in a buffer of cap rows.
+    bool track_cells = false;
+    float* d_cells = nullptr;
+    int ncells = 0;
+    int fail_in = 0;  // test hook: the feed that fails on purpose (0: none)
 
+    size_t cell_floats() const { return (size_t)(dims.layers + 1) * dims.d; }
     ~nh_session() {
         if (ev_status) (void)hipEventDestroy(ev_status);
         if (h_status) (void)hipHostFree(h_status);
+        if (d_cells) (void)hipFree(d_cells);
         if (d_buf) (void)hipFree(d_buf);
     }
 };
@@ -405,6 +413,7 @@ int build_model(nh_model* m, const nh::ArchiveSmall& sm) {
         for (int j = 0; j < 4; ++j) L.b_pre[j] = sm.mhc[3][l * 4 + j], L.b_post[j] = sm.mhc[4][l * 4 + j];
         for (int j = 0; j < 16; ++j) L.b_res[j] = sm.mhc[5][l * 16 + j];
         L.site = site_of[l];
+        L.index = l;
         L.lane = l % D.lanes;
         L.window = (window > 0 && !((gmask >> l) & 1)) ? window : 0;
         m->layers.push_back(L);
@@ -523,10 +532,12 @@ int out_width(const nh_session* s, int outputs) {
 // `outputs` picks what the rows give (chunk.rs:331-353, step.rs:715-729),
 // written to `out` (device, rows x width, or null to keep only the
 // session's copies); for several chunks the Last* modes mean the last
-// chunk's last row, All* every row.
-int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
+// chunk's last row, All* every row.  `cells` (device, or null): the rows'
+// cells [t][layers + 1][d] (step.rs:240-243,672-714, chunk.rs:69-70,310).
+int feed(nh_session* s, int t, int outputs, float* out, float* cells, hipStream_t st) {
     const nh_model* m = s->m;
-    const nh::SessDev& S = s->S;
+    nh::SessDev S = s->S;
+    S.cells = cells;
     const int p0 = s->len;
     const uint8_t* flags = t > nh::FWD_ROWS ? S.flags : nullptr;
     nh::Dims D = s->dims;
@@ -535,6 +546,8 @@ int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
     D.sink = s->sink;
     D.ring = s->ring;
     mark_slots(s, p0, p0 + t);
+    if (s->fail_in > 0 && --s->fail_in == 0)
+        return fail(NH_EDEVICE, "a feed failed on purpose (nh_session_debug_fail_feed)");
     nh::KeySpan span{};
     const nh::KeySpan* sp = nullptr;
     if (s->ring > 0) {
@@ -587,9 +600,15 @@ int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
     // the outputs want, then the head (head_logits per row, decode combine)
     const int rows = out_rows_of(outputs, t), row0 = t - rows;
     const int d = D.d, Gd = (d + nh::GROUP - 1) / nh::GROUP;
+    const nh::LayerDev* last = D.layers > 0 ? &m->layers[D.layers - 1] : nullptr;
+    if (cells && last) {
+        // the last layer's post block over every row (its cells), the head's
+        // input for the rows the outputs want (hid and A8 rows 0 .. rows - 1)
+        NH_TRY(nh::fwd_layer(D, m->glob, S, last, nullptr, 0, t, 0, m->head_bits, st, row0), "last layer");
+    }
     if (rows > 0) {
-        const nh::LayerDev* last = D.layers > 0 ? &m->layers[D.layers - 1] : nullptr;
-        NH_TRY(nh::fwd_layer(D, m->glob, S, last, nullptr, row0, rows, 0, m->head_bits, st), "head input");
+        if (!cells || !last)
+            NH_TRY(nh::fwd_layer(D, m->glob, S, last, nullptr, row0, rows, 0, m->head_bits, st), "head input");
         const bool logits = outputs == NH_OUT_LAST_LOGITS || outputs == NH_OUT_ALL_LOGITS;
         for (int i = 0; i < rows && logits; ++i) {
             nh_qact a = s->a_in;
@@ -625,6 +644,17 @@ int feed(nh_session* s, int t, int outputs, float* out, hipStream_t st) {
     return rows;
 }
 
+// Back to an empty session, keeping the attention span and cell tracking
+// the caller set.
+void clear(nh_session* s) {
+    s->len = 0;
+    s->have_logits = s->have_hidden = false;
+    s->hrows = s->rope_n = 0;
+    s->slot_pos.clear();
+    s->toks.clear();
+    s->ncells = 0;
+}
+
 // The session's status word (bounded in-kernel waits that gave up).  A call
 // that feeds ends by queueing a copy of the word to pinned host memory and
 // an event behind it (post_status); the next call reads that copy if the
@@ -643,7 +673,7 @@ int check_status(nh_session* s, hipStream_t st, bool wait) {
     const int32_t zero = 0;
     NH_TRY(hipMemcpyAsync(s->S.status, &zero, 4, hipMemcpyHostToDevice, st), "status");
     NH_TRY(hipStreamSynchronize(st), "status");
-    nh_session_reset(s);
+    clear(s);
     return fail(NH_EDEVICE, "a bounded wait in the layer kernel gave up (the session was reset)");
 }
 
@@ -654,10 +684,38 @@ int post_status(nh_session* s, hipStream_t st) {
     return NH_OK;
 }
 
+// A feed that failed part way: the device caches hold part of it (the
+// reference would have panicked), so the session starts over rather than
+// keep them.
+int reset_after(nh_session* s, int rc) {
+    const std::string msg = nh_last_error();
+    clear(s);
+    return fail(rc, msg + " (the session was reset)");
+}
+
+// Session::cells.truncate(len * (L+1) * d) (model.rs:108-110,118-121,
+// infer.rs:1096-1099).
+void truncate_cells(nh_session* s, int len) { s->ncells = std::min(s->ncells, len); }
+
+// A ring shorter than a chunk takes only feeds that fit it: two rows of a
+// longer chunk would share a KV slot (the reference's members race there)
+// and a row could see no key at all (attend_head_ref's step_by(0) panics).
+int check_ring(const nh_session* s, int n) {
+    if (s->ring > 0 && s->ring < nh::FWD_ROWS && n > s->ring)
+        return fail(NH_EINVAL, "a feed longer than an attention ring shorter than 32 (two of its rows would share "
+                               "a KV slot)");
+    return NH_OK;
+}
+
 // Model::forward_native (infer.rs:1105-1132) over host token ids: chunks of
 // 32, a one-token chunk as a step, LastLogits / LastHidden from the last
-// chunk only.  Returns the rows written.
-int forward_ids(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, hipStream_t st) {
+// chunk only.  Returns the rows written.  want_cells: the cells are computed
+// (forward_inner, model.rs:339-343: requested or tracked; prefill_native
+// passes false, infer.rs:1089,1100), into `cells` (device [n][L+1][d], or
+// null) and appended to a tracking session's store (step.rs:730-732,
+// chunk.rs:353-355).
+int forward_ids(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, bool want_cells, float* cells,
+                hipStream_t st) {
     if (int rc = check_status(s, st, false)) return rc;
     NH_TRY(hipMemcpyAsync(s->S.tokens + s->len, toks, (size_t)n * 4, hipMemcpyHostToDevice, st), "tokens");
     s->toks.resize(s->len);
@@ -674,13 +732,15 @@ int forward_ids(nh_session* s, const uint32_t* toks, int n, int outputs, float* 
         const bool last = i + t == n;
         const int want =
             (!last && (outputs == NH_OUT_LAST_LOGITS || outputs == NH_OUT_LAST_HIDDEN)) ? NH_OUT_NONE : outputs;
-        const int r = feed(s, t, want, out ? out + (size_t)rows * width : nullptr, st);
-        if (r < 0) {
-            // The device caches hold part of the feed (the reference would
-            // have panicked): the session starts over rather than keep them.
-            const std::string msg = nh_last_error();
-            nh_session_reset(s);
-            return fail(r, msg + " (the session was reset)");
+        const size_t cw = s->cell_floats();
+        float* cdst = nullptr;
+        if (want_cells) cdst = s->track_cells ? s->d_cells + (size_t)s->ncells * cw : cells ? cells + i * cw : nullptr;
+        const int r = feed(s, t, want, out ? out + (size_t)rows * width : nullptr, cdst, st);
+        if (r < 0) return reset_after(s, r);
+        if (cdst && s->track_cells) {
+            if (cells)
+                NH_TRY(hipMemcpyAsync(cells + i * cw, cdst, (size_t)t * cw * 4, hipMemcpyDeviceToDevice, st), "cells");
+            s->ncells += t;
         }
         rows += r;
         i += t;
@@ -696,6 +756,12 @@ int check_feed(nh_session* s, const uint32_t* toks, int n, int outputs) {
     if (s->len + n > s->dims.cap) return fail(NH_EINVAL, "the tokens do not fit the session's capacity");
     for (int i = 0; i < n; ++i)
         if (toks[i] >= (uint32_t)s->dims.vocab) return fail(NH_EINVAL, "token id outside the vocabulary");
+    return NH_OK;
+}
+
+int check_cells(const nh_session* s, int n, const float* cells, int64_t cells_cap) {
+    if (cells && (int64_t)n * (int64_t)s->cell_floats() > cells_cap)
+        return fail(NH_ESMALL, "the cells buffer is too small");
     return NH_OK;
 }
 
@@ -843,12 +909,44 @@ int nh_session_len(const nh_session* s) {
 
 int nh_session_reset(nh_session* s) {
     if (!s) return fail(NH_EINVAL, "null session");
-    s->len = 0;
-    s->have_logits = s->have_hidden = false;
-    s->hrows = s->rope_n = 0;
+    clear(s);
     s->sink = s->ring = 0;
-    s->slot_pos.clear();
-    s->toks.clear();
+    s->track_cells = false;
+    return NH_OK;
+}
+
+int nh_session_track_cells(nh_session* s, int on) {
+    if (!s) return fail(NH_EINVAL, "null session");
+    if (on && s->len != 0) return fail(NH_EINVAL, "cell tracking starts at an empty session");
+    if (on && !s->d_cells) {
+        NH_TRY(hipMalloc(&s->d_cells, (size_t)s->dims.cap * s->cell_floats() * 4), "cells allocation");
+    }
+    s->track_cells = on != 0;
+    s->ncells = 0;
+    return NH_OK;
+}
+
+int nh_session_cell_rows(const nh_session* s) {
+    if (!s) return fail(NH_EINVAL, "null session");
+    if (!s->track_cells) return fail(NH_EINVAL, "the session does not track cells");
+    return s->ncells;
+}
+
+int nh_session_cells(const nh_session* s, int row0, int n, float* dst, void* stream) {
+    if (!s || row0 < 0 || n < 0 || (n > 0 && !dst)) return fail(NH_EINVAL, "bad arguments");
+    if (!s->track_cells) return fail(NH_EINVAL, "the session does not track cells");
+    if (row0 + n > s->ncells) return fail(NH_EINVAL, "rows past the tracked cells");
+    const size_t cw = s->cell_floats();
+    if (n > 0)
+        NH_TRY(hipMemcpyAsync(dst, s->d_cells + (size_t)row0 * cw, (size_t)n * cw * 4, hipMemcpyDeviceToDevice,
+                              (hipStream_t)stream),
+               "cells");
+    return n;
+}
+
+int nh_session_debug_fail_feed(nh_session* s, int after) {
+    if (!s || after < 0) return fail(NH_EINVAL, "bad arguments");
+    s->fail_in = after;
     return NH_OK;
 }
 
@@ -873,6 +971,30 @@ int nh_session_clone(const nh_session* s, void* stream, nh_session** out) {
     c->ring = s->ring;
     c->slot_pos = s->slot_pos;
     c->toks = s->toks;
+    c->dims.spin_limit = s->dims.spin_limit;
+    if (s->track_cells) {
+        c->track_cells = true;
+        c->ncells = s->ncells;
+        e = hipMalloc(&c->d_cells, (size_t)c->dims.cap * c->cell_floats() * 4);
+        if (e == hipSuccess && s->ncells > 0)
+            e = hipMemcpyAsync(c->d_cells, s->d_cells, (size_t)s->ncells * s->cell_floats() * 4,
+                               hipMemcpyDeviceToDevice, st);
+        if (e != hipSuccess) {
+            delete c;
+            return hip_fail(e, "session clone (cells)");
+        }
+    }
+    // A bounded wait of the source that gave up and has not been reported
+    // yet would travel with the copy: refuse, so the failure is reported by
+    // the source's own next feed.
+    int32_t word = 0;
+    e = hipMemcpyAsync(&word, c->S.status, 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess || word != 0) {
+        delete c;
+        if (e != hipSuccess) return hip_fail(e, "session clone");
+        return fail(NH_EDEVICE, "the source session has a failed bounded wait not yet reported (its next feed reports it)");
+    }
     *out = c;
     return NH_OK;
 }
@@ -885,10 +1007,7 @@ int nh_session_debug_spin_limit(nh_session* s, int limit) {
 
 int nh_session_set_attend(nh_session* s, int sink, int ring) {
     if (!s || sink < 0 || ring < 0) return fail(NH_EINVAL, "bad arguments");
-    // A shorter ring would give two rows of a 32-token chunk one KV slot (the
-    // reference's team races on it) and could leave a row no key at all (its
-    // attend_head_ref panics on step_by(0)).
-    if (ring > 0 && ring < nh::FWD_ROWS) return fail(NH_EINVAL, "an attention ring shorter than a 32-token chunk");
+    // (a ring shorter than a chunk takes only feeds that fit it: check_ring)
     s->sink = ring > 0 ? sink : 0;
     s->ring = ring;
     return NH_OK;
@@ -904,6 +1023,7 @@ int nh_session_rollback(nh_session* s, int n) {
     s->rope_n = std::max(0, s->rope_n - n);
     s->toks.resize(s->len);
     s->have_logits = false;
+    truncate_cells(s, s->len);
     return NH_OK;
 }
 
@@ -916,6 +1036,7 @@ int nh_session_rewind_zeroed(nh_session* s, int len) {
     }
     s->hrows = 0;
     s->rope_n = 0;
+    truncate_cells(s, len);
     return NH_OK;
 }
 
@@ -959,8 +1080,19 @@ int nh_forward_outputs(nh_session* s, const uint32_t* toks, int n, int outputs, 
                        void* stream) {
     if (int rc = check_feed(s, toks, n, outputs)) return rc;
     if (int rc = check_out(s, n, outputs, out, out_cap)) return rc;
+    if (int rc = check_ring(s, n)) return rc;
     if (n == 0) return 0;
-    return forward_ids(s, toks, n, outputs, out, (hipStream_t)stream);
+    return forward_ids(s, toks, n, outputs, out, s->track_cells, nullptr, (hipStream_t)stream);
+}
+
+int nh_forward_cells(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, int64_t out_cap,
+                     float* cells, int64_t cells_cap, void* stream) {
+    if (int rc = check_feed(s, toks, n, outputs)) return rc;
+    if (int rc = check_out(s, n, outputs, out, out_cap)) return rc;
+    if (int rc = check_cells(s, n, cells, cells_cap)) return rc;
+    if (int rc = check_ring(s, n)) return rc;
+    if (n == 0) return 0;
+    return forward_ids(s, toks, n, outputs, out, true, cells, (hipStream_t)stream);
 }
 
 int nh_prefill(nh_session* s, const uint32_t* toks, int n, int outputs, float* out, int64_t out_cap, void* stream) {
@@ -976,12 +1108,15 @@ int nh_prefill(nh_session* s, const uint32_t* toks, int n, int outputs, float* o
             std::vector<uint32_t> refeed(s->toks.begin() + p, s->toks.begin() + pos);
             refeed.insert(refeed.end(), toks, toks + n);
             if (int rc = check_out(s, (int)refeed.size(), outputs, out, out_cap)) return rc;
+            if (int rc = check_ring(s, (int)refeed.size())) return rc;
             nh_session_rewind_zeroed(s, p);
-            return forward_ids(s, refeed.data(), (int)refeed.size(), outputs, out, (hipStream_t)stream);
+            return forward_ids(s, refeed.data(), (int)refeed.size(), outputs, out, false, nullptr,
+                               (hipStream_t)stream);
         }
     }
+    if (int rc = check_ring(s, n)) return rc;
     if (n == 0) return 0;
-    return forward_ids(s, toks, n, outputs, out, (hipStream_t)stream);
+    return forward_ids(s, toks, n, outputs, out, false, nullptr, (hipStream_t)stream);
 }
 
 int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* stream) {
@@ -992,7 +1127,8 @@ int nh_forward(nh_session* s, const uint32_t* toks, int n, float* logits, void* 
         if (!logits) return NH_OK;
         if (!s->have_logits) return fail(NH_EINVAL, "no tokens and no logits of an earlier feed");
     } else {
-        const int r = forward_ids(s, toks, n, NH_OUT_LAST_LOGITS, nullptr, st);
+        if (int rc = check_ring(s, n)) return rc;
+        const int r = forward_ids(s, toks, n, NH_OUT_LAST_LOGITS, nullptr, s->track_cells, nullptr, st);
         if (r < 0) return r;
     }
     if (logits)
@@ -1017,8 +1153,10 @@ int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, v
     const int len0 = s->len;
     for (int i = 0; i < steps; ++i) {
         NH_TRY(nh::fwd_argmax(s->S.logits, s->dims.out_rows, s->S.tokens + s->len, st), "argmax");
-        const int r = feed(s, 1, NH_OUT_LAST_LOGITS, nullptr, st);
-        if (r < 0) return r;
+        float* cdst = s->track_cells ? s->d_cells + (size_t)s->ncells * s->cell_floats() : nullptr;
+        const int r = feed(s, 1, NH_OUT_LAST_LOGITS, nullptr, cdst, st);
+        if (r < 0) return reset_after(s, r);
+        if (cdst) ++s->ncells;
     }
     if (logits)
         NH_TRY(hipMemcpyAsync(logits, s->S.logits, (size_t)s->dims.out_rows * 4, hipMemcpyDeviceToDevice, st),

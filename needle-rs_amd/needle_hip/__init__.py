@@ -68,6 +68,11 @@ SIGNATURES = {
     "nh_session_reset": (I, [P]),
     "nh_forward": (I, [P, P, I, P, P]),
     "nh_forward_outputs": (I, [P, P, I, I, P, C.c_int64, P]),
+    "nh_forward_cells": (I, [P, P, I, I, P, C.c_int64, P, C.c_int64, P]),
+    "nh_session_track_cells": (I, [P, I]),
+    "nh_session_cell_rows": (I, [P]),
+    "nh_session_cells": (I, [P, I, I, P, P]),
+    "nh_session_debug_fail_feed": (I, [P, I]),
     "nh_prefill": (I, [P, P, I, I, P, C.c_int64, P]),
     "nh_session_clone": (I, [P, P, P]),
     "nh_session_set_attend": (I, [P, I, I]),
@@ -416,6 +421,7 @@ class Model:
         words = np.zeros(49, dtype=np.uint32)
         _check(_lib.nh_weights_header(w.value, _hptr(words), 49))
         self.d_model = int(words[7])  # the header's d_model word (cact.rs:80-118)
+        self.layers = int(words[10])  # num_layers
 
     @property
     def weights(self) -> "QWeights":
@@ -487,6 +493,36 @@ class Session:
             _check(_lib.nh_forward(self.h, _hptr(toks), toks.size, _dptr(logits), _stream(stream)))
             return logits
         return self._feed(_lib.nh_forward_outputs, tokens, outputs, stream)
+
+    def forward_cells(self, tokens, outputs: int = OUT_NONE, stream=None):
+        """Model::forward_cells (model.rs:330-345): (the rows `outputs` selects,
+        [rows][width], the feed's cells [n][L+1][d]), both on the device."""
+        toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(-1))
+        rows = toks.size if outputs in (OUT_ALL_LOGITS, OUT_HIDDEN) else (1 if outputs != OUT_NONE else 0)
+        width = self._width(outputs)
+        out = torch.empty(max(rows, 1) * width, dtype=torch.float32, device="cuda")
+        cw = (self.model.layers + 1) * self.model.d_model
+        cells = torch.empty(max(toks.size, 1) * cw, dtype=torch.float32, device="cuda")
+        r = _check(_lib.nh_forward_cells(self.h, _hptr(toks), toks.size, int(outputs), _dptr(out), out.numel(),
+                                         _dptr(cells), cells.numel(), _stream(stream)))
+        return out[:r * width].view(r, width), cells[:toks.size * cw].view(toks.size, self.model.layers + 1,
+                                                                            self.model.d_model)
+
+    def track_cells(self, on: bool = True):
+        """Session::cells = Some(vec![]) (on, at an empty session) or None (model.rs:60-62)."""
+        _check(_lib.nh_session_track_cells(self.h, int(bool(on))))
+
+    def cells(self, stream=None) -> torch.Tensor:
+        """Session::cells: the tracked rows [rows][L+1][d] (device)."""
+        n = _check(_lib.nh_session_cell_rows(self.h))
+        cw = (self.model.layers + 1) * self.model.d_model
+        out = torch.empty(max(n, 1) * cw, dtype=torch.float32, device="cuda")
+        _check(_lib.nh_session_cells(self.h, 0, n, _dptr(out), _stream(stream)))
+        return out[:n * cw].view(n, self.model.layers + 1, self.model.d_model)
+
+    def debug_fail_feed(self, after: int):
+        """Test hook: the `after`-th feed from now fails before it launches (0: off)."""
+        _check(_lib.nh_session_debug_fail_feed(self.h, int(after)))
 
     def prefill(self, tokens, outputs: int = OUT_LAST_LOGITS, stream=None) -> torch.Tensor:
         """Model::prefill on the native path (prefill_native, infer.rs:1078-1101)."""

@@ -11,8 +11,10 @@
  * Model::prefill_native's stale-slot re-feed (infer.rs:1078-1101), the
  * session attention span (sink, ring) with its KV slot ring and slot map
  * (model.rs:62-66, infer.rs:1749-1826), Session::rollback / rewind_zeroed /
- * clone (model.rs:81-121, infer.rs:1039-1071) and the head functions
- * (infer.rs:1135-1166).  No cells.
+ * clone (model.rs:81-121, infer.rs:1039-1071), the head functions
+ * (infer.rs:1135-1166) and the per-depth cells of Model::forward_cells and
+ * a tracking session (model.rs:60-62,330-345; infer/step.rs:240-243,
+ * 672-714; infer/chunk.rs:69-70,310,353-356; infer.rs:1105-1130).
  *
  * libm: off Apple targets the reference computes its f32 functions in f64
  * with the Rust `libm` crate (0.2.16, Cargo.lock:647-650) and rounds once
@@ -311,6 +313,11 @@ struct nf_session {
     /* NatState::last_hidden (infer.rs:996-998) */
     float* last_hidden;
     int have_hidden;
+    /* Session::cells (model.rs:60-62): when tracked, the cell rows
+     * [ncells][L+1][d] the feeds appended (room for cap rows) */
+    int track_cells;
+    float* cells;
+    size_t ncells;
 };
 
 static uint16_t* dup16(const uint16_t* p, size_t n) {
@@ -468,7 +475,7 @@ void nf_session_free(const nf_model* m, nf_session* s) {
     for (int l = 0; l < m->c.layers; ++l) free(s->k8[l]), free(s->ks[l]), free(s->v8t[l]), free(s->vs[l]), free(s->hist[l]);
     for (int e = 0; e < m->c.sites; ++e) free(s->ev8[e]), free(s->evs[e]);
     free(s->k8), free(s->ks), free(s->v8t), free(s->vs), free(s->hist), free(s->ev8), free(s->evs);
-    free(s->tokens), free(s->rope_c), free(s->rope_s), free(s->slot_pos), free(s->last_hidden);
+    free(s->tokens), free(s->rope_c), free(s->rope_s), free(s->slot_pos), free(s->last_hidden), free(s->cells);
     free(s);
 }
 
@@ -507,17 +514,18 @@ nf_session* nf_session_clone(const nf_model* m, const nf_session* s) {
     o->rope_s = (float*)dupb(s->rope_s, cap * 32 * 4);
     o->slot_pos = (int64_t*)dupb(s->slot_pos, cap * 8);
     o->last_hidden = (float*)dupb(s->last_hidden, (size_t)c->d * 4);
+    o->cells = s->cells ? (float*)dupb(s->cells, cap * (size_t)(c->layers + 1) * c->d * 4) : NULL;
     return o;
 }
 
 size_t nf_session_len(const nf_session* s) { return s->len; }
 
-/* Session::attend (model.rs:62-66): ring 0 is None.  A ring shorter than a
- * 32-token chunk is refused: two rows of one chunk would share a KV slot
- * (the reference's members race on it) and a row could see no key at all
+/* Session::attend (model.rs:62-66): ring 0 is None.  Any ring is taken; a
+ * feed with a chunk longer than a ring shorter than 32 is refused
+ * (nf_forward): two rows of that chunk would share a KV slot (the
+ * reference's members race on it) and a row could see no key at all
  * (attend_head_ref's step_by(0) panics). */
 int nf_session_set_attend(nf_session* s, size_t sink, size_t ring) {
-    if (ring > 0 && ring < 32) return -1;
     s->sink = sink;
     s->ring = ring;
     return 0;
@@ -533,6 +541,7 @@ int nf_session_rollback(const nf_model* m, nf_session* s, size_t n) {
     s->len -= n;
     s->hrows = s->hrows > n ? s->hrows - n : 0;
     s->rope_n = s->rope_n > n ? s->rope_n - n : 0; /* rope.retain(p < len) */
+    if (s->ncells > s->len) s->ncells = s->len;  /* cells.truncate(len (L+1) d) */
     return 0;
 }
 
@@ -544,7 +553,28 @@ int nf_session_rewind_zeroed(const nf_model* m, nf_session* s, size_t len) {
     if (len < s->len) s->len = len;
     s->hrows = 0;
     s->rope_n = 0;
+    if (s->ncells > len) s->ncells = len;  /* cells.truncate(len (L+1) d) */
     return 0;
+}
+
+/* Session::cells = Some(vec![]) (on) or None (off).  Tracking starts at an
+ * empty session: the store's truncations (rollback, rewind_zeroed, prefill's
+ * re-feed) index it by position. */
+int nf_session_track_cells(const nf_model* m, nf_session* s, int on) {
+    if (on && s->len != 0) return -1;
+    s->track_cells = on != 0;
+    s->ncells = 0;
+    if (on && !s->cells) s->cells = (float*)calloc(s->cap * (size_t)(m->c.layers + 1) * m->c.d, sizeof(float));
+    return 0;
+}
+
+/* The tracked cell rows [row0, row0 + n) into dst[n][L+1][d]; the count of
+ * rows held, or -1 (not tracking, or past the end). */
+int nf_session_cells(const nf_model* m, const nf_session* s, size_t row0, size_t n, float* dst) {
+    if (!s->track_cells || row0 + n > s->ncells) return -1;
+    const size_t w = (size_t)(m->c.layers + 1) * m->c.d;
+    if (n) memcpy(dst, s->cells + row0 * w, n * w * sizeof(float));
+    return (int)s->ncells;
 }
 
 /* NatState::last_hidden into out[d]; 0, or -1 when no feed has set it. */
@@ -842,8 +872,13 @@ int nf_head_logits_sparse(const nf_model* m, const float* h, const uint32_t* ids
  * attention chunking (nested, infer.rs:1888).  `outputs` (NF_OUT_*) picks
  * what goes to `out` (chunk.rs:331-353, step.rs:715-729): logits [rows]
  * [out_rows] or hidden states [rows][d]; returns the rows written, or -1. */
+/* One feed of t tokens (step_native for one, chunk_job for a chunk).
+ * `cells` (or NULL): the feed's cells [t][L+1][d], the lane mean
+ * (((x0 + x1) + x2) + x3) * 0.25 of every row after the embedding and after
+ * each layer's mHC write (step.rs:240-243,672-714; chunk.rs:69-70,310;
+ * lane_mean, infer.rs:1707-1711). */
 static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_t t, int outputs, float* outbuf,
-                   int nthreads) {
+                   float* cells, int nthreads) {
     const nf_config* c = &m->c;
     const int n = c->lanes, d = c->d, nc = n * d, L = c->layers;
     const int qk = c->qk, vd = c->vd, nh = c->nh, nkv = c->nkv;
@@ -872,6 +907,15 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
         for (int lane = 0; lane < n; ++lane)
             for (int k = 0; k < d; ++k) xs[i * nc + lane * d + k] = row[k] * scale;
     }
+    const size_t depths = (size_t)L + 1;
+#define NF_CELLS(depth)                                                                                  \
+    if (cells)                                                                                           \
+        for (size_t i = 0; i < t; ++i) {                                                                 \
+            const float* x = xs + i * nc;                                                                \
+            float* cr = cells + (i * depths + (depth)) * d;                                              \
+            for (int ch = 0; ch < d; ++ch) cr[ch] = (((x[ch] + x[d + ch]) + x[2 * d + ch]) + x[3 * d + ch]) * 0.25f; \
+        }
+    NF_CELLS(0)
 
     /* engram rows and their key|value products over the t rows, value
      * history and conv (engram_native, infer.rs:1244-1335) */
@@ -1071,7 +1115,9 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
             for (int ch = 0; ch < d; ++ch) z[ch] = (x2[ch] + t3[ch] * cq_f16_to_f32(Lw->d4[ch])) - u[i * d + ch];
             nf_mhc_write(d, z, hpost, hres, x);
         }
+        NF_CELLS((size_t)l + 1)
     }
+#undef NF_CELLS
 
     /* the history rows this feed wrote, then the trim (chunk.rs:319-329,
      * step.rs:706-712) */
@@ -1110,39 +1156,69 @@ done:
 }
 
 int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int nthreads) {
-    const int r = nf_rows(m, s, &tok, 1, logits ? NF_OUT_LAST_LOGITS : NF_OUT_NONE, logits, nthreads);
+    const int r = nf_rows(m, s, &tok, 1, logits ? NF_OUT_LAST_LOGITS : NF_OUT_NONE, logits, NULL, nthreads);
     return r < 0 ? -1 : 0;
 }
 
 int nf_chunk(const nf_model* m, nf_session* s, const uint32_t* toks, size_t t, float* logits, int nthreads) {
-    const int r = nf_rows(m, s, toks, t, logits ? NF_OUT_LAST_LOGITS : NF_OUT_NONE, logits, nthreads);
+    const int r = nf_rows(m, s, toks, t, logits ? NF_OUT_LAST_LOGITS : NF_OUT_NONE, logits, NULL, nthreads);
     return r < 0 ? -1 : 0;
 }
 
 /* Model::forward_native (infer.rs:1105-1132): chunks of 32, a one-token
  * chunk as a step; LastLogits / LastHidden only from the last chunk.
- * Returns the rows written to `out`, or -1. */
-int nf_forward(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out, int nthreads) {
+ * want_cells: the cells are computed (into `cells` [n][L+1][d] when not
+ * NULL, and appended to a tracking session's store, step.rs:730-732,
+ * chunk.rs:353-355).  A ring shorter than 32 with a chunk longer than it is
+ * refused (nf_session_set_attend).  Returns the rows written to `out`, or -1. */
+static int forward_native(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out,
+                          int want_cells, float* cells, int nthreads) {
     if (outputs < NF_OUT_NONE || outputs > NF_OUT_LAST_HIDDEN || s->len + n > s->cap) return -1;
+    if (s->ring > 0 && s->ring < 32 && n > s->ring) return -1;
     const size_t width = (outputs == NF_OUT_HIDDEN || outputs == NF_OUT_LAST_HIDDEN) ? (size_t)m->c.d
                                                                                     : (size_t)m->c.out_rows;
+    const size_t cw = (size_t)(m->c.layers + 1) * m->c.d;
+    float* tmp = want_cells ? (float*)malloc(32 * cw * sizeof(float)) : NULL;
     int rows = 0;
     for (size_t i = 0; i < n; i += 32) {
         const size_t t = n - i < 32 ? n - i : 32;
         const int last = i + t == n;
         const int want = (!last && (outputs == NF_OUT_LAST_LOGITS || outputs == NF_OUT_LAST_HIDDEN)) ? NF_OUT_NONE
                                                                                                        : outputs;
-        const int r = nf_rows(m, s, toks + i, t, want, out ? out + (size_t)rows * width : NULL, nthreads);
-        if (r < 0) return -1;
+        const int r = nf_rows(m, s, toks + i, t, want, out ? out + (size_t)rows * width : NULL, tmp, nthreads);
+        if (r < 0) {
+            free(tmp);
+            return -1;
+        }
+        if (tmp && cells) memcpy(cells + i * cw, tmp, t * cw * sizeof(float));
+        if (tmp && s->track_cells) {
+            memcpy(s->cells + s->ncells * cw, tmp, t * cw * sizeof(float));
+            s->ncells += t;
+        }
         rows += r;
     }
+    free(tmp);
     return rows;
+}
+
+/* Model::forward (model.rs:304-306): cells when the session tracks them. */
+int nf_forward(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out, int nthreads) {
+    return forward_native(m, s, toks, n, outputs, out, s->track_cells, NULL, nthreads);
+}
+
+/* Model::forward_cells (model.rs:330-345): as nf_forward, with the feed's
+ * cells [n][L+1][d] in `cells`. */
+int nf_forward_cells(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out,
+                     float* cells, int nthreads) {
+    return forward_native(m, s, toks, n, outputs, out, 1, cells, nthreads);
 }
 
 /* Model::prefill_native (infer.rs:1078-1101): with an attention span and
  * a slot map, the first position in max(end - ring, sink) .. len whose
  * slot another position holds now starts a re-feed with the conv history
- * zeroed (rewind_zeroed); else forward_native. */
+ * zeroed (rewind_zeroed, which also truncates tracked cells); else
+ * forward_native.  Either way forward_native runs with want_cells = false,
+ * so a prefill appends no cells to a tracking session. */
 int nf_prefill(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out, int nthreads) {
     const size_t pos = s->len, end = pos + n;
     if (s->ring > 0 && s->nslot > 0) {
@@ -1156,11 +1232,15 @@ int nf_prefill(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n,
             uint32_t* refeed = (uint32_t*)malloc((k + n + 1) * 4);
             memcpy(refeed, s->tokens + p, k * 4);
             if (n) memcpy(refeed + k, toks, n * 4);
+            if (s->ring < 32 && k + n > s->ring) {
+                free(refeed);
+                return -1;
+            }
             nf_session_rewind_zeroed(m, s, p);
-            const int r = nf_forward(m, s, refeed, k + n, outputs, out, nthreads);
+            const int r = forward_native(m, s, refeed, k + n, outputs, out, 0, NULL, nthreads);
             free(refeed);
             return r;
         }
     }
-    return nf_forward(m, s, toks, n, outputs, out, nthreads);
+    return forward_native(m, s, toks, n, outputs, out, 0, NULL, nthreads);
 }

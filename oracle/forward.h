@@ -61,6 +61,12 @@ int nf_session_last_hidden(const nf_model* m, const nf_session* s, float* out);
 /* Model::forward / Model::prefill on the native path: rows written or -1. */
 int nf_forward(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out, int nthreads);
 int nf_prefill(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out, int nthreads);
+/* Model::forward_cells (model.rs:330-345): also the feed's cells [n][L+1][d]. */
+int nf_forward_cells(const nf_model* m, nf_session* s, const uint32_t* toks, size_t n, int outputs, float* out,
+                     float* cells, int nthreads);
+/* Session::cells = Some(vec![]) / None (at an empty session); the tracked rows. */
+int nf_session_track_cells(const nf_model* m, nf_session* s, int on);
+int nf_session_cells(const nf_model* m, const nf_session* s, size_t row0, size_t n, float* dst);
 void nf_head_logits(const nf_model* m, const float* h, float* logits, int nthreads);
 int nf_head_logits_sparse(const nf_model* m, const float* h, const uint32_t* ids, size_t n, float* logits);
 int nf_attend_test(const nf_model* m, nf_session* s, const int8_t* k8, const float* ks, const int8_t* v8,

@@ -70,6 +70,9 @@ def _lib():
             "nf_session_last_hidden": (C.c_int, [P, P, P]),
             "nf_forward": (C.c_int, [P, P, P, C.c_size_t, C.c_int, P, C.c_int]),
             "nf_prefill": (C.c_int, [P, P, P, C.c_size_t, C.c_int, P, C.c_int]),
+            "nf_forward_cells": (C.c_int, [P, P, P, C.c_size_t, C.c_int, P, P, C.c_int]),
+            "nf_session_track_cells": (C.c_int, [P, P, C.c_int]),
+            "nf_session_cells": (C.c_int, [P, P, C.c_size_t, C.c_size_t, P]),
             "nf_head_logits": (None, [P, P, P, C.c_int]),
             "nf_head_logits_sparse": (C.c_int, [P, P, P, C.c_size_t, P]),
             "nf_attend_test": (C.c_int, [P, P, P, P, P, P, C.c_size_t, P, C.c_int, P]),
@@ -298,6 +301,35 @@ class Session:
         """Model::prefill on the native path (prefill_native, infer.rs:1078-1101)."""
         return self._run(_lib().nf_prefill, toks, outputs)
 
+    def forward_cells(self, toks, outputs: int = OUT_NONE):
+        """Model::forward_cells (model.rs:330-345): (the rows `outputs`
+        selects, the feed's cells [t][L+1][d])."""
+        t = np.ascontiguousarray(np.asarray(toks, dtype=np.uint32).reshape(-1))
+        rows_max = t.size if outputs in (OUT_ALL_LOGITS, OUT_HIDDEN) else 1
+        out = np.zeros((max(rows_max, 1), self._width(outputs)), dtype=np.float32)
+        cells = np.zeros((t.size, self.f.cfg.layers + 1, self.f.cfg.d), dtype=np.float32)
+        r = _lib().nf_forward_cells(self.f.m, self.s, _p(t), t.size, int(outputs), _p(out), _p(cells),
+                                    self.f.threads)
+        if r < 0:
+            raise ValueError("feed outside the session's capacity, geometry or key runs")
+        return out[:r], cells
+
+    def track_cells(self, on: bool = True):
+        """Session::cells = Some(vec![]) (on, at an empty session) or None."""
+        if _lib().nf_session_track_cells(self.f.m, self.s, int(bool(on))) != 0:
+            raise ValueError("cell tracking starts at an empty session")
+
+    def cells(self) -> np.ndarray:
+        """Session::cells: the tracked rows [rows][L+1][d]."""
+        l = _lib()
+        n = l.nf_session_cells(self.f.m, self.s, 0, 0, None)
+        if n < 0:
+            raise ValueError("the session does not track cells")
+        out = np.zeros((n, self.f.cfg.layers + 1, self.f.cfg.d), dtype=np.float32)
+        if n and l.nf_session_cells(self.f.m, self.s, 0, n, _p(out)) < 0:
+            raise ValueError("the session does not track cells")
+        return out
+
     def feed(self, toks) -> np.ndarray:
         """Model::forward with Outputs::LastLogits: the last row's logits."""
         return self.forward(toks, OUT_LAST_LOGITS)[0]
@@ -305,7 +337,7 @@ class Session:
     def set_attend(self, sink: int, ring: int):
         """Session::attend = Some((sink, ring)) (ring 0: None)."""
         if _lib().nf_session_set_attend(self.s, int(sink), int(ring)) != 0:
-            raise ValueError("attention ring shorter than a 32-token chunk")
+            raise ValueError("bad attention span")
 
     def rollback(self, n: int):
         if _lib().nf_session_rollback(self.f.m, self.s, int(n)) != 0:

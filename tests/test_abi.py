@@ -28,7 +28,7 @@ def test_library_exports_every_declared_symbol():
     lib = needle_hip.load_library()
     for name in declared():
         assert hasattr(lib, name), name
-    assert lib.nh_version() == 100
+    assert lib.nh_version() == 101
 
 
 def test_calls_before_init_fail_cleanly():

@@ -6,7 +6,9 @@ archive writer, seed 0) against the oracle on the same archive.
   steps (argmax, first maximum, crates/needle-engine/src/generate.rs:42-50)
   fed one token at a time; every step's logits are compared;
 - prefill: one sequence of 512 random tokens (16 chunks of 32) and its last
-  logits, then one step.
+  logits, then one step;
+- cells: the per-depth lane means of a 70-token prompt and two steps
+  (Model::forward_cells, crates/needle-engine/src/model.rs:330-345).
 
 The logits must be bit-identical (the device follows the reference's float
 order; see test_gpu_forward.py), the greedy picks equal; the max-abs and
@@ -99,4 +101,24 @@ def test_needle3_prefill_512(nh):
     t = int(np.argmax(want))
     e.add(s.forward([t]).cpu().numpy(), os_.step(t))
     say(f"prefill 512 + 1: {e}")
+    assert e.exact == e.n, str(e)
+
+
+def test_needle3_cells(nh):
+    say("Needle-3 cells (heads::cells: a fresh session, Outputs None) of a 70-token prompt, then 2 steps")
+    data = needle3(nh)
+    m = nh.Model.from_archive(data)
+    f = forward.Forward(data)
+    toks = np.random.default_rng(2).integers(0, m.out_rows, 72).astype(np.uint32)
+    s, os_ = m.session(128), f.session(128)
+    e = Err()
+    _, gc = s.forward_cells(toks[:70])
+    _, wc = os_.forward_cells(toks[:70])
+    e.add(gc.cpu().numpy(), wc)
+    for t in toks[70:]:
+        go, gc = s.forward_cells([int(t)], forward.OUT_LAST_LOGITS)
+        wo, wc = os_.forward_cells([int(t)], forward.OUT_LAST_LOGITS)
+        e.add(go.cpu().numpy(), wo)
+        e.add(gc.cpu().numpy(), wc)
+    say(f"cells 70 + 2: {e}")
     assert e.exact == e.n, str(e)

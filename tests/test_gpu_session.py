@@ -13,7 +13,15 @@ the same operations on the same archive (bit-identical at every step).
   (infer.rs:1135-1166, agent.rs:398-409);
 - the conv tap counts 1, 2, 4, 6 (the exact and the clamped unit kernels),
   with a one-token prompt and a prompt past one chunk;
-- a geometry with more taps than the kernels take is refused at load.
+- a geometry with more taps than the kernels take is refused at load;
+- a ring shorter than a chunk (feeds that fit it; a longer one refused);
+- cells (Model::forward_cells and a tracking session, model.rs:60-62,
+  108-123,330-345): fresh-session cells of a batched feed, steps and chunks
+  in every Outputs mode, the tracked store across rollback, clone, rewind,
+  prefill and the greedy loop;
+- failure paths: a greedy step or a feed that fails part way (injected from
+  the host) resets the session and keeps its span; a clone of a session
+  whose failed wait is unreported is refused.
 """
 import sys
 
@@ -173,8 +181,11 @@ def test_attention_span(nh, stepwise):
     p.steps(o.random_tokens(3, 300, seed=63), label="tail")
     p.heads([1, 2, 3])
     p.done(f"attention span {'steps' if stepwise else 'chunks'}")
-    with pytest.raises(nh.NeedleHipError, match="shorter than a 32-token chunk"):
-        p.g.set_attend(6, 16)
+    q = Pair(nh, data, 64)
+    q.attend(6, 16)  # a ring shorter than a chunk takes only feeds that fit it
+    with pytest.raises(nh.NeedleHipError, match="longer than an attention ring"):
+        q.g.forward(toks[:17])
+    assert len(q.g) == 0
 
 
 def test_attention_span_long(nh):
@@ -239,6 +250,115 @@ def test_bounded_wait_gives_up_and_reports(nh):
     got = s.forward([5, 6, 7]).cpu().numpy()
     want = forward.Forward(data).session(32).feed([5, 6, 7])
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # a clone of a session whose failed wait is not yet reported is refused,
+    # and the source's next feed reports it
+    s.debug_spin_limit(0)
+    s.forward([8, 9])
+    with pytest.raises(nh.NeedleHipError, match="not yet reported"):
+        s.clone()
+    s.debug_spin_limit(1 << 20)
+    torch.cuda.synchronize()
+    with pytest.raises(nh.NeedleHipError, match="gave up"):
+        s.forward([3])
+    assert len(s) == 0
+
+
+def test_failed_greedy_step_resets(nh):
+    say("a greedy step that fails part way (injected from the host) resets the session, keeping its span; "
+        "a prefill and steps then match a fresh oracle session")
+    data = archive(cact.Geometry(**SMALL), seed=84)
+    p = Pair(nh, data, 128)
+    p.attend(6, 32)
+    toks = o.random_tokens(60, 300, seed=85)
+    p.fwd(toks[:40])
+    p.g.debug_fail_feed(3)
+    with pytest.raises(nh.NeedleHipError, match="on purpose"):
+        p.g.generate_greedy(5)
+    assert len(p.g) == 0
+    p.o = p.f.session(128)
+    p.o.set_attend(6, 32)
+    p.prefill(toks[:40], label="prefill after the reset")
+    p.steps(toks[40:50], label="step after the reset")  # past the ring: the span was kept
+    p.g.debug_fail_feed(1)
+    with pytest.raises(nh.NeedleHipError, match="on purpose"):
+        p.g.forward(toks[50:53])
+    assert len(p.g) == 0
+    p.o = p.f.session(128)
+    p.o.set_attend(6, 32)
+    p.fwd(toks[:45], label="forward after the reset")
+    p.done("failed feeds")
+
+
+def test_short_ring(nh):
+    say("attention span with a ring of 8 (sink 3): feeds that fit the ring, steps, rollbacks, prefill re-feed")
+    data = archive(cact.Geometry(**SMALL), seed=86)
+    p = Pair(nh, data, 96)
+    p.attend(3, 8)
+    toks = o.random_tokens(60, 300, seed=87)
+    p.fwd(toks[:6])
+    p.steps(toks[6:30])
+    p.fwd(toks[30:38], forward.OUT_ALL_LOGITS, label="a feed of 8")
+    p.rollback(4)
+    p.steps(toks[38:41], label="after rollback")
+    p.prefill(toks[41:44], label="prefill")
+    p.steps(toks[44:50], label="tail")
+    p.heads([1, 2, 3])
+    with pytest.raises(nh.NeedleHipError, match="longer than an attention ring"):
+        p.g.forward(toks[50:59])
+    p.done("short ring")
+
+
+def test_cells(nh):
+    say("cells: forward_cells on a fresh session (a batched feed of 101 rows, Outputs None), steps and chunks "
+        "with outputs, a tracking session across rollback, clone, rewind, prefill and the greedy loop")
+    data = archive(cact.Geometry(**SMALL), seed=88)
+    p = Pair(nh, data, 200)
+    toks = o.random_tokens(140, 300, seed=89)
+    go, gc = p.g.forward_cells(toks[:101])
+    wo, wc = p.o.forward_cells(toks[:101])
+    assert go.shape[0] == 0 and gc.shape == wc.shape
+    same("cells of a batched feed", gc.cpu().numpy(), wc, p.stats)
+    for i, t in enumerate(toks[101:104]):
+        go, gc = p.g.forward_cells([int(t)], forward.OUT_LAST_LOGITS)
+        wo, wc = p.o.forward_cells([int(t)], forward.OUT_LAST_LOGITS)
+        same(f"step {i} logits", go.cpu().numpy(), wo, p.stats)
+        same(f"step {i} cells", gc.cpu().numpy(), wc, p.stats)
+    for mode in (forward.OUT_ALL_LOGITS, forward.OUT_HIDDEN, forward.OUT_LAST_HIDDEN):
+        go, gc = p.g.forward_cells(toks[104:111], mode)
+        wo, wc = p.o.forward_cells(toks[104:111], mode)
+        same(f"chunk mode {mode}", go.cpu().numpy(), wo, p.stats)
+        same(f"chunk mode {mode} cells", gc.cpu().numpy(), wc, p.stats)
+        p.rollback(7)
+    p.done("forward_cells")
+
+    q = Pair(nh, data, 200)
+    q.g.track_cells()
+    q.o.track_cells()
+
+    def cells(label, pair=None):
+        pair = pair or q
+        same(label, pair.g.cells().cpu().numpy(), pair.o.cells(), q.stats)
+
+    q.fwd(toks[:70])  # one batched feed of 70 rows (chunks of 32, 32 and 6)
+    q.steps(toks[70:75])
+    cells("tracked after feeds")
+    q.rollback(3)
+    cells("tracked after rollback")
+    c = q.clone()
+    q.rewind_zeroed(50)
+    cells("tracked after rewind")
+    cells("clone", c)
+    c.prefill(toks[75:80])  # appends nothing
+    cells("clone after prefill", c)
+    q.fwd(toks[80:84])
+    want = q.o.forward(toks[84:86])[0]
+    q.g.forward(toks[84:86])
+    picks, _ = q.g.generate_greedy(4)
+    for k in picks:
+        assert int(k) == int(np.argmax(want))
+        want = q.o.forward([int(k)])[0]
+    cells("tracked after the greedy loop")
+    q.done("tracked cells")
 
 
 def test_greedy_picks_into_pinned_memory(nh):

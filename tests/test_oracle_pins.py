@@ -424,8 +424,11 @@ def test_attention_span_receptive_field():
     for feed in (stepwise, chunk):
         seen = [p for p in probe if visible_changes(f, feed, p, sink, ring, n)]
         assert seen == [p for p in probe if p < sink or p >= n - ring], (feed.__name__, seen)
+    s = f.session(64)
+    s.set_attend(4, 16)  # a ring shorter than a chunk takes feeds that fit it
     with pytest.raises(ValueError):
-        f.session(64).set_attend(4, 16)  # a ring shorter than a chunk
+        s.forward(o.random_tokens(17, 300, seed=43))
+    assert len(s) == 0
 
 
 def test_attention_span_wide_is_no_span():
