@@ -282,6 +282,7 @@ struct nf_model {
  * this many extra rows. */
 #define NF_ROLLBACK 32
 #define NF_KEY_RUNS 16 /* KEY_RUNS (infer.rs:1760) */
+#define NF_MAX_TAPS 16
 
 struct nf_session {
     size_t cap;     /* positions */
@@ -872,6 +873,141 @@ int nf_head_logits_sparse(const nf_model* m, const float* h, const uint32_t* ids
  * attention chunking (nested, infer.rs:1888).  `outputs` (NF_OUT_*) picks
  * what goes to `out` (chunk.rs:331-353, step.rs:715-729): logits [rows]
  * [out_rows] or hidden states [rows][d]; returns the rows written, or -1. */
+/* The qkv conv of one row part (infer/step.rs:502-516): out[k] = w_0[k]
+ * cur[k], then for taps j = 1 .. taps - 1, out[k] = fma(w_j[k], prev_j[k],
+ * out[k]), where rows[j] is the part's pre-tap row of position pos - j, or
+ * NULL when the history no longer holds it (a zero row: fma_w16s(.., 0.0)).
+ * w is the tap tensor [taps][cw]. */
+void nf_conv_taps(const float* const* rows, int taps, const uint16_t* w, int cw, float* out) {
+    for (int k = 0; k < cw; ++k) out[k] = cq_f16_to_f32(w[k]) * rows[0][k];
+    for (int j = 1; j < taps; ++j) {
+        const uint16_t* wj = w + (size_t)j * cw;
+        for (int k = 0; k < cw; ++k) out[k] = fmaf(cq_f16_to_f32(wj[k]), rows[j] ? rows[j][k] : 0.0f, out[k]);
+    }
+}
+
+/* The engram conv of site e at pos (engram_native, infer.rs:1310-1325,
+ * engram_tap 667-689): out[k] = sum over taps j < 4 with pos >= j dil of
+ * fma(taps_j[k], vs[pos - j dil][k / 32] * v8[pos - j dil][k], out[k]), from
+ * zero, over the session's int8 value history. */
+void nf_engram_conv(const nf_model* m, const nf_session* s, int e, size_t pos, float* out) {
+    const int d = m->c.d, dil = m->c.dilation;
+    for (int k = 0; k < d; ++k) out[k] = 0.0f;
+    for (int j = 0; j < ENGRAM_CONV_TAPS; ++j) {
+        if (pos < (size_t)(j * dil)) break;
+        const size_t pj = pos - (size_t)j * dil;
+        const int8_t* q8 = s->ev8[e] + pj * d;
+        const float* qs = s->evs[e] + pj * (d / 32);
+        const float* tw = m->etaps[e] + (size_t)j * d;
+        for (int k = 0; k < d; ++k) out[k] = fmaf(tw[k], qs[k / 32] * (float)q8[k], out[k]);
+    }
+}
+
+/* The engram gate (infer.rs:1409-1412): alpha = 1 / (lexpf(-dot16(x r_x,
+ * k r_k) / sqrtf(d)) + 1), r = rinv(dot16(v, v), d). */
+float nf_engram_gate(const float* x, const float* k, int d) {
+    const float rx = cq_rinv(cq_dot16(x, x, d), d), rk = cq_rinv(cq_dot16(k, k, d), d);
+    float* ea = (float*)malloc(sizeof(float) * d);
+    float* eb = (float*)malloc(sizeof(float) * d);
+    for (int i = 0; i < d; ++i) ea[i] = x[i] * rx, eb[i] = k[i] * rk;
+    const float alpha = 1.0f / (lexpf((-cq_dot16(ea, eb, d)) / sqrtf((float)d)) + 1.0f);
+    free(ea), free(eb);
+    return alpha;
+}
+
+/* The Hadamard MLP of layer l for one pre-MLP row h2[d] (mlp_native,
+ * infer.rs:1610-1637): the conditioning weights, z = h2 d1 zero-padded,
+ * t = kron(z, A0, B0) = A0^T Z B0 (kron_native 2322-2330 as two mix8
+ * passes), cond = 1 + sum_k u_k w_k, z = fma(t[perm1], cond d2, b2), SiLU,
+ * t = kron(z, A1, B1), z = t[perm2] d3, t = kron(z, A2, B2); mlp[j] =
+ * t[j] d4[j] for j < d. */
+void nf_hada_mlp(const nf_model* m, int l, const float* h2, float* mlp) {
+    const struct nf_layer16* Lw = &m->L[l];
+    const int d = m->c.d;
+    float* z = (float*)malloc(sizeof(float) * HN);
+    float* mt = (float*)malloc(sizeof(float) * HN);
+    float* bt = (float*)malloc(sizeof(float) * HN);
+    float* cond = (float*)malloc(sizeof(float) * HN);
+    float* zs = (float*)malloc(sizeof(float) * HN);
+    float* t3 = (float*)malloc(sizeof(float) * HN);
+    float wk[8];
+    nf_cond_weights(h2, d, Lw->cond_v, wk);
+    for (int k = 0; k < d; ++k) z[k] = h2[k] * cq_f16_to_f32(Lw->d1[k]);
+    for (int k = d; k < HN; ++k) z[k] = 0.0f;
+    nf_mix8(1, Lw->kron[0], 1, z, 0, mt, 16);
+    nf_mix8(0, mt, 0, Lw->kron[1], 1, bt, 16);
+    for (int j = 0; j < HN; ++j) cond[j] = 1.0f;
+    for (int k = 0; k < HADA_COND_RANK; ++k)
+        for (int j = 0; j < HN; ++j) cond[j] = fmaf(cq_f16_to_f32(Lw->cond_u[(size_t)k * HN + j]), wk[k], cond[j]);
+    for (int j = 0; j < HN; ++j)
+        zs[j] = fmaf(bt[m->perm1[j]], cond[j] * cq_f16_to_f32(Lw->d2[j]), cq_f16_to_f32(Lw->b2[j]));
+    for (int j = 0; j < HN; ++j) zs[j] /= nf_nexp(-zs[j]) + 1.0f;
+    nf_mix8(1, Lw->kron[2], 1, zs, 0, mt, 16);
+    nf_mix8(0, mt, 0, Lw->kron[3], 1, bt, 16);
+    for (int j = 0; j < HN; ++j) zs[j] = bt[m->perm2[j]] * cq_f16_to_f32(Lw->d3[j]);
+    nf_mix8(1, Lw->kron[4], 1, zs, 0, mt, 16);
+    nf_mix8(0, mt, 0, Lw->kron[5], 1, t3, d / NB / 8 * 4);
+    for (int j = 0; j < d; ++j) mlp[j] = t3[j] * cq_f16_to_f32(Lw->d4[j]);
+    free(z), free(mt), free(bt), free(cond), free(zs), free(t3);
+}
+
+/* RoPE rows (rope_rows, infer.rs:1716-1747) for positions p0 .. p0 + t - 1
+ * into cs / sn [t][32]: for a single token right after the newest known
+ * row (c0, s0: its cos and sin, or NULL) the angle-addition recurrence
+ * cos = fma(-sd, s0, cd c0), sin = fma(sd, c0, cd s0); else sincosf(freq
+ * (p0 + i)) with the product in f32. */
+void nf_rope_rows(const nf_model* m, size_t p0, size_t t, const float* c0, const float* s0, float* cs, float* sn) {
+    const int half = m->c.qk / 2;
+    if (t == 1 && c0 && s0) {
+        for (int f = 0; f < half; ++f) {
+            cs[f] = fmaf(-m->sd[f], s0[f], m->cd[f] * c0[f]);
+            sn[f] = fmaf(m->sd[f], c0[f], m->cd[f] * s0[f]);
+        }
+    } else {
+        for (size_t i = 0; i < t; ++i)
+            for (int f = 0; f < half; ++f) lsincosf(m->freq[f] * (float)(p0 + i), &sn[i * 32 + f], &cs[i * 32 + f]);
+    }
+}
+
+/* The RoPE tables (Tables::new, infer.rs:942-947) into freq, sd, cd [qk/2]. */
+void nf_rope_tables(const nf_model* m, float* freq, float* sd, float* cd) {
+    const int half = m->c.qk / 2;
+    memcpy(freq, m->freq, half * sizeof(float));
+    memcpy(sd, m->sd, half * sizeof(float));
+    memcpy(cd, m->cd, half * sizeof(float));
+}
+
+/* Read-only views of a session for the checks: the RoPE row of a position
+ * fed; the KV slot contents of a layer (k8 [nkv][qk], ks [nkv], v8
+ * [nkv][vd], vs [nkv]); the int8 engram value history of a site at a
+ * position (v8 [d], vs [d / 32]).  0, or -1 out of range. */
+int nf_session_rope(const nf_session* s, size_t pos, float* c, float* sn, int half) {
+    if (pos >= s->len) return -1;
+    memcpy(c, s->rope_c + pos * 32, half * sizeof(float));
+    memcpy(sn, s->rope_s + pos * 32, half * sizeof(float));
+    return 0;
+}
+
+int nf_session_kv(const nf_model* m, const nf_session* s, int l, size_t slot, int8_t* k8, float* ks, int8_t* v8,
+                  float* vs) {
+    const nf_config* c = &m->c;
+    if (l < 0 || l >= c->layers || slot >= s->cap) return -1;
+    memcpy(k8, s->k8[l] + slot * c->nkv * c->qk, (size_t)c->nkv * c->qk);
+    memcpy(ks, s->ks[l] + slot * c->nkv, (size_t)c->nkv * sizeof(float));
+    memcpy(vs, s->vs[l] + slot * c->nkv, (size_t)c->nkv * sizeof(float));
+    for (int h = 0; h < c->nkv; ++h)
+        for (int i = 0; i < c->vd; ++i) v8[h * c->vd + i] = s->v8t[l][((size_t)h * c->vd + i) * s->cap + slot];
+    return 0;
+}
+
+int nf_session_engram_hist(const nf_model* m, const nf_session* s, int e, size_t pos, int8_t* v8, float* vs) {
+    const int d = m->c.d;
+    if (e < 0 || e >= m->c.sites || pos >= s->len) return -1;
+    memcpy(v8, s->ev8[e] + pos * d, d);
+    memcpy(vs, s->evs[e] + pos * (d / 32), (d / 32) * sizeof(float));
+    return 0;
+}
+
 /* One feed of t tokens (step_native for one, chunk_job for a chunk).
  * `cells` (or NULL): the feed's cells [t][L+1][d], the lane mean
  * (((x0 + x1) + x2) + x3) * 0.25 of every row after the embedding and after
@@ -883,10 +1019,12 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
     const int n = c->lanes, d = c->d, nc = n * d, L = c->layers;
     const int qk = c->qk, vd = c->vd, nh = c->nh, nkv = c->nkv;
     const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd, W = qd + kd + vdim, taps = c->taps;
-    const int half = qk / 2, group = nh / nkv, sites = c->sites;
+    const int group = nh / nkv, sites = c->sites;
     const size_t p0 = s->len;
     int rc = 0;
-    if (t == 0 || p0 + t > s->cap || n != 4 || qk > 64 || vd > 64 || c->norders * c->eheads > 16 || L > 64) return -1;
+    if (t == 0 || p0 + t > s->cap || n != 4 || qk > 64 || vd > 64 || c->norders * c->eheads > 16 || L > 64 ||
+        taps > NF_MAX_TAPS)
+        return -1;
     const int nested = t > 1;
     for (size_t i = 0; i < t; ++i) s->tokens[p0 + i] = toks[i];
     s->len = p0 + t;
@@ -946,37 +1084,17 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
                         cq_quant_i8(kv + i * 2 * d + d + g * 32, 32, s->ev8[e] + (p0 + i) * d + g * 32);
         }
         free(er), free(trow), free(erow);
-        const int dil = c->dilation;
         for (int e = 0; e < sites; ++e)
-            for (size_t i = 0; i < t; ++i) {
-                const size_t pos = p0 + i;
-                float* dst = evals + ((size_t)e * t + i) * d;
-                for (int j = 0; j < ENGRAM_CONV_TAPS; ++j) {
-                    if (pos < (size_t)(j * dil)) break;
-                    const size_t pj = pos - (size_t)j * dil;
-                    const int8_t* q8 = s->ev8[e] + pj * d;
-                    const float* qs = s->evs[e] + pj * (d / 32);
-                    const float* tw = m->etaps[e] + (size_t)j * d;
-                    for (int k = 0; k < d; ++k) dst[k] = fmaf(tw[k], qs[k / 32] * (float)q8[k], dst[k]);
-                }
-            }
+            for (size_t i = 0; i < t; ++i) nf_engram_conv(m, s, e, p0 + i, evals + ((size_t)e * t + i) * d);
     }
 
     /* RoPE rows (rope_rows, infer.rs:1716-1747): the recurrence for a single
      * token right after the newest known position, sincosf otherwise. */
     float* cs = s->rope_c + p0 * 32;
     float* sn = s->rope_s + p0 * 32;
-    if (t == 1 && s->rope_n > 0) {
-        /* the list ends at position p0 - 1 */
-        const float *c0 = s->rope_c + (p0 - 1) * 32, *s0 = s->rope_s + (p0 - 1) * 32;
-        for (int f = 0; f < half; ++f) {
-            cs[f] = fmaf(-m->sd[f], s0[f], m->cd[f] * c0[f]);
-            sn[f] = fmaf(m->sd[f], c0[f], m->cd[f] * s0[f]);
-        }
-    } else {
-        for (size_t i = 0; i < t; ++i)
-            for (int f = 0; f < half; ++f) lsincosf(m->freq[f] * (float)(p0 + i), &sn[i * 32 + f], &cs[i * 32 + f]);
-    }
+    /* with a RoPE list, it ends at position p0 - 1 */
+    const int prev = t == 1 && s->rope_n > 0;
+    nf_rope_rows(m, p0, t, prev ? s->rope_c + (p0 - 1) * 32 : NULL, prev ? s->rope_s + (p0 - 1) * 32 : NULL, cs, sn);
     /* push the rows, then trim to ROLLBACK + 1 past twice that */
     s->rope_n += t;
     if (s->rope_n > 2 * (NF_ROLLBACK + 1)) s->rope_n = NF_ROLLBACK + 1;
@@ -991,10 +1109,7 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
     float *qkv = (float*)malloc(sizeof(float) * t * W), *att = (float*)malloc(sizeof(float) * t * nh * vd);
     float *o = (float*)malloc(sizeof(float) * t * d), *on = (float*)malloc(sizeof(float) * d);
     float *x2 = (float*)malloc(sizeof(float) * d), *h2 = (float*)malloc(sizeof(float) * d);
-    float *ea = (float*)malloc(sizeof(float) * d), *eb = (float*)malloc(sizeof(float) * d);
-    float *z = (float*)malloc(sizeof(float) * HN), *mt = (float*)malloc(sizeof(float) * HN);
-    float *bt = (float*)malloc(sizeof(float) * HN), *cond = (float*)malloc(sizeof(float) * HN);
-    float *zs = (float*)malloc(sizeof(float) * HN), *t3 = (float*)malloc(sizeof(float) * HN);
+    float *z = (float*)malloc(sizeof(float) * d), *t3 = (float*)malloc(sizeof(float) * d);
 
     for (int l = 0; l < L; ++l) {
         const struct nf_layer16* Lw = &m->L[l];
@@ -1009,10 +1124,8 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
             nf_mhc_read(Lw->phi_q, Lw->phi_s, ncols, d, Lw->a_pre, Lw->b_pre, lane, x, pr, ur, nx, nx8);
             memcpy(xr, ur, sizeof(float) * d);
             if (site >= 0) {
-                const float* kr = ekv + ((size_t)site * t + i) * 2 * d;
-                const float rx = cq_rinv(cq_dot16(xr, xr, d), d), rkk = cq_rinv(cq_dot16(kr, kr, d), d);
-                for (int k = 0; k < d; ++k) ea[k] = xr[k] * rx, eb[k] = kr[k] * rkk;
-                const float alpha = 1.0f / (lexpf((-cq_dot16(ea, eb, d)) / sqrtf((float)d)) + 1.0f);
+                const float* kr = ekv + ((size_t)site * t + i) * 2 * d;  /* the key half */
+                const float alpha = nf_engram_gate(xr, kr, d);
                 const float* ev = evals + ((size_t)site * t + i) * d;
                 for (int k = 0; k < d; ++k) xr[k] = fmaf(ev[k], alpha, xr[k]);
             }
@@ -1036,17 +1149,11 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
                 const int start = part == 0 ? 0 : part == 1 ? qd : qd + kd;
                 const int cw = part == 0 ? qd : part == 1 ? kd : vdim;
                 const uint16_t* w = part == 0 ? Lw->q_taps : part == 1 ? Lw->k_taps : Lw->v_taps;
-                const float* cur = hist + pos * (size_t)W + start;
-                for (int k = 0; k < cw; ++k) out[start + k] = cq_f16_to_f32(w[k]) * cur[k];
-                for (int j = 1; j < taps; ++j) {
-                    const uint16_t* wj = w + (size_t)j * cw;
-                    if (pos >= hist_lo + (size_t)j) {
-                        const float* rr = hist + (pos - j) * (size_t)W + start;
-                        for (int k = 0; k < cw; ++k) out[start + k] = fmaf(cq_f16_to_f32(wj[k]), rr[k], out[start + k]);
-                    } else {
-                        for (int k = 0; k < cw; ++k) out[start + k] = fmaf(cq_f16_to_f32(wj[k]), 0.0f, out[start + k]);
-                    }
-                }
+                /* tap j reads the row of position pos - j while the history holds it */
+                const float* rows[NF_MAX_TAPS];
+                for (int j = 0; j < taps; ++j)
+                    rows[j] = (j == 0 || pos >= hist_lo + (size_t)j) ? hist + (pos - j) * (size_t)W + start : NULL;
+                nf_conv_taps(rows, taps, w, cw, out + start);
             }
             for (int hh = 0; hh < nh + nkv; ++hh) {
                 float* v = out + (hh < nh ? hh * qk : qd + (hh - nh) * qk);
@@ -1092,27 +1199,11 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
             cq_zcn16(o + i * d, Lw->post_norm, d, on);
             for (int k = 0; k < d; ++k) x2[k] = fmaf(on[k], ga, x1[i * d + k]);
             cq_zcn16(x2, Lw->pre_hada, d, h2);
-            float wk[8];
-            nf_cond_weights(h2, d, Lw->cond_v, wk);
-            for (int k = 0; k < d; ++k) z[k] = h2[k] * cq_f16_to_f32(Lw->d1[k]);
-            for (int k = d; k < HN; ++k) z[k] = 0.0f;
-            nf_mix8(1, Lw->kron[0], 1, z, 0, mt, 16);
-            nf_mix8(0, mt, 0, Lw->kron[1], 1, bt, 16);
-            for (int j = 0; j < HN; ++j) cond[j] = 1.0f;
-            for (int k = 0; k < HADA_COND_RANK; ++k)
-                for (int j = 0; j < HN; ++j) cond[j] = fmaf(cq_f16_to_f32(Lw->cond_u[(size_t)k * HN + j]), wk[k], cond[j]);
-            for (int j = 0; j < HN; ++j)
-                zs[j] = fmaf(bt[m->perm1[j]], cond[j] * cq_f16_to_f32(Lw->d2[j]), cq_f16_to_f32(Lw->b2[j]));
-            for (int j = 0; j < HN; ++j) zs[j] /= nf_nexp(-zs[j]) + 1.0f;
-            nf_mix8(1, Lw->kron[2], 1, zs, 0, mt, 16);
-            nf_mix8(0, mt, 0, Lw->kron[3], 1, bt, 16);
-            for (int j = 0; j < HN; ++j) zs[j] = bt[m->perm2[j]] * cq_f16_to_f32(Lw->d3[j]);
-            nf_mix8(1, Lw->kron[4], 1, zs, 0, mt, 16);
-            nf_mix8(0, mt, 0, Lw->kron[5], 1, t3, d / NB / 8 * 4);
+            nf_hada_mlp(m, l, h2, t3);
             float hpost[4], hres[16];
             nf_post_gates(pr, Lw->a_post, Lw->b_post, Lw->a_res, Lw->b_res, lane, hpost, hres);
-            /* y = (x2 + mlp) - u, mlp = t3 * d4 (mlp_native, infer.rs:1610-1637) */
-            for (int ch = 0; ch < d; ++ch) z[ch] = (x2[ch] + t3[ch] * cq_f16_to_f32(Lw->d4[ch])) - u[i * d + ch];
+            /* y = (x2 + mlp) - u (step.rs:675-681) */
+            for (int ch = 0; ch < d; ++ch) z[ch] = (x2[ch] + t3[ch]) - u[i * d + ch];
             nf_mhc_write(d, z, hpost, hres, x);
         }
         NF_CELLS((size_t)l + 1)
@@ -1150,8 +1241,7 @@ static int nf_rows(const nf_model* m, nf_session* s, const uint32_t* toks, size_
 done:
     free(sp);
     free(xs), free(row), free(ekv), free(evals), free(nx), free(nx8), free(u), free(x1), free(p);
-    free(hloc), free(proj), free(qkv), free(att), free(o), free(on), free(x2), free(h2), free(ea), free(eb), free(z);
-    free(mt), free(bt), free(cond), free(zs), free(t3);
+    free(hloc), free(proj), free(qkv), free(att), free(o), free(on), free(x2), free(h2), free(z), free(t3);
     return rc;
 }
 

@@ -78,6 +78,16 @@ int nf_step(const nf_model* m, nf_session* s, uint32_t tok, float* logits, int n
 int nf_chunk(const nf_model* m, nf_session* s, const uint32_t* toks, size_t t, float* logits, int nthreads);
 
 /* Helpers, exposed for their own checks. */
+void nf_conv_taps(const float* const* rows, int taps, const uint16_t* w, int cw, float* out);
+void nf_engram_conv(const nf_model* m, const nf_session* s, int e, size_t pos, float* out);
+float nf_engram_gate(const float* x, const float* k, int d);
+void nf_hada_mlp(const nf_model* m, int l, const float* h2, float* mlp);
+void nf_rope_rows(const nf_model* m, size_t p0, size_t t, const float* c0, const float* s0, float* cs, float* sn);
+void nf_rope_tables(const nf_model* m, float* freq, float* sd, float* cd);
+int nf_session_rope(const nf_session* s, size_t pos, float* c, float* sn, int half);
+int nf_session_kv(const nf_model* m, const nf_session* s, int l, size_t slot, int8_t* k8, float* ks, int8_t* v8,
+                  float* vs);
+int nf_session_engram_hist(const nf_model* m, const nf_session* s, int e, size_t pos, int8_t* v8, float* vs);
 void nf_engram_rows(const nf_model* m, const uint32_t* tokens, size_t pos, long* rows);
 void nf_engram_input(const nf_model* m, int site, const uint32_t* tokens, size_t pos, float* out);
 void nf_mhc_read(const int8_t* phi_q, const float* phi_s, int ncols, int d, float a_pre, const float* b_pre, int lane,

@@ -71,6 +71,15 @@ def _lib():
             "nf_forward": (C.c_int, [P, P, P, C.c_size_t, C.c_int, P, C.c_int]),
             "nf_prefill": (C.c_int, [P, P, P, C.c_size_t, C.c_int, P, C.c_int]),
             "nf_forward_cells": (C.c_int, [P, P, P, C.c_size_t, C.c_int, P, P, C.c_int]),
+            "nf_conv_taps": (None, [P, C.c_int, P, C.c_int, P]),
+            "nf_engram_conv": (None, [P, P, C.c_int, C.c_size_t, P]),
+            "nf_engram_gate": (C.c_float, [P, P, C.c_int]),
+            "nf_hada_mlp": (None, [P, C.c_int, P, P]),
+            "nf_rope_rows": (None, [P, C.c_size_t, C.c_size_t, P, P, P, P]),
+            "nf_rope_tables": (None, [P, P, P, P]),
+            "nf_session_rope": (C.c_int, [P, C.c_size_t, P, P, C.c_int]),
+            "nf_session_kv": (C.c_int, [P, P, C.c_int, C.c_size_t, P, P, P, P]),
+            "nf_session_engram_hist": (C.c_int, [P, P, C.c_int, C.c_size_t, P, P]),
             "nf_session_track_cells": (C.c_int, [P, P, C.c_int]),
             "nf_session_cells": (C.c_int, [P, P, C.c_size_t, C.c_size_t, P]),
             "nf_head_logits": (None, [P, P, P, C.c_int]),
@@ -220,6 +229,7 @@ class Forward:
             l.nf_set_engram_taps(m, s, _p(taps), taps.size)
         final_norm = np.ascontiguousarray(_f32(a, take()), dtype=np.float32)
         l.nf_set_globals(m, _p(final_norm), _p(perm1), _p(perm2))
+        self.final_norm, self.perm1, self.perm2 = final_norm, perm1, perm2
 
         def arr(objs):
             return (C.c_void_p * max(1, len(objs)))(*[C.cast(x.ptr, C.c_void_p).value for x in objs])
@@ -227,6 +237,60 @@ class Forward:
         self._arrs = (arr(qkvg), arr(outs), arr(etables), arr(ekv))
         l.nf_set_matrices(m, C.cast(emb.ptr, C.c_void_p), *[C.cast(x, C.c_void_p) for x in self._arrs])
         self._keep = (keep, qkvg, outs, etables, ekv, emb)
+
+    # -- the helpers the step is built from, for their own checks
+    def set_layer_f16(self, layer: int, which: int, values):
+        """Replace a small per-layer tensor (values in f32, stored as f16)."""
+        from . import f32_to_f16
+        v = np.ascontiguousarray(f32_to_f16(np.asarray(values, dtype=np.float32).reshape(-1)), dtype=np.uint16)
+        _lib().nf_set_layer_f16(self.m, int(layer), int(which), _p(v), v.size)
+
+    def set_perms(self, perm1, perm2):
+        """Replace the Hadamard MLP's permutations."""
+        self.perm1 = np.ascontiguousarray(perm1, dtype=np.int32)
+        self.perm2 = np.ascontiguousarray(perm2, dtype=np.int32)
+        _lib().nf_set_globals(self.m, _p(self.final_norm), _p(self.perm1), _p(self.perm2))
+
+    @staticmethod
+    def conv_taps(rows, w) -> np.ndarray:
+        """nf_conv_taps: rows[j] the pre-tap row of pos - j (None: not held), w [taps][cw] f16 bits."""
+        w = np.ascontiguousarray(w, dtype=np.uint16)
+        taps, cw = w.shape
+        keep = [None if r is None else np.ascontiguousarray(r, dtype=np.float32) for r in rows]
+        ptrs = (C.c_void_p * taps)(*[None if r is None else r.ctypes.data for r in keep])
+        out = np.zeros(cw, dtype=np.float32)
+        _lib().nf_conv_taps(ptrs, taps, _p(w), cw, _p(out))
+        return out
+
+    def engram_gate(self, x, k) -> float:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        k = np.ascontiguousarray(k, dtype=np.float32)
+        return float(_lib().nf_engram_gate(_p(x), _p(k), x.size))
+
+    def hada_mlp(self, layer: int, h2) -> np.ndarray:
+        h2 = np.ascontiguousarray(h2, dtype=np.float32)
+        out = np.zeros(self.cfg.d, dtype=np.float32)
+        _lib().nf_hada_mlp(self.m, int(layer), _p(h2), _p(out))
+        return out
+
+    def rope_tables(self):
+        half = self.cfg.qk // 2
+        fr, sd, cd = (np.zeros(half, dtype=np.float32) for _ in range(3))
+        _lib().nf_rope_tables(self.m, _p(fr), _p(sd), _p(cd))
+        return fr, sd, cd
+
+    def rope_rows(self, p0: int, t: int, prev=None):
+        """nf_rope_rows: (cos, sin) [t][qk/2]; prev = (cos, sin) of position p0 - 1 for the recurrence."""
+        half = self.cfg.qk // 2
+        cs, sn = np.zeros((t, 32), np.float32), np.zeros((t, 32), np.float32)
+        c0 = s0 = None
+        if prev is not None:
+            c0 = np.zeros(32, np.float32)
+            s0 = np.zeros(32, np.float32)
+            c0[:half], s0[:half] = prev
+        _lib().nf_rope_rows(self.m, int(p0), int(t), None if c0 is None else _p(c0), None if s0 is None else _p(s0),
+                            _p(cs), _p(sn))
+        return cs[:, :half], sn[:, :half]
 
     def session(self, cap: int = 256) -> "Session":
         return Session(self, cap)
@@ -366,6 +430,37 @@ class Session:
         if _lib().nf_attend_test(self.f.m, self.s, _p(k8), _p(ks), _p(v8), _p(vs), ks.size, _p(q), int(nested),
                                  _p(out)) != 0:
             raise ValueError("bad key count")
+        return out
+
+    def rope(self, pos: int):
+        """The RoPE row (cos, sin) [qk/2] the session computed for a position."""
+        half = self.f.cfg.qk // 2
+        c, s = np.zeros(half, np.float32), np.zeros(half, np.float32)
+        if _lib().nf_session_rope(self.s, int(pos), _p(c), _p(s), half) != 0:
+            raise ValueError("position not fed")
+        return c, s
+
+    def kv(self, layer: int, slot: int):
+        """A KV slot: (k8 [nkv][qk], ks [nkv], v8 [nkv][vd], vs [nkv])."""
+        c = self.f.cfg
+        k8 = np.zeros((c.nkv, c.qk), np.int8)
+        v8 = np.zeros((c.nkv, c.vd), np.int8)
+        ks, vs = np.zeros(c.nkv, np.float32), np.zeros(c.nkv, np.float32)
+        if _lib().nf_session_kv(self.f.m, self.s, int(layer), int(slot), _p(k8), _p(ks), _p(v8), _p(vs)) != 0:
+            raise ValueError("slot out of range")
+        return k8, ks, v8, vs
+
+    def engram_hist(self, site: int, pos: int):
+        """The int8 engram value history of a site at a position: (v8 [d], vs [d / 32])."""
+        d = self.f.cfg.d
+        v8, vs = np.zeros(d, np.int8), np.zeros(d // 32, np.float32)
+        if _lib().nf_session_engram_hist(self.f.m, self.s, int(site), int(pos), _p(v8), _p(vs)) != 0:
+            raise ValueError("position not fed")
+        return v8, vs
+
+    def engram_conv(self, site: int, pos: int) -> np.ndarray:
+        out = np.zeros(self.f.cfg.d, np.float32)
+        _lib().nf_engram_conv(self.f.m, self.s, int(site), int(pos), _p(out))
         return out
 
     def __len__(self):
