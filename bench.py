@@ -122,7 +122,9 @@ def time_graph(fn_sweep, reps: int, warmup: int, torch):
 def launch_floors(args, nh, torch):
     """What bounds one dependent launch of the GEMV's size: µs per launch, in the same graph replay of
     `copies` launches over distinct buffers, for a one-element fill (the launch itself), a write of the
-    GEMV's algorithmic bytes, a copy of them (read + write), and the GEMV."""
+    GEMV's algorithmic bytes, a copy of them (read + write), the GEMV's own loads with no arithmetic in
+    its grid (nh_debug_read_floor mode 0), a plain grid-stride read of its code and norm bytes (mode 1),
+    and the GEMV."""
     nbytes = algorithmic_bytes(1, K, N)
     n4 = nbytes // 4
     tiny = [torch.empty(1, device="cuda") for _ in range(args.copies)]
@@ -137,7 +139,15 @@ def launch_floors(args, nh, torch):
            "fill_bytes_us": us(lambda: [x.fill_(1.0) for x in dst]),
            "copy_bytes_us": us(lambda: [d.copy_(s_) for d, s_ in zip(dst, src)])}
     del tiny, dst, src
-    out["gemv_us"] = round(gpu_gemv(args, nh, torch)["ms_launch"] * 1e3, 4)
+    gpu = gpu_gemv(args, nh, torch)
+    mats, a = gpu["mats"], gpu["a"]
+    out["read_gemv_grid_us"] = us(lambda: [m.read_floor(a, 0) for m in mats])
+    out["read_stream_us"] = us(lambda: [m.read_floor(a, 1) for m in mats])
+    out["gemv_us"] = round(gpu["ms_launch"] * 1e3, 4)
+    out["gemv_again_us"] = round(time_graph(lambda: [m.matmul_into(a, gpu["y"], N, 0) for m in mats],
+                                            max(1, args.steps), max(1, args.warmup), torch) / args.copies * 1e3, 4)
+    for k in ("read_gemv_grid_us", "read_stream_us", "gemv_us"):
+        out[k.replace("_us", "_tb_s")] = round(nbytes / out[k] / 1e6, 3)
     return out
 
 
@@ -169,7 +179,7 @@ def gpu_gemv(args, nh, torch):
     nbytes = algorithmic_bytes(1, K, N)
     gbs = nbytes / (ms_launch * 1e-3) / 1e9
     return {"ms_launch": ms_launch, "ms_sweep": ms_sweep, "gbs": gbs, "bytes": nbytes, "launches": reps * len(mats),
-            "x": x, "packed": packed, "norms": norms, "G": G, "a": a}
+            "x": x, "packed": packed, "norms": norms, "G": G, "a": a, "mats": mats, "y": y}
 
 
 def gpu_gemv_steady(gpu, copies, nh, torch):

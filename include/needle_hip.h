@@ -144,6 +144,13 @@ int nh_head_logits_sparse(const nh_qmat* w, const nh_qact* a, const uint32_t* id
  * int32 totals[rows][out][groups]. */
 int nh_debug_partials(const nh_qmat* w, const nh_qact* a, int32_t* out, void* stream);
 
+/* No reference counterpart (measurement): the read floors of the decode
+ * product of a 4-bit w with a one-token a.  mode 0 issues exactly the loads
+ * the decode GEMV issues (codes, norms, activations, scales), in its grid,
+ * with no arithmetic; mode 1 reads the codes and norms as a plain
+ * grid-stride stream.  Nothing is written. */
+int nh_debug_read_floor(const nh_qmat* w, const nh_qact* a, int mode, void* stream);
+
 /* ---- archives (QWeights, crates/needle-engine/src/weights.rs:136-148) --- */
 /* Weights::from_archive_mode with fast = true (weights.rs:314-467) over the
  * bytes of a .cact archive (Archive::from_raw, crates/needle-core/src/cact.rs:577-583),

@@ -39,9 +39,17 @@ FLAGS = [
 ]
 
 
+# Per-file flags.  The forward's kernels run one to a few dozen workgroups
+# each and wait on their arguments first: their first 16 argument dwords
+# are preloaded into SGPRs at wave launch (the Needle-3 decode token 537.5 ->
+# 526 us).  The products' wide grids measured no gain (a 512-workgroup GEMV
+# 3.64 -> 3.69 us), so they keep the plain argument loads.
+FILE_FLAGS = {"nh_forward.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")

@@ -727,6 +727,13 @@ int nh_debug_partials(const nh_qmat* w, const nh_qact* a, int32_t* out, void* st
     return NH_OK;
 }
 
+int nh_debug_read_floor(const nh_qmat* w, const nh_qact* a, int mode, void* stream) {
+    if (int rc = check_pair(w, a)) return rc;
+    if (w->m.bits != 4 || a->rows != 1 || (mode != 0 && mode != 1)) return fail(NH_EINVAL, "a 4-bit one-token product, mode 0 or 1");
+    NH_HIP(launch_read_floor(w, a, mode, (hipStream_t)stream), "read floor");
+    return NH_OK;
+}
+
 int nh_normal(uint32_t key0, uint32_t key1, uint64_t n, float* out) {
     if (!out && n) return fail(NH_EINVAL, "null output");
     const float lo = bits_to_f32(0xbf7fffffu);  // nextafter(-1, 0)

@@ -297,6 +297,92 @@ hipError_t launch_gemv_batch(const nh_qmat* const* w, const nh_qact* const* a, f
     return w[0]->m.bits == 2 ? dispatch_batch<2>(w[0], b, n, s) : dispatch_batch<4>(w[0], b, n, s);
 }
 
+// Read floors of the decode product, for measurement only.  The tile form
+// issues exactly the loads k_gemv<GPS, S, 4> issues (codes with the
+// streaming hint, norms, activations, scales) in its grid, and no
+// arithmetic, LDS or barrier; the stream form reads the codes and the norms
+// as a plain grid-stride stream of 16-byte loads, four in flight per lane.
+// Neither stores anything: an empty asm statement consumes the loaded
+// values, so the loads stay.
+template <int GPS, int S>
+__global__ __launch_bounds__(S * 64) void k_read_floor_tile(const uint4* __restrict__ codes,
+                                                            const uint16_t* __restrict__ norms,
+                                                            const uint4* __restrict__ xq,
+                                                            const float* __restrict__ sx, int G) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane >> 2, l = lane & 3;
+    const int n = blockIdx.x * TILE_ROWS + r, g0 = wave * GPS;
+    uint32_t x = 0;
+    if (GPS == 1) {
+        const int g = g0 < G ? g0 : 0;
+        const uint4 a = xq[(g * 4 + l) * 2], b = xq[(g * 4 + l) * 2 + 1];
+        x ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w;
+    } else if ((int)threadIdx.x < G * 8) {
+        const uint4 a = xq[threadIdx.x];
+        x ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    uint4 c[GPS];
+    uint32_t nb[GPS], sv[GPS];
+#pragma unroll
+    for (int j = 0; j < GPS; ++j) {
+        const int g = g0 + j < G ? g0 + j : 0;
+        c[j] = load_stream(codes + ((size_t)(blockIdx.x * G + g) * 64 + lane));
+        nb[j] = norms[(size_t)n * G + g];
+        sv[j] = __float_as_uint(sx[g]);
+    }
+#pragma unroll
+    for (int j = 0; j < GPS; ++j) x ^= c[j].x ^ c[j].y ^ c[j].z ^ c[j].w ^ nb[j] ^ sv[j];
+    asm volatile("" ::"v"(x));
+}
+
+__global__ __launch_bounds__(256) void k_read_floor_stream(const uint4* __restrict__ a, size_t na,
+                                                          const uint4* __restrict__ b, size_t nb) {
+    constexpr int U = 4;
+    const size_t stride = (size_t)gridDim.x * 256 * U;
+    uint32_t x = 0;
+    for (size_t i = (size_t)blockIdx.x * 256 * U + threadIdx.x; i < na + nb; i += stride) {
+        uint4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const size_t k = i + (size_t)u * 256;
+            const size_t kk = k < na + nb ? k : 0;
+            v[u] = load_stream(kk < na ? a + kk : b + (kk - na));
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    asm volatile("" ::"v"(x));
+}
+
+template <int GPS, int S>
+static hipError_t run_floor(const nh_qmat* w, const nh_qact* a, hipStream_t s) {
+    hipLaunchKernelGGL((k_read_floor_tile<GPS, S>), dim3(w->m.out_pad / TILE_ROWS), dim3(S * 64), 0, s,
+                       (const uint4*)w->d_codes, w->d_norms, (const uint4*)a->d_xq, a->d_sx, w->m.groups);
+    return hipGetLastError();
+}
+
+hipError_t launch_read_floor(const nh_qmat* w, const nh_qact* a, int mode, hipStream_t s) {
+    if (mode == 1) {
+        // 16-byte units: codes out_pad x G x 64 bytes, norms out_pad x G x 2 bytes (out_pad: a multiple of 16)
+        const size_t na = (size_t)w->m.out_pad * w->m.groups * 64 / 16, nb = (size_t)w->m.out_pad * w->m.groups * 2 / 16;
+        const int grid = (int)((na + nb + 256 * 4 - 1) / (256 * 4));
+        hipLaunchKernelGGL(k_read_floor_stream, dim3(grid), dim3(256), 0, s, (const uint4*)w->d_codes, na,
+                           (const uint4*)w->d_norms, nb);
+        return hipGetLastError();
+    }
+    const int G = w->m.groups;  // the shapes dispatch<4> picks
+    if (G <= 1) return run_floor<1, 1>(w, a, s);
+    if (G <= 2) return run_floor<2, 1>(w, a, s);
+    if (G <= 3) return run_floor<3, 1>(w, a, s);
+    if (G <= 4) return run_floor<2, 2>(w, a, s);
+    if (G <= 6) return run_floor<1, 6>(w, a, s);
+    if (G <= 8) return run_floor<2, 4>(w, a, s);
+    if (G <= 12) return run_floor<3, 4>(w, a, s);
+    if (G <= 16) return run_floor<2, 8>(w, a, s);
+    if (G <= 24) return run_floor<4, 6>(w, a, s);
+    if (G <= 32) return run_floor<4, 8>(w, a, s);
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemv(const nh_qmat* w, const nh_qact* a, float* y, int col0, int32_t* dbg, hipStream_t s) {
     float* yc = y ? y + col0 : nullptr;
     return w->m.bits == 2 ? dispatch<2>(w, a, yc, dbg, s) : dispatch<4>(w, a, yc, dbg, s);
