@@ -35,6 +35,7 @@ constexpr int DG_MAX_TAPS = 8;      // conv taps the unit kernels are written fo
 constexpr int SPAN_RUNS = 24;       // runs of live positions an attention span passes to a feed
 constexpr int STATUS_SPIN = 1;      // a bounded in-kernel wait gave up (SessDev::status)
 constexpr int SPIN_LIMIT = 1 << 20; // polls of a bounded wait (~64 cycles each, ~30 ms)
+constexpr int DCOUNT_SLOTS = 16;    // arrival counters of the decode attention's chunk blocks
 
 struct Dims {
     int d, nh, nkv, qk, vd, lanes, taps, layers;
@@ -130,6 +131,7 @@ struct SessDev {
     int32_t* argmax;  // scratch of the greedy pick
     int32_t* status;  // STATUS_* bits set by a kernel that gave up a wait; the host reads and clears it
     uint8_t* flags;   // [rows] the prefill combine's block flag of each row of the feed
+    int32_t* dcount;  // [DCOUNT_SLOTS] chunk blocks of an A8 head group counted in; zero between launches
     float* cells;     // [rows][layers + 1][d] the feed's cells (lane means after the embedding
                       // and after each layer's mHC write), or null when not wanted; set per feed
 };
@@ -180,6 +182,11 @@ hipError_t fwd_attn_out(const Dims& D, const SessDev& S, const LayerDev& L, int 
 bool dec_group_fits(const Dims& D, int p0, int window);
 hipError_t fwd_dec_attn(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
                         hipStream_t s);
+// The same for any key count and with an attention span (`span`, or null):
+// the position's key chunks in blocks of their own, merged by the last.
+bool dec_chunks_fits(const Dims& D);
+hipError_t fwd_dec_chunks(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
+                          const KeySpan* span, hipStream_t s);
 hipError_t fwd_argmax(const float* logits, int n, uint32_t* dst, hipStream_t s);
 hipError_t fwd_phi8(const float* rows, int nrows, int width, int8_t* q, float* scale, hipStream_t s);
 

@@ -1375,7 +1375,7 @@ __device__ __forceinline__ int quad_sum_i32(int v) {
 // (key_ranges, infer.rs:1781-1791): [lo, max(lo, min(sink, pos + 1))) and
 // [min(max(end - ring, sink), pos + 1), pos + 1); the ring part is not cut
 // by the layer's window.
-__device__ __forceinline__ void span_ranges(const Dims& D, const KeySpan& K, int lo, int pos, int& alo, int& ahi,
+__host__ __device__ inline void span_ranges(const Dims& D, const KeySpan& K, int lo, int pos, int& alo, int& ahi,
                                             int& blo, int& bhi) {
     alo = lo;
     ahi = max(lo, min(D.sink, pos + 1));
@@ -1383,10 +1383,10 @@ __device__ __forceinline__ void span_ranges(const Dims& D, const KeySpan& K, int
     bhi = pos + 1;
 }
 
-__device__ __forceinline__ int span_overlap(int lo, int hi, int a, int b) { return max(0, min(hi, b) - max(lo, a)); }
+__host__ __device__ inline int span_overlap(int lo, int hi, int a, int b) { return max(0, min(hi, b) - max(lo, a)); }
 
 // The number of keys: the span's live runs cut to the two ranges.
-__device__ __forceinline__ int span_count(const KeySpan& K, int alo, int ahi, int blo, int bhi) {
+__host__ __device__ inline int span_count(const KeySpan& K, int alo, int ahi, int blo, int bhi) {
     int n = 0;
     for (int r = 0; r < K.nrun; ++r)
         n += span_overlap(K.lo[r], K.hi[r], alo, ahi) + span_overlap(K.lo[r], K.hi[r], blo, bhi);
@@ -2425,6 +2425,434 @@ hipError_t fwd_dec_attn(const Dims& D, const SessDev& S, const LayerDev& L, int 
     }
 #undef NH_DG_TAPS
 #undef NH_DG
+    return hipGetLastError();
+}
+
+// One decode token's units, attention, gate and A8 in one launch for any
+// key count and with an attention span: attend_head_ref's chunks
+// (key_chunks, infer.rs:1888-1893,2093-2101) run in blocks of their own.
+// Block (g, c) owns A8 group g's heads (as k_dec_group) and key chunk c:
+// its query waves compute the heads' query units (every block of the group
+// the same values), the last chunk's blocks also the kv head's new key and
+// value (the first of them appends them to the cache and the history
+// ring), and the staging waves load the chunk's cached keys, scales and
+// values (by position; with a span, through the chunk's KV slots, found
+// first).  Each chunk's attention gives the reference's part (max, sum,
+// P.V, infer.rs:1918-1987); one chunk finishes in its block.  With several,
+// each block stores its heads' parts and counts itself in (agent-scope
+// release); the group's block that counts last merges the parts in chunk
+// order (infer.rs:1990-2006), divides by the head gate and runs the
+// group's A8, then clears the count.  No block waits for another.  One
+// more block computes the row's post gates.
+template <int HP, int TAPS, bool EXACT, bool SPAN>
+__global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, LayerDev L, int layer, int p0,
+                                                           int out_bits, KeySpan K, int n, int nchunks, int chunk) {
+    constexpr int NT = HP * DG_HEAD_T;  // the attention's threads
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const int nh = D.nh, nkv = D.nkv, qk = D.qk, vd = D.vd, group = nh / nkv;
+    const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd;
+    const int ngroups = nh / HP;
+    if ((int)blockIdx.x >= ngroups * nchunks) {
+        if (wave == 0) post_gates(S.p, L, lane);
+        return;
+    }
+    const int g = blockIdx.x / nchunks, ci = blockIdx.x % nchunks;
+    const int hh0 = g * HP, kvh = hh0 / group;
+    const bool last = ci == nchunks - 1;              // the chunk holding the new key (key n - 1 = p0)
+    const bool owner = last && hh0 % group == 0;      // appends the new key and value
+    const int c0 = ci * chunk, len = min(chunk, n - c0), blocked = len / 4 * 4;
+    const int nold = last ? len - 1 : len;            // keys read from the cache
+    const int lo = window_lo(L.window, p0);
+    // without a span the chunk's keys are positions (= slots) slot0 ..;
+    // value columns and digits are kept from the dword boundary at or
+    // before slot0 (column j = i + sh for key i); with one, column j = key j
+    const int slot0 = lo + c0, sh = SPAN ? 0 : slot0 & 3, base = slot0 - sh;
+    const int h = t / DG_HEAD_T, u = t % DG_HEAD_T, hw = u >> 6;
+    const bool attends = t < NT;  // (wave-uniform)
+    __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][DG_KPITCH];
+    __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][DG_PITCH];
+    __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
+    __shared__ int kslot[SPAN ? ATT_CHUNK_MAX : 1];
+    __shared__ alignas(16) int8_t q8[HP][MAX_HEAD_DIM];
+    __shared__ float sc[HP][ATT_CHUNK_MAX];
+    __shared__ alignas(16) int8_t dig[HP][3][DG_PITCH];
+    __shared__ float red[HP][DG_HEAD_T / 64], wred[HP][DG_HEAD_T / 64];
+    __shared__ float s_qs[HP], s_sum[HP];
+    __shared__ float att[HP * MAX_HEAD_DIM];
+    __shared__ float gden[HP * MAX_HEAD_DIM];
+    __shared__ int s_merge;
+    const size_t lc = (size_t)layer * D.cap;
+    const int role = __builtin_amdgcn_readfirstlane(wave < HP ? 0 : min(wave - HP + 1, 3));  // 0 q, 1 k, 2 v, 3 keys
+    constexpr int NS = DG_THREADS - (HP + 2) * 64;  // staging threads
+    constexpr int KR = (ATT_CHUNK_MAX * 4 + NS - 1) / NS, SR = (ATT_CHUNK_MAX + NS - 1) / NS;
+    // values: dwords of the columns without a span, bytes gathered by slot with one
+    constexpr int VR = SPAN ? (MAX_HEAD_DIM * ATT_CHUNK_MAX + NS - 1) / NS : (MAX_HEAD_DIM * DG_VDW + NS - 1) / NS;
+    const int rq = qk / 16, vdw = (sh + nold + 3) / 4, ts = t - (HP + 2) * 64;
+    const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap;
+    UnitIn ui;
+    u32x4 kr[KR];
+    uint32_t vw[VR];
+    float ksr[SR], vsr[SR];
+    if (role == 0) {
+        ui = unit_load<TAPS, EXACT>(D, S, layer, p0, 0, (hh0 + wave) * qk, qd, (hh0 + wave) * qk, qk, L.q_taps,
+                                    L.q_norm, lane);
+    } else if (role == 1) {
+        if (last)
+            ui = unit_load<TAPS, EXACT>(D, S, layer, p0, 0, qd + kvh * qk, kd, kvh * qk, qk, L.k_taps, L.k_norm, lane);
+    } else if (role == 2) {
+        if (last)
+            ui = unit_load<TAPS, EXACT>(D, S, layer, p0, 0, qd + kd + kvh * vd, vdim, kvh * vd, vd, L.v_taps,
+                                        L.k_norm, lane);
+    } else if constexpr (!SPAN) {
+        // (clamped in-range addresses: past nold nothing is stored; with no
+        // cached key the clamp reads the new position's own slot)
+        const int im = max(nold - 1, 0);
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+            const int e = ts + r * NS, i = min(e >> 2, im), c = min(e & 3, rq - 1);
+            kr[r] = reinterpret_cast<const u32x4*>(S.k8 + ((lc + slot0 + i) * nkv + kvh) * qk)[c];
+        }
+#pragma unroll
+        for (int r = 0; r < SR; ++r) {
+            const int i = min(ts + r * NS, im);
+            ksr[r] = S.ks[(lc + slot0 + i) * nkv + kvh];
+            vsr[r] = S.vs[(lc + slot0 + i) * nkv + kvh];
+        }
+#pragma unroll
+        for (int r = 0; r < VR; ++r) {
+            const int e = ts + r * NS, dm = min(e / DG_VDW, vd - 1), k = min(e % DG_VDW, max(vdw - 1, 0));
+            vw[r] = reinterpret_cast<const uint32_t*>(vcol + base + (size_t)dm * D.vcap)[k];
+        }
+    } else {
+        // the chunk's KV slots: key c0 + i at its position in the span's runs
+        if (ts < len) {
+            int alo, ahi, blo, bhi;
+            span_ranges(D, K, lo, p0, alo, ahi, blo, bhi);
+            kslot[ts] = slot_of(D, span_key(K, alo, ahi, blo, bhi, c0 + ts));
+        }
+    }
+    if constexpr (SPAN) {
+        __syncthreads();  // the slots
+        if (role == 3) {
+            const int im = max(nold - 1, 0);
+#pragma unroll
+            for (int r = 0; r < KR; ++r) {
+                const int e = ts + r * NS, i = min(e >> 2, im), c = min(e & 3, rq - 1);
+                kr[r] = reinterpret_cast<const u32x4*>(S.k8 + ((lc + kslot[i]) * nkv + kvh) * qk)[c];
+            }
+#pragma unroll
+            for (int r = 0; r < SR; ++r) {
+                const int sl = kslot[min(ts + r * NS, im)];
+                ksr[r] = S.ks[(lc + sl) * nkv + kvh];
+                vsr[r] = S.vs[(lc + sl) * nkv + kvh];
+            }
+#pragma unroll
+            for (int r = 0; r < VR; ++r) {
+                const int e = ts + r * NS, dm = min(e / ATT_CHUNK_MAX, vd - 1), i = min(e % ATT_CHUNK_MAX, im);
+                vw[r] = (uint8_t)vcol[(size_t)dm * D.vcap + kslot[i]];
+            }
+        }
+    }
+    const float gate = S.proj[D.W + hh0 * vd + min(t, HP * vd - 1)];
+    if (wave < HP) {
+        // the query history row is written once (by the last chunk's block)
+        const float v = unit_finish<TAPS, EXACT>(D, S, layer, p0, (hh0 + wave) * qk, qk, ui, true, lane, last);
+        const float s = wave_quant_scale(lane < qk ? v : 0.0f);
+        if (lane < qk) q8[wave][lane] = quant_one(v, 1.0f / s);
+        if (lane == 0) s_qs[wave] = s * bits_f32(0x3e13cd3au);
+        if (t < HP * vd) gden[t] = nexp(-gate) + 1.0f;
+    } else if (wave == HP) {
+        if (last) {
+            const float v = unit_finish<TAPS, EXACT>(D, S, layer, p0, qd + kvh * qk, qk, ui, true, lane, owner);
+            const float s = wave_quant_scale(lane < qk ? v : 0.0f);
+            const int8_t q = quant_one(v, 1.0f / s);
+            const int slot = slot_of(D, p0);
+            if (lane < qk) {
+                ks8[len - 1][lane] = q;
+                if (owner) S.k8[((lc + slot) * nkv + kvh) * qk + lane] = q;
+            }
+            if (lane == 0) {
+                kss[len - 1] = s;
+                if (owner) S.ks[(lc + slot) * nkv + kvh] = s;
+            }
+        }
+    } else if (wave == HP + 1) {
+        if (last) {
+            const float v = unit_finish<TAPS, EXACT>(D, S, layer, p0, qd + kd + kvh * vd, vd, ui, false, lane, owner);
+            const float s = wave_quant_scale(lane < vd ? v : 0.0f);
+            const int8_t q = quant_one(v, 1.0f / s);
+            const int slot = slot_of(D, p0);
+            if (lane < vd) {
+                vs8[lane][sh + len - 1] = q;
+                if (owner) S.v8t[(((size_t)layer * nkv + kvh) * vd + lane) * D.vcap + slot] = q;
+            }
+            if (lane == 0) {
+                vss[len - 1] = s;
+                if (owner) S.vs[(lc + slot) * nkv + kvh] = s;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+            const int e = ts + r * NS, i = e >> 2, c = e & 3;
+            if (i < nold && c < rq) reinterpret_cast<u32x4*>(ks8[i])[c] = kr[r];
+        }
+#pragma unroll
+        for (int r = 0; r < SR; ++r) {
+            const int i = ts + r * NS;
+            if (i < nold) {
+                kss[i] = ksr[r];
+                vss[i] = vsr[r];
+            }
+        }
+        if constexpr (SPAN) {
+#pragma unroll
+            for (int r = 0; r < VR; ++r) {
+                const int e = ts + r * NS, dm = e / ATT_CHUNK_MAX, i = e % ATT_CHUNK_MAX;
+                if (dm < vd && i < nold) vs8[dm][i] = (int8_t)vw[r];
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < VR; ++r) {
+                const int e = ts + r * NS, dm = e / DG_VDW, k = e % DG_VDW;
+                if (dm < vd && k < vdw) {
+                    if (4 * k + 3 < sh + nold) {
+                        reinterpret_cast<uint32_t*>(vs8[dm])[k] = vw[r];
+                    } else {
+#pragma unroll
+                        for (int b = 0; b < 4; ++b)
+                            if (4 * k + b < sh + nold) vs8[dm][4 * k + b] = (int8_t)(vw[r] >> (8 * b));
+                    }
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // the chunk's attend_head_ref steps, one head per 256 threads
+    float mx = -__builtin_inff(), wmax = 0.0f;
+    if (attends) {
+        const float qs = s_qs[h];
+        uint4 qv[MAX_HEAD_DIM / 16];
+#pragma unroll
+        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) qv[c] = reinterpret_cast<const uint4*>(q8[h])[c];
+        for (int i = u; i < len; i += DG_HEAD_T) {
+            int dp[4] = {0, 0, 0, 0};
+#pragma unroll
+            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
+                if (c < rq) {
+                    const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
+                    dp[0] = __builtin_amdgcn_sdot4((int)kv.x, (int)qv[c].x, dp[0], false);
+                    dp[1] = __builtin_amdgcn_sdot4((int)kv.y, (int)qv[c].y, dp[1], false);
+                    dp[2] = __builtin_amdgcn_sdot4((int)kv.z, (int)qv[c].z, dp[2], false);
+                    dp[3] = __builtin_amdgcn_sdot4((int)kv.w, (int)qv[c].w, dp[3], false);
+                }
+            const int dot = (dp[0] + dp[1]) + (dp[2] + dp[3]);
+            const float ksc = kss[i];
+            const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
+            sc[h][i] = sv;
+            mx = fmaxf(mx, sv);
+        }
+        mx = wave_max(mx);
+        if (lane == 0) red[h][hw] = mx;
+    }
+    __syncthreads();
+    if (attends) {
+        mx = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
+        for (int i = u; i < len; i += DG_HEAD_T) {
+            const float e = i < blocked ? nexp(sc[h][i] - mx) : lexpf(sc[h][i] - mx);
+            sc[h][i] = e;
+            wmax = fmaxf(wmax, e * vss[i]);
+        }
+        wmax = wave_max(wmax);
+        if (lane == 0) wred[h][hw] = wmax;
+    }
+    __syncthreads();
+    if (attends) {
+        if (hw == 0) {
+            // chunk_exp's sum order (as k_dec_group)
+            float acc = 0.0f;
+            const int nb8 = len / 8;
+            if (lane < 8) {
+                const int k = lane & 3, hi = lane >> 2;
+                const float* col = &sc[h][hi * 4 + k];
+                int b = 0;
+                for (; b + 8 <= nb8; b += 8) {
+                    float v[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) v[j] = col[(b + j) * 8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) acc += v[j];
+                }
+                for (; b < nb8; ++b) acc += col[b * 8];
+                if (hi == 0 && len - nb8 * 8 >= 4) acc += sc[h][nb8 * 8 + k];
+            }
+            const float tk = acc + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                                                                 0, __builtin_bit_cast(int, acc), 0x104, 0xF, 0xF, false));
+            const int ti = __builtin_bit_cast(int, tk);
+            const float t0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x00, 0xF, 0xF, false));
+            const float t1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0x55, 0xF, 0xF, false));
+            const float t2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xAA, 0xF, 0xF, false));
+            const float t3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, ti, 0xFF, 0xF, 0xF, false));
+            float sum = (t0 + t1) + (t2 + t3);
+            int i = blocked;
+            if (len - i >= 2) {
+                sum = (sc[h][i] + sum) + sc[h][i + 1];
+                i += 2;
+            }
+            if (len - i == 1) sum += sc[h][i];
+            if (lane == 0) s_sum[h] = sum;
+        }
+        wmax = fmaxf(fmaxf(wred[h][0], wred[h][1]), fmaxf(wred[h][2], wred[h][3]));
+        const float qw = bits_f32(0x49fffff8u) / wmax;
+        for (int i = u; i < len; i += DG_HEAD_T) {
+            const float w = sc[h][i] * vss[i];
+            const int32_t wq = (int32_t)roundf(w * qw);
+            dig[h][0][sh + i] = (int8_t)(wq >> 14);
+            dig[h][1][sh + i] = (int8_t)((wq >> 7) & 127);
+            dig[h][2][sh + i] = (int8_t)(wq & 127);
+        }
+        if (u < 4) {
+            const int j0 = u, j1 = sh + len + u;
+            if (j0 < sh) dig[h][0][j0] = dig[h][1][j0] = dig[h][2][j0] = 0;
+            if (j1 < (sh + len + 3) / 4 * 4) dig[h][0][j1] = dig[h][1][j1] = dig[h][2][j1] = 0;
+        }
+    }
+    __syncthreads();
+    if (attends) {
+        const float cw = wmax * bits_f32(0x35000004u);
+        const int dm = u >> 2, part = u & 3, cols = sh + len;
+        int a = 0, b = 0, c = 0;
+        if (dm < vd) {
+            const int* vrow = reinterpret_cast<const int*>(vs8[dm]);
+            const int* d0 = reinterpret_cast<const int*>(dig[h][0]);
+            const int* d1 = reinterpret_cast<const int*>(dig[h][1]);
+            const int* d2 = reinterpret_cast<const int*>(dig[h][2]);
+            int i = part;
+            for (; 4 * (i + 12) < cols; i += 16) {
+                int v[4], x0[4], x1[4], x2[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    v[q] = vrow[i + 4 * q];
+                    x0[q] = d0[i + 4 * q];
+                    x1[q] = d1[i + 4 * q];
+                    x2[q] = d2[i + 4 * q];
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    a = __builtin_amdgcn_sdot4(x0[q], v[q], a, false);
+                    b = __builtin_amdgcn_sdot4(x1[q], v[q], b, false);
+                    c = __builtin_amdgcn_sdot4(x2[q], v[q], c, false);
+                }
+            }
+            for (; 4 * i < cols; i += 4) {
+                const int v = vrow[i];
+                a = __builtin_amdgcn_sdot4(d0[i], v, a, false);
+                b = __builtin_amdgcn_sdot4(d1[i], v, b, false);
+                c = __builtin_amdgcn_sdot4(d2[i], v, c, false);
+            }
+        }
+        a = quad_sum_i32(a);
+        b = quad_sum_i32(b);
+        c = quad_sum_i32(c);
+        if (dm < vd && part == 0) {
+            const float po = __builtin_fmaf(16384.0f, (float)a, __builtin_fmaf(128.0f, (float)b, (float)c)) * cw;
+            if (nchunks == 1) {
+                att[h * vd + dm] = (po * (1.0f / s_sum[h])) / gden[h * vd + dm];
+            } else {
+                const size_t pi = (size_t)(hh0 + h) * D.max_chunks + ci;
+                S.po[pi * vd + dm] = po;
+                if (dm == 0) {
+                    S.pm[pi] = mx;
+                    S.psum[pi] = s_sum[h];
+                }
+            }
+        }
+    }
+    if (nchunks > 1) {
+        // count this block in; the group's last block merges
+        __syncthreads();
+        if (t == 0) {
+            const int before = __hip_atomic_fetch_add(S.dcount + g, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            s_merge = before == nchunks - 1;
+        }
+        __syncthreads();
+        if (!s_merge) return;
+        if (t < HP * vd) {
+            // merge_parts (infer.rs:2143-2166) in chunk order
+            const int hh = hh0 + t / vd, i = t % vd;
+            const size_t pb = (size_t)hh * D.max_chunks;
+            float big = -1e30f;
+            for (int p = 0; p < nchunks; ++p)
+                big = fmaxf(big, __hip_atomic_load(S.pm + pb + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            float acc = 0.0f, total = 0.0f;
+            for (int p = 0; p < nchunks; ++p) {
+                const float m = __hip_atomic_load(S.pm + pb + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const float o = __hip_atomic_load(S.po + (pb + p) * vd + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const float sm = __hip_atomic_load(S.psum + pb + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const float w = lexpf(m - big);
+                acc = __builtin_fmaf(o, w, acc);
+                total = __builtin_fmaf(w, sm, total);
+            }
+            const float inv = 1.0f / total;
+            att[t] = (acc * inv) / gden[t];
+        }
+        if (t == 0) __hip_atomic_store(S.dcount + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (wave == 0) {
+        const int Kg = HP * vd;
+        a8_group(lane < Kg ? att[lane] : 0.0f, lane + 64 < Kg ? att[lane + 64] : 0.0f, lane, out_bits,
+                 S.xq_att + (size_t)g * GROUP, S.sx_att + g);
+    }
+}
+
+bool dec_chunks_fits(const Dims& D) {
+    if (GROUP % D.vd != 0 || D.taps > DG_MAX_TAPS) return false;
+    const int hp = GROUP / D.vd;
+    return (hp == 2 || hp == 4) && D.nh % hp == 0 && (D.nh / D.nkv) % hp == 0 && D.qk % 16 == 0 &&
+           D.nh / hp <= DCOUNT_SLOTS;
+}
+
+hipError_t fwd_dec_chunks(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
+                          const KeySpan* span, hipStream_t s) {
+    const int hp = GROUP / D.vd, lo = window_lo(L.window, p0);
+    int n = p0 + 1 - lo;
+    if (span) {
+        int alo, ahi, blo, bhi;
+        span_ranges(D, *span, lo, p0, alo, ahi, blo, bhi);
+        n = span_count(*span, alo, ahi, blo, bhi);
+    }
+    int count, chunk;
+    key_chunks(n, D.nkv, false, count, chunk);
+    if (n < 1 || count < 1 || count > D.max_chunks || chunk > ATT_CHUNK_MAX) return hipErrorInvalidValue;
+    const int blocks = D.nh / hp * count + 1;
+    const KeySpan K = span ? *span : KeySpan{};
+#define NH_DC(HP, TP, EX, SP)                                                                                      \
+    hipLaunchKernelGGL((k_dec_chunks<HP, TP, EX, SP>), dim3(blocks), dim3(DG_THREADS), 0, s, D, S, L, layer, p0, \
+                       out_bits, K, n, count, chunk)
+#define NH_DC_TAPS(HP, SP)                          \
+    switch (D.taps) {                               \
+        case 1: NH_DC(HP, 1, true, SP); break;      \
+        case 2: NH_DC(HP, 2, true, SP); break;      \
+        case 3: NH_DC(HP, 3, true, SP); break;      \
+        case 4: NH_DC(HP, 4, true, SP); break;      \
+        default: NH_DC(HP, DG_MAX_TAPS, false, SP); \
+    }
+    if (hp == 2) {
+        if (span) {
+            NH_DC_TAPS(2, true)
+        } else {
+            NH_DC_TAPS(2, false)
+        }
+    } else {
+        if (span) {
+            NH_DC_TAPS(4, true)
+        } else {
+            NH_DC_TAPS(4, false)
+        }
+    }
+#undef NH_DC_TAPS
+#undef NH_DC
     return hipGetLastError();
 }
 

@@ -589,6 +589,8 @@ int feed(nh_session* s, int t, int outputs, float* out, float* cells, hipStream_
         NH_TRY(product(m->qkvg[l], &s->a_in, t, S.proj, D.nq, flags, st), "q|k|v|gate");
         if (t == 1 && nh::dec_group_fits(D, p0, m->layers[l].window)) {
             NH_TRY(nh::fwd_dec_attn(D, S, m->layers[l], l, p0, m->out[l]->m.bits, st), "decode attention");
+        } else if (t == 1 && nh::dec_chunks_fits(D)) {
+            NH_TRY(nh::fwd_dec_chunks(D, S, m->layers[l], l, p0, m->out[l]->m.bits, sp, st), "decode attention");
         } else {
             NH_TRY(nh::fwd_units(D, S, m->layers[l], l, p0, t, st), "units");
             NH_TRY(nh::fwd_attend(D, S, m->layers[l], l, p0, t, sp, st), "attend");
@@ -850,7 +852,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     const size_t o_xi = Y.take(AR * Gd * nh::GROUP), o_si = Y.take(AR * Gd * 4);
     const size_t o_xa = Y.take(AR * Ga * nh::GROUP), o_sa = Y.take(AR * Ga * 4);
     const size_t o_xe = Y.take(E * AR * Gd * nh::GROUP), o_se = Y.take(E * AR * Gd * 4);
-    const size_t o_am = Y.take(16), o_st = Y.take(16), o_fl = Y.take(R);
+    const size_t o_am = Y.take(16), o_st = Y.take(16), o_fl = Y.take(R), o_dc = Y.take(nh::DCOUNT_SLOTS * 4);
     hipError_t e = hipMalloc(&s->d_buf, Y.size);
     if (e == hipSuccess) e = hipMemset(s->d_buf, 0, Y.size);
     if (e == hipSuccess) e = hipHostMalloc((void**)&s->h_status, sizeof(int32_t), hipHostMallocDefault);
@@ -878,6 +880,7 @@ int nh_session_new(const nh_model* m, int cap, nh_session** out) {
     S.argmax = (int32_t*)(b + o_am);
     S.status = (int32_t*)(b + o_st);
     S.flags = (uint8_t*)(b + o_fl);
+    S.dcount = (int32_t*)(b + o_dc);
     D.spin_limit = nh::SPIN_LIMIT;
     auto view = [](int8_t* xq, float* sx, int in_dim, int groups) {
         nh_qact a{};

@@ -199,6 +199,28 @@ def test_attention_span_long(nh):
     p.done("attention span long")
 
 
+def test_attention_span_agent(nh):
+    say("attention span as the agent sets it (sink 118, ring 256): a 118-token prefix, 300 more, then greedy steps "
+        "past 418 positions (374 keys: four key chunks), every step against the oracle")
+    g = cact.Geometry(vocab=300, num_layers=3, engram_slots=64, engram_sites=(1,), global_layers=(0, 2),
+                      sliding_window=64)
+    p = Pair(nh, archive(g, seed=67), 448)
+    p.attend(118, 256)
+    toks = o.random_tokens(418, 300, seed=68)
+    p.prefill(toks[:118], forward.OUT_NONE, label="prefix")
+    p.prefill(toks[118:418], label="fill")
+    want = p.o.forward(o.random_tokens(1, 300, seed=69))[0]
+    p.g.forward(o.random_tokens(1, 300, seed=69))
+    picks, logits = p.g.generate_greedy(12)
+    for i, k in enumerate(picks):
+        assert int(k) == int(np.argmax(want)), i
+        want = p.o.forward([int(k)])[0]
+    same("greedy logits", logits.cpu().numpy(), want, p.stats)
+    p.rollback(5)
+    p.steps(o.random_tokens(8, 300, seed=70), label="after rollback")
+    p.done("attention span (118, 256)")
+
+
 @pytest.mark.parametrize("taps", [1, 2, 4, 6])
 def test_conv_taps(nh, taps):
     say(f"qkv conv taps {taps}: a one-token prompt, steps, a 40-token prompt, steps")
