@@ -36,14 +36,26 @@ NEEDLE3_VOCAB = 8192
 
 
 def host_cpu() -> str:
-    """The host's CPU model, as /proc/cpuinfo names it."""
+    """The host's CPU as /proc/cpuinfo describes it: the model name, its
+    family / model / stepping numbers (which identify the core generation
+    when a virtual machine shortens the name), the logical CPUs and the
+    vector extensions the oracle's compiler may use."""
+    info = {}
+    cpus = 0
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" not in line:
+                continue
+            k, v = (x.strip() for x in line.split(":", 1))
+            if k == "processor":
+                cpus += 1
+            info.setdefault(k, v)
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    flags = set(info.get("flags", "").split())
+    vec = [f for f in ("avx2", "avx512f", "avx512_vnni", "avx512_bf16") if f in flags]
+    return (f"{info.get('model name', 'unknown')} (family {info.get('cpu family', '?')}, model {info.get('model', '?')}, "
+            f"stepping {info.get('stepping', '?')}; {cpus} logical CPUs; {'/'.join(vec) or 'no AVX2'})")
 
 
 def logits_err(got, want):
