@@ -2428,6 +2428,9 @@ hipError_t fwd_dec_attn(const Dims& D, const SessDev& S, const LayerDev& L, int 
     return hipGetLastError();
 }
 
+// Chunk parts the merge of k_dec_chunks loads at once.
+constexpr int MERGE_AHEAD = 8;
+
 // One decode token's units, attention, gate and A8 in one launch for any
 // key count and with an attention span: attend_head_ref's chunks
 // (key_chunks, infer.rs:1888-1893,2093-2101) run in blocks of their own.
@@ -2778,20 +2781,46 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, La
         __syncthreads();
         if (!s_merge) return;
         if (t < HP * vd) {
-            // merge_parts (infer.rs:2143-2166) in chunk order
+            // merge_parts (infer.rs:2143-2166) in chunk order.  The first
+            // MERGE_AHEAD parts' loads are all issued before any is used (the
+            // parts come from other CUs, a memory round trip each), and their
+            // exponentials are independent of one another; only the two fma
+            // chains run in chunk order.  Parts past those (over 2,048 keys)
+            // are read one by one.
+            constexpr int MA = MERGE_AHEAD;
             const int hh = hh0 + t / vd, i = t % vd;
             const size_t pb = (size_t)hh * D.max_chunks;
+            float mv[MA], ov[MA], sv[MA];
+#pragma unroll
+            for (int p = 0; p < MA; ++p) {
+                const size_t pp = pb + min(p, nchunks - 1);
+                mv[p] = __hip_atomic_load(S.pm + pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                ov[p] = __hip_atomic_load(S.po + pp * vd + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                sv[p] = __hip_atomic_load(S.psum + pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             float big = -1e30f;
-            for (int p = 0; p < nchunks; ++p)
+#pragma unroll
+            for (int p = 0; p < MA; ++p) big = fmaxf(big, mv[p]);  // (clamped repeats change no maximum)
+            for (int p = MA; p < nchunks; ++p)
                 big = fmaxf(big, __hip_atomic_load(S.pm + pb + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+            float w[MA];
+#pragma unroll
+            for (int p = 0; p < MA; ++p) w[p] = lexpf(mv[p] - big);
             float acc = 0.0f, total = 0.0f;
-            for (int p = 0; p < nchunks; ++p) {
+#pragma unroll
+            for (int p = 0; p < MA; ++p) {
+                if (p < nchunks) {
+                    acc = __builtin_fmaf(ov[p], w[p], acc);
+                    total = __builtin_fmaf(w[p], sv[p], total);
+                }
+            }
+            for (int p = MA; p < nchunks; ++p) {
                 const float m = __hip_atomic_load(S.pm + pb + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const float o = __hip_atomic_load(S.po + (pb + p) * vd + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const float sm = __hip_atomic_load(S.psum + pb + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const float w = lexpf(m - big);
-                acc = __builtin_fmaf(o, w, acc);
-                total = __builtin_fmaf(w, sm, total);
+                const float wp = lexpf(m - big);
+                acc = __builtin_fmaf(o, wp, acc);
+                total = __builtin_fmaf(wp, sm, total);
             }
             const float inv = 1.0f / total;
             att[t] = (acc * inv) / gden[t];
