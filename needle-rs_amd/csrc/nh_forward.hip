@@ -373,6 +373,26 @@ __device__ __forceinline__ void chain_pipe_n(Load load, Chain chain) {
     }
 }
 
+template <int DEPTH, typename Buf, typename Load, typename Chain>
+__device__ __forceinline__ void chain_pipe(int nb, Load load, Chain chain);
+
+// chain_pipe with the batch counts of the model's own widths (d = 768: 6
+// batches of 8 chunks; 4 d, and cond_weights' 192 steps: 24) fully
+// unrolled.  In the loop form the compiler's LDS wait at the loop head
+// counts every read in flight, the batch just issued included, so each
+// trip through the loop exposes one LDS round trip; unrolled, every wait
+// counts exactly and only the reads a batch uses are waited for.
+template <int DEPTH, typename Buf, typename Load, typename Chain>
+__device__ __forceinline__ void chain_pipe_any(int nb, Load load, Chain chain) {
+    auto ch = [&](const Buf& d, int) __attribute__((always_inline)) { chain(d); };
+    if (nb == 6)
+        chain_pipe_n<6, DEPTH, Buf>(load, ch);
+    else if (nb == 24)
+        chain_pipe_n<24, DEPTH, Buf>(load, ch);
+    else
+        chain_pipe<DEPTH, Buf>(nb, load, chain);
+}
+
 // mix8 (infer.rs:2343-2380), portable branch: out[r][c] =
 // sum_j ct[j][r] * rows[j][c], each output an fma chain from j = 0.  Thread
 // u < 256 computes the 2 x 2 block r = 2 (u / 16) + {0, 1}, c = 2 (u % 16) +
@@ -517,7 +537,7 @@ __device__ __forceinline__ float dot16_t(const float* xT, const float* yT, int p
                 a = __builtin_fmaf(x.w, y.w, a);
             }
         };
-        if (nb > 0) chain_pipe<3, Buf>(nb, load, chain);
+        if (nb > 0) chain_pipe_any<3, Buf>(nb, load, chain);
         const float* xs = xT + lane * pitch;
         const float* ys = yT + lane * pitch;
         for (int c = nb * 8; c < chunks; ++c) a = __builtin_fmaf(xs[c], ys[c], a);
@@ -685,7 +705,7 @@ __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int l
                 a = __builtin_fmaf(hv[2 * u + 1], h2f((uint16_t)(cw[u] >> 16)), a);
             }
         };
-        if (nb > 0) chain_pipe<3, Buf>(nb, load, chain);
+        if (nb > 0) chain_pipe_any<3, Buf>(nb, load, chain);
         for (int u = nb * 8; u < steps; ++u)
             a = __builtin_fmaf(sh.hT[jm * TP_H + u], h2f(sh.cvT[(jm * COND_RANK + k) * TP_C + u]), a);
     }
