@@ -1557,18 +1557,20 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
     {
         uint4 qw[MAX_HEAD_DIM / 16];
 #pragma unroll
-        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) qw[c] = reinterpret_cast<const uint4*>(q8)[c];
+        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
+            qw[c] = c < rq ? reinterpret_cast<const uint4*>(q8)[c] : make_uint4(0, 0, 0, 0);
         for (int i = t; i < len; i += ATT_THREADS) {
             int dot = 0;
+            // every 16-byte chunk of the key row, the query's past qk zero
+            // (the integer dot is the same; no branch between the reads)
 #pragma unroll
-            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
-                if (c < rq) {
-                    const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
-                    dot = __builtin_amdgcn_sdot4((int)kv.x, (int)qw[c].x, dot, false);
-                    dot = __builtin_amdgcn_sdot4((int)kv.y, (int)qw[c].y, dot, false);
-                    dot = __builtin_amdgcn_sdot4((int)kv.z, (int)qw[c].z, dot, false);
-                    dot = __builtin_amdgcn_sdot4((int)kv.w, (int)qw[c].w, dot, false);
-                }
+            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) {
+                const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
+                dot = __builtin_amdgcn_sdot4((int)kv.x, (int)qw[c].x, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)kv.y, (int)qw[c].y, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)kv.z, (int)qw[c].z, dot, false);
+                dot = __builtin_amdgcn_sdot4((int)kv.w, (int)qw[c].w, dot, false);
+            }
             const float ksc = kss[i];
             const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
             sc[i] = sv;
@@ -2265,19 +2267,21 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
         const float qs = s_qs[h];
         uint4 qv[MAX_HEAD_DIM / 16];
 #pragma unroll
-        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) qv[c] = reinterpret_cast<const uint4*>(q8[h])[c];
+        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
+            qv[c] = c < rq ? reinterpret_cast<const uint4*>(q8[h])[c] : make_uint4(0, 0, 0, 0);
         for (int i = u; i < n; i += DG_HEAD_T) {
-            // (four partial integer sums: exact in any order)
+            // (four partial integer sums: exact in any order; every 16-byte
+            // chunk of the key row, the query's past qk zero, so no branch
+            // sits between the reads)
             int dp[4] = {0, 0, 0, 0};
 #pragma unroll
-            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
-                if (c < rq) {
-                    const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
-                    dp[0] = __builtin_amdgcn_sdot4((int)kv.x, (int)qv[c].x, dp[0], false);
-                    dp[1] = __builtin_amdgcn_sdot4((int)kv.y, (int)qv[c].y, dp[1], false);
-                    dp[2] = __builtin_amdgcn_sdot4((int)kv.z, (int)qv[c].z, dp[2], false);
-                    dp[3] = __builtin_amdgcn_sdot4((int)kv.w, (int)qv[c].w, dp[3], false);
-                }
+            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) {
+                const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
+                dp[0] = __builtin_amdgcn_sdot4((int)kv.x, (int)qv[c].x, dp[0], false);
+                dp[1] = __builtin_amdgcn_sdot4((int)kv.y, (int)qv[c].y, dp[1], false);
+                dp[2] = __builtin_amdgcn_sdot4((int)kv.z, (int)qv[c].z, dp[2], false);
+                dp[3] = __builtin_amdgcn_sdot4((int)kv.w, (int)qv[c].w, dp[3], false);
+            }
             const int dot = (dp[0] + dp[1]) + (dp[2] + dp[3]);
             const float ksc = kss[i];
             const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
@@ -2657,18 +2661,18 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, La
         const float qs = s_qs[h];
         uint4 qv[MAX_HEAD_DIM / 16];
 #pragma unroll
-        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) qv[c] = reinterpret_cast<const uint4*>(q8[h])[c];
+        for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
+            qv[c] = c < rq ? reinterpret_cast<const uint4*>(q8[h])[c] : make_uint4(0, 0, 0, 0);
         for (int i = u; i < len; i += DG_HEAD_T) {
             int dp[4] = {0, 0, 0, 0};
 #pragma unroll
-            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c)
-                if (c < rq) {
-                    const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
-                    dp[0] = __builtin_amdgcn_sdot4((int)kv.x, (int)qv[c].x, dp[0], false);
-                    dp[1] = __builtin_amdgcn_sdot4((int)kv.y, (int)qv[c].y, dp[1], false);
-                    dp[2] = __builtin_amdgcn_sdot4((int)kv.z, (int)qv[c].z, dp[2], false);
-                    dp[3] = __builtin_amdgcn_sdot4((int)kv.w, (int)qv[c].w, dp[3], false);
-                }
+            for (int c = 0; c < MAX_HEAD_DIM / 16; ++c) {
+                const uint4 kv = reinterpret_cast<const uint4*>(ks8[i])[c];
+                dp[0] = __builtin_amdgcn_sdot4((int)kv.x, (int)qv[c].x, dp[0], false);
+                dp[1] = __builtin_amdgcn_sdot4((int)kv.y, (int)qv[c].y, dp[1], false);
+                dp[2] = __builtin_amdgcn_sdot4((int)kv.z, (int)qv[c].z, dp[2], false);
+                dp[3] = __builtin_amdgcn_sdot4((int)kv.w, (int)qv[c].w, dp[3], false);
+            }
             const int dot = (dp[0] + dp[1]) + (dp[2] + dp[3]);
             const float ksc = kss[i];
             const float sv = i < blocked ? (ksc * (float)dot) * qs : (ksc * qs) * (float)dot;
