@@ -728,9 +728,9 @@ __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int l
 // The Hadamard MLP and mHC write of layer P (step.rs:600-705): xl holds the
 // thread's element of the 4 lanes (t < d) and gets the new ones; returns
 // this thread's max |new lane value| (for the next layer's mHC read).
-template <typename AfterMlp>
+template <typename BeforeMix, typename AfterMlp>
 __device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, const OutRegs& q, LayerShared& sh,
-                           float (&xl)[MHC_LANES], AfterMlp after_mlp) {
+                           float (&xl)[MHC_LANES], BeforeMix before_mix, AfterMlp after_mlp) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d;
     // mix8 runs on waves 4..7 (threads 256..511), beside cond_weights on wave 0
     const bool mixer = t >= MIX_T && t < 2 * MIX_T;
@@ -761,6 +761,7 @@ __device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, c
     __syncthreads();
     // cond_weights (wavefront 0) spans both passes of the first mix8; the
     // mixers meet between their passes on their own
+    before_mix();
     if (wave == 0) cond_weights(sh, d, lane, sh.wk);
     if (mixer) {
         mix8_t(mu, sh.kp[0], sh.A, sh.B);
@@ -1097,12 +1098,22 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     }
     if constexpr (has_prev) store_out(D, qo, sh);
     __syncthreads();
-    if constexpr (has_next && has_prev) qi = load_in<!BATCH, PC>(D, R, N);
-    // (batched: the Phi8 rows are read once the MLP's registers are free)
+    if constexpr (has_next && has_prev) qi = load_in<false, PC>(D, R, N);
+    // The Phi8 rows (72 KB at d = 768, ~16 cycles of the CU's address unit
+    // per 1 KB wavefront load): one row alone issues them where wavefront 0
+    // runs cond_weights, the longest chain of the MLP, and the other
+    // wavefronts wait for it anyway (issued right after the first barrier
+    // they held the post norm's barrier back); batched, once the MLP's
+    // registers are free.
     if constexpr (has_prev)
-        m = layer_out(D, S, P, qo, sh, xl, [&]() __attribute__((always_inline)) {
-            if constexpr (has_next && BATCH) load_phi(D, N, qi);
-        });
+        m = layer_out(
+            D, S, P, qo, sh, xl,
+            [&]() __attribute__((always_inline)) {
+                if constexpr (has_next && !BATCH) load_phi(D, N, qi);
+            },
+            [&]() __attribute__((always_inline)) {
+                if constexpr (has_next && BATCH) load_phi(D, N, qi);
+            });
     // the wavefronts' maxima of |xs| for the mHC read
     m = wave_max(m);
     if (lane == 0) sh.red[wave] = m;
