@@ -157,6 +157,24 @@ __device__ __forceinline__ void fwht128(float& v0, float& v1, int lane) {
 // the device library; exact, order-free for non-NaN inputs).
 __device__ __forceinline__ float wave_max(float v) { return __ockl_wfred_max_f32(v); }
 
+// The same for values >= +0 (absolute values, exps and their weights):
+// their bit patterns order as unsigned integers as the values do, so four
+// DPP integer max steps (within quads, then rows of 16 by rotations of 4
+// and 8) and the four rows' maxima read into scalar registers give the
+// exact maximum, in ~a third of the library reduction's instructions
+// (which also quiets each float operand).  All 64 lanes must be active.
+__device__ __forceinline__ unsigned umax_dpp_step(unsigned x, unsigned y) { return x > y ? x : y; }
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    unsigned x = __builtin_bit_cast(unsigned, v);
+    x = umax_dpp_step(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xF, 0xF, false));
+    x = umax_dpp_step(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xF, 0xF, false));
+    x = umax_dpp_step(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x124, 0xF, 0xF, false));
+    x = umax_dpp_step(x, (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, 0x128, 0xF, 0xF, false));
+    const unsigned r0 = (unsigned)__builtin_amdgcn_readlane((int)x, 0), r1 = (unsigned)__builtin_amdgcn_readlane((int)x, 16),
+                   r2 = (unsigned)__builtin_amdgcn_readlane((int)x, 32), r3 = (unsigned)__builtin_amdgcn_readlane((int)x, 48);
+    return __builtin_bit_cast(float, umax_dpp_step(umax_dpp_step(r0, r1), umax_dpp_step(r2, r3)));
+}
+
 // `(v * inv).round().clamp(-128, 127) as i8` (crates/needle-engine/src/qlinear.rs:137-139).
 __device__ __forceinline__ int8_t quant_one(float v, float inv) {
     float r = roundf(v * inv);
@@ -209,7 +227,7 @@ __device__ __forceinline__ void a8_group(float v0, float v1, int lane, int bits,
     const float hs = bits_f32(0x3db504f3u);
     v0 *= hs;
     v1 *= hs;
-    const float m = wave_max(fmaxf(fabsf(v0), fabsf(v1)));
+    const float m = wave_max_nonneg(fmaxf(fabsf(v0), fabsf(v1)));
     const float s = m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
     const float inv = 1.0f / s;
     q[act_offset(lane, bits)] = quant_one(v0, inv);

@@ -102,7 +102,7 @@ __device__ __forceinline__ float dot16_lanes(float v, int n, int lane) {
 // quant_i8's scale (qlinear.rs:92-108) of a value per lane, max over the
 // whole wavefront (lanes outside the vector hold 0).
 __device__ __forceinline__ float wave_quant_scale(float v) {
-    const float m = wave_max(fabsf(v));
+    const float m = wave_max_nonneg(fabsf(v));
     return m > 0.0f ? m * bits_f32(0x3c010204u) : 1.0f;
 }
 
@@ -1115,7 +1115,7 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
                 if constexpr (has_next && BATCH) load_phi(D, N, qi);
             });
     // the wavefronts' maxima of |xs| for the mHC read
-    m = wave_max(m);
+    m = wave_max_nonneg(m);
     if (lane == 0) sh.red[wave] = m;
     __syncthreads();
     // (the new lanes go back to HBM last: nothing here reads them there, and
@@ -1638,7 +1638,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
         sc[i] = w;
         wmax = fmaxf(wmax, w);
     }
-    wmax = wave_max(wmax);
+    wmax = wave_max_nonneg(wmax);
     if (lane == 0) red[wave] = wmax;
     __syncthreads();
     wmax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -1959,7 +1959,7 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
                 wmax = fmaxf(wmax, e[j]);
             }
         }
-        wmax = wave_max(wmax);
+        wmax = wave_max_nonneg(wmax);
         const float qwt = bits_f32(0x49fffff8u) / wmax;
         int8_t(*dg)[AG_COLS] = dig[wave];
 #pragma unroll
@@ -2312,7 +2312,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
             sc[h][i] = e;
             wmax = fmaxf(wmax, e * vss[i]);
         }
-        wmax = wave_max(wmax);
+        wmax = wave_max_nonneg(wmax);
         if (lane == 0) wred[h][hw] = wmax;
     }
     __syncthreads();
@@ -2701,7 +2701,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, La
             sc[h][i] = e;
             wmax = fmaxf(wmax, e * vss[i]);
         }
-        wmax = wave_max(wmax);
+        wmax = wave_max_nonneg(wmax);
         if (lane == 0) wred[h][hw] = wmax;
     }
     __syncthreads();
@@ -2981,7 +2981,7 @@ __global__ __launch_bounds__(256) void k_phi8(const float* __restrict__ rows, in
     const float* x = rows + (size_t)r * width;
     float m = 0.0f;
     for (int i = t; i < width; i += 256) m = fmaxf(m, fabsf(x[i]));
-    m = wave_max(m);
+    m = wave_max_nonneg(m);
     __shared__ float red[4];
     if (lane == 0) red[wave] = m;
     __syncthreads();
