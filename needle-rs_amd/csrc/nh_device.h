@@ -175,6 +175,25 @@ __device__ __forceinline__ float wave_max_nonneg(float v) {
     return __builtin_bit_cast(float, umax_dpp_step(umax_dpp_step(r0, r1), umax_dpp_step(r2, r3)));
 }
 
+// The same for any non-NaN values (scores): the key b ^ ((b >> 31) &
+// 0x7fffffff) of bit pattern b orders as a signed integer as the values do
+// (negative values get their magnitude bits flipped) and is its own
+// inverse.  (-0 keys below +0: no score here is -0.)  All 64 lanes must be
+// active.
+__device__ __forceinline__ int imax_dpp_step(int x, int y) { return x > y ? x : y; }
+__device__ __forceinline__ float wave_max_ordered(float v) {
+    const int b = __builtin_bit_cast(int, v);
+    int x = b ^ ((b >> 31) & 0x7fffffff);
+    x = imax_dpp_step(x, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+    x = imax_dpp_step(x, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+    x = imax_dpp_step(x, __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false));
+    x = imax_dpp_step(x, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+    const int r0 = __builtin_amdgcn_readlane(x, 0), r1 = __builtin_amdgcn_readlane(x, 16),
+              r2 = __builtin_amdgcn_readlane(x, 32), r3 = __builtin_amdgcn_readlane(x, 48);
+    const int k = imax_dpp_step(imax_dpp_step(r0, r1), imax_dpp_step(r2, r3));
+    return __builtin_bit_cast(float, k ^ ((k >> 31) & 0x7fffffff));
+}
+
 // `(v * inv).round().clamp(-128, 127) as i8` (crates/needle-engine/src/qlinear.rs:137-139).
 __device__ __forceinline__ int8_t quant_one(float v, float inv) {
     float r = roundf(v * inv);

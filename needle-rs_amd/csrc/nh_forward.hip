@@ -1588,7 +1588,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attend(Dims D, SessDev S, Layer
             mx = fmaxf(mx, sv);
         }
     }
-    mx = wave_max(mx);
+    mx = wave_max_ordered(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
     mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -1895,7 +1895,7 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
             e[j] = i < len ? scw[i] : -__builtin_inff();
             mx = fmaxf(mx, e[j]);
         }
-        mx = wave_max(mx);
+        mx = wave_max_ordered(mx);
 #pragma unroll
         for (int j = 0; j < AG_KPL; ++j) {
             const int i = lane + 64 * j;
@@ -2299,7 +2299,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
             sc[h][i] = sv;
             mx = fmaxf(mx, sv);
         }
-        mx = wave_max(mx);
+        mx = wave_max_ordered(mx);
         if (lane == 0) red[h][hw] = mx;
     }
     __syncthreads();
@@ -2690,7 +2690,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, La
             sc[h][i] = sv;
             mx = fmaxf(mx, sv);
         }
-        mx = wave_max(mx);
+        mx = wave_max_ordered(mx);
         if (lane == 0) red[h][hw] = mx;
     }
     __syncthreads();
