@@ -6,10 +6,6 @@
 
 #include "nh_internal.h"
 
-// Wavefront reductions of the device library (DPP sequences).
-extern "C" __device__ __attribute__((const)) float __ockl_wfred_max_f32(float);
-extern "C" __device__ __attribute__((const)) int __ockl_wfred_add_i32(int);
-extern "C" __device__ __attribute__((const)) int __ockl_wfred_min_i32(int);
 
 namespace nh {
 
@@ -153,16 +149,13 @@ __device__ __forceinline__ void fwht128(float& v0, float& v1, int lane) {
     v1 = a - b;
 }
 
-// The maximum over the 64 lanes (v_max_f32 through the DPP reduction of
-// the device library; exact, order-free for non-NaN inputs).
-__device__ __forceinline__ float wave_max(float v) { return __ockl_wfred_max_f32(v); }
-
-// The same for values >= +0 (absolute values, exps and their weights):
-// their bit patterns order as unsigned integers as the values do, so four
-// DPP integer max steps (within quads, then rows of 16 by rotations of 4
-// and 8) and the four rows' maxima read into scalar registers give the
-// exact maximum, in ~a third of the library reduction's instructions
-// (which also quiets each float operand).  All 64 lanes must be active.
+// Wavefront reductions.  The maximum over the 64 lanes of values >= +0
+// (absolute values, exps and their weights): their bit patterns order as
+// unsigned integers as the values do, so four DPP integer max steps
+// (within quads, then rows of 16 by rotations of 4 and 8) and the four
+// rows' maxima read into scalar registers give the exact maximum, in ~a
+// third of the instructions of a float reduction (which also quiets each
+// operand).  All 64 lanes must be active.
 __device__ __forceinline__ unsigned umax_dpp_step(unsigned x, unsigned y) { return x > y ? x : y; }
 __device__ __forceinline__ float wave_max_nonneg(float v) {
     unsigned x = __builtin_bit_cast(unsigned, v);
@@ -192,6 +185,18 @@ __device__ __forceinline__ float wave_max_ordered(float v) {
               r2 = __builtin_amdgcn_readlane(x, 32), r3 = __builtin_amdgcn_readlane(x, 48);
     const int k = imax_dpp_step(imax_dpp_step(r0, r1), imax_dpp_step(r2, r3));
     return __builtin_bit_cast(float, k ^ ((k >> 31) & 0x7fffffff));
+}
+
+// The minimum of an integer over the 64 lanes by the same four DPP steps
+// and four lane reads.  All 64 lanes must be active.
+__device__ __forceinline__ int imin_dpp_step(int x, int y) { return x < y ? x : y; }
+__device__ __forceinline__ int wave_min_i32(int x) {
+    x = imin_dpp_step(x, __builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false));
+    x = imin_dpp_step(x, __builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false));
+    x = imin_dpp_step(x, __builtin_amdgcn_update_dpp(0, x, 0x124, 0xF, 0xF, false));
+    x = imin_dpp_step(x, __builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false));
+    return imin_dpp_step(imin_dpp_step(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+                         imin_dpp_step(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
 }
 
 // `(v * inv).round().clamp(-128, 127) as i8` (crates/needle-engine/src/qlinear.rs:137-139).

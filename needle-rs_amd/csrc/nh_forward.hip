@@ -883,6 +883,11 @@ __device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InReg
     }
 }
 
+// (The device library's wavefront sum: the DPP form of wave_sum_i32
+// measured no faster in the one-row kernel and spilled 8 more bytes in the
+// 64-VGPR batched one.)
+extern "C" __device__ __attribute__((const)) int __ockl_wfred_add_i32(int);
+
 template <int PC>
 __device__ __forceinline__ int dot_row(const uint4* r, const int8_t* x8, int per, int lane) {
     const uint4* xv = reinterpret_cast<const uint4*>(x8);
@@ -2926,7 +2931,8 @@ hipError_t fwd_dec_chunks(const Dims& D, const SessDev& S, const LayerDev& L, in
 // greater) and otherwise never moves to a NaN, so NaNs are skipped and a
 // NaN first element gives 0.  Each thread keeps the first maximum of its
 // strided share (all its loads issued first); a wavefront's first maximum is the smallest index among
-// the lanes holding the wavefront's maximum (two DPP reductions), and the
+// the lanes holding the wavefront's maximum (two DPP reductions; the maximum's sign of zero does not
+// matter, the lanes compare equal to it), and the
 // same again over the wavefronts' results.
 __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, uint32_t* __restrict__ dst) {
     constexpr int PER = 16;  // elements per thread read in one batch
@@ -2948,8 +2954,8 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
             }
         }
     }
-    const float wm = wave_max(best);
-    const int wi = __ockl_wfred_min_i32(best == wm && bi < n ? bi : 0x7fffffff);
+    const float wm = wave_max_ordered(best);
+    const int wi = wave_min_i32(best == wm && bi < n ? bi : 0x7fffffff);
     __shared__ float sv[16];
     __shared__ int si[16];
     if (lane == 0) {
@@ -2960,8 +2966,8 @@ __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, in
     if (wave == 0) {
         const float v = lane < 16 && si[min(lane, 15)] != 0x7fffffff ? sv[min(lane, 15)] : -__builtin_inff();
         const int ix = lane < 16 ? si[min(lane, 15)] : 0x7fffffff;
-        const float m = wave_max(v);
-        const int first = __ockl_wfred_min_i32(v == m && ix != 0x7fffffff ? ix : 0x7fffffff);
+        const float m = wave_max_ordered(v);
+        const int first = wave_min_i32(v == m && ix != 0x7fffffff ? ix : 0x7fffffff);
         // with x[0] NaN nothing is greater than x[best = 0]: the reference keeps 0
         if (lane == 0) dst[0] = (uint32_t)(first < n && x0 == x0 ? first : 0);
     }
