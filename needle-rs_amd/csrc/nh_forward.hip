@@ -820,21 +820,27 @@ __device__ float layer_out(const Dims& D, const SessDev& S, const LayerDev& P, c
 constexpr int PHI_CHUNKS = MHC_LANES * FWD_MAX_D / 16 / 64;
 constexpr int PHI_B = LT / 64 - 1;  // wavefronts holding Phi8 rows
 static_assert(2 * PHI_B >= MHC_COLS, "two Phi8 rows per wavefront cover the 24 rows");
+// The one-row kernel issues the rows beside cond_weights, where the mix8
+// wavefronts (4-7) are busy: there they are held by the other eleven (MF,
+// mixer-free), rows h, h + 11 and, for h < 2, h + 22 on holder h.
+constexpr int PHI_MF = PHI_B - MIX_T / 64;
+static_assert(3 * PHI_MF >= MHC_COLS && 2 * PHI_MF < MHC_COLS, "holders 0 and 1 take a third row");
+__device__ __forceinline__ int phi_holder(int wave) { return wave >= 1 && wave <= 3 ? wave - 1 : wave >= 8 ? wave - 5 : -1; }
 // PC: the 1 KB chunks a Phi8 row has (its 4 d int8 / 1024), fixed at compile
 // time so a narrower model holds no registers for chunks it never reads (3
 // at d = 768: 24 VGPRs instead of 32, which the 64-VGPR batched kernel needs).
 template <int PC>
 struct InRegs {
     uint32_t norm;
-    float kr, ev, ps0, ps1;
-    uint4 r0[PC], r1[PC];
+    float kr, ev, ps0, ps1, ps2;
+    uint4 r0[PC], r1[PC], r2[PC];
 };
 
-template <int PC>
+template <int PC, bool MF>
 __device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InRegs<PC>& q);
 
 // PHI: the Phi8 rows too (else layer_in reads them itself).
-template <bool PHI, int PC>
+template <bool PHI, int PC, bool MF>
 __device__ __forceinline__ InRegs<PC> load_in(const Dims& D, const SessDev& S, const LayerDev& N) {
     const int t = threadIdx.x, d = D.d;
     // Unconditional loads at clamped addresses (threads, rows and chunks
@@ -849,13 +855,37 @@ __device__ __forceinline__ InRegs<PC> load_in(const Dims& D, const SessDev& S, c
     const float* ep = site ? S.evals + (size_t)N.site * BATCH_ROWS * d : S.proj + d;
     q.kr = kp[td];
     q.ev = ep[td];
-    if constexpr (PHI) load_phi(D, N, q);
+    if constexpr (PHI) load_phi<PC, MF>(D, N, q);
     return q;
 }
 
-template <int PC>
+template <int PC, bool MF>
 __device__ __forceinline__ void load_phi(const Dims& D, const LayerDev& N, InRegs<PC>& q) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, nc = MHC_LANES * D.d;
+    if constexpr (MF) {
+        const int h = phi_holder(__builtin_amdgcn_readfirstlane(wave));
+        if (h >= 0) {
+            const int per = nc / 16;
+            const bool three = h + 2 * PHI_MF < MHC_COLS;
+            const int k2 = min(h + 2 * PHI_MF, MHC_COLS - 1);
+            const uint4* row0 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)h * nc);
+            const uint4* row1 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)(h + PHI_MF) * nc);
+            const uint4* row2 = reinterpret_cast<const uint4*>(N.phi_q + (size_t)k2 * nc);
+#pragma unroll
+            for (int j = 0; j < PC; ++j) {
+                if (64 * j < per) {
+                    const int c = min(lane + 64 * j, per - 1);
+                    q.r0[j] = row0[c];
+                    q.r1[j] = row1[c];
+                    if (three) q.r2[j] = row2[c];
+                }
+            }
+            q.ps0 = N.phi_s[h];
+            q.ps1 = N.phi_s[h + PHI_MF];
+            q.ps2 = N.phi_s[k2];
+        }
+        return;
+    }
     // Phi8 rows: wavefront w >= 1 holds row w - 1, and row w + PHI_B - 1
     // while that is below 24; wavefront 0, which runs the first chain of the
     // MLP right after these loads are issued, holds none, so it never waits
@@ -912,12 +942,12 @@ __device__ __forceinline__ int dot_row(const uint4* r, const int8_t* x8, int per
 // behind a barrier.  The post and residual
 // gates of the layer (hpost, the Sinkhorn hres) are computed beside its
 // units, off this kernel's path.
-template <bool LATE_PHI, int PC>
+template <bool LATE_PHI, int PC, bool MF>
 __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, InRegs<PC> q, int in_bits,
                          LayerShared& sh, const float (&xl)[MHC_LANES]) {
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63, d = D.d, nc = MHC_LANES * d;
     // (the Phi8 rows read now land while wavefront 0 runs the norm chain)
-    if constexpr (LATE_PHI) load_phi(D, N, q);
+    if constexpr (LATE_PHI) load_phi<PC, MF>(D, N, q);
     // every wavefront: r = rinv(dot16(xs)), the amax over the wavefronts'
     // maxima of |xs| (rounding is monotonic, so max_i |xs_i r| =
     // max_i |xs_i| r for r > 0), then the int8 lanes
@@ -940,7 +970,21 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, InR
     {
         const float sx = sh.r_sx;
         const int per = nc / 16;
-        if (wave >= 1) {
+        if constexpr (MF) {
+            const int h = phi_holder(wave);
+            if (h >= 0) {
+                const int acc = dot_row<PC>(q.r0, sh.nx8, per, lane);
+                const int acc1 = dot_row<PC>(q.r1, sh.nx8, per, lane);
+                if (lane == 0) {
+                    sh.p[h] = (sx * q.ps0) * (float)acc;
+                    sh.p[h + PHI_MF] = (sx * q.ps1) * (float)acc1;
+                }
+                if (h + 2 * PHI_MF < MHC_COLS) {
+                    const int acc2 = dot_row<PC>(q.r2, sh.nx8, per, lane);
+                    if (lane == 0) sh.p[h + 2 * PHI_MF] = (sx * q.ps2) * (float)acc2;
+                }
+            }
+        } else if (wave >= 1) {
             const int acc = dot_row<PC>(q.r0, sh.nx8, per, lane);
             if (lane == 0) sh.p[wave - 1] = (sx * q.ps0) * (float)acc;
             if (wave - 1 + PHI_B < MHC_COLS) {
@@ -1086,7 +1130,7 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     // go now.  With one they go after the first barrier: the Phi8 rows are
     // half the kernel's bytes and are not needed before the mHC read, so
     // they stay out of the way of the tables the MLP waits for.
-    if constexpr (has_next && !has_prev) qi = load_in<!BATCH, PC>(D, R, N);
+    if constexpr (has_next && !has_prev) qi = load_in<!BATCH, PC, !BATCH>(D, R, N);
     if constexpr (!has_next) fnorm = G.final_norm[min(t, d - 1)];
     float m = 0.0f;
     if (t == 0) sh.mix_count = 0;
@@ -1103,7 +1147,7 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     }
     if constexpr (has_prev) store_out(D, qo, sh);
     __syncthreads();
-    if constexpr (has_next && has_prev) qi = load_in<false, PC>(D, R, N);
+    if constexpr (has_next && has_prev) qi = load_in<false, PC, !BATCH>(D, R, N);
     // The Phi8 rows (72 KB at d = 768, ~16 cycles of the CU's address unit
     // per 1 KB wavefront load): one row alone issues them where wavefront 0
     // runs cond_weights, the longest chain of the MLP, and the other
@@ -1114,10 +1158,10 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
         m = layer_out(
             D, S, P, qo, sh, xl,
             [&]() __attribute__((always_inline)) {
-                if constexpr (has_next && !BATCH) load_phi(D, N, qi);
+                if constexpr (has_next && !BATCH) load_phi<PC, true>(D, N, qi);
             },
             [&]() __attribute__((always_inline)) {
-                if constexpr (has_next && BATCH) load_phi(D, N, qi);
+                if constexpr (has_next && BATCH) load_phi<PC, false>(D, N, qi);
             });
     // the wavefronts' maxima of |xs| for the mHC read
     m = wave_max_nonneg(m);
@@ -1127,7 +1171,7 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
     // stores issued earlier would sit in the memory counter ahead of loads
     // that are waited for)
     if constexpr (has_next)
-        layer_in<BATCH && !has_prev, PC>(D, R, N, qi, in_bits, sh, xl);
+        layer_in<BATCH && !has_prev, PC, !BATCH>(D, R, N, qi, in_bits, sh, xl);
     else if ((int)blockIdx.x >= head_row0)  // (uniform over the block)
         head_in(D, S, fnorm, head_bits, blockIdx.x - head_row0, sh, xl);  // row i - row0 - head_row0
     if constexpr (has_prev) {
