@@ -719,7 +719,8 @@ __device__ __forceinline__ void cond_weights(const LayerShared& sh, int d, int l
     const float e = lexpf(lg - m);
     float ev[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ev[i] = __shfl(e, i, 64);
+    for (int i = 0; i < 8; ++i)
+        ev[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, e), i));
     const float sum = ev[7] + ((ev[6] + (ev[5] + ev[4])) + ((ev[3] + ev[2]) + (ev[1] + ev[0])));
     const float inv = 1.0f / sum;
     if (lane < 8) wk[lane] = e * inv;
@@ -1004,7 +1005,8 @@ __device__ void layer_in(const Dims& D, const SessDev& S, const LayerDev& N, InR
             g = 1.0f / (lexpf(-zz) + 1.0f);
         }
 #pragma unroll
-        for (int b = 0; b < MHC_LANES; ++b) hp[b] = __shfl(g, b, 64);
+        for (int b = 0; b < MHC_LANES; ++b)
+            hp[b] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, g), b));
     }
     float u = 0.0f, x1 = 0.0f;
     if (t < d) {
@@ -1238,8 +1240,12 @@ __device__ __forceinline__ double dpp64(double x) {
 
 __device__ __forceinline__ float sinkhorn_lane(float z, int lane) {
     const int r = (lane >> 2) & 3;
-    const float z0 = __shfl(z, 4 * r, 64), z1 = __shfl(z, 4 * r + 1, 64), z2 = __shfl(z, 4 * r + 2, 64),
-                z3 = __shfl(z, 4 * r + 3, 64);
+    // the row's four elements by DPP quad broadcasts (row r is a quad)
+    const int zi = __builtin_bit_cast(int, z);
+    const float z0 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, zi, 0x00, 0xF, 0xF, false)),
+                z1 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, zi, 0x55, 0xF, 0xF, false)),
+                z2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, zi, 0xAA, 0xF, 0xF, false)),
+                z3 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, zi, 0xFF, 0xF, 0xF, false));
     const double m = (double)fmaxf(fmaxf(z0, z1), fmaxf(z2, z3));
     double e = exp((double)z - m);
     // Both sums are (x0 + x1) + (x2 + x3) over the row's (column's)
