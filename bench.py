@@ -632,7 +632,7 @@ def main():
         print(json.dumps({"copy_bytes": args.copy_calibration, "launches": 5}))
         return
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus above 1 is not supported "
+        print(json.dumps({"error": "the library runs on one GPU; --gpus above 1 is not supported "
                                    "(the W4A8 products would shard by output rows)"}))
         sys.exit(2)
     if args.copies < 1:
