@@ -293,6 +293,13 @@ int nh_session_rewind_zeroed(nh_session* s, int len);
  * and resets the session.  No call waits for earlier work to check it.
  * 0 makes every such wait give up at once, for tests of that path. */
 int nh_session_debug_spin_limit(nh_session* s, int limit);
+/* No reference counterpart (the reference's calls are synchronous and a
+ * failure surfaces in the call that caused it): waits for everything queued
+ * on `stream` and reports a bounded wait that gave up in the session's feeds
+ * so far (NH_EDEVICE, the session reset, as above), so a caller that wants
+ * the failure attributed to the feed that caused it calls this after the
+ * feed.  NH_OK when none did. */
+int nh_session_sync(nh_session* s, void* stream);
 /* No reference counterpart (a test hook for the failure path): the
  * `after`-th feed from now (each nh_forward* / nh_prefill chunk group or
  * greedy step counts one) fails with NH_EDEVICE before it launches anything,

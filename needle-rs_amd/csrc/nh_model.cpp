@@ -1002,6 +1002,13 @@ int nh_session_clone(const nh_session* s, void* stream, nh_session** out) {
     return NH_OK;
 }
 
+int nh_session_sync(nh_session* s, void* stream) {
+    if (!s) return fail(NH_EINVAL, "null argument");
+    hipStream_t st = (hipStream_t)stream;
+    NH_TRY(hipStreamSynchronize(st), "session sync");
+    return check_status(s, st, true);
+}
+
 int nh_session_debug_spin_limit(nh_session* s, int limit) {
     if (!s || limit < 0) return fail(NH_EINVAL, "bad arguments");
     s->dims.spin_limit = limit > 0 ? limit : 0;

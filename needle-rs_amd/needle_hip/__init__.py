@@ -79,6 +79,7 @@ SIGNATURES = {
     "nh_session_set_attend": (I, [P, I, I]),
     "nh_session_rollback": (I, [P, I]),
     "nh_session_debug_spin_limit": (I, [P, I]),
+    "nh_session_sync": (I, [P, P]),
     "nh_session_rewind_zeroed": (I, [P, I]),
     "nh_session_last_hidden": (I, [P, P, P]),
     "nh_session_head_logits": (I, [P, P, P]),
@@ -547,6 +548,12 @@ class Session:
     def debug_spin_limit(self, limit: int):
         """Test hook: the polls a bounded in-kernel wait makes before giving up."""
         _check(_lib.nh_session_debug_spin_limit(self.h, int(limit)))
+
+    def sync(self, stream=None):
+        """Wait for the session's queued work and report a bounded wait that gave
+        up in its feeds (raises, and the session is reset); no reference
+        counterpart (its calls are synchronous)."""
+        _check(_lib.nh_session_sync(self.h, _stream(stream)))
 
     def rollback(self, n: int):
         """Session::rollback (model.rs:81-113)."""

@@ -283,6 +283,17 @@ def test_bounded_wait_gives_up_and_reports(nh):
     with pytest.raises(nh.NeedleHipError, match="gave up"):
         s.forward([3])
     assert len(s) == 0
+    # an explicit sync attributes the failure to the feed that caused it
+    s.sync()  # nothing pending: no error
+    s.debug_spin_limit(0)
+    s.forward([4, 5])
+    with pytest.raises(nh.NeedleHipError, match="gave up"):
+        s.sync()
+    assert len(s) == 0
+    s.debug_spin_limit(1 << 20)
+    s.forward([5, 6, 7])
+    s.sync()
+    assert len(s) == 3
 
 
 def test_failed_greedy_step_resets(nh):
