@@ -136,7 +136,8 @@ def launch_floors(args, nh, torch):
     `copies` launches over distinct buffers, for a one-element fill (the launch itself), a write of the
     GEMV's algorithmic bytes, a copy of them (read + write), the GEMV's own loads with no arithmetic in
     its grid (nh_debug_read_floor mode 0), a plain grid-stride read of its code and norm bytes (mode 1),
-    and the GEMV."""
+    the loads in its grid ending as the GEMV ends (a workgroup barrier, then one float stored per row:
+    mode 2), and the GEMV."""
     nbytes = algorithmic_bytes(1, K, N)
     n4 = nbytes // 4
     tiny = [torch.empty(1, device="cuda") for _ in range(args.copies)]
@@ -155,10 +156,11 @@ def launch_floors(args, nh, torch):
     mats, a = gpu["mats"], gpu["a"]
     out["read_gemv_grid_us"] = us(lambda: [m.read_floor(a, 0) for m in mats])
     out["read_stream_us"] = us(lambda: [m.read_floor(a, 1) for m in mats])
+    out["read_gemv_grid_store_us"] = us(lambda: [m.read_floor(a, 2, gpu["y"]) for m in mats])
     out["gemv_us"] = round(gpu["ms_launch"] * 1e3, 4)
     out["gemv_again_us"] = round(time_graph(lambda: [m.matmul_into(a, gpu["y"], N, 0) for m in mats],
                                             max(1, args.steps), max(1, args.warmup), torch) / args.copies * 1e3, 4)
-    for k in ("read_gemv_grid_us", "read_stream_us", "gemv_us"):
+    for k in ("read_gemv_grid_us", "read_stream_us", "read_gemv_grid_store_us", "gemv_us"):
         out[k.replace("_us", "_tb_s")] = round(nbytes / out[k] / 1e6, 3)
     return out
 

@@ -148,8 +148,10 @@ int nh_debug_partials(const nh_qmat* w, const nh_qact* a, int32_t* out, void* st
  * product of a 4-bit w with a one-token a.  mode 0 issues exactly the loads
  * the decode GEMV issues (codes, norms, activations, scales), in its grid,
  * with no arithmetic; mode 1 reads the codes and norms as a plain
- * grid-stride stream.  Nothing is written. */
-int nh_debug_read_floor(const nh_qmat* w, const nh_qact* a, int mode, void* stream);
+ * grid-stride stream; mode 2 is mode 0 ending as the product does (a
+ * workgroup barrier, then one float per row stored to y[0 .. w's out), a
+ * value with no meaning).  Modes 0 and 1 write nothing and ignore y. */
+int nh_debug_read_floor(const nh_qmat* w, const nh_qact* a, int mode, float* y, void* stream);
 
 /* ---- archives (QWeights, crates/needle-engine/src/weights.rs:136-148) --- */
 /* Weights::from_archive_mode with fast = true (weights.rs:314-467) over the

@@ -727,10 +727,12 @@ int nh_debug_partials(const nh_qmat* w, const nh_qact* a, int32_t* out, void* st
     return NH_OK;
 }
 
-int nh_debug_read_floor(const nh_qmat* w, const nh_qact* a, int mode, void* stream) {
+int nh_debug_read_floor(const nh_qmat* w, const nh_qact* a, int mode, float* y, void* stream) {
     if (int rc = check_pair(w, a)) return rc;
-    if (w->m.bits != 4 || a->rows != 1 || (mode != 0 && mode != 1)) return fail(NH_EINVAL, "a 4-bit one-token product, mode 0 or 1");
-    NH_HIP(launch_read_floor(w, a, mode, (hipStream_t)stream), "read floor");
+    if (w->m.bits != 4 || a->rows != 1 || mode < 0 || mode > 2)
+        return fail(NH_EINVAL, "a 4-bit one-token product, mode 0, 1 or 2");
+    if (mode == 2 && !y) return fail(NH_EINVAL, "mode 2 stores to y");
+    NH_HIP(launch_read_floor(w, a, mode, y, (hipStream_t)stream), "read floor");
     return NH_OK;
 }
 

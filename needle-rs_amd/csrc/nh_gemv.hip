@@ -300,15 +300,18 @@ hipError_t launch_gemv_batch(const nh_qmat* const* w, const nh_qact* const* a, f
 // Read floors of the decode product, for measurement only.  The tile form
 // issues exactly the loads k_gemv<GPS, S, 4> issues (codes with the
 // streaming hint, norms, activations, scales) in its grid, and no
-// arithmetic, LDS or barrier; the stream form reads the codes and the norms
-// as a plain grid-stride stream of 16-byte loads, four in flight per lane.
-// Neither stores anything: an empty asm statement consumes the loaded
-// values, so the loads stay.
-template <int GPS, int S>
+// arithmetic or LDS; the stream form reads the codes and the norms as a
+// plain grid-stride stream of 16-byte loads, four in flight per lane.  An
+// empty asm statement consumes the loaded values, so the loads stay.  With
+// STORE the tile form then ends as the product does: a workgroup barrier
+// (every wavefront's loads have arrived) and wavefront 0's store of one
+// float per row; without it, nothing is stored.
+template <int GPS, int S, bool STORE>
 __global__ __launch_bounds__(S * 64) void k_read_floor_tile(const uint4* __restrict__ codes,
                                                             const uint16_t* __restrict__ norms,
                                                             const uint4* __restrict__ xq,
-                                                            const float* __restrict__ sx, int G) {
+                                                            const float* __restrict__ sx, int G,
+                                                            float* __restrict__ y, int out) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane >> 2, l = lane & 3;
     const int n = blockIdx.x * TILE_ROWS + r, g0 = wave * GPS;
     uint32_t x = 0;
@@ -332,6 +335,10 @@ __global__ __launch_bounds__(S * 64) void k_read_floor_tile(const uint4* __restr
 #pragma unroll
     for (int j = 0; j < GPS; ++j) x ^= c[j].x ^ c[j].y ^ c[j].z ^ c[j].w ^ nb[j] ^ sv[j];
     asm volatile("" ::"v"(x));
+    if constexpr (STORE) {
+        __syncthreads();
+        if (wave == 0 && l == 0 && n < out) y[n] = __uint_as_float(x & 0x3fffffffu);
+    }
 }
 
 __global__ __launch_bounds__(256) void k_read_floor_stream(const uint4* __restrict__ a, size_t na,
@@ -354,13 +361,14 @@ __global__ __launch_bounds__(256) void k_read_floor_stream(const uint4* __restri
 }
 
 template <int GPS, int S>
-static hipError_t run_floor(const nh_qmat* w, const nh_qact* a, hipStream_t s) {
-    hipLaunchKernelGGL((k_read_floor_tile<GPS, S>), dim3(w->m.out_pad / TILE_ROWS), dim3(S * 64), 0, s,
-                       (const uint4*)w->d_codes, w->d_norms, (const uint4*)a->d_xq, a->d_sx, w->m.groups);
+static hipError_t run_floor(const nh_qmat* w, const nh_qact* a, float* y, hipStream_t s) {
+    auto kern = y ? k_read_floor_tile<GPS, S, true> : k_read_floor_tile<GPS, S, false>;
+    hipLaunchKernelGGL(kern, dim3(w->m.out_pad / TILE_ROWS), dim3(S * 64), 0, s, (const uint4*)w->d_codes,
+                       w->d_norms, (const uint4*)a->d_xq, a->d_sx, w->m.groups, y, w->m.out);
     return hipGetLastError();
 }
 
-hipError_t launch_read_floor(const nh_qmat* w, const nh_qact* a, int mode, hipStream_t s) {
+hipError_t launch_read_floor(const nh_qmat* w, const nh_qact* a, int mode, float* y, hipStream_t s) {
     if (mode == 1) {
         // 16-byte units: codes out_pad x G x 64 bytes, norms out_pad x G x 2 bytes (out_pad: a multiple of 16)
         const size_t na = (size_t)w->m.out_pad * w->m.groups * 64 / 16, nb = (size_t)w->m.out_pad * w->m.groups * 2 / 16;
@@ -369,17 +377,18 @@ hipError_t launch_read_floor(const nh_qmat* w, const nh_qact* a, int mode, hipSt
                            (const uint4*)w->d_norms, nb);
         return hipGetLastError();
     }
+    if (mode != 2) y = nullptr;
     const int G = w->m.groups;  // the shapes dispatch<4> picks
-    if (G <= 1) return run_floor<1, 1>(w, a, s);
-    if (G <= 2) return run_floor<2, 1>(w, a, s);
-    if (G <= 3) return run_floor<3, 1>(w, a, s);
-    if (G <= 4) return run_floor<2, 2>(w, a, s);
-    if (G <= 6) return run_floor<1, 6>(w, a, s);
-    if (G <= 8) return run_floor<2, 4>(w, a, s);
-    if (G <= 12) return run_floor<3, 4>(w, a, s);
-    if (G <= 16) return run_floor<2, 8>(w, a, s);
-    if (G <= 24) return run_floor<4, 6>(w, a, s);
-    if (G <= 32) return run_floor<4, 8>(w, a, s);
+    if (G <= 1) return run_floor<1, 1>(w, a, y, s);
+    if (G <= 2) return run_floor<2, 1>(w, a, y, s);
+    if (G <= 3) return run_floor<3, 1>(w, a, y, s);
+    if (G <= 4) return run_floor<2, 2>(w, a, y, s);
+    if (G <= 6) return run_floor<1, 6>(w, a, y, s);
+    if (G <= 8) return run_floor<2, 4>(w, a, y, s);
+    if (G <= 12) return run_floor<3, 4>(w, a, y, s);
+    if (G <= 16) return run_floor<2, 8>(w, a, y, s);
+    if (G <= 24) return run_floor<4, 6>(w, a, y, s);
+    if (G <= 32) return run_floor<4, 8>(w, a, y, s);
     return hipErrorInvalidValue;
 }
 

@@ -146,7 +146,7 @@ hipError_t launch_act_prep(const float* x, int rows, int in_dim, int groups, int
                            int8_t* xq, float* sx, hipStream_t s);
 hipError_t launch_gemv(const nh_qmat* w, const nh_qact* a, float* y, int col0, int32_t* dbg_lanes, hipStream_t s);
 // The decode product's read floors (0: its loads in its grid, 1: a plain stream of its bytes).
-hipError_t launch_read_floor(const nh_qmat* w, const nh_qact* a, int mode, hipStream_t s);
+hipError_t launch_read_floor(const nh_qmat* w, const nh_qact* a, int mode, float* y, hipStream_t s);
 hipError_t launch_expand_w8(const nh_qmat* w, hipStream_t s);
 hipError_t launch_gemm(const nh_qmat* w, const nh_qact* a, const uint8_t* block, float* y, int ldy, int col0,
                        int32_t* dbg_totals, hipStream_t s);

@@ -69,7 +69,7 @@ SIGNATURES = {
     "nh_forward": (I, [P, P, I, P, P]),
     "nh_forward_outputs": (I, [P, P, I, I, P, C.c_int64, P]),
     "nh_forward_cells": (I, [P, P, I, I, P, C.c_int64, P, C.c_int64, P]),
-    "nh_debug_read_floor": (I, [P, P, I, P]),
+    "nh_debug_read_floor": (I, [P, P, I, P, P]),
     "nh_session_track_cells": (I, [P, I]),
     "nh_session_cell_rows": (I, [P]),
     "nh_session_cells": (I, [P, I, I, P, P]),
@@ -293,10 +293,14 @@ class QMat:
     def row(self, r: int) -> torch.Tensor:
         return self.rows(torch.tensor([r], dtype=torch.int32, device="cuda"))[0]
 
-    def read_floor(self, a: QAct, mode: int, stream=None):
-        """Measurement: the decode product's loads with no arithmetic (mode 0, its grid) or a
-        plain stream of its code and norm bytes (mode 1)."""
-        _check(_lib.nh_debug_read_floor(self.h, a.h, int(mode), _stream(stream)))
+    def read_floor(self, a: QAct, mode: int, y: torch.Tensor | None = None, stream=None):
+        """Measurement: the decode product's loads with no arithmetic (mode 0, its grid), a plain
+        stream of its code and norm bytes (mode 1), or mode 0 ending as the product does, with a
+        workgroup barrier and one float stored per row to y (mode 2; y: float32, at least out)."""
+        if mode == 2 and (y is None or y.dtype != torch.float32 or y.numel() < self.out or not y.is_cuda):
+            raise ValueError("mode 2 stores one float32 per row to a device tensor y")
+        _check(_lib.nh_debug_read_floor(self.h, a.h, int(mode), _dptr(y) if mode == 2 else None,
+                                        _stream(stream)))
 
     def partials(self, a: QAct, stream=None) -> torch.Tensor:
         """int32 lanes [out, groups, 4] (one token) or totals [rows, out, groups]."""

@@ -299,6 +299,28 @@ def test_edge_cases(nh):
         small.prep(dev(np.zeros(70 * K, np.float32)), 70)
 
 
+def test_read_floors(nh):
+    """The measurement-only read floors run in the product's grid and write nothing but
+    mode 2's one float per row."""
+    say("read floors")
+    K, N = 2048, 40
+    w, x = seeded(N, K, 1, seed=11)
+    q, _ = pair(nh, w, N, K)
+    a = nh.QAct.new(dev(x), 1, K)
+    y = torch.full((N + 8,), 7.0, device="cuda")
+    q.read_floor(a, 0)
+    q.read_floor(a, 1)
+    q.read_floor(a, 2, y)
+    yh = y.cpu().numpy()
+    # the stored bits have bit 30 clear: finite, below 2, never the 7.0 sentinel
+    assert np.all(np.isfinite(yh[:N])) and np.all(np.abs(yh[:N]) < 2.0)
+    assert np.all(yh[N:] == 7.0)
+    with pytest.raises(ValueError):
+        q.read_floor(a, 2, y[:N - 1])
+    with pytest.raises(nh.NeedleHipError):
+        q.read_floor(a, 3)
+
+
 def test_repeatable(nh):
     say("determinism")
     K, N, M = 768, 2304, 64
