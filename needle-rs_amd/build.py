@@ -20,8 +20,8 @@ OUT_DIR = os.path.join(HERE, "needle_hip")
 LIB = os.path.join(OUT_DIR, "libneedle_hip.so")
 OBJ_DIR = os.path.join(HERE, "_build")
 
-SOURCES = ["nh_api.hip", "nh_act.hip", "nh_gemv.hip", "nh_gemm.hip", "nh_misc.hip", "nh_forward.hip", "nh_archive.cpp",
-           "nh_model.cpp"]
+SOURCES = ["nh_api.hip", "nh_act.hip", "nh_gemv.hip", "nh_gemv_res.hip", "nh_gemm.hip", "nh_misc.hip", "nh_forward.hip",
+           "nh_archive.cpp", "nh_model.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [
@@ -42,9 +42,12 @@ FLAGS = [
 # Per-file flags.  The forward's kernels run one to a few dozen workgroups
 # each and wait on their arguments first: their first 16 argument dwords
 # are preloaded into SGPRs at wave launch (the Needle-3 decode token 537.5 ->
-# 526 us).  The products' wide grids measured no gain (a 512-workgroup GEMV
-# 3.64 -> 3.69 us), so they keep the plain argument loads.
-FILE_FLAGS = {"nh_forward.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"]}
+# 526 us).  So are the resident matrices' GEMVs, the decode step's products
+# (520.7 -> 510.8 us).  The streamed GEMV measured slower with it (the
+# 512-workgroup K = 2048 product 3.63 -> 3.68 us), so it and the GEMMs keep
+# the plain argument loads.
+PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
+FILE_FLAGS = {"nh_forward.hip": PRELOAD, "nh_gemv_res.hip": PRELOAD}
 
 
 def _compile(src: str) -> str:

@@ -17,113 +17,13 @@
 // group-ordered fma chain from LDS.
 #include <string.h>
 
-#include <type_traits>
-
-#include "nh_device.h"
-#include "nh_internal.h"
+#include "nh_gemv_tile.h"
 
 namespace nh {
 
 // Workgroups per CU of the streaming variant, and the tile count from which
 // it replaces one workgroup per tile (8 tiles per workgroup).
 constexpr int STREAM_WG_PER_CU = 4;
-
-// NT: the code loads carry the non-temporal hint (a matrix read once per
-// sweep of more than the caches hold); without it (a resident matrix, read
-// again at every token) their lines stay cached.
-template <int GPS, int S, int BITS, bool DBG, bool NT>
-__device__ __forceinline__ void gemv_tile(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
-                                          const uint4* __restrict__ xq, const float* __restrict__ sx,
-                                          float* __restrict__ y, int32_t* __restrict__ dbg, int out, int G, float cbs,
-                                          Lut lut, int tile) {
-    const int wave = threadIdx.x >> 6;
-    const int lane = threadIdx.x & 63;
-    const int r = lane >> 2, l = lane & 3;
-    const int n = tile * TILE_ROWS + r;
-    const int g0 = wave * GPS;
-
-    // The token's activations, issued ahead of the code stream.  With one
-    // group per wavefront a lane reads its decode lane's 32 bytes itself (the
-    // 16 rows' lanes with the same l share them: one 128-byte span per
-    // wavefront, an L2 hit after the first workgroup) and no barrier waits
-    // for the slowest wavefront; with more, the G * 128 bytes go to LDS once
-    // per workgroup (two direct reads per group measured slower there).
-    constexpr bool DIRECT = GPS == 1;
-    static_assert(DIRECT || S * 64 >= GPS * S * 8, "one thread per activation uint4");
-    __shared__ uint4 xs[DIRECT ? 1 : GPS * S * 8];
-    uint4 xa[GPS], xb[GPS], xv = make_uint4(0, 0, 0, 0);
-    if constexpr (DIRECT) {
-        const int g = g0 < G ? g0 : 0;
-        xa[0] = xq[(g * 4 + l) * 2];
-        xb[0] = xq[(g * 4 + l) * 2 + 1];
-    } else if (threadIdx.x < G * 8) {
-        xv = xq[threadIdx.x];
-    }
-    // A lane's chunk: 16 bytes (4-bit: 32 codes) or 8 (2-bit: 32 codes).
-    using Chunk = typename std::conditional<BITS == 4, uint4, uint2>::type;
-    Chunk c[GPS];
-    uint16_t nb[GPS];
-    float sxv[GPS];
-#pragma unroll
-    for (int j = 0; j < GPS; ++j) {
-        // Groups past G (when S * GPS > G) reload group 0; never used.
-        const int g = g0 + j < G ? g0 + j : 0;
-        if constexpr (BITS == 4) {
-            const uint4* p = reinterpret_cast<const uint4*>(codes) + ((size_t)(tile * G + g) * 64 + lane);
-            c[j] = NT ? load_stream(p) : *p;
-        } else
-            c[j] = reinterpret_cast<const uint2*>(codes)[(size_t)(tile * G + g) * 64 + lane];
-        nb[j] = norms[(size_t)n * G + g];
-        sxv[j] = sx[g];
-    }
-    if constexpr (!DIRECT) {
-        if (threadIdx.x < G * 8) xs[threadIdx.x] = xv;
-        __syncthreads();
-    }
-    float lf[GPS], sc[GPS];
-#pragma unroll
-    for (int j = 0; j < GPS; ++j) {
-        uint4 x0, x1;
-        if constexpr (DIRECT) {
-            x0 = xa[j];
-            x1 = xb[j];
-        } else {
-            const int g = g0 + j < G ? g0 + j : 0;
-            const uint4* xp = xs + (g * 4 + l) * 2;
-            x0 = xp[0];
-            x1 = xp[1];
-        }
-        int isum;
-        if constexpr (BITS == 4)
-            isum = dot_chunk(c[j], x0, x1, lut);
-        else
-            isum = dot_chunk2(c[j], x0, x1, lut.a_lo);
-        if (DBG && n < out && g0 + j < G) dbg[((size_t)n * G + g0 + j) * 4 + l] = isum;
-        lf[j] = (float)isum;
-        sc[j] = (sxv[j] * cbs) * f16_bits_to_f32(nb[j]);
-    }
-
-    float acc = 0.0f;
-    if constexpr (S == 1) {
-#pragma unroll
-        for (int j = 0; j < GPS; ++j)
-            if (j < G) acc = __builtin_fmaf(lf[j], sc[j], acc);
-    } else {
-        __shared__ float2 part[GPS * S][64];
-#pragma unroll
-        for (int j = 0; j < GPS; ++j) part[g0 + j][lane] = make_float2(lf[j], sc[j]);
-        __syncthreads();
-        if (wave != 0) return;
-        for (int g = 0; g < G; ++g) {
-            const float2 p = part[g][lane];
-            acc = __builtin_fmaf(p.x, p.y, acc);
-        }
-    }
-    // (l0 + l1) + (l2 + l3) across the row's four lanes.
-    const float t = acc + quad_xor1(acc);
-    const float u = t + quad_xor2(t);
-    if (y && l == 0 && n < out) y[n] = u;
-}
 
 template <int GPS, int S, int BITS, bool DBG, bool NT>
 __global__ __launch_bounds__(S * 64) void k_gemv(const void* __restrict__ codes, const uint16_t* __restrict__ norms,
@@ -210,70 +110,47 @@ __global__ __launch_bounds__(S * 64) void k_gemv_stream(const uint4* __restrict_
     }
 }
 
+// A 4-bit matrix tall enough for the persistent streaming grid.
+static bool gemv_tall(const nh_qmat* w) {
+    return w->m.bits == 4 && w->m.out_pad / TILE_ROWS >= 8 * device_cus() * STREAM_WG_PER_CU;
+}
+
+// Streamed matrices (codes read with the non-temporal hint) and the debug
+// partials; a resident matrix's product is launched by nh_gemv_res.hip.
 template <int GPS, int S, int BITS>
 static hipError_t run(const nh_qmat* w, const nh_qact* a, float* y, int32_t* dbg, hipStream_t s) {
     const QMatMeta& m = w->m;
     const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
     dim3 grid(m.out_pad / TILE_ROWS), block(S * 64);
-    const int tiles = m.out_pad / TILE_ROWS, slots = device_cus() * STREAM_WG_PER_CU;
-    if (BITS == 4 && !dbg && tiles >= 8 * slots) {
+    if (BITS == 4 && !dbg && gemv_tall(w)) {
+        const int tiles = m.out_pad / TILE_ROWS, slots = device_cus() * STREAM_WG_PER_CU;
         hipLaunchKernelGGL((k_gemv_stream<GPS, S>), dim3(slots), block, 0, s, (const uint4*)w->d_codes, w->d_norms,
                            (const uint4*)a->d_xq, a->d_sx, y, m.out, m.groups, m.cbs, lut, tiles);
         return hipGetLastError();
     }
-    auto kern = dbg ? k_gemv<GPS, S, BITS, true, true>
-                    : w->resident ? k_gemv<GPS, S, BITS, false, false> : k_gemv<GPS, S, BITS, false, true>;
+    auto kern = dbg ? k_gemv<GPS, S, BITS, true, true> : k_gemv<GPS, S, BITS, false, true>;
     hipLaunchKernelGGL(kern, grid, block, 0, s, w->d_codes, w->d_norms, (const uint4*)a->d_xq, a->d_sx, y, dbg, m.out,
                        m.groups, m.cbs, lut);
     return hipGetLastError();
 }
 
-// Groups per wavefront (GPS) and wavefronts per tile (S) by group count:
-// two to four groups per lane keeps 2-4 KiB of loads in flight per
-// wavefront while giving the big shapes several wavefronts per CU (at
-// K = 2048, 8 wavefronts x 2 groups measured 2.4 % faster than 4 x 4; at
-// K = 768, 6 x 1 5 % faster than 2 x 3).  Any G
-// up to 32 maps to the smallest listed G' >= G (wavefronts skip the
-// groups past G).
 template <int BITS>
 static hipError_t dispatch(const nh_qmat* w, const nh_qact* a, float* y, int32_t* dbg, hipStream_t s) {
-    const int G = w->m.groups;
-    if (G <= 1) return run<1, 1, BITS>(w, a, y, dbg, s);
-    if (G <= 2) return run<2, 1, BITS>(w, a, y, dbg, s);
-    if (G <= 3) return run<3, 1, BITS>(w, a, y, dbg, s);
-    if (G <= 4) return run<2, 2, BITS>(w, a, y, dbg, s);
-    if (G <= 6) return run<1, 6, BITS>(w, a, y, dbg, s);
-    if (G <= 8) return run<2, 4, BITS>(w, a, y, dbg, s);
-    if (G <= 12) return run<3, 4, BITS>(w, a, y, dbg, s);
-    if (G <= 16) return run<2, 8, BITS>(w, a, y, dbg, s);
-    if (G <= 24) return run<4, 6, BITS>(w, a, y, dbg, s);
-    if (G <= 32) return run<4, 8, BITS>(w, a, y, dbg, s);
-    return hipErrorInvalidValue;
-}
-
-template <int GPS, int S, int BITS>
-static hipError_t run_batch(const nh_qmat* w, const GemvBatch& b, int n, hipStream_t s) {
-    const QMatMeta& m = w->m;
-    const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
-    auto kern = w->resident ? k_gemv_batch<GPS, S, BITS, false> : k_gemv_batch<GPS, S, BITS, true>;
-    hipLaunchKernelGGL(kern, dim3(m.out_pad / TILE_ROWS, n), dim3(S * 64), 0, s, b, m.out, m.groups, m.cbs, lut);
-    return hipGetLastError();
+    return gemv_shape(w->m.groups, [&](auto sh) {
+        return run<decltype(sh)::GPS, decltype(sh)::S, BITS>(w, a, y, dbg, s);
+    });
 }
 
 template <int BITS>
 static hipError_t dispatch_batch(const nh_qmat* w, const GemvBatch& b, int n, hipStream_t s) {
-    const int G = w->m.groups;
-    if (G <= 1) return run_batch<1, 1, BITS>(w, b, n, s);
-    if (G <= 2) return run_batch<2, 1, BITS>(w, b, n, s);
-    if (G <= 3) return run_batch<3, 1, BITS>(w, b, n, s);
-    if (G <= 4) return run_batch<2, 2, BITS>(w, b, n, s);
-    if (G <= 6) return run_batch<3, 2, BITS>(w, b, n, s);
-    if (G <= 8) return run_batch<2, 4, BITS>(w, b, n, s);
-    if (G <= 12) return run_batch<3, 4, BITS>(w, b, n, s);
-    if (G <= 16) return run_batch<4, 4, BITS>(w, b, n, s);
-    if (G <= 24) return run_batch<4, 6, BITS>(w, b, n, s);
-    if (G <= 32) return run_batch<4, 8, BITS>(w, b, n, s);
-    return hipErrorInvalidValue;
+    const QMatMeta& m = w->m;
+    const Lut lut{m.lut.a_hi, m.lut.a_lo, m.lut.b_hi, m.lut.b_lo};
+    return gemv_batch_shape(m.groups, [&](auto sh) {
+        constexpr int GPS = decltype(sh)::GPS, S = decltype(sh)::S;
+        hipLaunchKernelGGL((k_gemv_batch<GPS, S, BITS, true>), dim3(m.out_pad / TILE_ROWS, n), dim3(S * 64), 0, s, b,
+                           m.out, m.groups, m.cbs, lut);
+        return hipGetLastError();
+    });
 }
 
 bool gemv_batchable(const nh_qmat* const* w, int n) {
@@ -294,6 +171,7 @@ hipError_t launch_gemv_batch(const nh_qmat* const* w, const nh_qact* const* a, f
         b.sx[i] = a[i]->d_sx;
         b.y[i] = y[i];
     }
+    if (w[0]->resident) return launch_gemv_batch_resident(w[0], b, n, s);
     return w[0]->m.bits == 2 ? dispatch_batch<2>(w[0], b, n, s) : dispatch_batch<4>(w[0], b, n, s);
 }
 
@@ -394,6 +272,7 @@ hipError_t launch_read_floor(const nh_qmat* w, const nh_qact* a, int mode, float
 
 hipError_t launch_gemv(const nh_qmat* w, const nh_qact* a, float* y, int col0, int32_t* dbg, hipStream_t s) {
     float* yc = y ? y + col0 : nullptr;
+    if (w->resident && !dbg && !gemv_tall(w)) return launch_gemv_resident(w, a, yc, s);
     return w->m.bits == 2 ? dispatch<2>(w, a, yc, dbg, s) : dispatch<4>(w, a, yc, dbg, s);
 }
 
