@@ -2185,11 +2185,13 @@ constexpr int DG_KPITCH = MAX_HEAD_DIM + 16;     // key row (80 bytes: 8 rows co
 constexpr int DG_VDW = (ATT_CHUNK_MAX + 3 + 3) / 4;  // value dwords per column (alignment offset + slots)
 
 template <int HP, int TAPS, bool EXACT>
-__global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, LayerDev L, int layer, int p0,
-                                                          int out_bits) {
+__global__ __launch_bounds__(DG_THREADS) void k_dec_group(const int8_t* k8l, const float* ksl, const float* vsl,
+                                                          int8_t* v8l, int p0, int lo, int geom, int vcap, Dims D,
+                                                          SessDev S, LayerDev L, int layer, int out_bits) {
     constexpr int NT = HP * DG_HEAD_T;  // the attention's threads (the rest only stage keys)
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const int nh = D.nh, nkv = D.nkv, qk = D.qk, vd = D.vd, group = nh / nkv;
+    const int nh = geom & 255, nkv = (geom >> 8) & 255, qk = (geom >> 16) & 255, vd = (int)((unsigned)geom >> 24),
+              group = nh / nkv;
     const int qd = nh * qk, kd = nkv * qk, vdim = nkv * vd;
     if ((int)blockIdx.x * HP >= nh) {
         if (wave == 0) post_gates(S.p, L, lane);
@@ -2197,7 +2199,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
     }
     const int hh0 = blockIdx.x * HP, kvh = hh0 / group;
     const bool owner = hh0 % group == 0;
-    const int lo = window_lo(L.window, p0), n = p0 + 1 - lo, blocked = n / 4 * 4;
+    const int n = p0 + 1 - lo, blocked = n / 4 * 4;
     // value columns and digits are kept from slot lo - sh (a dword
     // boundary of the cache row): column index j = i + sh for key i
     const int sh = lo & 3, base = lo - sh;
@@ -2213,7 +2215,6 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
     __shared__ float s_qs[HP], s_sum[HP];
     __shared__ float att[HP * MAX_HEAD_DIM];
     __shared__ float gden[HP * MAX_HEAD_DIM];  // exp(-gate) + 1 of output hh0 * vd + j
-    const size_t lc = (size_t)layer * D.cap;
     // Waves 0 .. HP-1 load the query units' inputs, the next two those of
     // the new key and value, and the rest (the staging waves) the keys
     // before the position: int8 rows (16-byte chunks), scales and value
@@ -2246,19 +2247,19 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
 #pragma unroll
         for (int r = 0; r < KR; ++r) {
             const int e = ts + r * NS, i = min(e >> 2, n - 1), c = min(e & 3, rq - 1);
-            kr[r] = reinterpret_cast<const u32x4*>(S.k8 + ((lc + lo + i) * nkv + kvh) * qk)[c];
+            kr[r] = reinterpret_cast<const u32x4*>(k8l + ((size_t)(lo + i) * nkv + kvh) * qk)[c];
         }
 #pragma unroll
         for (int r = 0; r < SR; ++r) {
             const int i = min(ts + r * NS, n - 1);
-            ksr[r] = S.ks[(lc + lo + i) * nkv + kvh];
-            vsr[r] = S.vs[(lc + lo + i) * nkv + kvh];
+            ksr[r] = ksl[(size_t)(lo + i) * nkv + kvh];
+            vsr[r] = vsl[(size_t)(lo + i) * nkv + kvh];
         }
-        const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base;
+        const int8_t* vcol = v8l + (size_t)kvh * vd * vcap + base;
 #pragma unroll
         for (int r = 0; r < VR; ++r) {
             const int e = ts + r * NS, dm = min(e / DG_VDW, vd - 1), k = min(e % DG_VDW, max(vdw - 1, 0));
-            vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * D.vcap)[k];
+            vw[r] = reinterpret_cast<const uint32_t*>(vcol + (size_t)dm * vcap)[k];
         }
     }
     // the head gates of the group's HP * vd = GROUP outputs, one per thread
@@ -2277,11 +2278,11 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
         const int8_t q = quant_one(v, 1.0f / s);
         if (lane < qk) {
             ks8[n - 1][lane] = q;
-            if (owner) S.k8[((lc + p0) * nkv + kvh) * qk + lane] = q;
+            if (owner) S.k8[(((size_t)layer * D.cap + p0) * nkv + kvh) * qk + lane] = q;
         }
         if (lane == 0) {
             kss[n - 1] = s;
-            if (owner) S.ks[(lc + p0) * nkv + kvh] = s;
+            if (owner) S.ks[((size_t)layer * D.cap + p0) * nkv + kvh] = s;
         }
     } else if (wave == HP + 1) {
         const float v = unit_finish<TAPS, EXACT>(D, S, layer, p0, qd + kd + kvh * vd, vd, ui, false, lane, owner);
@@ -2289,11 +2290,11 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_group(Dims D, SessDev S, Lay
         const int8_t q = quant_one(v, 1.0f / s);
         if (lane < vd) {
             vs8[lane][sh + n - 1] = q;
-            if (owner) S.v8t[(((size_t)layer * nkv + kvh) * vd + lane) * D.vcap + p0] = q;
+            if (owner) v8l[((size_t)kvh * vd + lane) * vcap + p0] = q;
         }
         if (lane == 0) {
             vss[n - 1] = s;
-            if (owner) S.vs[(lc + p0) * nkv + kvh] = s;
+            if (owner) S.vs[((size_t)layer * D.cap + p0) * nkv + kvh] = s;
         }
     } else {
 #pragma unroll
@@ -2490,16 +2491,26 @@ bool dec_group_fits(const Dims& D, int p0, int window) {
     if (c > 1 || n > ATT_CHUNK_MAX || D.ring > 0) return false;
     if (GROUP % D.vd != 0 || D.taps > DG_MAX_TAPS) return false;
     const int hp = GROUP / D.vd;
-    return (hp == 2 || hp == 4) && D.nh % hp == 0 && (D.nh / D.nkv) % hp == 0 && D.qk % 16 == 0;
+    return (hp == 2 || hp == 4) && D.nh % hp == 0 && (D.nh / D.nkv) % hp == 0 && D.qk % 16 == 0 && D.nh < 256 &&
+           D.nkv < 256 && D.qk < 256 && D.vd < 256;
 }
 
 hipError_t fwd_dec_attn(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
                         hipStream_t s) {
     const int hp = GROUP / D.vd, blocks = D.nh / hp + 1;
+    // The staging loads' operands lead the arguments (scalars, preloaded
+    // into SGPRs at wave launch): the layer's key rows, scales and value
+    // columns, the window start and the geometry (nh, nkv, qk, vd < 256).
+    const size_t lc = (size_t)layer * D.cap;
+    const int8_t* k8l = S.k8 + lc * D.nkv * D.qk;
+    const float* ksl = S.ks + lc * D.nkv;
+    const float* vsl = S.vs + lc * D.nkv;
+    int8_t* v8l = S.v8t + (size_t)layer * D.nkv * D.vd * D.vcap;
+    const int lo = window_lo(L.window, p0), geom = D.nh | D.nkv << 8 | D.qk << 16 | D.vd << 24;
     // exact tap counts 1..4, clamped loads up to DG_MAX_TAPS otherwise
 #define NH_DG(HP, TP, EX)                                                                                        \
-    hipLaunchKernelGGL((k_dec_group<HP, TP, EX>), dim3(blocks), dim3(DG_THREADS), 0, s, D, S, L, layer, p0,     \
-                       out_bits)
+    hipLaunchKernelGGL((k_dec_group<HP, TP, EX>), dim3(blocks), dim3(DG_THREADS), 0, s, k8l, ksl, vsl, v8l, p0, \
+                       lo, geom, D.vcap, D, S, L, layer, out_bits)
 #define NH_DG_TAPS(HP)                          \
     switch (D.taps) {                           \
         case 1: NH_DG(HP, 1, true); break;      \
