@@ -44,8 +44,8 @@ FLAGS = [
 # are preloaded into SGPRs at wave launch (the Needle-3 decode token 537.5 ->
 # 526 us).  So are the resident matrices' GEMVs, the decode step's products
 # (520.7 -> 510.8 us).  The streamed GEMV measured slower with it (the
-# 512-workgroup K = 2048 product 3.63 -> 3.68 us), so it and the GEMMs keep
-# the plain argument loads.
+# 512-workgroup K = 2048 product 3.63 -> 3.68 us) and the GEMMs the same, so
+# they keep the plain argument loads.
 PRELOAD = ["-mllvm", "-amdgpu-kernarg-preload-count=16"]
 FILE_FLAGS = {"nh_forward.hip": PRELOAD, "nh_gemv_res.hip": PRELOAD}
 
