@@ -608,24 +608,28 @@ struct OutRegs {
     uint4 cu;  // cond_u [k][t], k < 8, as f16 pairs
 };
 
-__device__ __forceinline__ OutRegs load_out(const Dims& D, const Globals& G, const SessDev& S, const LayerDev& P,
-                                            LayerShared& sh) {
-    const int t = threadIdx.x, d = D.d;
+__device__ __forceinline__ OutRegs load_out(int d, const uint4* stage, const uint16_t* pn, const Globals& G,
+                                            const SessDev& S, const LayerDev& P) {
+    const int t = threadIdx.x;
     OutRegs q{};
     const int kron_n = 6 * HADA_N / 8, cv_n = d * COND_RANK / 8;
     static_assert(STAGE_PER * LT >= 6 * HADA_N / 8 + FWD_MAX_D * COND_RANK / 8, "the stage loads cover the tables");
 #pragma unroll
     for (int r = 0; r < STAGE_PER; ++r) {
         const int e = min(t + r * LT, kron_n + cv_n - 1);
-        q.st[r] = reinterpret_cast<const uint4*>(P.stage)[e];
+        q.st[r] = stage[e];
     }
-    q.cu = reinterpret_cast<const uint4*>(P.stage)[kron_n + cv_n + t];
+    q.cu = stage[kron_n + cv_n + t];
     // (unconditional loads: threads past d read element d - 1 and ignore it)
     const int td = min(t, d - 1);
     q.o = S.o[td];
+    q.pv = S.p[t & 63];
     q.x1 = S.x1[td];
     q.u = S.u[td];
-    q.pn = P.post_norm[td];
+    // (the loads above take preloaded operands only: none waits for the
+    // argument segment, which those below need)
+    __builtin_amdgcn_sched_barrier(0);
+    q.pn = pn[td];
     q.ph = P.pre_hada[td];
     q.d1 = P.d1[td];
     q.d4 = P.d4[td];
@@ -634,7 +638,6 @@ __device__ __forceinline__ OutRegs load_out(const Dims& D, const Globals& G, con
     q.d3 = P.d3[t];
     q.p1 = G.perm1[t];
     q.p2 = G.perm2[t];
-    q.pv = S.p[t & 63];
     return q;
 }
 
@@ -645,9 +648,9 @@ __device__ __forceinline__ float h2f_late(uint32_t b) {
     return h2f((uint16_t)b);
 }
 
-__device__ __forceinline__ void store_out(const Dims& D, const OutRegs& q, LayerShared& sh) {
+__device__ __forceinline__ void store_out(int d, const OutRegs& q, LayerShared& sh) {
     const int t = threadIdx.x;
-    const int kron_n = 6 * HADA_N / 8, cv_n = D.d * COND_RANK / 8;
+    const int kron_n = 6 * HADA_N / 8, cv_n = d * COND_RANK / 8;
 #pragma unroll
     for (int r = 0; r < STAGE_PER; ++r) {
         const int e = t + r * LT;
@@ -671,7 +674,7 @@ __device__ __forceinline__ void store_out(const Dims& D, const OutRegs& q, Layer
             }
         }
     }
-    if (t < D.d) put_t(sh.tA, TP_D, t, q.o);
+    if (t < d) put_t(sh.tA, TP_D, t, q.o);
     if (t < 64) sh.p[t] = q.pv;
 }
 
@@ -1099,21 +1102,26 @@ __device__ void head_in(const Dims& D, const SessDev& S, float fnorm, int head_b
 // BATCH (a feed of several rows): two rows per CU (at most 64 VGPRs), so
 // the next layer's Phi8 rows are read at the start of the mHC read instead
 // of beside the MLP.
+//
+// The operands of everything the first barrier waits for lead the arguments
+// as scalars (the previous layer's staged tables and post norm, the row
+// buffers, d and row0), so they are preloaded into SGPRs at wave launch.
 template <bool PREV, bool NEXT, bool BATCH, int PC>
-__global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 1))) void k_layer(Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int row0,
-                                              int in_bits, int head_bits, int head_row0) {
+__global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 1))) void k_layer(
+    const uint4* stage, const float* o, const float* p, float* xs, const float* x1, const float* u, int d, int row0,
+    Dims D, Globals G, SessDev S, LayerDev P, LayerDev N, int in_bits, int head_bits, int head_row0) {
     constexpr bool has_prev = PREV, has_next = NEXT;
     __shared__ LayerShared sh;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, d = D.d, nc = MHC_LANES * d;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, nc = MHC_LANES * d;
     const int Gd = (d + GROUP - 1) / GROUP;
     // this block's row of every row buffer
     const int row = row0 + blockIdx.x;
     SessDev R = S;
-    R.xs += (size_t)row * nc;
-    R.u += (size_t)row * d;
-    R.x1 += (size_t)row * d;
-    R.p += (size_t)row * 64;
-    R.o += (size_t)row * d;
+    R.xs = xs + (size_t)row * nc;
+    R.u = const_cast<float*>(u) + (size_t)row * d;
+    R.x1 = const_cast<float*>(x1) + (size_t)row * d;
+    R.p = const_cast<float*>(p) + (size_t)row * 64;
+    R.o = const_cast<float*>(o) + (size_t)row * d;
     R.ekv += (size_t)row * 2 * d;
     R.evals += (size_t)row * d;
     R.xq_in += (size_t)row * Gd * GROUP;
@@ -1125,7 +1133,7 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
 #pragma unroll
     for (int k = 0; k < MHC_LANES; ++k) xl[k] = R.xs[k * d + td];
     OutRegs qo;
-    if constexpr (has_prev) qo = load_out(D, G, R, P, sh);
+    if constexpr (has_prev) qo = load_out(d, stage, P.post_norm, G, R, P);
     InRegs<PC> qi;
     float fnorm = 0.0f;
     // Without a previous layer nothing else loads: the next layer's reads
@@ -1147,7 +1155,7 @@ __global__ __launch_bounds__(LT) __attribute__((amdgpu_waves_per_eu(BATCH ? 8 : 
             }
         }
     }
-    if constexpr (has_prev) store_out(D, qo, sh);
+    if constexpr (has_prev) store_out(d, qo, sh);
     __syncthreads();
     if constexpr (has_next && has_prev) qi = load_in<false, PC, !BATCH>(D, R, N);
     // The Phi8 rows (72 KB at d = 768, ~16 cycles of the CU's address unit
@@ -1194,18 +1202,19 @@ static void launch_layer(const Dims& D, const Globals& G, const SessDev& S, cons
                          const LayerDev* next, int row0, int rows, int in_bits, int head_bits, int head_row0,
                          hipStream_t s) {
     const LayerDev none{};
+    const uint4* stage = prev ? reinterpret_cast<const uint4*>(prev->stage) : nullptr;
+#define NH_LAYER(HP, HN, PV, NX)                                                                                  \
+    hipLaunchKernelGGL((k_layer<HP, HN, BATCH, PC>), dim3(rows), dim3(LT), 0, s, stage, S.o, S.p, S.xs, S.x1,     \
+                       S.u, D.d, row0, D, G, S, PV, NX, in_bits, head_bits, head_row0)
     if (prev && next)
-        hipLaunchKernelGGL((k_layer<true, true, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, *next, row0,
-                           in_bits, head_bits, head_row0);
+        NH_LAYER(true, true, *prev, *next);
     else if (next)
-        hipLaunchKernelGGL((k_layer<false, true, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, none, *next, row0,
-                           in_bits, head_bits, head_row0);
+        NH_LAYER(false, true, none, *next);
     else if (prev)
-        hipLaunchKernelGGL((k_layer<true, false, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, *prev, none, row0,
-                           in_bits, head_bits, head_row0);
+        NH_LAYER(true, false, *prev, none);
     else
-        hipLaunchKernelGGL((k_layer<false, false, BATCH, PC>), dim3(rows), dim3(LT), 0, s, D, G, S, none, none, row0,
-                           in_bits, head_bits, head_row0);
+        NH_LAYER(false, false, none, none);
+#undef NH_LAYER
 }
 
 hipError_t fwd_layer(const Dims& D, const Globals& G, const SessDev& S, const LayerDev* prev, const LayerDev* next,
