@@ -1798,7 +1798,15 @@ constexpr int AG_TP = ATT_CHUNK_MAX / 8 + 4;  // a lane class's exps (16-byte ro
 // leaves the last workgroup's second row empty.
 template <int RP>
 __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP == 2 ? 8 : 1))) void k_attend_group(
-    Dims D, SessDev S, LayerDev L, int layer, int p0, int rows) {
+    const float* qbuf, const int8_t* k8l, const float* ksl, const float* vsl, const int8_t* v8l, int p0, int rows,
+    int wv, int geom, Dims D, SessDev S, LayerDev L, int layer) {
+    // (the staging's operands lead the arguments as scalars, preloaded at
+    // wave launch: the queries, the layer's key rows, scales and value
+    // columns, the window | value stride << 16 and the geometry
+    // nh | nkv | qk | vd; nothing before the first barrier reads the
+    // argument segment, so the barrier's LDS wait holds no scalar load)
+    const int g_nh = geom & 255, g_nkv = (geom >> 8) & 255, g_qk = (geom >> 16) & 255,
+              g_vd = (int)((unsigned)geom >> 24), window = wv & 0xffff, vcap = (int)((unsigned)wv >> 16);
     constexpr int NTT = AG_T * RP;
     // (the row half and the wavefront are wave-uniform: in scalar registers,
     // so the lengths and bounds derived from them are too)
@@ -1811,20 +1819,23 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
     // share lo and the chunking).
     __shared__ int prm[6];
     if (tb < 64) {
-        const int pr = (int)blockIdx.x / D.nkv, rA = rows - 1 - RP * pr, pA = p0 + rA;
-        const int l0 = window_lo(L.window, pA);
+        const int pr = (int)blockIdx.x / g_nkv, rA = rows - 1 - RP * pr, pA = p0 + rA;
+        const int l0 = window_lo(window, pA);
         int cnt, chk;
-        key_chunks(pA + 1 - l0, D.nkv, rows > 1, cnt, chk);
+        key_chunks(pA + 1 - l0, g_nkv, rows > 1, cnt, chk);
         if (tb == 0) {
             prm[0] = rA;
-            prm[1] = (int)blockIdx.x - pr * D.nkv;
+            prm[1] = (int)blockIdx.x - pr * g_nkv;
             prm[2] = l0;
             prm[3] = cnt;
             prm[4] = chk;
-            prm[5] = D.nh / D.nkv;
+            prm[5] = g_nh / g_nkv;
         }
     }
+    // (no argument-segment read is hoisted above here)
+    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
     const int rowA = __builtin_amdgcn_readfirstlane(prm[0]), kvh = __builtin_amdgcn_readfirstlane(prm[1]);
     const int lo = __builtin_amdgcn_readfirstlane(prm[2]), count = __builtin_amdgcn_readfirstlane(prm[3]);
     const int chunk = __builtin_amdgcn_readfirstlane(prm[4]), hpg = __builtin_amdgcn_readfirstlane(prm[5]);
@@ -1834,7 +1845,7 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
     const bool live = RP == 1 || row >= 0;  // (wave-uniform)
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63, posA = p0 + rowA,
               pos = p0 + (live ? row : 0);
-    const int nkv = D.nkv, qk = D.qk, vd = D.vd;
+    const int nkv = g_nkv, qk = g_qk, vd = g_vd;
     const int nA = posA + 1 - lo, n = pos + 1 - lo;
     const int c0 = ci * chunk, lenA = min(chunk, nA - c0), slot0 = lo + c0;
     const int len = live ? min(chunk, n - c0) : 0, blocked = len / 4 * 4;
@@ -1862,21 +1873,19 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
     auto& pv = lds.pv[rr];
     auto& q8 = q8s[rr];
     auto& qsc = qscs[rr];
-    const size_t lc = (size_t)layer * D.cap;
     const int hw = min(wave, hpg - 1), hh = kvh * hpg + hw;
     // every load first (unconditional, at clamped in-range addresses)
-    const float qv = S.qbuf[((size_t)(live ? row : 0) * D.nh + hh) * qk + min(lane, qk - 1)];
+    const float qv = qbuf[((size_t)(live ? row : 0) * g_nh + hh) * qk + min(lane, qk - 1)];
     constexpr int VQ = AG_COLS / 16;  // 16-byte value chunks per column
     constexpr int KR = ATT_CHUNK_MAX * 4 / NTT, VR = (MAX_HEAD_DIM * VQ + NTT - 1) / NTT;
     const int rq = qk / 16, vq = (colsA + 15) / 16;
     // buffer resources over the chunk's key rows (this kv head's, from
     // slot0), their scales and the value columns (from base)
     const int kstride = nkv * qk;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(S.k8 + (lc + slot0) * kstride + kvh * qk, (size_t)lenA * kstride);
-    const __amdgpu_buffer_rsrc_t rks = make_rsrc(S.ks + (lc + slot0) * nkv + kvh, (size_t)lenA * nkv * 4);
-    const __amdgpu_buffer_rsrc_t rvs = make_rsrc(S.vs + (lc + slot0) * nkv + kvh, (size_t)lenA * nkv * 4);
-    const __amdgpu_buffer_rsrc_t rv =
-        make_rsrc(S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap + base, (size_t)vd * D.vcap);
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(k8l + (size_t)slot0 * kstride + kvh * qk, (size_t)lenA * kstride);
+    const __amdgpu_buffer_rsrc_t rks = make_rsrc(ksl + (size_t)slot0 * nkv + kvh, (size_t)lenA * nkv * 4);
+    const __amdgpu_buffer_rsrc_t rvs = make_rsrc(vsl + (size_t)slot0 * nkv + kvh, (size_t)lenA * nkv * 4);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(v8l + (size_t)kvh * vd * vcap + base, (size_t)vd * vcap);
     u32x4 kr[KR], vw[VR];
 #pragma unroll
     for (int r = 0; r < KR; ++r) {
@@ -1892,7 +1901,7 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
 #pragma unroll
     for (int r = 0; r < VR; ++r) {
         const int e = tb + r * NTT, dm = min(e / VQ, vd - 1), k = min(e % VQ, vq - 1);
-        vw[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, __mul24(dm, D.vcap) + k * 16, 0, 0));
+        vw[r] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, __mul24(dm, vcap) + k * 16, 0, 0));
     }
     // the int8 query of this wavefront's head, zero past qk (the key rows'
     // bytes there are not staged)
@@ -2083,7 +2092,8 @@ hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int la
     if (span)
         hipLaunchKernelGGL(k_attend<true>, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer, p0,
                            t, *span);
-    else if (D.nh / D.nkv <= AG_WAVES) {
+    else if (D.nh / D.nkv <= AG_WAVES && D.nh < 256 && D.nkv < 256 && D.qk < 256 && D.vd < 256 &&
+             L.window >= 0 && L.window < 65536 && D.vcap < 65536) {
         // the most chunks a row of the feed needs
         int most = 1;
         for (int i = 0; i < t; ++i) {
@@ -2103,11 +2113,18 @@ hipError_t fwd_attend(const Dims& D, const SessDev& S, const LayerDev& L, int la
             key_chunks(pb + 1 - lb, D.nkv, true, cb, sb);
             pairs = la == lb && ca == cb && (ca == 1 || sa == sb);
         }
+        const size_t lc = (size_t)layer * D.cap;
+        const int8_t* k8l = S.k8 + lc * D.nkv * D.qk;
+        const float* ksl = S.ks + lc * D.nkv;
+        const float* vsl = S.vs + lc * D.nkv;
+        const int8_t* v8l = S.v8t + (size_t)layer * D.nkv * D.vd * D.vcap;
+        const int geom = D.nh | D.nkv << 8 | D.qk << 16 | D.vd << 24, wv = L.window | D.vcap << 16;
         if (pairs)
-            hipLaunchKernelGGL(k_attend_group<2>, dim3((t + 1) / 2 * D.nkv, most), dim3(2 * AG_T), 0, s, D, S, L,
-                               layer, p0, t);
+            hipLaunchKernelGGL(k_attend_group<2>, dim3((t + 1) / 2 * D.nkv, most), dim3(2 * AG_T), 0, s, S.qbuf, k8l,
+                               ksl, vsl, v8l, p0, t, wv, geom, D, S, L, layer);
         else
-            hipLaunchKernelGGL(k_attend_group<1>, dim3(t * D.nkv, most), dim3(AG_T), 0, s, D, S, L, layer, p0, t);
+            hipLaunchKernelGGL(k_attend_group<1>, dim3(t * D.nkv, most), dim3(AG_T), 0, s, S.qbuf, k8l, ksl, vsl,
+                               v8l, p0, t, wv, geom, D, S, L, layer);
     }
     else
         hipLaunchKernelGGL(k_attend<false>, dim3(t * D.nh, D.max_chunks), dim3(ATT_THREADS), 0, s, D, S, L, layer,
