@@ -1803,8 +1803,8 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
     // (the staging's operands lead the arguments as scalars, preloaded at
     // wave launch: the queries, the layer's key rows, scales and value
     // columns, the window | value stride << 16 and the geometry
-    // nh | nkv | qk | vd; nothing before the first barrier reads the
-    // argument segment, so the barrier's LDS wait holds no scalar load)
+    // nh | nkv | qk | vd; the parameters and the loads need no read of the
+    // argument segment)
     const int g_nh = geom & 255, g_nkv = (geom >> 8) & 255, g_qk = (geom >> 16) & 255,
               g_vd = (int)((unsigned)geom >> 24), window = wv & 0xffff, vcap = (int)((unsigned)wv >> 16);
     constexpr int NTT = AG_T * RP;
@@ -1832,10 +1832,7 @@ __global__ __launch_bounds__(AG_T * RP) __attribute__((amdgpu_waves_per_eu(RP ==
             prm[5] = g_nh / g_nkv;
         }
     }
-    // (no argument-segment read is hoisted above here)
-    __builtin_amdgcn_sched_barrier(0);
     __syncthreads();
-    __builtin_amdgcn_sched_barrier(0);
     const int rowA = __builtin_amdgcn_readfirstlane(prm[0]), kvh = __builtin_amdgcn_readfirstlane(prm[1]);
     const int lo = __builtin_amdgcn_readfirstlane(prm[2]), count = __builtin_amdgcn_readfirstlane(prm[3]);
     const int chunk = __builtin_amdgcn_readfirstlane(prm[4]), hpg = __builtin_amdgcn_readfirstlane(prm[5]);
