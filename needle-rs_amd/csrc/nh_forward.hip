@@ -25,6 +25,8 @@
 // f64 exp rounded once (lexpf, crates/needle-engine/src/infer.rs:84-101);
 // here too, with the device library's f64 exp: two f64 exps accurate to an
 // ulp give the same f32 unless an f32 rounding boundary falls between them.
+#include <algorithm>
+
 #include "nh_device.h"
 #include "nh_forward.h"
 #include "nh_internal.h"
@@ -2563,17 +2565,52 @@ constexpr int MERGE_AHEAD = 8;
 // the same values), the last chunk's blocks also the kv head's new key and
 // value (the first of them appends them to the cache and the history
 // ring), and the staging waves load the chunk's cached keys, scales and
-// values (by position; with a span, through the chunk's KV slots, found
-// first).  Each chunk's attention gives the reference's part (max, sum,
+// values (by position; with a span, through the chunk's KV slots: from the
+// chunk's slot runs, or found first into LDS when the runs do not fit).  Each chunk's attention gives the reference's part (max, sum,
 // P.V, infer.rs:1918-1987); one chunk finishes in its block.  With several,
 // each block stores its heads' parts and counts itself in (agent-scope
 // release); the group's block that counts last merges the parts in chunk
 // order (infer.rs:1990-2006), divides by the head gate and runs the
 // group's A8, then clears the count.  No block waits for another.  One
 // more block computes the row's post gates.
-template <int HP, int TAPS, bool EXACT, bool SPAN>
+// Under a span, the KV slots of each key chunk as runs of consecutive keys
+// in consecutive slots (a span's live positions are a few position runs;
+// past the sink a run's slots only break where the ring wraps), worked out
+// on the host per launch: chunk c's run r holds its keys key0 ..
+// key0 + len - 1 (chunk-local) at slots slot0 .. slot0 + len - 1; unused
+// runs have key0 = RUN_NONE and len 0 (so the last run starting at or
+// before a key is the key's run).
+constexpr int DC_RUNS = 4;         // runs per chunk
+constexpr int DC_RUN_CHUNKS = 8;   // chunks
+constexpr int RUN_NONE = 1 << 30;
+constexpr int RUN_CHUNK = 128;     // the most keys a chunk has on the run path
+struct ChunkRuns {
+    int nrun[DC_RUN_CHUNKS];
+    int key0[DC_RUN_CHUNKS][DC_RUNS], slot0[DC_RUN_CHUNKS][DC_RUNS], len[DC_RUN_CHUNKS][DC_RUNS];
+};
+
+// One chunk's runs, read once into registers.
+struct Runs {
+    int k0[DC_RUNS], s0[DC_RUNS];
+};
+
+// The slot of chunk-local key j (j within the chunk's runs): the last run
+// starting at or before j (selects, no branches).
+__device__ __forceinline__ int run_slot(const Runs& q, int j) {
+    int slot = q.s0[0] + (j - q.k0[0]);
+#pragma unroll
+    for (int r = 1; r < DC_RUNS; ++r) slot = j >= q.k0[r] ? q.s0[r] + (j - q.k0[r]) : slot;
+    return slot;
+}
+
+// RUNS (with SPAN, chunks of at most RUN_CHUNK keys): the staging reads
+// keys, scales and value bytes at slots taken from the chunk's slot runs
+// (R) in registers, with no slot list in LDS and no barrier for it, and
+// gathers RUN_CHUNK value bytes per column instead of ATT_CHUNK_MAX.
+template <int HP, int TAPS, bool EXACT, bool SPAN, bool RUNS>
 __global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, LayerDev L, int layer, int p0,
-                                                           int out_bits, KeySpan K, int n, int nchunks, int chunk) {
+                                                           int out_bits, KeySpan K, int n, int nchunks, int chunk,
+                                                           ChunkRuns R) {
     constexpr int NT = HP * DG_HEAD_T;  // the attention's threads
     const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
     const int nh = D.nh, nkv = D.nkv, qk = D.qk, vd = D.vd, group = nh / nkv;
@@ -2599,7 +2636,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, La
     __shared__ alignas(16) int8_t ks8[ATT_CHUNK_MAX][DG_KPITCH];
     __shared__ alignas(16) int8_t vs8[MAX_HEAD_DIM][DG_PITCH];
     __shared__ float kss[ATT_CHUNK_MAX], vss[ATT_CHUNK_MAX];
-    __shared__ int kslot[SPAN ? ATT_CHUNK_MAX : 1];
+    __shared__ int kslot[SPAN && !RUNS ? ATT_CHUNK_MAX : 1];
     __shared__ alignas(16) int8_t q8[HP][MAX_HEAD_DIM];
     __shared__ float sc[HP][ATT_CHUNK_MAX];
     __shared__ alignas(16) int8_t dig[HP][3][DG_PITCH];
@@ -2612,8 +2649,21 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, La
     const int role = __builtin_amdgcn_readfirstlane(wave < HP ? 0 : min(wave - HP + 1, 3));  // 0 q, 1 k, 2 v, 3 keys
     constexpr int NS = DG_THREADS - (HP + 2) * 64;  // staging threads
     constexpr int KR = (ATT_CHUNK_MAX * 4 + NS - 1) / NS, SR = (ATT_CHUNK_MAX + NS - 1) / NS;
-    // values: dwords of the columns without a span, bytes gathered by slot with one
-    constexpr int VR = SPAN ? (MAX_HEAD_DIM * ATT_CHUNK_MAX + NS - 1) / NS : (MAX_HEAD_DIM * DG_VDW + NS - 1) / NS;
+    // values: dwords of the columns without a span, bytes gathered by slot
+    // with one (RUNS: chunks of at most RUN_CHUNK keys, so RUN_CHUNK
+    // elements per column)
+    constexpr int VR = RUNS ? (MAX_HEAD_DIM * RUN_CHUNK + NS - 1) / NS
+                     : SPAN ? (MAX_HEAD_DIM * ATT_CHUNK_MAX + NS - 1) / NS
+                            : (MAX_HEAD_DIM * DG_VDW + NS - 1) / NS;
+    // the chunk's runs, read once, unconditionally
+    Runs q{};
+    if constexpr (RUNS) {
+#pragma unroll
+        for (int r = 0; r < DC_RUNS; ++r) {
+            q.k0[r] = R.key0[ci][r];
+            q.s0[r] = R.slot0[ci][r];
+        }
+    }
     const int rq = qk / 16, vdw = (sh + nold + 3) / 4, ts = t - (HP + 2) * 64;
     const int8_t* vcol = S.v8t + ((size_t)layer * nkv + kvh) * vd * D.vcap;
     UnitIn ui;
@@ -2630,6 +2680,28 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, La
         if (last)
             ui = unit_load<TAPS, EXACT>(D, S, layer, p0, 0, qd + kd + kvh * vd, vdim, kvh * vd, vd, L.v_taps,
                                         L.k_norm, lane);
+    } else if constexpr (RUNS) {
+        // keys and scales at their runs' slots; values as the runs' dwords
+        // (clamped in-range: past nold, or past the runs' dwords, nothing is
+        // stored)
+        const int im = max(nold - 1, 0);
+#pragma unroll
+        for (int r = 0; r < KR; ++r) {
+            const int e = ts + r * NS, i = min(e >> 2, im), c = min(e & 3, rq - 1);
+            kr[r] = reinterpret_cast<const u32x4*>(S.k8 + ((lc + run_slot(q, i)) * nkv + kvh) * qk)[c];
+        }
+#pragma unroll
+        for (int r = 0; r < SR; ++r) {
+            const int sl = run_slot(q, min(ts + r * NS, im));
+            ksr[r] = S.ks[(lc + sl) * nkv + kvh];
+            vsr[r] = S.vs[(lc + sl) * nkv + kvh];
+        }
+        // element e: column dm = e / RUN_CHUNK, key i = e % RUN_CHUNK
+#pragma unroll
+        for (int r = 0; r < VR; ++r) {
+            const int e = ts + r * NS, dm = min(e / RUN_CHUNK, vd - 1), i = min(e % RUN_CHUNK, im);
+            vw[r] = (uint8_t)vcol[(size_t)dm * D.vcap + run_slot(q, i)];
+        }
     } else if constexpr (!SPAN) {
         // (clamped in-range addresses: past nold nothing is stored; with no
         // cached key the clamp reads the new position's own slot)
@@ -2658,7 +2730,7 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, La
             kslot[ts] = slot_of(D, span_key(K, alo, ahi, blo, bhi, c0 + ts));
         }
     }
-    if constexpr (SPAN) {
+    if constexpr (SPAN && !RUNS) {
         __syncthreads();  // the slots
         if (role == 3) {
             const int im = max(nold - 1, 0);
@@ -2732,7 +2804,13 @@ __global__ __launch_bounds__(DG_THREADS) void k_dec_chunks(Dims D, SessDev S, La
                 vss[i] = vsr[r];
             }
         }
-        if constexpr (SPAN) {
+        if constexpr (RUNS) {
+#pragma unroll
+            for (int r = 0; r < VR; ++r) {
+                const int e = ts + r * NS, dm = e / RUN_CHUNK, i = e % RUN_CHUNK;
+                if (dm < vd && i < nold) vs8[dm][i] = (int8_t)vw[r];
+            }
+        } else if constexpr (SPAN) {
 #pragma unroll
             for (int r = 0; r < VR; ++r) {
                 const int e = ts + r * NS, dm = e / ATT_CHUNK_MAX, i = e % ATT_CHUNK_MAX;
@@ -2966,6 +3044,50 @@ bool dec_chunks_fits(const Dims& D) {
            D.nh / hp <= DCOUNT_SLOTS;
 }
 
+// The slot runs of every key chunk of position p0 under span K (keys in
+// span_key's order: per live run, its part below the sink, then its part in
+// the ring's range; a ring part's slots break where the ring wraps); false
+// when a chunk needs more than DC_RUNS runs or there are more than
+// DC_RUN_CHUNKS chunks.
+static bool chunk_runs(const Dims& D, const KeySpan& K, int lo, int p0, int n, int count, int chunk, ChunkRuns& R) {
+    if (count > DC_RUN_CHUNKS || chunk > RUN_CHUNK || D.ring <= 0) return false;
+    int alo, ahi, blo, bhi;
+    span_ranges(D, K, lo, p0, alo, ahi, blo, bhi);
+    R = ChunkRuns{};
+    for (int c = 0; c < DC_RUN_CHUNKS; ++c)
+        for (int r = 0; r < DC_RUNS; ++r) R.key0[c][r] = RUN_NONE;
+    int k = 0;  // keys so far
+    auto add = [&](int pa, int pb) -> bool {
+        // positions pa .. pb - 1 (all below the sink or all in the ring's range)
+        while (pa < pb) {
+            int m = pb - pa, slot = pa;
+            if (pa >= D.sink) {
+                slot = (pa - D.sink) % D.ring + D.sink;
+                m = std::min(m, D.sink + D.ring - slot);  // to the ring's wrap
+            }
+            // the keys k .. k + m - 1 at slots slot .., cut into chunks
+            for (int j = 0; j < m;) {
+                const int c = (k + j) / chunk, cend = std::min(n, (c + 1) * chunk);
+                const int take = std::min(m - j, cend - (k + j));
+                if (c >= count || R.nrun[c] >= DC_RUNS) return false;
+                const int r = R.nrun[c]++;
+                R.key0[c][r] = k + j - c * chunk;
+                R.slot0[c][r] = slot + j;
+                R.len[c][r] = take;
+                j += take;
+            }
+            k += m;
+            pa += m;
+        }
+        return true;
+    };
+    for (int r = 0; r < K.nrun; ++r) {
+        if (!add(std::max(K.lo[r], alo), std::min(K.hi[r], ahi))) return false;
+        if (!add(std::max(K.lo[r], blo), std::min(K.hi[r], bhi))) return false;
+    }
+    return k == n;
+}
+
 hipError_t fwd_dec_chunks(const Dims& D, const SessDev& S, const LayerDev& L, int layer, int p0, int out_bits,
                           const KeySpan* span, hipStream_t s) {
     const int hp = GROUP / D.vd, lo = window_lo(L.window, p0);
@@ -2980,28 +3102,34 @@ hipError_t fwd_dec_chunks(const Dims& D, const SessDev& S, const LayerDev& L, in
     if (n < 1 || count < 1 || count > D.max_chunks || chunk > ATT_CHUNK_MAX) return hipErrorInvalidValue;
     const int blocks = D.nh / hp * count + 1;
     const KeySpan K = span ? *span : KeySpan{};
-#define NH_DC(HP, TP, EX, SP)                                                                                      \
-    hipLaunchKernelGGL((k_dec_chunks<HP, TP, EX, SP>), dim3(blocks), dim3(DG_THREADS), 0, s, D, S, L, layer, p0, \
-                       out_bits, K, n, count, chunk)
-#define NH_DC_TAPS(HP, SP)                          \
-    switch (D.taps) {                               \
-        case 1: NH_DC(HP, 1, true, SP); break;      \
-        case 2: NH_DC(HP, 2, true, SP); break;      \
-        case 3: NH_DC(HP, 3, true, SP); break;      \
-        case 4: NH_DC(HP, 4, true, SP); break;      \
-        default: NH_DC(HP, DG_MAX_TAPS, false, SP); \
+    ChunkRuns R{};
+    const bool runs = span && chunk_runs(D, K, lo, p0, n, count, chunk, R);
+#define NH_DC(HP, TP, EX, SP, RN)                                                                                      \
+    hipLaunchKernelGGL((k_dec_chunks<HP, TP, EX, SP, RN>), dim3(blocks), dim3(DG_THREADS), 0, s, D, S, L, layer, p0, \
+                       out_bits, K, n, count, chunk, R)
+#define NH_DC_TAPS(HP, SP, RN)                          \
+    switch (D.taps) {                                   \
+        case 1: NH_DC(HP, 1, true, SP, RN); break;      \
+        case 2: NH_DC(HP, 2, true, SP, RN); break;      \
+        case 3: NH_DC(HP, 3, true, SP, RN); break;      \
+        case 4: NH_DC(HP, 4, true, SP, RN); break;      \
+        default: NH_DC(HP, DG_MAX_TAPS, false, SP, RN); \
     }
     if (hp == 2) {
-        if (span) {
-            NH_DC_TAPS(2, true)
+        if (runs) {
+            NH_DC_TAPS(2, true, true)
+        } else if (span) {
+            NH_DC_TAPS(2, true, false)
         } else {
-            NH_DC_TAPS(2, false)
+            NH_DC_TAPS(2, false, false)
         }
     } else {
-        if (span) {
-            NH_DC_TAPS(4, true)
+        if (runs) {
+            NH_DC_TAPS(4, true, true)
+        } else if (span) {
+            NH_DC_TAPS(4, true, false)
         } else {
-            NH_DC_TAPS(4, false)
+            NH_DC_TAPS(4, false, false)
         }
     }
 #undef NH_DC_TAPS
