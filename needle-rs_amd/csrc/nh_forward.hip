@@ -584,10 +584,12 @@ __device__ __forceinline__ float block_rinv_t(const float* xT, int pitch, int n,
 // the result is wavefront-uniform and identical in all of them), so no
 // barrier hands it over.  The chain is latency-bound (~13 cycles a step),
 // so four wavefronts on a SIMD run their copies side by side at about the
-// cost of one for d-long operands (measured: 0.5 k cycles saved); for the
-// 4d-long mHC operand the sixteen copies' LDS reads cost more than the
-// barrier (0.7 k cycles lost), so that one stays on wavefront 0.  The phase
-// that follows must not write the operand.
+// cost of one for d-long operands: the MLP's h2 norm (measured: 0.5 k cycles
+// saved).  The other d-long norms (post norm, input norm, the head's norm)
+// measured slower this way (decode 501.6 -> 507.5 us per token, prefill
+// 1.303 -> 1.332 ms), and for the 4d-long mHC operand the sixteen copies'
+// LDS reads cost more than the barrier (0.7 k cycles lost), so those stay on
+// wavefront 0.  The phase that follows must not write the operand.
 __device__ __forceinline__ float block_rinv_all(const float* xT, int pitch, int n) {
     return rinv(dot16_t<true>(xT, xT, pitch, n, threadIdx.x & 63), n);
 }
