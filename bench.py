@@ -396,10 +396,11 @@ def needle3_decode(nh, torch, cpu_seconds: float, with_cpu: bool):
            "decode_tok_s": round(DECODE_STEPS * 1e3 / decode_ms, 1),
            "decode_ms_per_token": round(decode_ms / DECODE_STEPS, 4),
            "prompt_tok_s": round(DECODE_PROMPT * 1e3 / prompt_ms, 1),
-           # begin, batched engram key | value, engram history; per layer
-           # the layer boundary, q|k|v|gate, decode attention, out; head
-           # input, head, argmax (positions below 256 keys)
-           "runs": len(runs), "launches_per_token": 3 + 4 * layers + 3,
+           # begin (which also picks the step's token: the argmax of the
+           # previous logits), batched engram key | value, engram history;
+           # per layer the layer boundary, q|k|v|gate, decode attention,
+           # out; head input, head (positions below 256 keys)
+           "runs": len(runs), "launches_per_token": 3 + 4 * layers + 2,
            "first_picks": [int(t) for t in picks[:8]]}
     progress(f"Needle-3 decode: {out['decode_ms_per_token'] * 1e3:.1f} us per token")
     out["span"] = needle3_decode_span(nh, torch, model, prompt)

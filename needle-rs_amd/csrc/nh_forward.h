@@ -156,9 +156,11 @@ struct BeginArgs {
 // 32c .. 32c + 31): every row keeps its chunk's semantics (the block flag of
 // its products, nested key chunking, sincosf RoPE rows).
 // The start of a feed: the embedding rows into the lanes, the RoPE rows, and
-// per engram site the hashed table rows as A8 rows.
+// per engram site the hashed table rows as A8 rows.  pick (t = 1): the
+// row's token is first taken as the argmax of S.logits and stored at
+// S.tokens[p0].
 hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const BeginArgs& B, int p0, int t,
-                     hipStream_t s);
+                     hipStream_t s, bool pick = false);
 hipError_t fwd_engram_hist(const Dims& D, const Globals& G, const SessDev& S, int p0, int t, hipStream_t s);
 // The per-layer boundary for rows row0 .. row0 + rows - 1: the Hadamard MLP
 // and mHC write of layer `prev` (null: none, the lanes hold the embedding

@@ -135,6 +135,52 @@ __host__ __device__ inline int window_lo(int window, int p0) {
 
 }  // namespace
 
+// argmax (crates/needle-engine/src/generate.rs:42-50): the first maximum.
+// The reference's loop keeps index 0 when x[0] is NaN (nothing compares
+// greater) and otherwise never moves to a NaN, so NaNs are skipped and a
+// NaN first element gives 0.  Each thread keeps the first maximum of its
+// strided share (all its loads issued first); a wavefront's first maximum is the smallest index among
+// the lanes holding the wavefront's maximum (two DPP reductions; the maximum's sign of zero does not
+// matter, the lanes compare equal to it), and the
+// same again over the wavefronts' results, by every wavefront (so every
+// thread of the NT-thread block returns it; sv / si: NT / 64 entries of LDS).
+template <int NT>
+__device__ __forceinline__ uint32_t block_argmax(const float* __restrict__ x, int n, float* sv, int* si) {
+    constexpr int PER = 16;  // elements per thread read in one batch
+    constexpr int NW = NT / 64;
+    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+    const float x0 = x[0];
+    float best = -__builtin_inff();
+    int bi = n;
+    for (int base = 0; base < n; base += NT * PER) {
+        float v[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) v[k] = x[min(base + k * NT + t, n - 1)];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int i = base + k * NT + t;
+            // a NaN is never greater than the best so far: it never wins
+            if (i < n && v[k] == v[k] && (bi == n || v[k] > best)) {
+                best = v[k];
+                bi = i;
+            }
+        }
+    }
+    const float wm = wave_max_ordered(best);
+    const int wi = wave_min_i32(best == wm && bi < n ? bi : 0x7fffffff);
+    if (lane == 0) {
+        sv[wave] = wm;
+        si[wave] = wi;
+    }
+    __syncthreads();
+    const float v = lane < NW && si[min(lane, NW - 1)] != 0x7fffffff ? sv[min(lane, NW - 1)] : -__builtin_inff();
+    const int ix = lane < NW ? si[min(lane, NW - 1)] : 0x7fffffff;
+    const float m = wave_max_ordered(v);
+    const int first = wave_min_i32(v == m && ix != 0x7fffffff ? ix : 0x7fffffff);
+    return (uint32_t)(first < n && x0 == x0 ? first : 0);
+}
+
+
 // ------------------------------------------------------------------ begin
 // Per row i of the feed (position p0 + i): waves for the embedding row
 // groups (step.rs:228-235, chunk.rs:58-66: row * sqrt(d) into every lane),
@@ -146,8 +192,21 @@ __host__ __device__ inline int window_lo(int window, int p0) {
 // after the newest row the reference still keeps (D.rope_prev, the host's
 // mirror of its list) the angle-addition recurrence from that row, else
 // sincosf(freq * pos); every row also goes to the ring of recent rows.
+// PICK (one row, the greedy loop): the row's token is the argmax of the
+// previous step's logits (S.logits), worked out by every workgroup (block 0
+// stores it at S.tokens[p0]) in place of a launch of its own.
+template <bool PICK>
 __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, BeginArgs B, int p0, int t) {
     const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6, lane = threadIdx.x & 63;
+    uint32_t pick = 0;
+    if constexpr (PICK) {
+        __shared__ float sv[4];
+        __shared__ int si[4];
+        pick = block_argmax<256>(S.logits, D.out_rows, sv, si);
+        if (blockIdx.x == 0 && threadIdx.x == 0) S.tokens[p0] = pick;
+    }
+    // the token at position q of the feed (the picked one at p0)
+    auto token = [&](int q) { return PICK && q == p0 ? pick : S.tokens[q]; };
     const int Gd = (D.d + GROUP - 1) / GROUP;
     const int per_row = Gd * (1 + D.sites);
     if (wave < t * per_row) {
@@ -159,7 +218,7 @@ __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, Beg
             S.flags[i] = (i & (FWD_ROWS - 1)) < tc / 4 * 4;
         }
         if (r < Gd) {
-            const uint32_t tok = S.tokens[pos];
+            const uint32_t tok = token(pos);
             float v0, v1;
             if (B.emb.bits == 2)
                 row_group<2>(B.emb.codes, B.emb.norms, B.emb.fsel, B.emb.groups, tok, r, lane, v0, v1);
@@ -187,7 +246,7 @@ __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, Beg
                 const int oi = g / D.eheads, h = g % D.eheads, order = D.orders[oi];
                 if (pos + 1 >= order) {
                     uint32_t acc = ENGRAM_SEED * (uint32_t)(oi * D.seed_stride + h + 1);
-                    for (int j = 0; j < order; ++j) acc = (acc ^ S.tokens[pos - j]) * ENGRAM_PRIME;
+                    for (int j = 0; j < order; ++j) acc = (acc ^ token(pos - j)) * ENGRAM_PRIME;
                     acc ^= acc >> 15;
                     const uint32_t row = (uint32_t)g * (uint32_t)D.slots + acc % (uint32_t)D.slots;
                     const RowSrc& tb = B.tab[e];
@@ -228,10 +287,14 @@ __global__ __launch_bounds__(256) void k_begin(Dims D, Globals G, SessDev S, Beg
 }
 
 hipError_t fwd_begin(const Dims& D, const Globals& G, const SessDev& S, const BeginArgs& B, int p0, int t,
-                     hipStream_t s) {
+                     hipStream_t s, bool pick) {
     const int Gd = (D.d + GROUP - 1) / GROUP;
     const int waves = t * Gd * (1 + D.sites) + t;
-    hipLaunchKernelGGL(k_begin, dim3((waves + 3) / 4), dim3(256), 0, s, D, G, S, B, p0, t);
+    if (pick && t != 1) return hipErrorInvalidValue;
+    if (pick)
+        hipLaunchKernelGGL(k_begin<true>, dim3((waves + 3) / 4), dim3(256), 0, s, D, G, S, B, p0, t);
+    else
+        hipLaunchKernelGGL(k_begin<false>, dim3((waves + 3) / 4), dim3(256), 0, s, D, G, S, B, p0, t);
     return hipGetLastError();
 }
 
@@ -3140,51 +3203,12 @@ hipError_t fwd_dec_chunks(const Dims& D, const SessDev& S, const LayerDev& L, in
 }
 
 // ----------------------------------------------------------------- argmax
-// argmax (crates/needle-engine/src/generate.rs:42-50): the first maximum.
-// The reference's loop keeps index 0 when x[0] is NaN (nothing compares
-// greater) and otherwise never moves to a NaN, so NaNs are skipped and a
-// NaN first element gives 0.  Each thread keeps the first maximum of its
-// strided share (all its loads issued first); a wavefront's first maximum is the smallest index among
-// the lanes holding the wavefront's maximum (two DPP reductions; the maximum's sign of zero does not
-// matter, the lanes compare equal to it), and the
-// same again over the wavefronts' results.
+// k_argmax: block_argmax (above) by one workgroup of 1024 threads.
 __global__ __launch_bounds__(1024) void k_argmax(const float* __restrict__ x, int n, uint32_t* __restrict__ dst) {
-    constexpr int PER = 16;  // elements per thread read in one batch
-    const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
-    const float x0 = x[0];
-    float best = -__builtin_inff();
-    int bi = n;
-    for (int base = 0; base < n; base += 1024 * PER) {
-        float v[PER];
-#pragma unroll
-        for (int k = 0; k < PER; ++k) v[k] = x[min(base + k * 1024 + t, n - 1)];
-#pragma unroll
-        for (int k = 0; k < PER; ++k) {
-            const int i = base + k * 1024 + t;
-            // a NaN is never greater than the best so far: it never wins
-            if (i < n && v[k] == v[k] && (bi == n || v[k] > best)) {
-                best = v[k];
-                bi = i;
-            }
-        }
-    }
-    const float wm = wave_max_ordered(best);
-    const int wi = wave_min_i32(best == wm && bi < n ? bi : 0x7fffffff);
     __shared__ float sv[16];
     __shared__ int si[16];
-    if (lane == 0) {
-        sv[wave] = wm;
-        si[wave] = wi;
-    }
-    __syncthreads();
-    if (wave == 0) {
-        const float v = lane < 16 && si[min(lane, 15)] != 0x7fffffff ? sv[min(lane, 15)] : -__builtin_inff();
-        const int ix = lane < 16 ? si[min(lane, 15)] : 0x7fffffff;
-        const float m = wave_max_ordered(v);
-        const int first = wave_min_i32(v == m && ix != 0x7fffffff ? ix : 0x7fffffff);
-        // with x[0] NaN nothing is greater than x[best = 0]: the reference keeps 0
-        if (lane == 0) dst[0] = (uint32_t)(first < n && x0 == x0 ? first : 0);
-    }
+    const uint32_t r = block_argmax<1024>(x, n, sv, si);
+    if (threadIdx.x == 0) dst[0] = r;
 }
 
 hipError_t fwd_argmax(const float* logits, int n, uint32_t* dst, hipStream_t s) {

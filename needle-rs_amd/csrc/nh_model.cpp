@@ -534,7 +534,9 @@ int out_width(const nh_session* s, int outputs) {
 // session's copies); for several chunks the Last* modes mean the last
 // chunk's last row, All* every row.  `cells` (device, or null): the rows'
 // cells [t][layers + 1][d] (step.rs:240-243,672-714, chunk.rs:69-70,310).
-int feed(nh_session* s, int t, int outputs, float* out, float* cells, hipStream_t st) {
+// pick: the greedy loop's step, whose token is the argmax of the previous
+// step's logits, taken by the feed's first kernel.
+int feed(nh_session* s, int t, int outputs, float* out, float* cells, hipStream_t st, bool pick = false) {
     const nh_model* m = s->m;
     nh::SessDev S = s->S;
     S.cells = cells;
@@ -554,7 +556,7 @@ int feed(nh_session* s, int t, int outputs, float* out, float* cells, hipStream_
         if (int rc = span_keys(s, D, m->layers, p0, p0 + t, &span)) return rc;
         sp = &span;
     }
-    NH_TRY(nh::fwd_begin(D, m->glob, S, m->begin, p0, t, st), "feed begin");
+    NH_TRY(nh::fwd_begin(D, m->glob, S, m->begin, p0, t, st, pick), "feed begin");
     if (t == 1 && D.sites > 1 && nh::gemv_batchable(m->ekv.data(), D.sites)) {
         // every site's key | value product in one launch
         const nh_qact* acts[nh::GEMV_BATCH_MAX];
@@ -1162,9 +1164,10 @@ int nh_generate_greedy(nh_session* s, int steps, uint32_t* out, float* logits, v
     hipStream_t st = (hipStream_t)stream;
     const int len0 = s->len;
     for (int i = 0; i < steps; ++i) {
-        NH_TRY(nh::fwd_argmax(s->S.logits, s->dims.out_rows, s->S.tokens + s->len, st), "argmax");
+        // (the step's first kernel picks its token: the argmax of the
+        // previous step's logits, stored at S.tokens[len])
         float* cdst = s->track_cells ? s->d_cells + (size_t)s->ncells * s->cell_floats() : nullptr;
-        const int r = feed(s, 1, NH_OUT_LAST_LOGITS, nullptr, cdst, st);
+        const int r = feed(s, 1, NH_OUT_LAST_LOGITS, nullptr, cdst, st, true);
         if (r < 0) return reset_after(s, r);
         if (cdst) ++s->ncells;
     }
