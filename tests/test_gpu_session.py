@@ -427,8 +427,9 @@ def test_greedy_picks_into_pinned_memory(nh):
 def test_random_session_scripts(nh, seed):
     """A seeded random script of feeds (every Outputs mode, lengths across the
     chunk and batch boundaries), prefills, single steps, rollbacks within the
-    last feeds, clones, rewinds and, for some seeds, an attention span; every
-    result bit-identical to the oracle running the same script."""
+    last feeds, clones, rewinds and, for some seeds, an attention span and
+    tracked cells (compared after every rollback, clone and rewind and at the
+    end); every result bit-identical to the oracle running the same script."""
     rng = np.random.default_rng(1000 + seed)
     geoms = [SMALL, dict(vocab=300, num_layers=2, engram_slots=64, engram_sites=(0,), global_layers=(0,),
                          sliding_window=48, qkv_conv_taps=4)]
@@ -438,6 +439,14 @@ def test_random_session_scripts(nh, seed):
     p = Pair(nh, data, cap)
     if seed == 1:
         p.attend(int(rng.integers(2, 9)), int(rng.choice([32, 48, 64])))
+    track = seed != 0
+    if track:
+        p.g.track_cells()
+        p.o.track_cells()
+
+    def check_cells(label):
+        if track:
+            same(f"cells {label}", p.g.cells().cpu().numpy(), p.o.cells(), p.stats)
     since = 0  # positions fed since the last rollback or rewind (what a rollback may drop)
     hidden = False
     say(f"random session script, seed {seed}")
@@ -467,12 +476,16 @@ def test_random_session_scripts(nh, seed):
                 continue
             p.rollback(n)
             since -= n
+            check_cells(f"after rollback {n} at op {op}")
         elif kind == "clone":
             p = p.clone()
+            check_cells(f"of a clone at op {op}")
         elif kind == "rewind":
             length = int(rng.integers(0, len(p.g) + 1))
             p.rewind_zeroed(length)
             since = 0
+            check_cells(f"after rewind to {length} at op {op}")
         elif kind == "heads" and hidden:
             p.heads(rng.integers(0, 300, 5))
+    check_cells("at the end")
     p.done(f"random session script {seed}")
