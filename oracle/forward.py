@@ -349,9 +349,13 @@ class Session:
 
     def _run(self, fn, toks, outputs):
         t = np.ascontiguousarray(np.asarray(toks, dtype=np.uint32).reshape(-1))
-        rows_max = t.size if outputs in (OUT_ALL_LOGITS, OUT_HIDDEN) else 1
+        # a prefill's re-feed returns rows for the positions it feeds again
+        # too (infer.rs:1090-1100): up to the session's length more
+        rows_max = t.size + (len(self) if fn is _lib().nf_prefill else 0) \
+            if outputs in (OUT_ALL_LOGITS, OUT_HIDDEN) else 1
         out = np.zeros((max(rows_max, 1), self._width(outputs)), dtype=np.float32)
         r = fn(self.f.m, self.s, _p(t), t.size, int(outputs), _p(out), self.f.threads)
+        assert r <= out.shape[0], "the oracle wrote past its output rows"
         if r < 0:
             raise ValueError("feed outside the session's capacity, geometry or key runs")
         return out[:r]

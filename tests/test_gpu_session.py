@@ -423,7 +423,7 @@ def test_greedy_picks_into_pinned_memory(nh):
     p.done("greedy picks into pinned memory")
 
 
-@pytest.mark.parametrize("seed", [0, 1, 2])
+@pytest.mark.parametrize("seed", [0, 1, 2, 3, 4, 5])
 def test_random_session_scripts(nh, seed):
     """A seeded random script of feeds (every Outputs mode, lengths across the
     chunk and batch boundaries), prefills, single steps, rollbacks within the
@@ -437,7 +437,7 @@ def test_random_session_scripts(nh, seed):
     data = archive(g, seed=90 + seed)
     cap = 260
     p = Pair(nh, data, cap)
-    if seed == 1:
+    if seed in (1, 4):
         p.attend(int(rng.integers(2, 9)), int(rng.choice([32, 48, 64])))
     track = seed != 0
     if track:

@@ -478,6 +478,21 @@ def test_stale_slots_are_skipped_and_prefill_refeeds():
         fresh.forward([int(t)], forward.OUT_NONE)
     want = fresh.forward(np.concatenate([toks[26:57], [5]]))
     assert len(s) == 58 and np.array_equal(bits(got), bits(want))
+    # with AllLogits the re-feed returns a row for every position it feeds
+    # (two new tokens end the ring at 59, so 27 is the first stale slot: 30
+    # again and the two new ones), not only the new tokens'
+    s2 = f.session(96)
+    s2.set_attend(sink, ring)
+    for t in toks:
+        s2.forward([int(t)], forward.OUT_NONE)
+    s2.rollback(3)
+    rows = s2.prefill([5, 6], forward.OUT_ALL_LOGITS)
+    fresh = f.session(96)
+    fresh.set_attend(sink, ring)
+    for t in toks[:27]:
+        fresh.forward([int(t)], forward.OUT_NONE)
+    want = fresh.forward(np.concatenate([toks[27:57], [5, 6]]), forward.OUT_ALL_LOGITS)
+    assert rows.shape == want.shape == (32, 300) and np.array_equal(bits(rows), bits(want))
 
 
 # ---------------------------------------------------------------- outputs
